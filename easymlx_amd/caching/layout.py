@@ -1,0 +1,66 @@
+"""Host-side conversions between the MLX-style logical affine KV layout and pages.
+
+Logical layout (what ``mlx.core.quantize`` of a ``[tokens, Hkv, D]`` K/V
+tensor gives, scattered into ``[num_blocks, block_size, ...]`` like the
+reference's dense cache ``lib/python/easymlx/caching/paged/cache.py:790-791``):
+
+    codes  uint32 [nb, bs, Hkv, D*bits/32]
+    scales fp16   [nb, bs, Hkv, D/gs]        (biases likewise)
+
+Page layout used by the kernels (see ``include/emx_attn.h``):
+
+    key codes    uint32 [nb, Hkv, bs, D*bits/32]   token-major
+    value codes  uint32 [nb, Hkv, D, bs*bits/32]   dim-major (tokens packed along a word)
+    scales       fp16   [nb, Hkv, D/gs, bs]         (biases likewise)
+
+NumPy only; used to build pages from host data and to read pages back.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+
+def _unpack(words: np.ndarray, bits: int) -> np.ndarray:
+    per = 32 // bits
+    sh = (np.arange(per, dtype=np.uint32) * np.uint32(bits)).astype(np.uint32)
+    q = (words.astype(np.uint32)[..., None] >> sh) & np.uint32((1 << bits) - 1)
+    return q.reshape(*words.shape[:-1], words.shape[-1] * per)
+
+
+def _pack(q: np.ndarray, bits: int) -> np.ndarray:
+    per = 32 // bits
+    q = q.astype(np.uint32).reshape(*q.shape[:-1], q.shape[-1] // per, per)
+    sh = (np.arange(per, dtype=np.uint32) * np.uint32(bits)).astype(np.uint32)
+    return np.bitwise_or.reduce(q << sh, axis=-1).astype(np.uint32)
+
+
+def key_pages_from_logical(codes: np.ndarray) -> np.ndarray:
+    """``[nb, bs, Hkv, W]`` -> ``[nb, Hkv, bs, W]``."""
+    return np.ascontiguousarray(np.asarray(codes, dtype=np.uint32).transpose(0, 2, 1, 3))
+
+
+def key_logical_from_pages(pages: np.ndarray) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(pages).view(np.uint32).transpose(0, 2, 1, 3))
+
+
+def value_pages_from_logical(codes: np.ndarray, bits: int) -> np.ndarray:
+    """``[nb, bs, Hkv, W]`` -> ``[nb, Hkv, D, bs*bits/32]`` (tokens packed per word)."""
+    q = _unpack(np.asarray(codes, dtype=np.uint32), bits)  # [nb, bs, Hkv, D]
+    q = q.transpose(0, 2, 3, 1)  # [nb, Hkv, D, bs]
+    return np.ascontiguousarray(_pack(q, bits))
+
+
+def value_logical_from_pages(pages: np.ndarray, bits: int) -> np.ndarray:
+    q = _unpack(np.asarray(pages).view(np.uint32), bits)  # [nb, Hkv, D, bs]
+    q = q.transpose(0, 3, 1, 2)  # [nb, bs, Hkv, D]
+    return np.ascontiguousarray(_pack(q, bits))
+
+
+def params_pages_from_logical(p: np.ndarray) -> np.ndarray:
+    """scales/biases ``[nb, bs, Hkv, G]`` -> ``[nb, Hkv, G, bs]``."""
+    return np.ascontiguousarray(np.asarray(p).transpose(0, 2, 3, 1))
+
+
+def params_logical_from_pages(p: np.ndarray) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(p).transpose(0, 3, 1, 2))

@@ -1,0 +1,436 @@
+"""Paged KV cache views on the GPU (torch tensors, HIP write kernels).
+
+Mirrors the write-side contract of the reference's ``PageCacheView``
+(``lib/python/easymlx/caching/paged/cache.py:499-1306``) and its metadata
+(``PageMetadata`` ``:1468-1543``, ``build_query_start_loc`` ``:1448-1465``):
+
+* ``PageCacheView`` -- unquantized cache in the reference layout
+  ``[num_blocks, block_size, Hkv, D]``.
+* ``AffinePageCacheView`` -- int4/int8 affine pages (codes + per-(token, group)
+  fp16 scale and bias), written by the fused quantize-on-write kernel.
+
+``concatenate_to_cache`` keeps the reference's signature and return value
+``(queries, key_cache, value_cache, resolved_metadata)``.  Block tables and
+``kv_lens`` live on the device; slot arithmetic for a step is done with a few
+device ops, never with a host round trip of device data.
+"""
+
+from __future__ import annotations
+
+import math
+import typing as tp
+from dataclasses import dataclass
+
+import torch
+
+from .. import _native
+
+
+@dataclass
+class PageMetadata:
+    """Kernel-agnostic paged-attention metadata (``cache.py:1468-1543``)."""
+
+    query_start_loc: tp.Any
+    block_tables: tp.Any = None
+    kv_lens: tp.Any = None
+    block_size: int | None = None
+    sliding_window: int | None = None
+    is_single_token_decode: bool = False
+    slot_ids: tuple[int, ...] | None = None
+
+    def with_cache_state(self, *, block_tables, kv_lens, block_size: int) -> "PageMetadata":
+        return PageMetadata(
+            query_start_loc=self.query_start_loc,
+            block_tables=block_tables,
+            kv_lens=kv_lens,
+            block_size=int(block_size),
+            sliding_window=self.sliding_window,
+            is_single_token_decode=self.is_single_token_decode,
+            slot_ids=self.slot_ids,
+        )
+
+    def with_sliding_window(self, sliding_window: int | None) -> "PageMetadata":
+        return PageMetadata(
+            query_start_loc=self.query_start_loc,
+            block_tables=self.block_tables,
+            kv_lens=self.kv_lens,
+            block_size=self.block_size,
+            sliding_window=sliding_window,
+            is_single_token_decode=self.is_single_token_decode,
+            slot_ids=self.slot_ids,
+        )
+
+
+def build_query_start_loc(query_lens: tp.Iterable[int], device=None) -> torch.Tensor:
+    """Cumulative query start offsets starting at zero, int32 (``cache.py:1448-1465``)."""
+    offsets = [0]
+    for n in query_lens:
+        offsets.append(offsets[-1] + int(n))
+    return torch.tensor(offsets, dtype=torch.int32, device=device)
+
+
+def _stream_ptr(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _contiguous_tables(num_seqs: int, blocks_per_seq: int, device) -> torch.Tensor:
+    # Each sequence owns ``blocks_per_seq`` consecutive blocks (``cache.py:779-786``).
+    return torch.arange(num_seqs * blocks_per_seq, dtype=torch.int32, device=device).reshape(num_seqs, blocks_per_seq)
+
+
+class PageCacheView:
+    """Unquantized paged cache ``[num_blocks, block_size, Hkv, D]`` (``cache.py:700-825``)."""
+
+    is_affine = False
+
+    def __init__(self, *, key_cache, value_cache, block_tables, kv_lens, block_size, num_kv_heads, head_dim):
+        self.key_cache = key_cache
+        self.value_cache = value_cache
+        self.block_tables = block_tables
+        self.kv_lens = kv_lens
+        self.block_size = int(block_size)
+        self.num_kv_heads = int(num_kv_heads)
+        self.head_dim = int(head_dim)
+
+    @classmethod
+    def init(
+        cls,
+        *,
+        num_seqs: int,
+        max_seq_len: int,
+        num_kv_heads: int,
+        head_dim: int,
+        block_size: int = 16,
+        dtype: torch.dtype = torch.float16,
+        device: tp.Any = "cuda",
+    ) -> "PageCacheView":
+        if num_seqs <= 0:
+            raise ValueError("num_seqs must be positive")
+        if max_seq_len <= 0:
+            raise ValueError("max_seq_len must be positive")
+        if block_size <= 0:
+            raise ValueError("block_size must be positive")
+        bps = math.ceil(max_seq_len / block_size)
+        nb = bps * num_seqs
+        shape = (nb, block_size, num_kv_heads, head_dim)
+        return cls(
+            key_cache=torch.zeros(shape, dtype=dtype, device=device),
+            value_cache=torch.zeros(shape, dtype=dtype, device=device),
+            block_tables=_contiguous_tables(num_seqs, bps, device),
+            kv_lens=torch.zeros((num_seqs,), dtype=torch.int32, device=device),
+            block_size=block_size,
+            num_kv_heads=num_kv_heads,
+            head_dim=head_dim,
+        )
+
+    allocate = init
+
+    @property
+    def num_seqs(self) -> int:
+        return int(self.block_tables.shape[0])
+
+    @property
+    def blocks_per_seq(self) -> int:
+        return int(self.block_tables.shape[1])
+
+    @property
+    def max_seq_len(self) -> int:
+        return self.blocks_per_seq * self.block_size
+
+    @property
+    def num_blocks(self) -> int:
+        return int(self.key_cache.shape[0])
+
+    # -- slot arithmetic shared by both views (cache.py:1127-1170, 1230-1261)
+    def _slot_mapping(self, slot_ids, query_lens) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+        dev = self.block_tables.device
+        qlens = [max(0, int(q)) for q in query_lens]
+        slots = torch.tensor(list(slot_ids), dtype=torch.long, device=dev)
+        base = self.kv_lens.index_select(0, slots).to(torch.long)
+        total = sum(qlens)
+        if total == 0:
+            return torch.empty((0,), dtype=torch.int32, device=dev), slots, base
+        qlen_t = torch.tensor(qlens, dtype=torch.long, device=dev)
+        tok_slot = torch.repeat_interleave(slots, qlen_t, output_size=total)
+        starts = [0]
+        for q in qlens[:-1]:
+            starts.append(starts[-1] + q)
+        local = torch.arange(total, device=dev) - torch.repeat_interleave(
+            torch.tensor(starts, dtype=torch.long, device=dev), qlen_t, output_size=total
+        )
+        pos = torch.repeat_interleave(base, qlen_t, output_size=total) + local
+        col = torch.clamp(pos // self.block_size, max=self.blocks_per_seq - 1)
+        blk = self.block_tables[tok_slot, col].to(torch.long)
+        ok = (blk >= 0) & (pos // self.block_size < self.blocks_per_seq)
+        mapping = torch.where(ok, blk * self.block_size + pos % self.block_size, torch.full_like(blk, -1))
+        return mapping.to(torch.int32), slots, base
+
+    def _resolve(self, cache_metadata, slot_ids, query_lens, n_tokens):
+        if slot_ids is None:
+            slot_ids = getattr(cache_metadata, "slot_ids", None) or ()
+        slot_ids = tuple(int(s) for s in slot_ids)
+        if query_lens is not None:
+            qlens = [int(q) for q in query_lens]
+        else:
+            qsl = cache_metadata.query_start_loc
+            qsl = qsl.tolist() if isinstance(qsl, torch.Tensor) else list(qsl)
+            qlens = [int(qsl[i + 1]) - int(qsl[i]) for i in range(len(slot_ids))]
+        single = bool(qlens) and n_tokens == len(qlens) and all(q == 1 for q in qlens)
+        return slot_ids, qlens, single
+
+    def _apply_rope(self, rope, queries, keys, slots, base, qlens, single):
+        if rope is None:
+            return queries, keys
+        if single:
+            qb = queries.unsqueeze(1).transpose(1, 2)
+            kb = keys.unsqueeze(1).transpose(1, 2)
+            return (
+                rope(qb, offset=base).transpose(1, 2)[:, 0],
+                rope(kb, offset=base).transpose(1, 2)[:, 0],
+            )
+        q_out, k_out, start = [], [], 0
+        base_host = base.tolist()
+        for i, n in enumerate(qlens):
+            if n <= 0:
+                continue
+            qc = queries[start : start + n][None].transpose(1, 2)
+            kc = keys[start : start + n][None].transpose(1, 2)
+            q_out.append(rope(qc, offset=int(base_host[i])).transpose(1, 2)[0])
+            k_out.append(rope(kc, offset=int(base_host[i])).transpose(1, 2)[0])
+            start += n
+        if not q_out:
+            return queries[:0], keys[:0]
+        return torch.cat(q_out), torch.cat(k_out)
+
+    def _write(self, keys, values, slot_mapping):
+        ok = slot_mapping >= 0
+        idx = slot_mapping[ok].to(torch.long)
+        kc = self.key_cache.view(-1, self.num_kv_heads, self.head_dim)
+        vc = self.value_cache.view(-1, self.num_kv_heads, self.head_dim)
+        kc[idx] = keys[ok].to(kc.dtype)
+        vc[idx] = values[ok].to(vc.dtype)
+
+    def concatenate_to_cache(
+        self,
+        queries: torch.Tensor,
+        keys: torch.Tensor,
+        values: torch.Tensor,
+        *,
+        cache_metadata: tp.Any,
+        rope: tp.Any = None,
+        slot_ids: tp.Sequence[int] | None = None,
+        query_lens: tp.Sequence[int] | None = None,
+    ):
+        """Append K/V for the scheduled slots (``cache.py:1088-1306``)."""
+        slot_ids, qlens, single = self._resolve(cache_metadata, slot_ids, query_lens, int(queries.shape[0]))
+        slot_mapping, slots, base = self._slot_mapping(slot_ids, qlens)
+        queries, keys = self._apply_rope(rope, queries, keys, slots, base, qlens, single)
+        if slot_mapping.numel():
+            self._write(keys.contiguous(), values.contiguous(), slot_mapping)
+        if len(slot_ids):
+            add = torch.tensor(qlens, dtype=torch.int32, device=self.kv_lens.device)
+            self.kv_lens.index_copy_(0, slots, (base + add).to(torch.int32))
+        md = cache_metadata.with_cache_state(
+            block_tables=self.block_tables.index_select(0, slots) if len(slot_ids) else self.block_tables[:0],
+            kv_lens=self.kv_lens.index_select(0, slots) if len(slot_ids) else self.kv_lens[:0],
+            block_size=self.block_size,
+        )
+        md.is_single_token_decode = single
+        return queries, self.key_cache, self.value_cache, md
+
+    def append(self, seq_idx: int, key: torch.Tensor, value: torch.Tensor) -> None:
+        """Append ``[num_tokens, Hkv, D]`` tokens to one sequence (``cache.py:834-872``)."""
+        if key.shape != value.shape:
+            raise ValueError("key and value must have the same shape")
+        if key.ndim != 3:
+            raise ValueError("key/value must be rank-3: [num_tokens, num_kv_heads, head_dim]")
+        if key.shape[1] != self.num_kv_heads or key.shape[2] != self.head_dim:
+            raise ValueError("key/value head dims do not match cache")
+        if seq_idx < 0 or seq_idx >= self.num_seqs:
+            raise IndexError(f"Invalid seq_idx {seq_idx}")
+        start = int(self.kv_lens[seq_idx].item())
+        n = int(key.shape[0])
+        if start + n > self.max_seq_len:
+            raise ValueError("Cannot append tokens: sequence length would exceed cache capacity")
+        slot_mapping, _, _ = self._slot_mapping([seq_idx], [n])
+        if n:
+            self._write(key.to(self.block_tables.device).contiguous(), value.to(self.block_tables.device).contiguous(),
+                        slot_mapping)
+        self.kv_lens[seq_idx] = start + n
+
+    def reset(self, seq_idx: int) -> None:
+        """Zero one sequence's pages and its length (``cache.py:874-906``, with page ids used correctly)."""
+        if seq_idx < 0 or seq_idx >= self.num_seqs:
+            raise IndexError(f"Invalid seq_idx {seq_idx}")
+        ids = self.block_tables[seq_idx]
+        ids = ids[(ids >= 0) & (ids < self.num_blocks)].to(torch.long)
+        self._zero_blocks(ids)
+        self.kv_lens[seq_idx] = 0
+
+    def _zero_blocks(self, ids: torch.Tensor) -> None:
+        self.key_cache[ids] = 0
+        self.value_cache[ids] = 0
+
+
+class AffinePageCacheView(PageCacheView):
+    """Affine int4/int8 KV pages with fused quantize-on-write.
+
+    Storage (see ``include/emx_attn.h``): key codes ``[nb, Hkv, bs, D*b/32]``,
+    value codes ``[nb, Hkv, D, bs*b/32]`` (int32 tensors holding uint32 words),
+    scales/biases ``[nb, Hkv, D/gs, bs]`` fp16.  The reference has no affine KV
+    cache; its FP8 cache (``cache.py:770-797, 1171-1184``) is the structural
+    analogue, with the per-block running-max scale replaced by MLX's affine
+    per-(token, group) scale and bias.
+    """
+
+    is_affine = True
+
+    def __init__(self, *, k_codes, k_scales, k_biases, v_codes, v_scales, v_biases, block_tables, kv_lens, block_size,
+                 num_kv_heads, head_dim, bits, group_size):
+        super().__init__(key_cache=k_codes, value_cache=v_codes, block_tables=block_tables, kv_lens=kv_lens,
+                         block_size=block_size, num_kv_heads=num_kv_heads, head_dim=head_dim)
+        self.k_scales = k_scales
+        self.k_biases = k_biases
+        self.v_scales = v_scales
+        self.v_biases = v_biases
+        self.bits = int(bits)
+        self.group_size = int(group_size)
+
+    @classmethod
+    def init(
+        cls,
+        *,
+        num_seqs: int,
+        max_seq_len: int,
+        num_kv_heads: int,
+        head_dim: int,
+        block_size: int = 128,
+        bits: int = 4,
+        group_size: int = 64,
+        num_blocks: int | None = None,
+        device: tp.Any = "cuda",
+    ) -> "AffinePageCacheView":
+        if num_seqs <= 0:
+            raise ValueError("num_seqs must be positive")
+        if max_seq_len <= 0:
+            raise ValueError("max_seq_len must be positive")
+        if block_size <= 0:
+            raise ValueError("block_size must be positive")
+        if bits not in (4, 8):
+            raise ValueError("bits must be 4 or 8")
+        if group_size <= 0 or head_dim % group_size or group_size % 8:
+            raise ValueError("head_dim must be a multiple of group_size, itself a multiple of 8")
+        if (block_size * bits) % 32 or (head_dim * bits) % 32:
+            raise ValueError("block_size * bits and head_dim * bits must be multiples of 32")
+        bps = math.ceil(max_seq_len / block_size)
+        nb = num_blocks if num_blocks is not None else bps * num_seqs
+        if nb < bps * num_seqs:
+            raise ValueError("num_blocks is smaller than num_seqs * ceil(max_seq_len / block_size)")
+        G = head_dim // group_size
+        z = lambda shape, dt: torch.zeros(shape, dtype=dt, device=device)  # noqa: E731
+        return cls(
+            k_codes=z((nb, num_kv_heads, block_size, head_dim * bits // 32), torch.int32),
+            k_scales=z((nb, num_kv_heads, G, block_size), torch.float16),
+            k_biases=z((nb, num_kv_heads, G, block_size), torch.float16),
+            v_codes=z((nb, num_kv_heads, head_dim, block_size * bits // 32), torch.int32),
+            v_scales=z((nb, num_kv_heads, G, block_size), torch.float16),
+            v_biases=z((nb, num_kv_heads, G, block_size), torch.float16),
+            block_tables=_contiguous_tables(num_seqs, bps, device),
+            kv_lens=z((num_seqs,), torch.int32),
+            block_size=block_size,
+            num_kv_heads=num_kv_heads,
+            head_dim=head_dim,
+            bits=bits,
+            group_size=group_size,
+        )
+
+    allocate = init
+
+    @property
+    def k_codes(self) -> torch.Tensor:
+        return self.key_cache
+
+    @property
+    def v_codes(self) -> torch.Tensor:
+        return self.value_cache
+
+    def _write(self, keys, values, slot_mapping):
+        if keys.dtype != torch.float16 or values.dtype != torch.float16:
+            keys = keys.to(torch.float16)
+            values = values.to(torch.float16)
+        keys = keys.contiguous()
+        values = values.contiguous()
+        slot_mapping = slot_mapping.to(torch.int32).contiguous()
+        lib = _native.load()
+        _native.check(
+            lib.emx_affine_cache_write(
+                keys.data_ptr(),
+                values.data_ptr(),
+                slot_mapping.data_ptr(),
+                int(keys.shape[0]),
+                self.num_kv_heads,
+                self.head_dim,
+                self.group_size,
+                self.bits,
+                self.block_size,
+                self.num_blocks,
+                self.key_cache.data_ptr(),
+                self.k_scales.data_ptr(),
+                self.k_biases.data_ptr(),
+                self.value_cache.data_ptr(),
+                self.v_scales.data_ptr(),
+                self.v_biases.data_ptr(),
+                _stream_ptr(keys.device),
+            )
+        )
+
+    def write_slots(self, keys: torch.Tensor, values: torch.Tensor, slot_mapping: torch.Tensor) -> None:
+        """Quantize-on-write ``[T, Hkv, D]`` tokens to flat slots ``block * bs + offset`` (-1 = skip).
+
+        The affine counterpart of the reference's ``reshape_and_cache``
+        (``cache.py:36-93, 281-337``); ``kv_lens`` is not touched.
+        """
+        if keys.shape != values.shape or keys.ndim != 3:
+            raise ValueError("keys/values must be [num_tokens, num_kv_heads, head_dim] of equal shape")
+        if keys.shape[1] != self.num_kv_heads or keys.shape[2] != self.head_dim:
+            raise ValueError("key/value head dims do not match cache")
+        if slot_mapping.shape != (keys.shape[0],):
+            raise ValueError("slot_mapping must be [num_tokens]")
+        if keys.shape[0]:
+            self._write(keys, values, slot_mapping)
+
+    def _zero_blocks(self, ids: torch.Tensor) -> None:
+        for t in (self.key_cache, self.value_cache, self.k_scales, self.k_biases, self.v_scales, self.v_biases):
+            t[ids] = 0
+
+
+def affine_pool(
+    *,
+    num_blocks: int,
+    num_kv_heads: int,
+    head_dim: int,
+    block_size: int,
+    bits: int,
+    group_size: int,
+    block_tables: torch.Tensor,
+    kv_lens: torch.Tensor,
+) -> AffinePageCacheView:
+    """An empty affine page pool with caller-provided block tables / lengths."""
+    dev = block_tables.device
+    G = head_dim // group_size
+    z = lambda shape, dt: torch.zeros(shape, dtype=dt, device=dev)  # noqa: E731
+    return AffinePageCacheView(
+        k_codes=z((num_blocks, num_kv_heads, block_size, head_dim * bits // 32), torch.int32),
+        k_scales=z((num_blocks, num_kv_heads, G, block_size), torch.float16),
+        k_biases=z((num_blocks, num_kv_heads, G, block_size), torch.float16),
+        v_codes=z((num_blocks, num_kv_heads, head_dim, block_size * bits // 32), torch.int32),
+        v_scales=z((num_blocks, num_kv_heads, G, block_size), torch.float16),
+        v_biases=z((num_blocks, num_kv_heads, G, block_size), torch.float16),
+        block_tables=block_tables.to(torch.int32).contiguous(),
+        kv_lens=kv_lens.to(torch.int32).contiguous(),
+        block_size=block_size,
+        num_kv_heads=num_kv_heads,
+        head_dim=head_dim,
+        bits=bits,
+        group_size=group_size,
+    )

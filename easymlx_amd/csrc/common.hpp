@@ -1,0 +1,77 @@
+// Shared device helpers for the emx_attn kernels (gfx950 / CDNA4, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace emx {
+
+typedef _Float16 h16;
+typedef h16 h16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kTwo24 = 16777216.0f;  // codes enter the MFMA as fp16 subnormals n * 2^-24
+
+__device__ __forceinline__ h16x8 as_h8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+  u32x4 v = {a, b, c, d};
+  return __builtin_bit_cast(h16x8, v);
+}
+
+// One uint32 of eight 4-bit codes -> eight exact fp16 subnormals (code * 2^-24).
+// Element order: (n0, n4, n1, n5, n2, n6, n3, n7).
+__device__ __forceinline__ h16x8 unpack4(uint32_t w) {
+  return as_h8(w & 0x000F000Fu, (w >> 4) & 0x000F000Fu, (w >> 8) & 0x000F000Fu, (w >> 12) & 0x000F000Fu);
+}
+
+// Two uint32 of four 8-bit codes each -> eight exact fp16 subnormals, in order.
+__device__ __forceinline__ h16x8 unpack8(uint32_t w0, uint32_t w1) {
+  return as_h8(__builtin_amdgcn_perm(0u, w0, 0x0C010C00u), __builtin_amdgcn_perm(0u, w0, 0x0C030C02u),
+               __builtin_amdgcn_perm(0u, w1, 0x0C010C00u), __builtin_amdgcn_perm(0u, w1, 0x0C030C02u));
+}
+
+// Position (0..7 within the 8 codes of one MFMA k-slice) of MFMA element i.
+template <int BITS>
+__device__ __forceinline__ constexpr int slot_perm(int i) {
+  return BITS == 4 ? ((i >> 1) + ((i & 1) << 2)) : i;
+}
+
+__device__ __forceinline__ f32x4 mfma16x16x32(h16x8 a, h16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t v) { return __uint_as_float(((uint32_t)v) << 16); }
+
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t x = __float_as_uint(f);
+  if ((x & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((x >> 16) | 0x40u);  // quiet NaN
+  uint32_t r = x + 0x7fffu + ((x >> 16) & 1u);
+  return (uint16_t)(r >> 16);
+}
+
+// Element type tags for the dense (unquantized) cache path.
+struct F16 { typedef h16 T; };
+struct BF16 { typedef uint16_t T; };
+struct F32 { typedef float T; };
+
+__device__ __forceinline__ float to_f32(h16 v) { return (float)v; }
+__device__ __forceinline__ float to_f32(float v) { return v; }
+__device__ __forceinline__ float to_f32(uint16_t v) { return bf16_to_f32(v); }
+__device__ __forceinline__ void from_f32(float f, h16* p) { *p = (h16)f; }
+__device__ __forceinline__ void from_f32(float f, float* p) { *p = f; }
+__device__ __forceinline__ void from_f32(float f, uint16_t* p) { *p = f32_to_bf16(f); }
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+}  // namespace emx

@@ -1,0 +1,373 @@
+// C-ABI entry points of libemx_attn.so (declared in include/emx_attn.h).
+// Host-side validation happens here so that no kernel is launched with shapes
+// it does not assume.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "../../include/emx_attn.h"
+#include "decode_affine.hpp"
+#include "paged_generic.hpp"
+#include "quantize.hpp"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(EMX_ERR_HIP, "%s: launch failed: %s", what, hipGetErrorString(e));
+  return EMX_OK;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+constexpr int kTile = 128;        // tokens per decode tile
+constexpr int kWavesPerWG = 4;
+constexpr int kMaxSplits = 512;
+
+// Tiles per split for the decode kernel: one tile per wave unless that would
+// exceed kMaxSplits partitions for the longest possible sequence.
+int decode_tiles_per_split(int max_blocks, int page_size) {
+  const long max_tiles = (long)max_blocks * page_size / kTile;
+  int tps = kWavesPerWG;
+  while ((max_tiles + tps - 1) / tps > kMaxSplits) tps += kWavesPerWG;
+  return tps;
+}
+
+int decode_max_splits(int max_blocks, int page_size) {
+  const long max_tiles = (long)max_blocks * page_size / kTile;
+  const int tps = decode_tiles_per_split(max_blocks, page_size);
+  return (int)((max_tiles + tps - 1) / tps);
+}
+
+bool decode_fast_path(int head_dim, int page_size, int bits, int group_size, int hg) {
+  if (head_dim != 128 || page_size % kTile != 0) return false;
+  if (bits != 4 && bits != 8) return false;
+  if (group_size != 32 && group_size != 64 && group_size != 128) return false;
+  if (hg < 1 || hg > 16 || (hg & (hg - 1)) != 0) return false;
+  return hg * (head_dim / group_size) <= 16;
+}
+
+typedef void (*DecodeFn)(emx::DecodeArgs);
+
+template <int BITS, int GS>
+DecodeFn pick_decode_hg(int hg) {
+  constexpr int G = 128 / GS;
+  switch (hg) {
+    case 1: return emx::decode_affine_d128<BITS, GS, 1>;
+    case 2: return emx::decode_affine_d128<BITS, GS, 2>;
+    case 4: return emx::decode_affine_d128<BITS, GS, 4>;
+    case 8: if constexpr (8 * G <= 16) return emx::decode_affine_d128<BITS, GS, 8>; else return nullptr;
+    case 16: if constexpr (16 * G <= 16) return emx::decode_affine_d128<BITS, GS, 16>; else return nullptr;
+  }
+  return nullptr;
+}
+
+template <int BITS>
+DecodeFn pick_decode_gs(int gs, int hg) {
+  switch (gs) {
+    case 32: return pick_decode_hg<BITS, 32>(hg);
+    case 64: return pick_decode_hg<BITS, 64>(hg);
+    case 128: return pick_decode_hg<BITS, 128>(hg);
+  }
+  return nullptr;
+}
+
+int validate_common(const void* q, int num_tokens, int hq, int d, int hkv, int nb, int bs, const int32_t* bt, int S,
+                    int max_blocks, const int32_t* kv_lens, const int32_t* qsl, int decode, const void* out) {
+  if (num_tokens < 0 || S < 0) return fail(EMX_ERR_INVALID, "num_tokens/num_seqs must be >= 0");
+  if (hq <= 0 || hkv <= 0 || d <= 0) return fail(EMX_ERR_INVALID, "head counts and head_dim must be positive");
+  if (hq % hkv != 0) return fail(EMX_ERR_INVALID, "num_q_heads must be divisible by num_kv_heads (GQA)");
+  if (d > 256) return fail(EMX_ERR_UNSUPPORTED, "head_dim %d > 256 is not supported", d);
+  if (bs <= 0 || nb <= 0) return fail(EMX_ERR_INVALID, "page_size and num_blocks must be positive");
+  if (max_blocks <= 0 && S > 0) return fail(EMX_ERR_INVALID, "max_blocks_per_seq must be positive");
+  if (num_tokens > 0 && (!q || !out)) return fail(EMX_ERR_INVALID, "queries/out must not be null");
+  if (S > 0 && (!bt || !kv_lens)) return fail(EMX_ERR_INVALID, "block_tables/kv_lens must not be null");
+  if (decode) {
+    if (num_tokens != S) return fail(EMX_ERR_INVALID, "single_token_decode requires num_tokens == num_seqs");
+  } else if (S > 0 && !qsl) {
+    return fail(EMX_ERR_INVALID, "query_start_loc must not be null");
+  }
+  return EMX_OK;
+}
+
+template <typename QT, typename KV>
+int launch_generic(const emx::GenericArgs& ga, const KV& kv, hipStream_t st) {
+  const int hg = ga.Hq / ga.Hkv;
+  dim3 grid(ga.T, ga.Hkv, (hg + 15) / 16);
+  hipLaunchKernelGGL((emx::paged_generic<QT, KV>), grid, dim3(64), 0, st, ga, kv);
+  return check_launch("paged_generic");
+}
+
+}  // namespace
+
+extern "C" {
+
+int emx_version(void) { return 100; }
+
+const char* emx_last_error(void) { return g_last_error.c_str(); }
+
+int emx_affine_quantize(const void* x, long rows, int head_dim, int group_size, int bits, uint32_t* codes,
+                        void* scales, void* biases, void* stream) {
+  if (rows < 0) return fail(EMX_ERR_INVALID, "rows must be >= 0");
+  if (bits != 4 && bits != 8) return fail(EMX_ERR_UNSUPPORTED, "bits must be 4 or 8, got %d", bits);
+  if (group_size <= 0 || group_size % 8 != 0 || head_dim % group_size != 0)
+    return fail(EMX_ERR_INVALID, "head_dim %d must be a multiple of group_size %d (a multiple of 8)", head_dim,
+                group_size);
+  if (rows == 0) return EMX_OK;
+  if (!x || !codes || !scales || !biases) return fail(EMX_ERR_INVALID, "null pointer");
+  if (!aligned16(x)) return fail(EMX_ERR_INVALID, "x must be 16-byte aligned");
+  const long n = rows * (head_dim / group_size);
+  const int blocks = (int)((n + 255) / 256);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const emx::h16* xp = reinterpret_cast<const emx::h16*>(x);
+  emx::h16* sp = reinterpret_cast<emx::h16*>(scales);
+  emx::h16* bp = reinterpret_cast<emx::h16*>(biases);
+  if (bits == 4)
+    hipLaunchKernelGGL(emx::affine_quantize_rows<4>, dim3(blocks), dim3(256), 0, st, xp, rows, head_dim, group_size,
+                       codes, sp, bp);
+  else
+    hipLaunchKernelGGL(emx::affine_quantize_rows<8>, dim3(blocks), dim3(256), 0, st, xp, rows, head_dim, group_size,
+                       codes, sp, bp);
+  return check_launch("affine_quantize");
+}
+
+int emx_affine_cache_write(const void* keys, const void* values, const int32_t* slot_mapping, int num_tokens,
+                           int num_kv_heads, int head_dim, int group_size, int bits, int page_size, int num_blocks,
+                           uint32_t* k_codes, void* k_scales, void* k_biases, uint32_t* v_codes, void* v_scales,
+                           void* v_biases, void* stream) {
+  if (num_tokens < 0) return fail(EMX_ERR_INVALID, "num_tokens must be >= 0");
+  if (bits != 4 && bits != 8) return fail(EMX_ERR_UNSUPPORTED, "bits must be 4 or 8, got %d", bits);
+  if (num_kv_heads <= 0 || head_dim <= 0 || page_size <= 0 || num_blocks <= 0)
+    return fail(EMX_ERR_INVALID, "num_kv_heads, head_dim, page_size, num_blocks must be positive");
+  if (group_size <= 0 || group_size % 8 != 0 || head_dim % group_size != 0)
+    return fail(EMX_ERR_INVALID, "head_dim %d must be a multiple of group_size %d (a multiple of 8)", head_dim,
+                group_size);
+  if ((page_size * bits) % 32 != 0)
+    return fail(EMX_ERR_INVALID, "page_size * bits must be a multiple of 32 (page_size %d)", page_size);
+  if (num_tokens == 0) return EMX_OK;
+  if (!keys || !values || !slot_mapping || !k_codes || !k_scales || !k_biases || !v_codes || !v_scales || !v_biases)
+    return fail(EMX_ERR_INVALID, "null pointer");
+  if (!aligned16(keys) || !aligned16(values)) return fail(EMX_ERR_INVALID, "keys/values must be 16-byte aligned");
+  emx::WriteArgs a;
+  a.keys = reinterpret_cast<const emx::h16*>(keys);
+  a.values = reinterpret_cast<const emx::h16*>(values);
+  a.slot_mapping = slot_mapping;
+  a.kc = k_codes;
+  a.ks = reinterpret_cast<emx::h16*>(k_scales);
+  a.kb = reinterpret_cast<emx::h16*>(k_biases);
+  a.vc = v_codes;
+  a.vs = reinterpret_cast<emx::h16*>(v_scales);
+  a.vb = reinterpret_cast<emx::h16*>(v_biases);
+  a.T = num_tokens;
+  a.Hkv = num_kv_heads;
+  a.D = head_dim;
+  a.gs = group_size;
+  a.bs = page_size;
+  a.nb = num_blocks;
+  const long n = (long)num_tokens * num_kv_heads * (head_dim / group_size) * 2;
+  const int blocks = (int)((n + 255) / 256);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (bits == 4)
+    hipLaunchKernelGGL(emx::affine_cache_write<4>, dim3(blocks), dim3(256), 0, st, a);
+  else
+    hipLaunchKernelGGL(emx::affine_cache_write<8>, dim3(blocks), dim3(256), 0, st, a);
+  return check_launch("affine_cache_write");
+}
+
+size_t emx_paged_workspace_bytes(int num_seqs, int num_q_heads, int num_kv_heads, int head_dim,
+                                 int max_blocks_per_seq, int page_size) {
+  if (num_seqs <= 0 || num_kv_heads <= 0 || num_q_heads <= 0 || max_blocks_per_seq <= 0 || page_size <= 0 ||
+      head_dim != 128 || page_size % kTile != 0)
+    return 0;
+  const int hg = num_q_heads / num_kv_heads;
+  const int ms = decode_max_splits(max_blocks_per_seq, page_size);
+  if (ms <= 1) return 0;
+  const size_t units = (size_t)num_seqs * num_kv_heads;
+  size_t bytes = units * ms * hg * head_dim * sizeof(float);  // partial accumulators
+  bytes += units * ms * hg * 2 * sizeof(float);                // partial (max, sum)
+  return bytes;
+}
+
+int emx_paged_attention_affine(const void* queries, int num_tokens, int num_q_heads, int head_dim,
+                               const uint32_t* k_codes, const void* k_scales, const void* k_biases,
+                               const uint32_t* v_codes, const void* v_scales, const void* v_biases, int num_blocks,
+                               int page_size, int num_kv_heads, int bits, int group_size,
+                               const int32_t* block_tables, int num_seqs, int max_blocks_per_seq,
+                               const int32_t* kv_lens, const int32_t* query_start_loc, float softmax_scale,
+                               int sliding_window, int single_token_decode, void* workspace, size_t workspace_bytes,
+                               int32_t* counters, int counters_len, void* out, void* stream) {
+  int rc = validate_common(queries, num_tokens, num_q_heads, head_dim, num_kv_heads, num_blocks, page_size,
+                           block_tables, num_seqs, max_blocks_per_seq, kv_lens, query_start_loc, single_token_decode,
+                           out);
+  if (rc) return rc;
+  if (bits != 4 && bits != 8) return fail(EMX_ERR_UNSUPPORTED, "bits must be 4 or 8, got %d", bits);
+  if (group_size <= 0 || head_dim % group_size != 0)
+    return fail(EMX_ERR_INVALID, "head_dim %d must be a multiple of group_size %d", head_dim, group_size);
+  if ((head_dim * bits) % 32 != 0 || (page_size * bits) % 32 != 0)
+    return fail(EMX_ERR_INVALID, "head_dim * bits and page_size * bits must be multiples of 32");
+  if (!std::isfinite(softmax_scale)) return fail(EMX_ERR_INVALID, "softmax_scale must be finite");
+  if (num_tokens == 0) return EMX_OK;
+  if (!k_codes || !k_scales || !k_biases || !v_codes || !v_scales || !v_biases)
+    return fail(EMX_ERR_INVALID, "null cache pointer");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const int hg = num_q_heads / num_kv_heads;
+  const float scale_log2 = softmax_scale * emx::kLog2e;
+  const int window = sliding_window > 0 ? sliding_window : 0;
+
+  if (single_token_decode && decode_fast_path(head_dim, page_size, bits, group_size, hg)) {
+    if (!aligned16(queries) || !aligned16(k_codes) || !aligned16(v_codes) || !aligned16(k_scales) ||
+        !aligned16(k_biases) || !aligned16(v_scales) || !aligned16(v_biases))
+      return fail(EMX_ERR_INVALID, "queries and cache tensors must be 16-byte aligned");
+    const int tps = decode_tiles_per_split(max_blocks_per_seq, page_size);
+    const int ms = decode_max_splits(max_blocks_per_seq, page_size);
+    const size_t need =
+        emx_paged_workspace_bytes(num_seqs, num_q_heads, num_kv_heads, head_dim, max_blocks_per_seq, page_size);
+    if (need > 0 && (workspace == nullptr || workspace_bytes < need))
+      return fail(EMX_ERR_INVALID, "workspace too small: need %zu bytes, got %zu", need, workspace_bytes);
+    if (need > 0 && (counters == nullptr || (long)counters_len < (long)num_seqs * num_kv_heads))
+      return fail(EMX_ERR_INVALID, "counters must hold num_seqs * num_kv_heads = %ld int32 (got %d)",
+                  (long)num_seqs * num_kv_heads, counters_len);
+    emx::DecodeArgs a;
+    a.q = reinterpret_cast<const emx::h16*>(queries);
+    a.kc = k_codes;
+    a.ks = reinterpret_cast<const emx::h16*>(k_scales);
+    a.kb = reinterpret_cast<const emx::h16*>(k_biases);
+    a.vc = v_codes;
+    a.vs = reinterpret_cast<const emx::h16*>(v_scales);
+    a.vb = reinterpret_cast<const emx::h16*>(v_biases);
+    a.block_tables = block_tables;
+    a.kv_lens = kv_lens;
+    a.out = reinterpret_cast<emx::h16*>(out);
+    const size_t units = (size_t)num_seqs * num_kv_heads;
+    char* ws = reinterpret_cast<char*>(workspace);
+    a.ws_o = reinterpret_cast<float*>(ws);
+    a.ws_ml = need ? reinterpret_cast<float*>(ws + units * ms * hg * head_dim * sizeof(float)) : nullptr;
+    a.ws_cnt = need ? counters : nullptr;
+    a.S = num_seqs;
+    a.Hq = num_q_heads;
+    a.Hkv = num_kv_heads;
+    a.bs = page_size;
+    a.nb = num_blocks;
+    a.max_blocks = max_blocks_per_seq;
+    a.scale_log2 = scale_log2;
+    a.window = window;
+    a.tiles_per_split = tps;
+    a.max_splits = ms;
+    DecodeFn fn = bits == 4 ? pick_decode_gs<4>(group_size, hg) : pick_decode_gs<8>(group_size, hg);
+    if (!fn) return fail(EMX_ERR_UNSUPPORTED, "no decode kernel for bits=%d group_size=%d gqa=%d", bits, group_size, hg);
+    const long grid = (long)ms * num_seqs * num_kv_heads;
+    if (grid > 0x7fffffffL) return fail(EMX_ERR_UNSUPPORTED, "decode grid too large");
+    hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(256), 0, st, a);
+    return check_launch("decode_affine_d128");
+  }
+
+  if (queries && !aligned16(queries)) return fail(EMX_ERR_INVALID, "queries must be 16-byte aligned");
+  emx::GenericArgs ga;
+  ga.q = queries;
+  ga.out = out;
+  ga.block_tables = block_tables;
+  ga.kv_lens = kv_lens;
+  ga.qsl = query_start_loc;
+  ga.T = num_tokens;
+  ga.S = num_seqs;
+  ga.Hq = num_q_heads;
+  ga.Hkv = num_kv_heads;
+  ga.D = head_dim;
+  ga.bs = page_size;
+  ga.nb = num_blocks;
+  ga.max_blocks = max_blocks_per_seq;
+  ga.scale_log2 = scale_log2;
+  ga.window = window;
+  ga.decode = single_token_decode ? 1 : 0;
+  if (bits == 4) {
+    emx::AffineKV<4> kv{k_codes,
+                        reinterpret_cast<const emx::h16*>(k_scales),
+                        reinterpret_cast<const emx::h16*>(k_biases),
+                        v_codes,
+                        reinterpret_cast<const emx::h16*>(v_scales),
+                        reinterpret_cast<const emx::h16*>(v_biases),
+                        num_kv_heads,
+                        head_dim,
+                        page_size,
+                        group_size};
+    return launch_generic<emx::h16>(ga, kv, st);
+  }
+  emx::AffineKV<8> kv{k_codes,
+                      reinterpret_cast<const emx::h16*>(k_scales),
+                      reinterpret_cast<const emx::h16*>(k_biases),
+                      v_codes,
+                      reinterpret_cast<const emx::h16*>(v_scales),
+                      reinterpret_cast<const emx::h16*>(v_biases),
+                      num_kv_heads,
+                      head_dim,
+                      page_size,
+                      group_size};
+  return launch_generic<emx::h16>(ga, kv, st);
+}
+
+int emx_paged_attention_dense(const void* queries, int num_tokens, int num_q_heads, int head_dim, int dtype,
+                              const void* key_cache, const void* value_cache, int num_blocks, int page_size,
+                              int num_kv_heads, const int32_t* block_tables, int num_seqs, int max_blocks_per_seq,
+                              const int32_t* kv_lens, const int32_t* query_start_loc, float softmax_scale,
+                              int sliding_window, int single_token_decode, void* out, void* stream) {
+  int rc = validate_common(queries, num_tokens, num_q_heads, head_dim, num_kv_heads, num_blocks, page_size,
+                           block_tables, num_seqs, max_blocks_per_seq, kv_lens, query_start_loc, single_token_decode,
+                           out);
+  if (rc) return rc;
+  if (!std::isfinite(softmax_scale)) return fail(EMX_ERR_INVALID, "softmax_scale must be finite");
+  if (num_tokens == 0) return EMX_OK;
+  if (!key_cache || !value_cache) return fail(EMX_ERR_INVALID, "null cache pointer");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  emx::GenericArgs ga;
+  ga.q = queries;
+  ga.out = out;
+  ga.block_tables = block_tables;
+  ga.kv_lens = kv_lens;
+  ga.qsl = query_start_loc;
+  ga.T = num_tokens;
+  ga.S = num_seqs;
+  ga.Hq = num_q_heads;
+  ga.Hkv = num_kv_heads;
+  ga.D = head_dim;
+  ga.bs = page_size;
+  ga.nb = num_blocks;
+  ga.max_blocks = max_blocks_per_seq;
+  ga.scale_log2 = softmax_scale * emx::kLog2e;
+  ga.window = sliding_window > 0 ? sliding_window : 0;
+  ga.decode = single_token_decode ? 1 : 0;
+  switch (dtype) {
+    case EMX_DTYPE_F16: {
+      emx::DenseKV<emx::F16> kv{reinterpret_cast<const emx::h16*>(key_cache),
+                                reinterpret_cast<const emx::h16*>(value_cache), num_kv_heads, head_dim, page_size};
+      return launch_generic<emx::h16>(ga, kv, st);
+    }
+    case EMX_DTYPE_BF16: {
+      emx::DenseKV<emx::BF16> kv{reinterpret_cast<const uint16_t*>(key_cache),
+                                 reinterpret_cast<const uint16_t*>(value_cache), num_kv_heads, head_dim, page_size};
+      return launch_generic<uint16_t>(ga, kv, st);
+    }
+    case EMX_DTYPE_F32: {
+      emx::DenseKV<emx::F32> kv{reinterpret_cast<const float*>(key_cache),
+                                reinterpret_cast<const float*>(value_cache), num_kv_heads, head_dim, page_size};
+      return launch_generic<float>(ga, kv, st);
+    }
+  }
+  return fail(EMX_ERR_UNSUPPORTED, "unknown dtype code %d", dtype);
+}
+
+}  // extern "C"

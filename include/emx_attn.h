@@ -1,0 +1,113 @@
+/*
+ * emx_attn -- MI355X (gfx950) paged attention over affine-quantized KV pages.
+ *
+ * C ABI: plain device pointers, sizes and a hipStream_t passed as void*.
+ * The library never allocates on these paths; the caller owns every buffer.
+ * Every entry point returns EMX_OK (0) or a negative status; the message of the
+ * last failure on the calling thread is available from emx_last_error().
+ *
+ * Page layout (per block `b`, kv head `h`; G = head_dim / group_size):
+ *   key codes    uint32 [num_blocks, Hkv, page_size, head_dim*bits/32]  token-major
+ *   value codes  uint32 [num_blocks, Hkv, head_dim, page_size*bits/32]  dim-major
+ *   k/v scales   fp16   [num_blocks, Hkv, G, page_size]
+ *   k/v biases   fp16   [num_blocks, Hkv, G, page_size]
+ * Codes are packed little-endian (element j of a word at bits [j*bits,(j+1)*bits)),
+ * value w = scale * code + bias, as produced by mlx.core.quantize(mode="affine").
+ */
+#ifndef EMX_ATTN_H_
+#define EMX_ATTN_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define EMX_OK 0
+#define EMX_ERR_INVALID (-1)     /* bad argument / shape (Python: ValueError) */
+#define EMX_ERR_UNSUPPORTED (-2) /* valid but unsupported configuration (NotImplementedError) */
+#define EMX_ERR_HIP (-3)         /* HIP runtime error (RuntimeError) */
+
+#define EMX_DTYPE_F16 0
+#define EMX_DTYPE_BF16 1
+#define EMX_DTYPE_F32 2
+
+/* Library version (major*10000 + minor*100 + patch). */
+int emx_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* emx_last_error(void);
+
+/*
+ * Affine quantize, MLX layout: x fp16 [rows, head_dim] ->
+ * codes uint32 [rows, head_dim*bits/32], scales/biases fp16 [rows, head_dim/group_size].
+ * Replaces: mlx.core.quantize(w, group_size, bits) as called at
+ *   lib/python/easymlx/infra/mixins/bridge.py:304,361 and
+ *   lib/python/easymlx/layers/linears/_linear_moe.py:113 (format: infra/etils.py:74-94).
+ */
+int emx_affine_quantize(const void* x, long rows, int head_dim, int group_size, int bits, uint32_t* codes,
+                        void* scales, void* biases, void* stream);
+
+/*
+ * Fused quantize-on-write of new K/V tokens into their pages.
+ * keys/values fp16 [num_tokens, Hkv, head_dim]; slot_mapping int32 [num_tokens]
+ * (block * page_size + offset, or -1 to skip the token).
+ * Replaces the K/V write of PageCacheView.concatenate_to_cache
+ *   lib/python/easymlx/caching/paged/cache.py:1088-1306 (decode :1155-1190,
+ *   multi-token :1254-1290; its Metal reshape_and_cache :36-93) and the
+ *   compiled-proxy write lib/python/easymlx/inference/esurge/runners/model_runner.py:139-189.
+ */
+int emx_affine_cache_write(const void* keys, const void* values, const int32_t* slot_mapping, int num_tokens,
+                           int num_kv_heads, int head_dim, int group_size, int bits, int page_size, int num_blocks,
+                           uint32_t* k_codes, void* k_scales, void* k_biases, uint32_t* v_codes, void* v_scales,
+                           void* v_biases, void* stream);
+
+/*
+ * Bytes of device workspace emx_paged_attention_affine needs for split-K
+ * partial results (0 if the call needs none).  Its contents need no
+ * initialisation.  Calls that need a workspace also need `counters`: int32
+ * [>= num_seqs * num_kv_heads], zero before the first call; every call returns
+ * the entries it uses to zero, so one zeroed buffer serves all later calls
+ * that are ordered after it (same stream).
+ * No direct reference counterpart: replaces the tmp_out/exp_sums/max_logits
+ * allocation of lib/python/easymlx/operations/kernels/page_attention.py:2205-2272.
+ */
+size_t emx_paged_workspace_bytes(int num_seqs, int num_q_heads, int num_kv_heads, int head_dim,
+                                 int max_blocks_per_seq, int page_size);
+
+/*
+ * Paged attention over affine pages; queries/out fp16 [num_tokens, Hq, head_dim].
+ * block_tables int32 [num_seqs, max_blocks_per_seq]; kv_lens int32 [num_seqs];
+ * query_start_loc int32 [num_seqs+1].  single_token_decode != 0 means token i
+ * belongs to sequence i (num_tokens == num_seqs) and selects the split-K MFMA
+ * decode kernel when head_dim == 128 and page_size % 128 == 0.
+ * Replaces: paged_attention(...) lib/python/easymlx/operations/kernels/unified_attention.py:1377-1512
+ *   (kernels :290-609 and FP8 in-kernel dequant :776-1268), with
+ *   k_scale/v_scale generalised to per-(token, group) scales and biases.
+ */
+int emx_paged_attention_affine(const void* queries, int num_tokens, int num_q_heads, int head_dim,
+                               const uint32_t* k_codes, const void* k_scales, const void* k_biases,
+                               const uint32_t* v_codes, const void* v_scales, const void* v_biases, int num_blocks,
+                               int page_size, int num_kv_heads, int bits, int group_size,
+                               const int32_t* block_tables, int num_seqs, int max_blocks_per_seq,
+                               const int32_t* kv_lens, const int32_t* query_start_loc, float softmax_scale,
+                               int sliding_window, int single_token_decode, void* workspace, size_t workspace_bytes,
+                               int32_t* counters, int counters_len, void* out, void* stream);
+
+/*
+ * Paged attention over an unquantized cache in the reference layout
+ * key/value [num_blocks, page_size, Hkv, head_dim] (dtype = queries' dtype).
+ * Replaces: paged_attention(...) unified_attention.py:1377-1512 for fp16/bf16/fp32 caches.
+ */
+int emx_paged_attention_dense(const void* queries, int num_tokens, int num_q_heads, int head_dim, int dtype,
+                              const void* key_cache, const void* value_cache, int num_blocks, int page_size,
+                              int num_kv_heads, const int32_t* block_tables, int num_seqs, int max_blocks_per_seq,
+                              const int32_t* kv_lens, const int32_t* query_start_loc, float softmax_scale,
+                              int sliding_window, int single_token_decode, void* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* EMX_ATTN_H_ */
