@@ -38,8 +38,7 @@ SIGNATURES: dict[str, tuple] = {
     "emx_paged_workspace_bytes": (_SZ, [_I, _I, _I, _I, _I, _I]),
     "emx_paged_attention_affine": (
         _I,
-        [_P, _I, _I, _I, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _I, _I, _P, _P, _F, _I, _I, _P, _SZ, _P, _I,
-         _P, _P],
+        [_P, _I, _I, _I, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _I, _I, _P, _P, _F, _I, _I, _P, _SZ, _P, _P],
     ),
     "emx_paged_attention_dense": (
         _I,

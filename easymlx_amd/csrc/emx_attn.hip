@@ -77,6 +77,17 @@ DecodeFn pick_decode_hg(int hg) {
   return nullptr;
 }
 
+DecodeFn pick_merge(int hg) {
+  switch (hg) {
+    case 1: return emx::decode_merge_d128<1>;
+    case 2: return emx::decode_merge_d128<2>;
+    case 4: return emx::decode_merge_d128<4>;
+    case 8: return emx::decode_merge_d128<8>;
+    case 16: return emx::decode_merge_d128<16>;
+  }
+  return nullptr;
+}
+
 template <int BITS>
 DecodeFn pick_decode_gs(int gs, int hg) {
   switch (gs) {
@@ -210,7 +221,7 @@ int emx_paged_attention_affine(const void* queries, int num_tokens, int num_q_he
                                const int32_t* block_tables, int num_seqs, int max_blocks_per_seq,
                                const int32_t* kv_lens, const int32_t* query_start_loc, float softmax_scale,
                                int sliding_window, int single_token_decode, void* workspace, size_t workspace_bytes,
-                               int32_t* counters, int counters_len, void* out, void* stream) {
+                               void* out, void* stream) {
   int rc = validate_common(queries, num_tokens, num_q_heads, head_dim, num_kv_heads, num_blocks, page_size,
                            block_tables, num_seqs, max_blocks_per_seq, kv_lens, query_start_loc, single_token_decode,
                            out);
@@ -239,9 +250,6 @@ int emx_paged_attention_affine(const void* queries, int num_tokens, int num_q_he
         emx_paged_workspace_bytes(num_seqs, num_q_heads, num_kv_heads, head_dim, max_blocks_per_seq, page_size);
     if (need > 0 && (workspace == nullptr || workspace_bytes < need))
       return fail(EMX_ERR_INVALID, "workspace too small: need %zu bytes, got %zu", need, workspace_bytes);
-    if (need > 0 && (counters == nullptr || (long)counters_len < (long)num_seqs * num_kv_heads))
-      return fail(EMX_ERR_INVALID, "counters must hold num_seqs * num_kv_heads = %ld int32 (got %d)",
-                  (long)num_seqs * num_kv_heads, counters_len);
     emx::DecodeArgs a;
     a.q = reinterpret_cast<const emx::h16*>(queries);
     a.kc = k_codes;
@@ -257,7 +265,6 @@ int emx_paged_attention_affine(const void* queries, int num_tokens, int num_q_he
     char* ws = reinterpret_cast<char*>(workspace);
     a.ws_o = reinterpret_cast<float*>(ws);
     a.ws_ml = need ? reinterpret_cast<float*>(ws + units * ms * hg * head_dim * sizeof(float)) : nullptr;
-    a.ws_cnt = need ? counters : nullptr;
     a.S = num_seqs;
     a.Hq = num_q_heads;
     a.Hkv = num_kv_heads;
@@ -269,11 +276,18 @@ int emx_paged_attention_affine(const void* queries, int num_tokens, int num_q_he
     a.tiles_per_split = tps;
     a.max_splits = ms;
     DecodeFn fn = bits == 4 ? pick_decode_gs<4>(group_size, hg) : pick_decode_gs<8>(group_size, hg);
-    if (!fn) return fail(EMX_ERR_UNSUPPORTED, "no decode kernel for bits=%d group_size=%d gqa=%d", bits, group_size, hg);
+    DecodeFn merge = pick_merge(hg);
+    if (!fn || !merge)
+      return fail(EMX_ERR_UNSUPPORTED, "no decode kernel for bits=%d group_size=%d gqa=%d", bits, group_size, hg);
     const long grid = (long)ms * num_seqs * num_kv_heads;
     if (grid > 0x7fffffffL) return fail(EMX_ERR_UNSUPPORTED, "decode grid too large");
     hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(256), 0, st, a);
-    return check_launch("decode_affine_d128");
+    if (int r = check_launch("decode_affine_d128")) return r;
+    if (ms > 1) {
+      hipLaunchKernelGGL(merge, dim3((unsigned)(num_seqs * num_kv_heads)), dim3(256), 0, st, a);
+      return check_launch("decode_merge_d128");
+    }
+    return EMX_OK;
   }
 
   if (queries && !aligned16(queries)) return fail(EMX_ERR_INVALID, "queries must be 16-byte aligned");

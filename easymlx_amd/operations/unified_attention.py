@@ -90,34 +90,25 @@ def _is_single_token_decode(query_start_loc: torch.Tensor, total_tokens: int) ->
 
 _ws_lock = threading.Lock()
 _ws_cache: dict[tuple[int, int], torch.Tensor] = {}
-_cnt_cache: dict[tuple[int, int], torch.Tensor] = {}
 
 
-def _split_buffers(device: torch.device, stream: int, nbytes: int, ncounters: int):
-    """Split-K scratch shared by the launches of one stream.
+def _workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor | None:
+    """Split-K partials buffer shared by the launches of one stream (grow-only).
 
-    Returns ``(workspace uint8, counters int32)``.  The workspace needs no
-    initialisation; the counters are zero when allocated and every launch
-    returns the entries it used to zero.  Launches on one stream are serialised,
-    so one pair per (device, stream) is race-free.
+    Launches on one stream are serialised, so one buffer per (device, stream)
+    is race-free; its contents need no initialisation.
     """
     if nbytes == 0:
-        return None, None
+        return None
     key = (device.index if device.index is not None else torch.cuda.current_device(), stream)
     with _ws_lock:
         ws = _ws_cache.get(key)
-        cnt = _cnt_cache.get(key)
-        grow_ws = ws is None or ws.numel() < nbytes
-        grow_cnt = cnt is None or cnt.numel() < ncounters
-        if (grow_ws and ws is not None) or (grow_cnt and cnt is not None):
-            torch.cuda.current_stream(device).synchronize()  # old buffers may still be in use
-        if grow_ws:
+        if ws is None or ws.numel() < nbytes:
+            if ws is not None:
+                torch.cuda.current_stream(device).synchronize()  # the old buffer may still be in use
             ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
             _ws_cache[key] = ws
-        if grow_cnt:
-            cnt = torch.zeros(max(ncounters, 1024), dtype=torch.int32, device=device)
-            _cnt_cache[key] = cnt
-        return ws, cnt
+        return ws
 
 
 def _i32(t, device) -> torch.Tensor:
@@ -144,7 +135,6 @@ def paged_attention(
     bits: int | None = None,
     group_size: int | None = None,
     workspace: torch.Tensor | None = None,
-    counters: torch.Tensor | None = None,
     out: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Execute paged attention over block-tabled KV caches.
@@ -189,14 +179,10 @@ def paged_attention(
             raise NotImplementedError("affine paged attention takes fp16 queries")
         nb, hkv, bs = int(key_cache.shape[0]), int(key_cache.shape[1]), int(key_cache.shape[2])
         need = int(lib.emx_paged_workspace_bytes(S, hq, hkv, d, max_blocks, bs)) if single_token_decode else 0
-        if need and (workspace is None or counters is None):
-            ws_default, cnt_default = _split_buffers(dev, stream, need, S * hkv)
-            workspace = ws_default if workspace is None else workspace
-            counters = cnt_default if counters is None else counters
+        if need and workspace is None:
+            workspace = _workspace(dev, stream, need)
         ws_ptr = workspace.data_ptr() if workspace is not None else None
         ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
-        cnt_ptr = counters.data_ptr() if counters is not None else None
-        cnt_len = counters.numel() if counters is not None else 0
         tensors = [key_cache, value_cache, k_scales, k_biases, v_scales, v_biases]
         if any(not t.is_contiguous() for t in tensors):
             raise ValueError("affine cache tensors must be contiguous")
@@ -208,7 +194,7 @@ def paged_attention(
                 nb, bs, hkv, int(bits), int(group_size),
                 block_tables.data_ptr(), S, max_blocks, kv_lens.data_ptr(), query_start_loc.data_ptr(),
                 float(softmax_scale), int(sliding_window), int(bool(single_token_decode)),
-                ws_ptr, ws_bytes, cnt_ptr, cnt_len, out.data_ptr(), stream,
+                ws_ptr, ws_bytes, out.data_ptr(), stream,
             )
         )
         return out

@@ -66,10 +66,7 @@ int emx_affine_cache_write(const void* keys, const void* values, const int32_t* 
 /*
  * Bytes of device workspace emx_paged_attention_affine needs for split-K
  * partial results (0 if the call needs none).  Its contents need no
- * initialisation.  Calls that need a workspace also need `counters`: int32
- * [>= num_seqs * num_kv_heads], zero before the first call; every call returns
- * the entries it uses to zero, so one zeroed buffer serves all later calls
- * that are ordered after it (same stream).
+ * initialisation; calls sharing one workspace must be ordered (same stream).
  * No direct reference counterpart: replaces the tmp_out/exp_sums/max_logits
  * allocation of lib/python/easymlx/operations/kernels/page_attention.py:2205-2272.
  */
@@ -93,7 +90,7 @@ int emx_paged_attention_affine(const void* queries, int num_tokens, int num_q_he
                                const int32_t* block_tables, int num_seqs, int max_blocks_per_seq,
                                const int32_t* kv_lens, const int32_t* query_start_loc, float softmax_scale,
                                int sliding_window, int single_token_decode, void* workspace, size_t workspace_bytes,
-                               int32_t* counters, int counters_len, void* out, void* stream);
+                               void* out, void* stream);
 
 /*
  * Paged attention over an unquantized cache in the reference layout
