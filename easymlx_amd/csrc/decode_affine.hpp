@@ -4,27 +4,32 @@
 // (lib/python/easymlx/operations/kernels/unified_attention.py:467-609) and its
 // split-K variant (page_attention.py:1718-2059) for affine int4/int8 pages.
 //
-// Work decomposition
-//   workgroup = (seq, kv_head, split) with 4 waves; a split is a run of
-//   `tiles_per_split` 128-token tiles, wave w takes tiles w, w+4, ... of it.
-//   All Hq/Hkv query heads of the GQA group are served from one read of each
-//   K/V byte.  Splits of one (seq, kv_head) write fp32 partials that
-//   decode_merge_d128 combines (no cross-workgroup fences in the hot kernel).
+// Work decomposition (persistent, one resident round of waves)
+//   A work item is one NT-token iteration (64 tokens at 4-bit, 32 at 8-bit) of
+//   one unit = (sequence, kv_head); items are ordered unit-major, and the live
+//   items of every unit are counted on the device from kv_lens.  Wave w of NW
+//   takes the contiguous item range [w*I/NW, (w+1)*I/NW) and streams it with a
+//   two-stage pipeline (the loads of item i+1 are in flight while item i
+//   computes).  All Hq/Hkv query heads of the GQA group are served from one
+//   read of each K/V byte.  A unit that lies inside one wave's range is written
+//   straight to the output; a unit cut by range boundaries leaves one fp32
+//   partial per wave (slot wave + unit, unique because ranges are monotone)
+//   that decode_merge_d128 combines -- no cross-workgroup fences anywhere.
 //
-// Per 128-token tile and wave (lane l: col = l%16, jj = l/16)
-//   QK^T : 8 token sub-tiles x 4 k-slices of v_mfma_f32_16x16x32_f16.
-//          A = K codes as fp16 subnormals (row rho of sub-tile a is token
-//          32*(rho/4) + 4a + rho%4), B = query columns: column c holds query
-//          head c % HG restricted to quantization group c / HG (zeros elsewhere),
-//          so one MFMA produces per-group partial dots and the affine scale /
-//          bias is applied per (token, group) afterwards:
-//            s = sum_g 2^24 * scale[t,g] * C[t,(h,g)] + bias[t,g] * sum_{d in g} q_hd
-//   softmax: online, base-2, fp32; row max over the lane's 32 tokens then
-//          across the 4 lane groups.
-//   PV   : 8 dim sub-tiles x 4 token k-slices.  A = V codes (V pages are stored
-//          dim-major, so a lane's uint32 is 8 consecutive tokens of one dim),
-//          B = p * v_scale[t, g(col)] in fp16; the bias term
-//          sum_t p_t * v_bias[t,g] is accumulated in fp32 on the side.
+// Per iteration (lane l: col = l%16, jj = l/16)
+//   QK^T : NT/16 token sub-tiles x 4 k-slices of v_mfma_f32_16x16x32_f16.
+//          A = K codes as exact fp16 subnormals (code * 2^-24); row rho of
+//          sub-tile a is token TPL*(rho/4) + 4a + rho%4.  B = query columns:
+//          column h + (16/G)*g holds query head h restricted to quantization
+//          group g (zeros elsewhere), so one MFMA yields per-group partial dots
+//          and the affine scale / bias are applied per (token, group):
+//            s = 2^24 * sum_g scale[t,g] * C[t,(h,g)] + bias[t,g] * sum_{d in g} q_hd
+//          The group sum is a DPP row rotation.
+//   softmax: online, base 2, fp32.
+//   PV   : 8 dim sub-tiles x NT/32 token k-slices.  A = V codes (V pages are
+//          dim-major, so a lane's uint32 holds consecutive tokens of one dim),
+//          B = p * v_scale[t, g] in fp16; sum_t p_t * v_bias[t, g] is kept in fp32.
+//   Scales and biases of the iteration are staged through a per-wave LDS slot.
 #pragma once
 
 #include "common.hpp"
@@ -42,16 +47,19 @@ struct DecodeArgs {
   const int32_t* block_tables;  // [S, max_blocks]
   const int32_t* kv_lens;       // [S]
   h16* out;                   // [S, Hq, 128]
-  float* ws_o;                // [S, Hkv, max_splits, HG, 128]
-  float* ws_ml;               // [S, Hkv, max_splits, HG, 2]
+  float* ws_o;                // [num_waves + S*Hkv, HG, 128] partial accumulators, slot = wave + unit
+  float* ws_ml;               // [num_waves + S*Hkv, HG, 2]   partial (max, sum)
+  int* ws_cum;                // [S + 1] live-item prefix written by the decode kernel for the merge
   int S, Hq, Hkv, bs, nb, max_blocks;
   float scale_log2;           // softmax_scale * log2(e)
   int window;                 // sliding window, 0 = off
-  int tiles_per_split;
-  int max_splits;
+  int num_waves;              // waves of the persistent decode grid
+  int nt;                     // tokens per work item (64 at 4-bit, 32 at 8-bit)
 };
 
-// Rotate within each row of 16 lanes (DPP row_ror:N); sums over lanes c, c+N, ...
+constexpr int kMaxSeqs = 2048;  // per-sequence table held in LDS by both kernels
+
+// DPP row_ror:N -- rotate within each row of 16 lanes.
 template <int N>
 __device__ __forceinline__ float row_ror(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x120 + N, 0xF, 0xF,
@@ -65,87 +73,116 @@ struct DecodeCfg {
   static constexpr int GSTRIDE = 16 / G;     // MFMA column of (head h, group g) = h + GSTRIDE * g
   static constexpr int TPL = 64 / BITS;      // tokens per lane group per iteration
   static constexpr int NT = 4 * TPL;         // tokens per iteration (64 at 4-bit, 32 at 8-bit)
+  static constexpr int NIT = 128 / NT;       // iterations per 128-token tile
   static constexpr int NA = TPL / 4;         // 16-token MFMA sub-tiles per iteration
   static constexpr int KW = BITS;            // K code words a lane holds per sub-tile (32 dims)
   static constexpr int NWS = TPL / 8;        // PV k-slices (8 tokens each) per iteration
   static constexpr int W = D * BITS / 32;    // code words per token
-  static constexpr int SROW = NT;            // halves per staged (array, group) row
-  static constexpr int SHALVES = 4 * G * NT; // staged ks, kb, vs, vb halves per iteration
+  static constexpr int SPIECES = G * NT / 2; // dwords of one staged (scale|bias) array per iteration
+  static constexpr int SK = (SPIECES + 63) / 64;
+  static constexpr int SHALVES = 4 * G * NT;
   static_assert(HG <= GSTRIDE, "GQA group x quant groups must fit 16 MFMA columns");
-};
-
-// Buffer resources of one 128-token tile of one (page, kv_head); built in SGPRs
-// per tile, so every per-lane load address is a single 32-bit offset.
-struct TileRsrc {
-  __amdgpu_buffer_rsrc_t k, v, s[4];
+  static_assert(SK <= 2, "staging assumes <= 2 dwords per lane per array");
 };
 
 constexpr int kRsrcFlags = 0x00020000;  // raw 32-bit buffer, gfx9 family
 constexpr int kLoadAux = 0;             // default cache policy
 
-// One NT-token iteration of one wave.  `full`: every token of the iteration is
-// inside [start_k, kv_len) (all but the first / last iteration of a sequence).
-template <int BITS, int GS, int HG>
-__device__ __forceinline__ void decode_iteration(const bool full, const TileRsrc& rs, const int RW, const int it, const int lk,
-                                                 const int lv, const int (&ls)[2], const int (&lsd)[2],
-                                                 const int jj, const bool col_ok, const int gg,
-                                                 const int tok_base, const int start_k, const int kv_len,
-                                                 const h16x8 (&qB)[4], const float qs, const float sc_l2,
-                                                 h16* stage, float& m_run, float& l_part, float& pb,
-                                                 f32x4 (&acc)[8]) {
-  using C = DecodeCfg<BITS, GS, HG>;
-  constexpr int G = C::G, TPL = C::TPL, NT = C::NT, NA = C::NA, KW = C::KW, NWS = C::NWS, W = C::W;
-  constexpr int SPIECES = G * NT / 2;  // dwords of one staged array per iteration
+// Buffer resources of one 128-token tile of one (page, kv_head), held in SGPRs:
+// every per-lane address is then a single 32-bit offset.
+struct TileRsrc {
+  __amdgpu_buffer_rsrc_t k, v, s[4];
+};
 
-  // ---- issue the iteration's loads: K sub-tiles, V dim rows, staged scale/bias dwords
-  uint32_t kw[NA][KW];
+template <int BITS, int GS, int HG>
+__device__ __forceinline__ TileRsrc make_tile_rsrc(const DecodeArgs& a, const int blk, const int kvh, const int off) {
+  using C = DecodeCfg<BITS, GS, HG>;
+  const int RW = a.bs * BITS / 32;
+  const size_t ph = (size_t)blk * a.Hkv + kvh;
+  TileRsrc rs;
+  rs.k = __builtin_amdgcn_make_buffer_rsrc((void*)(a.kc + (ph * a.bs + off) * C::W), (short)0, 128 * C::W * 4,
+                                           kRsrcFlags);
+  rs.v = __builtin_amdgcn_make_buffer_rsrc((void*)(a.vc + ph * C::D * RW + off * BITS / 32), (short)0,
+                                           (C::D * RW - off * BITS / 32) * 4, kRsrcFlags);
+  const h16* sp[4] = {a.ks, a.kb, a.vs, a.vb};
 #pragma unroll
-  for (int at = 0; at < NA; ++at) {
+  for (int arr = 0; arr < 4; ++arr)
+    rs.s[arr] = __builtin_amdgcn_make_buffer_rsrc((void*)(sp[arr] + ph * C::G * a.bs + off), (short)0,
+                                                  (C::G * a.bs - off) * 2, kRsrcFlags);
+  return rs;
+}
+
+// Register image of one iteration's loads.
+template <int BITS, int GS, int HG>
+struct IterLoads {
+  using C = DecodeCfg<BITS, GS, HG>;
+  uint32_t kw[C::NA][C::KW];
+  uint32_t vw[8][2];
+  uint32_t sw[4][C::SK];
+};
+
+template <int BITS, int GS, int HG>
+__device__ __forceinline__ void issue_loads(IterLoads<BITS, GS, HG>& L, const TileRsrc& rs, const int RW,
+                                            const int it, const int lk, const int lv, const int (&ls)[2]) {
+  using C = DecodeCfg<BITS, GS, HG>;
 #pragma unroll
-    for (int v = 0; v < KW / 4; ++v) {
-      const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(rs.k, lk + (4 * at * W + 4 * v) * 4, it * NT * W * 4,
-                                                            kLoadAux);
-      kw[at][4 * v + 0] = x[0];
-      kw[at][4 * v + 1] = x[1];
-      kw[at][4 * v + 2] = x[2];
-      kw[at][4 * v + 3] = x[3];
+  for (int at = 0; at < C::NA; ++at) {
+#pragma unroll
+    for (int v = 0; v < C::KW / 4; ++v) {
+      const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(rs.k, lk + (4 * at * C::W + 4 * v) * 4,
+                                                            it * C::NT * C::W * 4, kLoadAux);
+      L.kw[at][4 * v + 0] = x[0];
+      L.kw[at][4 * v + 1] = x[1];
+      L.kw[at][4 * v + 2] = x[2];
+      L.kw[at][4 * v + 3] = x[3];
     }
   }
-  uint32_t vw[8][2];
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt) {
     typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-    const u32x2 x = __builtin_amdgcn_raw_buffer_load_b64(rs.v, lv, dt * 16 * RW * 4 + it * NT * BITS / 8, kLoadAux);
-    vw[dt][0] = x[0];
-    vw[dt][1] = x[1];
+    const u32x2 x =
+        __builtin_amdgcn_raw_buffer_load_b64(rs.v, lv, dt * 16 * RW * 4 + it * C::NT * BITS / 8, kLoadAux);
+    L.vw[dt][0] = x[0];
+    L.vw[dt][1] = x[1];
   }
-  uint32_t sw[4][2];
 #pragma unroll
   for (int arr = 0; arr < 4; ++arr) {
 #pragma unroll
-    for (int k = 0; k < (SPIECES + 63) / 64; ++k) {
-      if (SPIECES % 64 == 0 || lsd[k] >= 0)
-        sw[arr][k] = __builtin_amdgcn_raw_buffer_load_b32(rs.s[arr], ls[k], it * NT * 2, kLoadAux);
+    for (int k = 0; k < C::SK; ++k) {
+      if (C::SPIECES % 64 == 0 || ls[k] >= 0)
+        L.sw[arr][k] = __builtin_amdgcn_raw_buffer_load_b32(rs.s[arr], ls[k], it * C::NT * 2, kLoadAux);
     }
   }
+}
+
+// One NT-token iteration of one wave.  `full`: every token of the iteration is
+// inside [start_k, kv_len) (all but the first / last iteration of a sequence).
+template <int BITS, int GS, int HG>
+__device__ __forceinline__ void compute_iteration(IterLoads<BITS, GS, HG>& L, const bool full, const int (&lsd)[2],
+                                                  const int jj, const bool col_ok, const int gg, const int tok_base,
+                                                  const int start_k, const int kv_len, const h16x8 (&qB)[4],
+                                                  const float qs, const float sc_l2, h16* stage, float& m_run,
+                                                  float& l_part, float& pb, f32x4 (&acc)[8]) {
+  using C = DecodeCfg<BITS, GS, HG>;
+  constexpr int G = C::G, TPL = C::TPL, NT = C::NT, NA = C::NA, NWS = C::NWS, SK = C::SK;
+
+  // ---- stage this iteration's scales / biases (dead tokens' may be garbage: zero them)
   if (!full) {
-    // scale/bias of tokens outside [start_k, kv_len) may be garbage: stage zeros instead
 #pragma unroll
-    for (int k = 0; k < (SPIECES + 63) / 64; ++k) {
-      const int t = lsd[k] % NT;  // token of the dword's low half
-      const int pos = tok_base + t;
+    for (int k = 0; k < SK; ++k) {
+      const int pos = tok_base + (lsd[k] >= 0 ? lsd[k] % NT : 0);
       const uint32_t keep = (pos >= start_k && pos < kv_len ? 0x0000FFFFu : 0u) |
                             (pos + 1 >= start_k && pos + 1 < kv_len ? 0xFFFF0000u : 0u);
 #pragma unroll
-      for (int arr = 0; arr < 4; ++arr) sw[arr][k] &= keep;
+      for (int arr = 0; arr < 4; ++arr) L.sw[arr][k] &= keep;
     }
   }
 #pragma unroll
   for (int arr = 0; arr < 4; ++arr) {
 #pragma unroll
-    for (int k = 0; k < (SPIECES + 63) / 64; ++k) {
-      if (SPIECES % 64 == 0 || lsd[k] >= 0)
-        *reinterpret_cast<uint32_t*>(stage + arr * G * NT + lsd[k]) = sw[arr][k];
+    for (int k = 0; k < SK; ++k) {
+      if (C::SPIECES % 64 == 0 || lsd[k] >= 0)
+        *reinterpret_cast<uint32_t*>(stage + arr * G * NT + lsd[k]) = L.sw[arr][k];
     }
   }
 
@@ -158,7 +195,7 @@ __device__ __forceinline__ void decode_iteration(const bool full, const TileRsrc
     f32x4 c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
-      const h16x8 A = BITS == 4 ? unpack4(kw[at][w]) : unpack8(kw[at][2 * w], kw[at][2 * w + 1]);
+      const h16x8 A = BITS == 4 ? unpack4(L.kw[at][w]) : unpack8(L.kw[at][2 * w], L.kw[at][2 * w + 1]);
       c = mfma16x16x32(A, qB[w], c);
     }
     typedef h16 h16x4 __attribute__((ext_vector_type(4)));
@@ -173,7 +210,7 @@ __device__ __forceinline__ void decode_iteration(const bool full, const TileRsrc
     }
   }
 
-  // ---- online softmax in base 2 (scores scaled by sc_l2 = softmax_scale*log2(e)*2^24)
+  // ---- online softmax in base 2 (scores scaled by sc_l2 = softmax_scale * log2(e) * 2^24)
   if (!full) {
 #pragma unroll
     for (int at = 0; at < NA; ++at) {
@@ -228,17 +265,72 @@ __device__ __forceinline__ void decode_iteration(const bool full, const TileRsrc
     }
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) {
-      const h16x8 A = BITS == 4 ? unpack4(vw[dt][w]) : unpack8(vw[dt][0], vw[dt][1]);
+      const h16x8 A = BITS == 4 ? unpack4(L.vw[dt][w]) : unpack8(L.vw[dt][0], L.vw[dt][1]);
       acc[dt] = mfma16x16x32(A, pB, acc[dt]);
     }
   }
 }
 
+// Block-wide exclusive prefix of per-sequence live item counts into LDS.
+// cum[s] = sum_{s' < s} n(s'), cum[S] = total; kvl[s] = clamped kv_len.
+__device__ __forceinline__ void seq_table(const DecodeArgs& a, int* cum, int* kvl) {
+  const int S = a.S;
+  const int ch = (S + 255) / 256;
+  const int s0 = threadIdx.x * ch;
+  int tsum = 0;
+  for (int i = 0; i < ch; ++i) {
+    const int s = s0 + i;
+    if (s < S) {
+      int kl = min(a.kv_lens[s], a.max_blocks * a.bs);
+      kl = max(kl, 0);
+      kvl[s] = kl;
+      int n = 0;
+      if (kl > 0) {
+        const int start_k = a.window > 0 ? max(0, kl - a.window) : 0;
+        n = (kl - 1) / a.nt - start_k / a.nt + 1;
+      }
+      cum[s] = n;  // temporarily the count
+      tsum += n;
+    }
+  }
+  // inclusive scan of tsum over the block
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  int x = tsum;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(x, o, 64);
+    if (lane >= o) x += y;
+  }
+  __shared__ int wsum[4];
+  if (lane == 63) wsum[wv] = x;
+  __syncthreads();
+  int base = 0;
+  for (int w = 0; w < wv; ++w) base += wsum[w];
+  int run = base + x - tsum;
+  for (int i = 0; i < ch; ++i) {
+    const int s = s0 + i;
+    if (s < S) {
+      const int n = cum[s];
+      cum[s] = run;
+      run += n;
+    }
+  }
+  if (threadIdx.x == 255) cum[S] = base + x;
+  __syncthreads();
+}
+
+// Wave containing item g of I items split over NW waves as [w*I/NW, (w+1)*I/NW).
+__device__ __forceinline__ int wave_of_item(long long g, long long I, int NW) {
+  int w = (int)((g * NW) / I);
+  while (w + 1 < NW && ((long long)(w + 1) * I) / NW <= g) ++w;
+  while (w > 0 && ((long long)w * I) / NW > g) --w;
+  return w;
+}
+
 template <int BITS, int GS, int HG>
-__global__ __launch_bounds__(256, 4) void decode_affine_d128(DecodeArgs a) {
+__global__ __launch_bounds__(256, 2) void decode_affine_d128(DecodeArgs a) {
   using C = DecodeCfg<BITS, GS, HG>;
   constexpr int D = C::D, G = C::G, GSTRIDE = C::GSTRIDE, NT = C::NT;
-  static_assert(G * NT / 2 <= 128, "staging assumes <= 2 dwords per lane per array");
 
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -248,43 +340,62 @@ __global__ __launch_bounds__(256, 4) void decode_affine_d128(DecodeArgs a) {
   const int gg = col / GSTRIDE;
   const bool col_ok = hh < HG;
 
-  int bid = blockIdx.x;
-  const int kvh = bid % a.Hkv;
-  bid /= a.Hkv;
-  const int s = bid % a.S;
-  const int split = bid / a.S;
-
-  __shared__ float so[4][HG * D];
-  __shared__ float sm[4][HG];
-  __shared__ float sl[4][HG];
+  __shared__ int cum[kMaxSeqs + 1];
+  __shared__ int kvl[kMaxSeqs];
   __shared__ __attribute__((aligned(16))) h16 stage_all[4][C::SHALVES];
+  seq_table(a, cum, kvl);
+  if (blockIdx.x == 0)
+    for (int i = threadIdx.x; i <= a.S; i += 256) a.ws_cum[i] = cum[i];
 
-  h16* out = a.out + ((size_t)s * a.Hq + (size_t)kvh * HG) * D;
-  int kv_len = a.kv_lens[s];
-  kv_len = min(kv_len, a.max_blocks * a.bs);
-  if (kv_len <= 0) {
-    if (split == 0)
-      for (int i = threadIdx.x; i < HG * D; i += 256) out[i] = (h16)0.0f;
-    return;
+  const int S = a.S, Hkv = a.Hkv;
+  const long long I = (long long)Hkv * cum[S];
+  const int NW = (int)min((long long)a.num_waves, I);  // every wave range non-empty
+  const int W = blockIdx.x * 4 + wv;
+  if (W >= NW) return;
+  const long long g0 = ((long long)W * I) / NW;
+  const long long g1 = ((long long)(W + 1) * I) / NW;
+
+  // ---- item g -> (sequence, kv_head, live iteration j, token base)
+  auto seq_of = [&](long long g, int s_from) {  // first s >= s_from with Hkv*cum[s+1] > g
+    int si = s_from;
+    while (si + 1 < S && (long long)Hkv * cum[si + 1] <= g) ++si;
+    return si;
+  };
+  auto lo_of = [&](int si) { return (a.window > 0 ? max(0, kvl[si] - a.window) : 0) / NT; };
+  int s = 0;
+  for (int c = 0; c < S; c += 64) {
+    const int si = c + lane;
+    s += __builtin_popcountll(__ballot(si < S && (long long)Hkv * cum[si + 1] <= g0));
   }
-  const int start_k = a.window > 0 ? max(0, kv_len - a.window) : 0;
-  const int tile_first = start_k >> 7;
-  const int tile_last = (kv_len - 1) >> 7;
-  const int n_splits = (tile_last - tile_first + a.tiles_per_split) / a.tiles_per_split;
-  if (split >= n_splits) return;
-  const int t_begin = tile_first + split * a.tiles_per_split;
-  const int t_end = min(t_begin + a.tiles_per_split, tile_last + 1);
+  s = __builtin_amdgcn_readfirstlane(s);
 
-  // ---- query operand: lane holds dims 32*jj .. 32*jj+31 of head hh, zero outside group gg
-  h16x8 qB[4];
-  float qsum = 0.f;
-  {
+  // ---- block id of every item of the range, one item per lane (64 items per chunk)
+  auto blk_chunk = [&](long long gb) {
+    const long long g = gb + lane;
+    int b = -1;
+    if (g < g1) {
+      const int si = seq_of(g, s);
+      const int n = cum[si + 1] - cum[si];
+      const int jn = (int)((g - (long long)Hkv * cum[si]) % n);
+      b = a.block_tables[(size_t)si * a.max_blocks + ((lo_of(si) + jn) * NT) / a.bs];
+    }
+    return b;
+  };
+  int blkv = blk_chunk(g0);
+
+  // ---- query operand of a unit: lane holds dims 32*jj .. 32*jj+31 of head hh, zero outside group gg
+  u32x4 qraw[4];
+  auto issue_q = [&](int seq, int kh) {
     const u32x4* qp = reinterpret_cast<const u32x4*>(
-        a.q + ((size_t)s * a.Hq + (size_t)kvh * HG + (col_ok ? hh : 0)) * D + 32 * jj);
-    u32x4 raw[4];
+        a.q + ((size_t)seq * a.Hq + (size_t)kh * HG + (col_ok ? hh : 0)) * D + 32 * jj);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) raw[i] = qp[i];
-    const h16* qv = reinterpret_cast<const h16*>(raw);
+    for (int i = 0; i < 4; ++i) qraw[i] = qp[i];
+  };
+  h16x8 qB[4];
+  float qs = 0.f;
+  auto build_q = [&]() {
+    const h16* qv = reinterpret_cast<const h16*>(qraw);
+    float qsum = 0.f;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
 #pragma unroll
@@ -298,169 +409,223 @@ __global__ __launch_bounds__(256, 4) void decode_affine_d128(DecodeArgs a) {
     }
     qsum += __shfl_xor(qsum, 16, 64);
     qsum += __shfl_xor(qsum, 32, 64);
+    qs = qsum * (1.0f / kTwo24);  // bias term in the 2^-24 units of the MFMA output
+  };
+
+  int n_s = cum[s + 1] - cum[s];
+  int kvh, j;
+  {
+    const int r = (int)(g0 - (long long)Hkv * cum[s]);
+    kvh = r / n_s;
+    j = r % n_s;
   }
-  const float qs = qsum * (1.0f / kTwo24);   // bias term in the 2^-24 units of the MFMA output
-  const float sc_l2 = a.scale_log2 * kTwo24;
+  issue_q(s, kvh);
+  int kv_len = kvl[s];
+  int start_k = a.window > 0 ? max(0, kv_len - a.window) : 0;
+  int it_lo = start_k / NT;
 
-  float m_run = -INFINITY;
-  float l_part = 0.f;
-  float pb = 0.f;
-  f32x4 acc[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-  h16* stage = stage_all[wv];
-
-  // per-lane byte offsets inside a tile (constant for the whole kernel)
-  const int RW = a.bs * BITS / 32;  // code words per V dim row
+  const int RW = a.bs * BITS / 32;
   const int lk = ((C::TPL * (col >> 2) + (col & 3)) * C::W + C::KW * jj) * 4;
   const int lv = (col * RW + C::TPL * jj * BITS / 32) * 4;
-  int ls[2], lsd[2];  // staged scale/bias dword: global byte offset, LDS half index (-1 = none)
+  int ls[2], lsd[2];  // staged scale/bias dword: global byte offset and LDS half index (-1 = none)
 #pragma unroll
   for (int k = 0; k < 2; ++k) {
     const int pc = lane + 64 * k;
     const int g = pc / (NT / 2), c2 = pc % (NT / 2);
     const bool ok = pc < G * NT / 2;
-    ls[k] = ok ? (g * a.bs + 2 * c2) * 2 : 0;
+    ls[k] = ok ? (g * a.bs + 2 * c2) * 2 : -1;
     lsd[k] = ok ? g * NT + 2 * c2 : -1;
   }
+  h16* stage = stage_all[wv];
+  const float sc_l2 = a.scale_log2 * kTwo24;
 
-  for (int tile = t_begin + wv; tile < t_end; tile += 4) {
-    const int tok0 = tile << 7;
-    const int page = tok0 / a.bs;
-    const int off = tok0 - page * a.bs;
-    const int blk = __builtin_amdgcn_readfirstlane(a.block_tables[(size_t)s * a.max_blocks + page]);
-    if (blk < 0 || blk >= a.nb) continue;
-    const size_t ph = (size_t)blk * a.Hkv + kvh;
-    TileRsrc rs;
-    rs.k = __builtin_amdgcn_make_buffer_rsrc((void*)(a.kc + (ph * a.bs + off) * C::W), (short)0, 128 * C::W * 4,
-                                             kRsrcFlags);
-    rs.v = __builtin_amdgcn_make_buffer_rsrc((void*)(a.vc + ph * D * RW + off * BITS / 32), (short)0,
-                                             (D * RW - off * BITS / 32) * 4, kRsrcFlags);
-    const h16* sp[4] = {a.ks, a.kb, a.vs, a.vb};
-#pragma unroll
-    for (int arr = 0; arr < 4; ++arr)
-      rs.s[arr] = __builtin_amdgcn_make_buffer_rsrc((void*)(sp[arr] + ph * G * a.bs + off), (short)0,
-                                                    (G * a.bs - off) * 2, kRsrcFlags);
-#pragma unroll 1
-    for (int it = 0; it < 128 / NT; ++it) {
-      const int tb = tok0 + it * NT;
-      if (tb >= kv_len) break;
-      if (tb + NT <= start_k) continue;
-      const bool full = tb >= start_k && tb + NT <= kv_len;
-      decode_iteration<BITS, GS, HG>(full, rs, RW, it, lk, lv, ls, lsd, jj, col_ok, gg, tb, start_k, kv_len, qB, qs,
-                                     sc_l2, stage, m_run, l_part, pb, acc);
-    }
-  }
+  // ---- first item's loads (its query is already in flight)
+  int tb = (it_lo + j) * NT;
+  int blk = __builtin_amdgcn_readfirstlane(__builtin_amdgcn_readlane(blkv, 0));
+  TileRsrc rs_cur = make_tile_rsrc<BITS, GS, HG>(a, (unsigned)blk < (unsigned)a.nb ? blk : 0, kvh, (tb & ~127) % a.bs);
+  // two load buffers used alternately, so the wait before an item's compute
+  // never covers the following item's loads
+  IterLoads<BITS, GS, HG> bufA, bufB;
+  issue_loads(bufA, rs_cur, RW, (tb & 127) / NT, lk, lv, ls);
+  build_q();
 
-  // ---- per-wave epilogue -> LDS (acc is in 2^-24 units)
-  l_part += __shfl_xor(l_part, 16, 64);
-  l_part += __shfl_xor(l_part, 32, 64);
-  pb += __shfl_xor(pb, 16, 64);
-  pb += __shfl_xor(pb, 32, 64);
-  if (col_ok && gg == 0 && jj == 0) {
-    sm[wv][hh] = m_run;
-    sl[wv][hh] = l_part;
-  }
+  float m_run = -INFINITY, l_part = 0.f, pb = 0.f;
+  f32x4 acc[8];
 #pragma unroll
-  for (int dt = 0; dt < 8; ++dt) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int d = 16 * dt + 4 * jj + r;
-      if (col_ok && d / GS == gg) so[wv][hh * D + d] = acc[dt][r] * kTwo24 + pb;
-    }
-  }
-  __syncthreads();
+  for (int i = 0; i < 8; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  long long unit_first = (long long)Hkv * cum[s] + (long long)kvh * n_s;  // first item of the current unit
 
-  // ---- merge the 4 waves
-  const size_t unit = (size_t)s * a.Hkv + kvh;
-  if (n_splits == 1) {
-    for (int i = threadIdx.x; i < HG * D; i += 256) {
-      const int h = i / D;
-      float M = -INFINITY;
-#pragma unroll
-      for (int w = 0; w < 4; ++w) M = fmaxf(M, sm[w][h]);
-      float L = 0.f, o = 0.f;
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        if (sm[w][h] != -INFINITY) {
-          const float f = exp2f(sm[w][h] - M);
-          L += sl[w][h] * f;
-          o += so[w][i] * f;
+  auto step = [&](IterLoads<BITS, GS, HG>& cur, IterLoads<BITS, GS, HG>& nxt, const long long g) {
+    // ---- next item
+    int s1 = s, kvh1 = kvh, j1 = j + 1, n1 = n_s, kl1 = kv_len, lo1 = it_lo;
+    if (j1 == n_s) {
+      j1 = 0;
+      if (++kvh1 == Hkv) {
+        kvh1 = 0;
+        do {
+          ++s1;
+        } while (s1 < S && cum[s1 + 1] == cum[s1]);
+        if (s1 < S) {
+          n1 = cum[s1 + 1] - cum[s1];
+          kl1 = kvl[s1];
+          lo1 = (a.window > 0 ? max(0, kl1 - a.window) : 0) / NT;
         }
       }
-      out[i] = (h16)(L > 0.f ? o / L : 0.f);
     }
-    return;
-  }
+    const bool has_next = g + 1 < g1;
+    const bool unit_end = !has_next || s1 != s || kvh1 != kvh;
+    TileRsrc rs_nxt = rs_cur;
+    int blk1 = blk, tb1 = (lo1 + j1) * NT;
+    if (has_next) {
+      const int k1 = (int)(g + 1 - g0);
+      if ((k1 & 63) == 0) blkv = blk_chunk(g + 1);
+      blk1 = __builtin_amdgcn_readfirstlane(__builtin_amdgcn_readlane(blkv, k1 & 63));
+      if (s1 != s || kvh1 != kvh || (tb1 >> 7) != (tb >> 7))
+        rs_nxt = make_tile_rsrc<BITS, GS, HG>(a, (unsigned)blk1 < (unsigned)a.nb ? blk1 : 0, kvh1, (tb1 & ~127) % a.bs);
+      issue_loads(nxt, rs_nxt, RW, (tb1 & 127) / NT, lk, lv, ls);
+      if (unit_end) issue_q(s1, kvh1);
+    }
 
-  float* wo = a.ws_o + (unit * a.max_splits + split) * (HG * D);
-  float* wml = a.ws_ml + (unit * a.max_splits + split) * (HG * 2);
-  for (int i = threadIdx.x; i < HG * D; i += 256) {
-    const int h = i / D;
-    float M = -INFINITY;
+    // ---- compute the current item (an invalid page is skipped like the reference's Metal kernel)
+    if ((unsigned)blk < (unsigned)a.nb) {
+      const bool full = tb >= start_k && tb + NT <= kv_len;
+      compute_iteration<BITS, GS, HG>(cur, full, lsd, jj, col_ok, gg, tb, start_k, kv_len, qB, qs, sc_l2, stage,
+                                      m_run, l_part, pb, acc);
+    }
+
+    // ---- unit finished (or range ends): write output / partial, reset
+    if (unit_end) {
+      float l = l_part + __shfl_xor(l_part, 16, 64);
+      l += __shfl_xor(l, 32, 64);
+      float pbs = pb + __shfl_xor(pb, 16, 64);
+      pbs += __shfl_xor(pbs, 32, 64);
+      const bool whole = unit_first >= g0 && unit_first + n_s <= g1;
+      const int u = s * Hkv + kvh;
+      if (whole) {
+        h16* out = a.out + ((size_t)s * a.Hq + (size_t)kvh * HG + hh) * D;
+        const float inv = l > 0.f ? 1.f / l : 0.f;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) M = fmaxf(M, sm[w][h]);
-    float L = 0.f, o = 0.f;
+        for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      if (sm[w][h] != -INFINITY) {
-        const float f = exp2f(sm[w][h] - M);
-        L += sl[w][h] * f;
-        o += so[w][i] * f;
+          for (int r = 0; r < 4; ++r) {
+            const int d = 16 * dt + 4 * jj + r;
+            if (col_ok && d / GS == gg) out[d] = (h16)((acc[dt][r] * kTwo24 + pbs) * inv);
+          }
+      } else {
+        const size_t slot = (size_t)W + u;
+        float* wo = a.ws_o + slot * (HG * D) + hh * D;
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int d = 16 * dt + 4 * jj + r;
+            if (col_ok && d / GS == gg) wo[d] = acc[dt][r] * kTwo24 + pbs;
+          }
+        if (col_ok && gg == 0 && jj == 0) {
+          a.ws_ml[slot * (HG * 2) + 2 * hh] = m_run;
+          a.ws_ml[slot * (HG * 2) + 2 * hh + 1] = l;
+        }
+      }
+      m_run = -INFINITY;
+      l_part = 0.f;
+      pb = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (has_next) {
+        unit_first = g + 1;
+        build_q();
       }
     }
-    wo[i] = o;
-    if ((i % D) == 0) {
-      wml[2 * h] = M;
-      wml[2 * h + 1] = L;
+
+    // ---- advance
+    rs_cur = rs_nxt;
+    if (s1 != s) {
+      kv_len = kl1;
+      start_k = a.window > 0 ? max(0, kv_len - a.window) : 0;
     }
+    s = s1;
+    kvh = kvh1;
+    j = j1;
+    n_s = n1;
+    it_lo = lo1;
+    tb = tb1;
+    blk = blk1;
+  };
+  for (long long g = g0; g < g1; g += 2) {
+    step(bufA, bufB, g);
+    if (g + 1 >= g1) break;
+    step(bufB, bufA, g + 1);
   }
 }
 
-// Merge the split-K partials of every (seq, kv_head) that was split (the
+// Merge the partials of every (seq, kv_head) cut by wave-range boundaries (the
 // reduce pass of page_attention.py:2006-2059): out = sum_p 2^(m_p - M) o_p /
-// sum_p 2^(m_p - M) l_p.  Launched after decode_affine_d128 on the same stream.
+// sum_p 2^(m_p - M) l_p.  One workgroup per unit; launched after
+// decode_affine_d128 on the same stream.  Units with no live token get zeros.
 template <int HG>
 __global__ __launch_bounds__(256) void decode_merge_d128(DecodeArgs a) {
   constexpr int D = 128;
-  const int unit = blockIdx.x;
-  const int kvh = unit % a.Hkv;
-  const int s = unit / a.Hkv;
-  int kv_len = min(a.kv_lens[s], a.max_blocks * a.bs);
-  if (kv_len <= 0) return;
-  const int start_k = a.window > 0 ? max(0, kv_len - a.window) : 0;
-  const int n_tiles = ((kv_len - 1) >> 7) - (start_k >> 7) + 1;
-  const int n_splits = (n_tiles + a.tiles_per_split - 1) / a.tiles_per_split;
-  if (n_splits <= 1) return;
-
-  __shared__ float wts[512 * HG];  // n_splits <= 512
-  __shared__ float sL[HG];
-  const float* po = a.ws_o + (size_t)unit * a.max_splits * (HG * D);
-  const float* pml = a.ws_ml + (size_t)unit * a.max_splits * (HG * 2);
-  if (threadIdx.x < HG) {
-    const int h = threadIdx.x;
-    float M = -INFINITY;
-    for (int sp = 0; sp < n_splits; ++sp) M = fmaxf(M, pml[sp * HG * 2 + 2 * h]);
-    float L = 0.f;
-    for (int sp = 0; sp < n_splits; ++sp) {
-      const float m = pml[sp * HG * 2 + 2 * h];
-      const float f = m != -INFINITY ? exp2f(m - M) : 0.f;
-      L += f * pml[sp * HG * 2 + 2 * h + 1];
-      wts[sp * HG + h] = f;
-    }
-    sL[h] = L;
-  }
-  __syncthreads();
+  constexpr int PER = (HG * D + 255) / 256;  // outputs per thread
+  constexpr int CH = 8;                      // partials whose loads are in flight together
+  const int u = blockIdx.x;
+  const int kvh = u % a.Hkv;
+  const int s = u / a.Hkv;
+  const int c0 = a.ws_cum[s], c1 = a.ws_cum[s + 1], cS = a.ws_cum[a.S];
+  const int n = c1 - c0;
   h16* out = a.out + ((size_t)s * a.Hq + (size_t)kvh * HG) * D;
-  for (int i = threadIdx.x; i < HG * D; i += 256) {
-    const int h = i / D;
-    float o = 0.f;
-    for (int sp = 0; sp < n_splits; ++sp) {
-      const float f = wts[sp * HG + h];
-      if (f != 0.f) o += f * po[(size_t)sp * HG * D + i];
-    }
-    const float L = sL[h];
-    out[i] = (h16)(L > 0.f ? o / L : 0.f);
+  if (n == 0) {
+    for (int i = threadIdx.x; i < HG * D; i += 256) out[i] = (h16)0.0f;
+    return;
+  }
+  const long long I = (long long)a.Hkv * cS;
+  const int NW = (int)min((long long)a.num_waves, I);
+  const long long P = (long long)a.Hkv * c0 + (long long)kvh * n;
+  const int w0 = wave_of_item(P, I, NW);
+  const int w1 = wave_of_item(P + n - 1, I, NW);
+  if (w0 == w1) return;  // one wave owned the whole unit and wrote it
+  const int np = w1 - w0 + 1;
+  const float* po = a.ws_o + ((size_t)w0 + u) * (HG * D);
+  const float* pml = a.ws_ml + ((size_t)w0 + u) * (HG * 2);
+
+  // online combine per output element: (M, L, O) <- (m_p, l_p, o_p)
+  float M[PER], L[PER], O[PER];
+#pragma unroll
+  for (int e = 0; e < PER; ++e) {
+    M[e] = -INFINITY;
+    L[e] = 0.f;
+    O[e] = 0.f;
+  }
+  for (int base = 0; base < np; base += CH) {
+    float ov[CH][PER], mv[CH][PER], lv[CH][PER];
+#pragma unroll
+    for (int c = 0; c < CH; ++c)
+#pragma unroll
+      for (int e = 0; e < PER; ++e) {
+        const int i = threadIdx.x + 256 * e;
+        const bool ok = base + c < np && i < HG * D;
+        const size_t pp = (size_t)(base + c);
+        const int h = i / D;
+        ov[c][e] = ok ? po[pp * HG * D + i] : 0.f;
+        mv[c][e] = ok ? pml[pp * HG * 2 + 2 * h] : -INFINITY;
+        lv[c][e] = ok ? pml[pp * HG * 2 + 2 * h + 1] : 0.f;
+      }
+#pragma unroll
+    for (int c = 0; c < CH; ++c)
+#pragma unroll
+      for (int e = 0; e < PER; ++e) {
+        if (mv[c][e] == -INFINITY) continue;
+        const float Mn = fmaxf(M[e], mv[c][e]);
+        const float fo = __builtin_amdgcn_exp2f(M[e] - Mn);  // 0 while M is -inf
+        const float fp = __builtin_amdgcn_exp2f(mv[c][e] - Mn);
+        O[e] = O[e] * fo + ov[c][e] * fp;
+        L[e] = L[e] * fo + lv[c][e] * fp;
+        M[e] = Mn;
+      }
+  }
+#pragma unroll
+  for (int e = 0; e < PER; ++e) {
+    const int i = threadIdx.x + 256 * e;
+    if (i < HG * D) out[i] = (h16)(L[e] > 0.f ? O[e] / L[e] : 0.f);
   }
 }
 

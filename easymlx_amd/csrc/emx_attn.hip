@@ -6,6 +6,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <string>
 
 #include "../../include/emx_attn.h"
@@ -35,27 +36,30 @@ int check_launch(const char* what) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-constexpr int kTile = 128;        // tokens per decode tile
-constexpr int kWavesPerWG = 4;
-constexpr int kMaxSplits = 512;
-
-// Tiles per split for the decode kernel: one tile per wave unless that would
-// exceed kMaxSplits partitions for the longest possible sequence.
-int decode_tiles_per_split(int max_blocks, int page_size) {
-  const long max_tiles = (long)max_blocks * page_size / kTile;
-  int tps = kWavesPerWG;
-  while ((max_tiles + tps - 1) / tps > kMaxSplits) tps += kWavesPerWG;
-  return tps;
+// Waves per SIMD the persistent decode grid is sized for (its launch bounds
+// allow 2); EMX_DECODE_WAVES_PER_SIMD overrides it for tuning (1..2).
+int decode_waves_per_simd() {
+  static const int v = [] {
+    const char* e = std::getenv("EMX_DECODE_WAVES_PER_SIMD");
+    const int x = e ? std::atoi(e) : 2;
+    return x >= 1 && x <= 2 ? x : 2;
+  }();
+  return v;
 }
 
-int decode_max_splits(int max_blocks, int page_size) {
-  const long max_tiles = (long)max_blocks * page_size / kTile;
-  const int tps = decode_tiles_per_split(max_blocks, page_size);
-  return (int)((max_tiles + tps - 1) / tps);
+// Compute units of the current device (256 on MI355X).
+int device_cus() {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) !=
+                                              hipSuccess || cus <= 0)
+    return 256;
+  return cus;
 }
 
-bool decode_fast_path(int head_dim, int page_size, int bits, int group_size, int hg) {
-  if (head_dim != 128 || page_size % kTile != 0) return false;
+int decode_num_waves() { return device_cus() * 4 * decode_waves_per_simd(); }
+
+bool decode_fast_path(int head_dim, int page_size, int bits, int group_size, int hg, int num_seqs) {
+  if (head_dim != 128 || page_size % 128 != 0 || num_seqs > emx::kMaxSeqs) return false;
   if (bits != 4 && bits != 8) return false;
   if (group_size != 32 && group_size != 64 && group_size != 128) return false;
   if (hg < 1 || hg > 16 || (hg & (hg - 1)) != 0) return false;
@@ -203,15 +207,11 @@ int emx_affine_cache_write(const void* keys, const void* values, const int32_t* 
 size_t emx_paged_workspace_bytes(int num_seqs, int num_q_heads, int num_kv_heads, int head_dim,
                                  int max_blocks_per_seq, int page_size) {
   if (num_seqs <= 0 || num_kv_heads <= 0 || num_q_heads <= 0 || max_blocks_per_seq <= 0 || page_size <= 0 ||
-      head_dim != 128 || page_size % kTile != 0)
+      head_dim != 128 || page_size % 128 != 0 || num_seqs > emx::kMaxSeqs)
     return 0;
   const int hg = num_q_heads / num_kv_heads;
-  const int ms = decode_max_splits(max_blocks_per_seq, page_size);
-  if (ms <= 1) return 0;
-  const size_t units = (size_t)num_seqs * num_kv_heads;
-  size_t bytes = units * ms * hg * head_dim * sizeof(float);  // partial accumulators
-  bytes += units * ms * hg * 2 * sizeof(float);                // partial (max, sum)
-  return bytes;
+  const size_t slots = (size_t)decode_num_waves() + (size_t)num_seqs * num_kv_heads;
+  return slots * hg * (head_dim + 2) * sizeof(float) + (num_seqs + 1) * sizeof(int);  // partials + prefix
 }
 
 int emx_paged_attention_affine(const void* queries, int num_tokens, int num_q_heads, int head_dim,
@@ -240,16 +240,15 @@ int emx_paged_attention_affine(const void* queries, int num_tokens, int num_q_he
   const float scale_log2 = softmax_scale * emx::kLog2e;
   const int window = sliding_window > 0 ? sliding_window : 0;
 
-  if (single_token_decode && decode_fast_path(head_dim, page_size, bits, group_size, hg)) {
+  if (single_token_decode && decode_fast_path(head_dim, page_size, bits, group_size, hg, num_seqs)) {
     if (!aligned16(queries) || !aligned16(k_codes) || !aligned16(v_codes) || !aligned16(k_scales) ||
         !aligned16(k_biases) || !aligned16(v_scales) || !aligned16(v_biases))
       return fail(EMX_ERR_INVALID, "queries and cache tensors must be 16-byte aligned");
-    const int tps = decode_tiles_per_split(max_blocks_per_seq, page_size);
-    const int ms = decode_max_splits(max_blocks_per_seq, page_size);
     const size_t need =
         emx_paged_workspace_bytes(num_seqs, num_q_heads, num_kv_heads, head_dim, max_blocks_per_seq, page_size);
-    if (need > 0 && (workspace == nullptr || workspace_bytes < need))
+    if (workspace == nullptr || workspace_bytes < need)
       return fail(EMX_ERR_INVALID, "workspace too small: need %zu bytes, got %zu", need, workspace_bytes);
+    const int nw = decode_num_waves();
     emx::DecodeArgs a;
     a.q = reinterpret_cast<const emx::h16*>(queries);
     a.kc = k_codes;
@@ -261,10 +260,10 @@ int emx_paged_attention_affine(const void* queries, int num_tokens, int num_q_he
     a.block_tables = block_tables;
     a.kv_lens = kv_lens;
     a.out = reinterpret_cast<emx::h16*>(out);
-    const size_t units = (size_t)num_seqs * num_kv_heads;
-    char* ws = reinterpret_cast<char*>(workspace);
-    a.ws_o = reinterpret_cast<float*>(ws);
-    a.ws_ml = need ? reinterpret_cast<float*>(ws + units * ms * hg * head_dim * sizeof(float)) : nullptr;
+    const size_t slots = (size_t)nw + (size_t)num_seqs * num_kv_heads;
+    a.ws_o = reinterpret_cast<float*>(workspace);
+    a.ws_ml = a.ws_o + slots * hg * head_dim;
+    a.ws_cum = reinterpret_cast<int*>(a.ws_ml + slots * hg * 2);
     a.S = num_seqs;
     a.Hq = num_q_heads;
     a.Hkv = num_kv_heads;
@@ -273,21 +272,16 @@ int emx_paged_attention_affine(const void* queries, int num_tokens, int num_q_he
     a.max_blocks = max_blocks_per_seq;
     a.scale_log2 = scale_log2;
     a.window = window;
-    a.tiles_per_split = tps;
-    a.max_splits = ms;
+    a.num_waves = nw;
+    a.nt = bits == 4 ? 64 : 32;
     DecodeFn fn = bits == 4 ? pick_decode_gs<4>(group_size, hg) : pick_decode_gs<8>(group_size, hg);
     DecodeFn merge = pick_merge(hg);
     if (!fn || !merge)
       return fail(EMX_ERR_UNSUPPORTED, "no decode kernel for bits=%d group_size=%d gqa=%d", bits, group_size, hg);
-    const long grid = (long)ms * num_seqs * num_kv_heads;
-    if (grid > 0x7fffffffL) return fail(EMX_ERR_UNSUPPORTED, "decode grid too large");
-    hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(256), 0, st, a);
+    hipLaunchKernelGGL(fn, dim3((unsigned)(nw / 4)), dim3(256), 0, st, a);
     if (int r = check_launch("decode_affine_d128")) return r;
-    if (ms > 1) {
-      hipLaunchKernelGGL(merge, dim3((unsigned)(num_seqs * num_kv_heads)), dim3(256), 0, st, a);
-      return check_launch("decode_merge_d128");
-    }
-    return EMX_OK;
+    hipLaunchKernelGGL(merge, dim3((unsigned)(num_seqs * num_kv_heads)), dim3(256), 0, st, a);
+    return check_launch("decode_merge_d128");
   }
 
   if (queries && !aligned16(queries)) return fail(EMX_ERR_INVALID, "queries must be 16-byte aligned");
