@@ -31,6 +31,9 @@ def write_positions(block_tables, kv_lens, query_start_loc, slot_ids, block_size
 
     Tokens whose block id is negative get ``slot_mapping = -1`` (not written),
     matching ``PageCacheView.append``'s skip of ``block < 0`` (``cache.py:859-861``).
+    A position past the end of the block table is also skipped: the reference
+    gathers ``block_tables[slot, pos // bs]`` unchecked (``cache.py:1168``), where
+    MLX's out-of-range gather is unspecified, so no value there is pinned.
     """
     bt = np.asarray(block_tables)
     kv = np.asarray(kv_lens).astype(np.int64).copy()
@@ -42,7 +45,8 @@ def write_positions(block_tables, kv_lens, query_start_loc, slot_ids, block_size
         base = int(kv[slot])
         for j in range(max(0, end - start)):
             pos = base + j
-            block = int(bt[slot, pos // block_size])
+            col = pos // block_size
+            block = int(bt[slot, col]) if col < bt.shape[1] else -1
             if block >= 0:
                 slot_mapping[start + j] = block * block_size + pos % block_size
         kv[slot] = base + max(0, end - start)

@@ -1,0 +1,241 @@
+"""Host-side logic, checked on the CPU: write-position arithmetic against the
+reference tests' own assertions, the page-layout conversions, the operator
+plugin surface, input validation, workloads, the C ABI's exports and its
+argument errors (no kernel is launched here)."""
+
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+import re
+import subprocess
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from easymlx_amd.caching import layout
+from easymlx_amd.caching.paged import PageCacheView, PageMetadata, build_query_start_loc
+from oracle.affine import affine_quantize
+from oracle.cache_write import build_query_start_loc as oracle_qsl
+from oracle.cache_write import write_positions
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+GOLDEN = os.path.join(ROOT, "tests", "golden")
+
+
+# ---------------------------------------------------------------- write positions
+@pytest.mark.parametrize("name,initial,qlens", [("write_rng2", [1, 0, 2], [2, 0, 3]), ("write_rng7", [2, 1, 3], [1, 1, 1])])
+def test_write_goldens(name, initial, qlens):
+    """``tests/operations/test_unified_attention.py:268-415``: kv_lens += q_len, token j of a slot lands at
+    ``[table[pos // bs], pos % bs]`` with ``pos = initial_len + j``."""
+    z = np.load(os.path.join(GOLDEN, name + ".npz"))
+    bs = z["key_cache"].shape[1]
+    assert z["kv_lens"].tolist() == initial
+    assert z["query_start_loc"].tolist() == oracle_qsl(qlens).tolist()
+    assert z["expected_kv_lens"].tolist() == [a + b for a, b in zip(initial, qlens)]
+    # the slot mapping written from first principles (tables are consecutive per sequence)
+    exp = []
+    for s, n in enumerate(qlens):
+        for j in range(n):
+            pos = initial[s] + j
+            exp.append(int(z["block_tables"][s, pos // bs]) * bs + pos % bs)
+    assert z["slot_mapping"].tolist() == exp
+    sm, lens = write_positions(z["block_tables"], z["kv_lens"], z["query_start_loc"], [0, 1, 2], bs)
+    assert sm.tolist() == exp and lens.tolist() == z["expected_kv_lens"].tolist()
+
+    # the host cache view (dense, CPU tensors) performs the same write
+    view = PageCacheView(key_cache=torch.from_numpy(z["key_cache"].copy()),
+                         value_cache=torch.from_numpy(z["value_cache"].copy()),
+                         block_tables=torch.from_numpy(z["block_tables"].copy()),
+                         kv_lens=torch.from_numpy(z["kv_lens"].copy()), block_size=bs,
+                         num_kv_heads=z["key_cache"].shape[2], head_dim=z["key_cache"].shape[3])
+    md = PageMetadata(query_start_loc=torch.from_numpy(z["query_start_loc"]))
+    q, kc, vc, md2 = view.concatenate_to_cache(torch.from_numpy(z["queries"]), torch.from_numpy(z["keys"]),
+                                               torch.from_numpy(z["values"]), cache_metadata=md, slot_ids=[0, 1, 2])
+    assert view.kv_lens.tolist() == z["expected_kv_lens"].tolist()
+    assert md2.kv_lens.tolist() == z["expected_kv_lens"].tolist()
+    assert md2.is_single_token_decode == (name == "write_rng7")
+    flat_k = kc.reshape(-1, *kc.shape[2:]).numpy()
+    flat_v = vc.reshape(-1, *vc.shape[2:]).numpy()
+    np.testing.assert_array_equal(flat_k[exp], z["keys"])
+    np.testing.assert_array_equal(flat_v[exp], z["values"])
+    untouched = np.ones(flat_k.shape[0], bool)
+    untouched[exp] = False
+    np.testing.assert_array_equal(flat_k[untouched], z["key_cache"].reshape(flat_k.shape)[untouched])
+
+
+def test_slot_mapping_out_of_table_and_negative_blocks():
+    tables = torch.tensor([[3, -1], [0, 1]], dtype=torch.int32)
+    view = PageCacheView(key_cache=torch.zeros(4, 4, 1, 2), value_cache=torch.zeros(4, 4, 1, 2), block_tables=tables,
+                         kv_lens=torch.tensor([3, 7], dtype=torch.int32), block_size=4, num_kv_heads=1, head_dim=2)
+    sm, _, _ = view._slot_mapping([0, 1], [2, 2])
+    # seq 0: pos 3 -> block 3 off 3; pos 4 -> block -1 -> skipped.  seq 1: pos 7 -> block 1 off 3; pos 8 -> past table
+    assert sm.tolist() == [15, -1, 7, -1]
+    exp, _ = write_positions(tables.numpy(), [3, 7], [0, 2, 4], [0, 1], 4)
+    assert exp.tolist()[:3] == [15, -1, 7]
+
+
+def test_build_query_start_loc():
+    assert build_query_start_loc([2, 0, 3]).tolist() == [0, 2, 2, 5]
+    assert build_query_start_loc([]).tolist() == [0]
+
+
+# ---------------------------------------------------------------- page layout
+@pytest.mark.parametrize("bits", [4, 8])
+def test_layout_round_trips(bits):
+    rng = np.random.default_rng(bits)
+    nb, bs, hkv, d, gs = 3, 16, 2, 128, 64
+    x = rng.standard_normal((nb, bs, hkv, d)).astype(np.float16)
+    c, s, b = affine_quantize(x, gs, bits)
+    kp = layout.key_pages_from_logical(c)
+    assert kp.shape == (nb, hkv, bs, d * bits // 32)
+    np.testing.assert_array_equal(layout.key_logical_from_pages(kp), c)
+    vp = layout.value_pages_from_logical(c, bits)
+    assert vp.shape == (nb, hkv, d, bs * bits // 32)
+    np.testing.assert_array_equal(layout.value_logical_from_pages(vp, bits), c)
+    # value page word w of dim j holds tokens w*per .. w*per+per-1 of that dim, low bits first
+    per = 32 // bits
+    from oracle.affine import unpack_codes
+
+    q = unpack_codes(c, bits)  # [nb, bs, hkv, d]
+    assert (vp[1, 1, 5, 0] & ((1 << bits) - 1)) == q[1, 0, 1, 5]
+    assert (int(vp[1, 1, 5, 0]) >> (bits * (per - 1))) == q[1, per - 1, 1, 5]
+    sp = layout.params_pages_from_logical(s)
+    assert sp.shape == (nb, hkv, d // gs, bs) and sp[2, 1, 1, 7] == s[2, 7, 1, 1]
+    np.testing.assert_array_equal(layout.params_logical_from_pages(sp), s)
+
+
+# ---------------------------------------------------------------- operator plugin surface
+def test_registry_and_requirements():
+    from easymlx_amd.operations import OperationRegistry, UnifiedAttention
+    from easymlx_amd.operations._base_operation import MetadataField
+
+    for name in ("unified_attention", "unified", "paged", "full_attention", "linear_attention"):
+        assert OperationRegistry.get(name) is UnifiedAttention
+    with pytest.raises(KeyError):
+        OperationRegistry.get("no_such_op")
+    req = UnifiedAttention.get_requirements()
+    for f in (MetadataField.QUERY_START_LOC, MetadataField.BLOCK_TABLES, MetadataField.KV_LENS,
+              MetadataField.BLOCK_SIZE):
+        assert f in req.required_metadata
+    assert MetadataField.SLIDING_WINDOW in req.optional_metadata
+    op = OperationRegistry.create("unified_attention")
+    with pytest.raises(ValueError, match="requires cache_metadata"):
+        op(query=torch.zeros(1, 2, 4), key=None, value=None, cache_metadata=None)
+    with pytest.raises(ValueError, match="must be resolved"):
+        op(query=torch.zeros(1, 2, 4), key=None, value=None, cache_metadata=PageMetadata(query_start_loc=[0, 1]))
+
+
+def _dense_args(T=2, hq=4, hkv=2, d=8, nb=3, bs=4, S=2):
+    return (torch.zeros(T, hq, d), torch.zeros(nb, bs, hkv, d), torch.zeros(nb, bs, hkv, d),
+            torch.zeros(S, 2, dtype=torch.int32), torch.ones(S, dtype=torch.int32),
+            torch.arange(S + 1, dtype=torch.int32))
+
+
+def test_validation_messages():
+    from easymlx_amd import paged_attention
+
+    q, k, v, bt, kl, qsl = _dense_args()
+    with pytest.raises(ValueError, match="queries must be rank-3"):
+        paged_attention(q[0], k, v, bt, kl, qsl)
+    with pytest.raises(ValueError, match="rank-4"):
+        paged_attention(q, k[0], v, bt, kl, qsl)
+    with pytest.raises(ValueError, match="same shape"):
+        paged_attention(q, k, v[:2], bt, kl, qsl)
+    with pytest.raises(ValueError, match="head_dim must match"):
+        paged_attention(q[..., :4], k, v, bt, kl, qsl)
+    with pytest.raises(ValueError, match="divisible by num_kv_heads"):
+        paged_attention(q[:, :3], k, v, bt, kl, qsl)
+    with pytest.raises(ValueError, match="block_tables must be rank-2"):
+        paged_attention(q, k, v, bt[0], kl, qsl)
+    with pytest.raises(ValueError, match="length num_seqs"):
+        paged_attention(q, k, v, bt, kl, qsl[:-1])
+    with pytest.raises(ValueError, match="affine caches need"):
+        paged_attention(q, k, v, bt, kl, qsl, k_scales=torch.zeros(1))
+    # zero tokens -> zeros without touching a device (unified_attention.py:1425-1426)
+    out = paged_attention(torch.ones(0, 4, 8), k, v, bt, kl, torch.zeros(3, dtype=torch.int32))
+    assert out.shape == (0, 4, 8)
+    # no CPU fallback: a CPU tensor is refused loudly
+    with pytest.raises(RuntimeError, match="GPU only"):
+        paged_attention(q, k, v, bt, kl, qsl)
+
+
+def test_single_token_decode_detection():
+    from easymlx_amd.operations.unified_attention import _is_single_token_decode
+
+    assert _is_single_token_decode(torch.tensor([0, 1, 2, 3]), 3)
+    assert not _is_single_token_decode(torch.tensor([0, 2, 3]), 3)
+    assert not _is_single_token_decode(torch.tensor([0, 1]), 0)
+    assert not _is_single_token_decode(torch.tensor([1, 2, 3]), 2)
+
+
+# ---------------------------------------------------------------- workloads
+def test_workload_bytes_and_determinism():
+    from easymlx_amd.workloads import config
+
+    c2 = config("c2")
+    assert (c2.num_seqs, c2.num_q_heads, c2.num_kv_heads, c2.head_dim, c2.block_size, c2.bits, c2.group_size) == \
+        (32, 32, 8, 128, 128, 4, 64)
+    assert c2.kv_lens.min() >= 512 and c2.kv_lens.max() <= 4096
+    assert c2.kv_bytes() == int(c2.kv_lens.sum()) * 8 * 144  # 4-bit: 64 B codes + 8 B params, K and V
+    c1 = config("c1")
+    assert c1.bits == 8 and c1.kv_bytes() == int(c1.kv_lens.sum()) * 8 * 272
+    again = config("c2")
+    np.testing.assert_array_equal(again.kv_lens, c2.kv_lens)
+    np.testing.assert_array_equal(again.block_tables, c2.block_tables)
+    # every live token has its own slot (no two tokens share a page slot)
+    assert len(np.unique(c2.slot)) == len(c2.slot) == int(c2.kv_lens.sum())
+
+
+# ---------------------------------------------------------------- C ABI
+def _header_functions():
+    text = open(os.path.join(ROOT, "include", "emx_attn.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return re.findall(r"^\s*(?:int|size_t|const char\*)\s+(emx_\w+)\s*\(", text, flags=re.M)
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from easymlx_amd import _native
+
+    if not os.path.exists(_native.LIB_PATH):
+        pytest.skip("libemx_attn.so not built (run __graft_entry__.build())")
+    return _native.load()
+
+
+def test_abi_exports_every_declared_symbol(lib):
+    from easymlx_amd import _native
+
+    names = _header_functions()
+    assert set(names) == set(_native.SIGNATURES), (names, list(_native.SIGNATURES))
+    for n in names:
+        assert hasattr(lib, n), n
+    assert lib.emx_version() >= 100
+
+
+def test_abi_argument_errors(lib):
+    from easymlx_amd import _native
+
+    assert lib.emx_affine_quantize(None, 4, 128, 64, 3, None, None, None, None) == _native.EMX_ERR_UNSUPPORTED
+    assert b"bits" in lib.emx_last_error()
+    assert lib.emx_affine_quantize(None, 4, 100, 64, 4, None, None, None, None) == _native.EMX_ERR_INVALID
+    assert lib.emx_affine_quantize(None, 0, 128, 64, 4, None, None, None, None) == _native.EMX_OK
+    assert lib.emx_affine_quantize(None, 4, 128, 64, 4, None, None, None, None) == _native.EMX_ERR_INVALID
+    with pytest.raises(ValueError):
+        _native.check(_native.EMX_ERR_INVALID)
+    with pytest.raises(NotImplementedError):
+        _native.check(_native.EMX_ERR_UNSUPPORTED)
+    with pytest.raises(RuntimeError):
+        _native.check(_native.EMX_ERR_HIP)
+    # decode workspace size is pure host arithmetic; 0 where the split-K path does not apply
+    assert lib.emx_paged_workspace_bytes(32, 32, 8, 128, 32, 128) > 0
+    assert lib.emx_paged_workspace_bytes(32, 32, 8, 64, 32, 128) == 0
+
+
+def test_bench_refuses_more_than_one_gpu():
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True, text=True,
+                       timeout=60)
+    assert r.returncode == 2 and "one GPU" in r.stdout
