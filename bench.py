@@ -36,6 +36,8 @@ def parse():
     p.add_argument("--pool-gib", type=float, default=1.5, help="total size of the rotated page pools")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seqs", type=int, default=0, help="sequences in the CPU baseline sample (0 = auto)")
+    p.add_argument("--copy-probe-mib", type=int, default=0,
+                   help="after the timed region, run 5 plain device copies of this size (counter calibration)")
     return p.parse_args()
 
 
@@ -51,7 +53,7 @@ def cpu_baseline(wl, n_seqs: int | None):
     os.environ.setdefault("OMP_NUM_THREADS", str(cores))
     P = ctypes.c_void_p
     lib.oracle_decode_affine.argtypes = [P] * 9 + [ctypes.c_int] * 9 + [ctypes.c_float, P]
-    n = n_seqs or 8
+    n = n_seqs or wl.num_seqs
     bs, hkv, d, g, bits = wl.block_size, wl.num_kv_heads, wl.head_dim, wl.group_size, wl.bits
     lens = wl.kv_lens[:n]
     ntok = int(lens.sum())
@@ -70,7 +72,7 @@ def cpu_baseline(wl, n_seqs: int | None):
     out = np.zeros((n, wl.num_q_heads, d), np.float32)
     ptr = lambda a: a.ctypes.data_as(P)  # noqa: E731
     reps, t_total = 0, 0.0
-    while t_total < 10.0 and reps < 50:
+    while t_total < 12.0 and reps < 2000:
         t0 = time.perf_counter()
         lib.oracle_decode_affine(ptr(q), ptr(res["k"][0]), ptr(res["k"][1]), ptr(res["k"][2]), ptr(res["v"][0]),
                                  ptr(res["v"][1]), ptr(res["v"][2]), ptr(tables), ptr(np.ascontiguousarray(lens)), n,
@@ -86,8 +88,8 @@ def cpu_baseline(wl, n_seqs: int | None):
         "unit": "GB/s",
         "cores": cores,
         "kind": "port",
-        "sample": f"C oracle (oracle/c/oracle.c, OpenMP) on the first {n} of 32 sequences of the same workload "
-                  f"({ntok} tokens), {reps} reps, {per * 1e3:.1f} ms each = {n / per:.1f} decode rows/s",
+        "sample": f"C oracle (oracle/c/oracle.c, OpenMP over (seq, kv_head)) on {n} of {wl.num_seqs} sequences of the "
+                  f"same workload ({ntok} tokens), {reps} reps, {per * 1e3:.1f} ms each = {n / per:.1f} decode rows/s",
     }
 
 
@@ -161,6 +163,16 @@ def main():
     kt = np.array([a.elapsed_time(b) for a, b in evs]) * 1e3  # us
     k_avg_us = float(kt.mean())
     achieved = bytes_per_step / (k_avg_us * 1e-6) / 1e9
+
+    if args.copy_probe_mib:
+        n = args.copy_probe_mib << 20
+        src = torch.ones(n // 4, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     value = bytes_per_step / (ms_per_step * 1e-3) / 1e9
     cpu = None if args.no_cpu_baseline else cpu_baseline(wl, args.cpu_seqs or None)
