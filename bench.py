@@ -93,6 +93,18 @@ def cpu_baseline(wl, n_seqs: int | None):
     }
 
 
+def measured_traffic():
+    """HBM bytes per decode call from the committed counter summary (two rocprofv3 --pmc passes)."""
+    path = os.path.join(ROOT, "profiles", "decode_affine_c2_hbm_traffic.md")
+    try:
+        for line in open(path):
+            if line.startswith("TRAFFIC_BYTES_PER_CALL:"):
+                return int(line.split(":")[1]), os.path.relpath(path, ROOT)
+    except OSError:
+        pass
+    return None, None
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -175,6 +187,7 @@ def main():
         del src, dst
 
     value = bytes_per_step / (ms_per_step * 1e-3) / 1e9
+    traffic, traffic_src = measured_traffic()
     cpu = None if args.no_cpu_baseline else cpu_baseline(wl, args.cpu_seqs or None)
     line = {
         "metric": "4-bit-KV paged decode: achieved HBM GB/s (% of peak) + tokens/s, batch 32",
@@ -209,8 +222,9 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
-            "kernel": "emx::decode_affine_d128<4,64,4>",
+            "traffic": traffic,
+            "traffic_source": traffic_src,
+            "kernel": "emx::decode_affine_d128<4,64,4> + emx::decode_merge_d128<4> (one decode call)",
         },
         "cpu_baseline": cpu,
     }
