@@ -10,7 +10,8 @@ reference's dense cache ``lib/python/easymlx/caching/paged/cache.py:790-791``):
 Page layout used by the kernels (see ``include/emx_attn.h``):
 
     key codes    uint32 [nb, Hkv, bs, D*bits/32]   token-major
-    value codes  uint32 [nb, Hkv, D, bs*bits/32]   dim-major (tokens packed along a word)
+    value codes  uint32 [nb, Hkv, bs/T, D, T*bits/32]   T = min(bs, 256/bits) tokens per tile,
+                                                     dim-major inside a tile (tokens packed along a word)
     scales       fp16   [nb, Hkv, D/gs, bs]         (biases likewise)
 
 NumPy only; used to build pages from host data and to read pages back.
@@ -44,16 +45,24 @@ def key_logical_from_pages(pages: np.ndarray) -> np.ndarray:
     return np.ascontiguousarray(np.asarray(pages).view(np.uint32).transpose(0, 2, 1, 3))
 
 
+def value_tile(block_size: int, bits: int) -> int:
+    """Tokens per value tile: ``min(block_size, 256 // bits)``."""
+    return min(block_size, 256 // bits)
+
+
 def value_pages_from_logical(codes: np.ndarray, bits: int) -> np.ndarray:
-    """``[nb, bs, Hkv, W]`` -> ``[nb, Hkv, D, bs*bits/32]`` (tokens packed per word)."""
+    """``[nb, bs, Hkv, W]`` -> ``[nb, Hkv, bs/T, D, T*bits/32]`` (tokens packed per word)."""
     q = _unpack(np.asarray(codes, dtype=np.uint32), bits)  # [nb, bs, Hkv, D]
-    q = q.transpose(0, 2, 3, 1)  # [nb, Hkv, D, bs]
+    nb, bs, hkv, d = q.shape
+    t = value_tile(bs, bits)
+    q = q.reshape(nb, bs // t, t, hkv, d).transpose(0, 3, 1, 4, 2)  # [nb, Hkv, bs/T, D, T]
     return np.ascontiguousarray(_pack(q, bits))
 
 
 def value_logical_from_pages(pages: np.ndarray, bits: int) -> np.ndarray:
-    q = _unpack(np.asarray(pages).view(np.uint32), bits)  # [nb, Hkv, D, bs]
-    q = q.transpose(0, 3, 1, 2)  # [nb, bs, Hkv, D]
+    q = _unpack(np.asarray(pages).view(np.uint32), bits)  # [nb, Hkv, bs/T, D, T]
+    nb, hkv, nt, d, t = q.shape
+    q = q.transpose(0, 2, 4, 1, 3).reshape(nb, nt * t, hkv, d)  # [nb, bs, Hkv, D]
     return np.ascontiguousarray(_pack(q, bits))
 
 

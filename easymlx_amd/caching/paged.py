@@ -78,6 +78,12 @@ def _contiguous_tables(num_seqs: int, blocks_per_seq: int, device) -> torch.Tens
     return torch.arange(num_seqs * blocks_per_seq, dtype=torch.int32, device=device).reshape(num_seqs, blocks_per_seq)
 
 
+def _v_shape(nb: int, hkv: int, d: int, bs: int, bits: int) -> tuple[int, ...]:
+    # value codes in tiles of T = min(bs, 256 // bits) tokens, dim-major inside a tile
+    t = min(bs, 256 // bits)
+    return (nb, hkv, bs // t, d, t * bits // 32)
+
+
 class PageCacheView:
     """Unquantized paged cache ``[num_blocks, block_size, Hkv, D]`` (``cache.py:700-825``)."""
 
@@ -276,7 +282,8 @@ class AffinePageCacheView(PageCacheView):
     """Affine int4/int8 KV pages with fused quantize-on-write.
 
     Storage (see ``include/emx_attn.h``): key codes ``[nb, Hkv, bs, D*b/32]``,
-    value codes ``[nb, Hkv, D, bs*b/32]`` (int32 tensors holding uint32 words),
+    value codes ``[nb, Hkv, bs/T, D, T*b/32]`` with ``T = min(bs, 256/b)`` (int32
+    tensors holding uint32 words),
     scales/biases ``[nb, Hkv, D/gs, bs]`` fp16.  The reference has no affine KV
     cache; its FP8 cache (``cache.py:770-797, 1171-1184``) is the structural
     analogue, with the per-block running-max scale replaced by MLX's affine
@@ -322,6 +329,8 @@ class AffinePageCacheView(PageCacheView):
             raise ValueError("head_dim must be a multiple of group_size, itself a multiple of 8")
         if (block_size * bits) % 32 or (head_dim * bits) % 32:
             raise ValueError("block_size * bits and head_dim * bits must be multiples of 32")
+        if block_size > 256 // bits and block_size % (256 // bits):
+            raise ValueError("block_size above 256 // bits must be a multiple of 256 // bits")
         bps = math.ceil(max_seq_len / block_size)
         nb = num_blocks if num_blocks is not None else bps * num_seqs
         if nb < bps * num_seqs:
@@ -332,7 +341,7 @@ class AffinePageCacheView(PageCacheView):
             k_codes=z((nb, num_kv_heads, block_size, head_dim * bits // 32), torch.int32),
             k_scales=z((nb, num_kv_heads, G, block_size), torch.float16),
             k_biases=z((nb, num_kv_heads, G, block_size), torch.float16),
-            v_codes=z((nb, num_kv_heads, head_dim, block_size * bits // 32), torch.int32),
+            v_codes=z(_v_shape(nb, num_kv_heads, head_dim, block_size, bits), torch.int32),
             v_scales=z((nb, num_kv_heads, G, block_size), torch.float16),
             v_biases=z((nb, num_kv_heads, G, block_size), torch.float16),
             block_tables=_contiguous_tables(num_seqs, bps, device),
@@ -423,7 +432,7 @@ def affine_pool(
         k_codes=z((num_blocks, num_kv_heads, block_size, head_dim * bits // 32), torch.int32),
         k_scales=z((num_blocks, num_kv_heads, G, block_size), torch.float16),
         k_biases=z((num_blocks, num_kv_heads, G, block_size), torch.float16),
-        v_codes=z((num_blocks, num_kv_heads, head_dim, block_size * bits // 32), torch.int32),
+        v_codes=z(_v_shape(num_blocks, num_kv_heads, head_dim, block_size, bits), torch.int32),
         v_scales=z((num_blocks, num_kv_heads, G, block_size), torch.float16),
         v_biases=z((num_blocks, num_kv_heads, G, block_size), torch.float16),
         block_tables=block_tables.to(torch.int32).contiguous(),

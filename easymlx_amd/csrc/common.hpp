@@ -62,6 +62,17 @@ __device__ __forceinline__ void from_f32(float f, h16* p) { *p = (h16)f; }
 __device__ __forceinline__ void from_f32(float f, float* p) { *p = f; }
 __device__ __forceinline__ void from_f32(float f, uint16_t* p) { *p = f32_to_bf16(f); }
 
+// Value pages are stored in tiles of T = min(page_size, 256/BITS) tokens; inside a
+// tile they are dim-major with T*BITS/32 words per dim (32 bytes when the page
+// holds a whole tile), so one decode iteration's value codes are one contiguous
+// 4 KiB block.  Word index of (page-head ph, token off, dim d):
+template <int BITS>
+__host__ __device__ __forceinline__ size_t v_word_index(size_t ph, int off, int d, int D, int bs) {
+  constexpr int TMAX = 256 / BITS;
+  const int T = bs < TMAX ? bs : TMAX;
+  return ((ph * (size_t)(bs / T) + (size_t)(off / T)) * D + d) * (size_t)(T * BITS / 32) + (off % T) / (32 / BITS);
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));

@@ -26,7 +26,7 @@
 //            s = 2^24 * sum_g scale[t,g] * C[t,(h,g)] + bias[t,g] * sum_{d in g} q_hd
 //          The group sum is a DPP row rotation.
 //   softmax: online, base 2, fp32.
-//   PV   : 8 dim sub-tiles x NT/32 token k-slices.  A = V codes (V pages are
+//   PV   : 8 dim sub-tiles x NT/32 token k-slices.  A = V codes (V tiles are
 //          dim-major, so a lane's uint32 holds consecutive tokens of one dim),
 //          B = p * v_scale[t, g] in fp16; sum_t p_t * v_bias[t, g] is kept in fp32.
 //   Scales and biases of the iteration are staged through a per-wave LDS slot.
@@ -41,7 +41,7 @@ struct DecodeArgs {
   const uint32_t* kc;         // [nb, Hkv, bs, 128*BITS/32]
   const h16* ks;              // [nb, Hkv, G, bs]
   const h16* kb;              // [nb, Hkv, G, bs]
-  const uint32_t* vc;         // [nb, Hkv, 128, bs*BITS/32]
+  const uint32_t* vc;         // [nb, Hkv, bs/NT, 128, 8] (NT-token tiles, dim-major, 32 B per dim)
   const h16* vs;              // [nb, Hkv, G, bs]
   const h16* vb;              // [nb, Hkv, G, bs]
   const int32_t* block_tables;  // [S, max_blocks]
@@ -102,8 +102,8 @@ __device__ __forceinline__ TileRsrc make_tile_rsrc(const DecodeArgs& a, const in
   TileRsrc rs;
   rs.k = __builtin_amdgcn_make_buffer_rsrc((void*)(a.kc + (ph * a.bs + off) * C::W), (short)0, 128 * C::W * 4,
                                            kRsrcFlags);
-  rs.v = __builtin_amdgcn_make_buffer_rsrc((void*)(a.vc + ph * C::D * RW + off * BITS / 32), (short)0,
-                                           (C::D * RW - off * BITS / 32) * 4, kRsrcFlags);
+  rs.v = __builtin_amdgcn_make_buffer_rsrc((void*)(a.vc + ph * C::D * RW + (off / C::NT) * C::D * 8), (short)0,
+                                           (C::D * RW - (off / C::NT) * C::D * 8) * 4, kRsrcFlags);
   const h16* sp[4] = {a.ks, a.kb, a.vs, a.vb};
 #pragma unroll
   for (int arr = 0; arr < 4; ++arr)
@@ -141,7 +141,7 @@ __device__ __forceinline__ void issue_loads(IterLoads<BITS, GS, HG>& L, const Ti
   for (int dt = 0; dt < 8; ++dt) {
     typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
     const u32x2 x =
-        __builtin_amdgcn_raw_buffer_load_b64(rs.v, lv, dt * 16 * RW * 4 + it * C::NT * BITS / 8, kLoadAux);
+        __builtin_amdgcn_raw_buffer_load_b64(rs.v, lv, dt * 16 * 8 * 4 + it * C::D * 8 * 4, kLoadAux);
     L.vw[dt][0] = x[0];
     L.vw[dt][1] = x[1];
   }
@@ -426,7 +426,7 @@ __global__ __launch_bounds__(256, 2) void decode_affine_d128(DecodeArgs a) {
 
   const int RW = a.bs * BITS / 32;
   const int lk = ((C::TPL * (col >> 2) + (col & 3)) * C::W + C::KW * jj) * 4;
-  const int lv = (col * RW + C::TPL * jj * BITS / 32) * 4;
+  const int lv = (col * 8 + C::TPL * jj * BITS / 32) * 4;
   int ls[2], lsd[2];  // staged scale/bias dword: global byte offset and LDS half index (-1 = none)
 #pragma unroll
   for (int k = 0; k < 2; ++k) {

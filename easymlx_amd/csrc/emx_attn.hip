@@ -172,8 +172,8 @@ int emx_affine_cache_write(const void* keys, const void* values, const int32_t* 
   if (group_size <= 0 || group_size % 8 != 0 || head_dim % group_size != 0)
     return fail(EMX_ERR_INVALID, "head_dim %d must be a multiple of group_size %d (a multiple of 8)", head_dim,
                 group_size);
-  if ((page_size * bits) % 32 != 0)
-    return fail(EMX_ERR_INVALID, "page_size * bits must be a multiple of 32 (page_size %d)", page_size);
+  if ((page_size * bits) % 32 != 0 || (page_size > 256 / bits && page_size % (256 / bits) != 0))
+    return fail(EMX_ERR_INVALID, "page_size %d must be a multiple of 32/bits, and of 256/bits when larger", page_size);
   if (num_tokens == 0) return EMX_OK;
   if (!keys || !values || !slot_mapping || !k_codes || !k_scales || !k_biases || !v_codes || !v_scales || !v_biases)
     return fail(EMX_ERR_INVALID, "null pointer");
@@ -231,6 +231,8 @@ int emx_paged_attention_affine(const void* queries, int num_tokens, int num_q_he
     return fail(EMX_ERR_INVALID, "head_dim %d must be a multiple of group_size %d", head_dim, group_size);
   if ((head_dim * bits) % 32 != 0 || (page_size * bits) % 32 != 0)
     return fail(EMX_ERR_INVALID, "head_dim * bits and page_size * bits must be multiples of 32");
+  if (page_size > 256 / bits && page_size % (256 / bits) != 0)
+    return fail(EMX_ERR_INVALID, "page_size %d above 256/bits must be a multiple of 256/bits", page_size);
   if (!std::isfinite(softmax_scale)) return fail(EMX_ERR_INVALID, "softmax_scale must be finite");
   if (num_tokens == 0) return EMX_OK;
   if (!k_codes || !k_scales || !k_biases || !v_codes || !v_scales || !v_biases)

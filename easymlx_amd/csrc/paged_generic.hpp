@@ -65,7 +65,7 @@ struct AffineKV {
   __device__ __forceinline__ float val(int blk, int off, int h, int d) const {
     constexpr int PW = 32 / BITS;
     const size_t ph = (size_t)blk * Hkv + h;
-    const uint32_t w = vc[(ph * D + d) * (bs / PW) + off / PW];
+    const uint32_t w = vc[v_word_index<BITS>(ph, off, d, D, bs)];
     const float q = (float)((w >> ((off % PW) * BITS)) & ((1u << BITS) - 1u));
     const size_t si = (ph * (D / gs) + d / gs) * bs + off;
     return (float)vs[si] * q + (float)vb[si];

@@ -88,7 +88,7 @@ struct WriteArgs {
   const int32_t* slot_mapping; // [T]
   uint32_t* kc;                // [nb, Hkv, bs, D*b/32]
   h16 *ks, *kb;                // [nb, Hkv, D/gs, bs]
-  uint32_t* vc;                // [nb, Hkv, D, bs*b/32]
+  uint32_t* vc;                // [nb, Hkv, bs/T, D, T*b/32], T = min(bs, 256/b) (v_word_index)
   h16 *vs, *vb;                // [nb, Hkv, D/gs, bs]
   int T, Hkv, D, gs, bs, nb;
 };
@@ -131,14 +131,12 @@ __global__ __launch_bounds__(256) void affine_cache_write(WriteArgs a) {
     a.ks[si] = (h16)scale;
     a.kb[si] = (h16)bias;
   } else {
-    const int RW = a.bs / PW;
     for (int i = 0; i < a.gs; ++i) {
       const uint32_t code = affine_code((float)src[i], scale, bias, n_bins);
-      const size_t row = ph * a.D + (size_t)g * a.gs + i;
+      uint32_t* wp = a.vc + v_word_index<BITS>(ph, off, g * a.gs + i, a.D, a.bs);
       if constexpr (BITS == 8) {
-        reinterpret_cast<uint8_t*>(a.vc)[row * a.bs + off] = (uint8_t)code;
+        reinterpret_cast<uint8_t*>(wp)[off % PW] = (uint8_t)code;
       } else {
-        uint32_t* wp = a.vc + row * RW + off / PW;
         const int sh = (off % PW) * BITS;
         atomicAnd(wp, ~(0xFu << sh));
         atomicOr(wp, code << sh);

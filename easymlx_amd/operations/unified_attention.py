@@ -54,8 +54,11 @@ def _validate_inputs(queries, key_cache, value_cache, block_tables, kv_lens, que
     """Shape checks with the reference's messages (``unified_attention.py:85-121``)."""
     if queries.ndim != 3:
         raise ValueError("queries must be rank-3: [total_tokens, num_q_heads, head_dim]")
-    if key_cache.ndim != 4 or value_cache.ndim != 4:
+    if not affine and (key_cache.ndim != 4 or value_cache.ndim != 4):
         raise ValueError("key_cache/value_cache must be rank-4: [num_blocks, block_size, num_kv_heads, head_dim]")
+    if affine and (key_cache.ndim != 4 or value_cache.ndim != 5):
+        raise ValueError("affine pages must be key codes [num_blocks, num_kv_heads, block_size, W] and value codes "
+                         "[num_blocks, num_kv_heads, block_size/T, head_dim, T*bits/32]")
     if not affine:
         if key_cache.shape != value_cache.shape:
             raise ValueError("key_cache and value_cache must have the same shape")
@@ -66,7 +69,7 @@ def _validate_inputs(queries, key_cache, value_cache, block_tables, kv_lens, que
     else:
         if key_cache.shape[0] != value_cache.shape[0] or key_cache.shape[1] != value_cache.shape[1]:
             raise ValueError("key_cache and value_cache must have the same [num_blocks, num_kv_heads]")
-        if value_cache.shape[2] != queries.shape[2]:
+        if value_cache.shape[3] != queries.shape[2]:
             raise ValueError("queries head_dim must match key/value cache head_dim")
         if queries.shape[1] % key_cache.shape[1] != 0:
             raise ValueError("num_q_heads must be divisible by num_kv_heads (GQA)")
@@ -142,7 +145,8 @@ def paged_attention(
     Dense caches use the reference layout ``[num_blocks, block_size, Hkv, D]``.
     Affine caches (``k_scales`` given) use the page layout of
     :class:`~easymlx_amd.caching.paged.AffinePageCacheView`:
-    ``key_cache [nb, Hkv, bs, D*bits/32]``, ``value_cache [nb, Hkv, D, bs*bits/32]``,
+    ``key_cache [nb, Hkv, bs, D*bits/32]``, ``value_cache [nb, Hkv, bs/T, D, T*bits/32]``
+    (``T = min(bs, 256/bits)``),
     scales/biases ``[nb, Hkv, D/group_size, bs]``.
 
     Returns ``[total_tokens, num_q_heads, head_dim]`` in the queries' dtype.

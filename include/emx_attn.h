@@ -8,7 +8,10 @@
  *
  * Page layout (per block `b`, kv head `h`; G = head_dim / group_size):
  *   key codes    uint32 [num_blocks, Hkv, page_size, head_dim*bits/32]  token-major
- *   value codes  uint32 [num_blocks, Hkv, head_dim, page_size*bits/32]  dim-major
+ *   value codes  uint32 [num_blocks, Hkv, page_size/T, head_dim, T*bits/32]
+ *                with T = min(page_size, 256/bits) tokens per tile, dim-major inside
+ *                a tile (a word packs 32/bits consecutive tokens of one dim);
+ *                page_size must be a multiple of T
  *   k/v scales   fp16   [num_blocks, Hkv, G, page_size]
  *   k/v biases   fp16   [num_blocks, Hkv, G, page_size]
  * Codes are packed little-endian (element j of a word at bits [j*bits,(j+1)*bits)),

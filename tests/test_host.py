@@ -87,22 +87,25 @@ def test_build_query_start_loc():
 @pytest.mark.parametrize("bits", [4, 8])
 def test_layout_round_trips(bits):
     rng = np.random.default_rng(bits)
-    nb, bs, hkv, d, gs = 3, 16, 2, 128, 64
+    nb, bs, hkv, d, gs = 3, 128, 2, 128, 64
     x = rng.standard_normal((nb, bs, hkv, d)).astype(np.float16)
     c, s, b = affine_quantize(x, gs, bits)
     kp = layout.key_pages_from_logical(c)
     assert kp.shape == (nb, hkv, bs, d * bits // 32)
     np.testing.assert_array_equal(layout.key_logical_from_pages(kp), c)
     vp = layout.value_pages_from_logical(c, bits)
-    assert vp.shape == (nb, hkv, d, bs * bits // 32)
+    t = min(bs, 256 // bits)
+    assert vp.shape == (nb, hkv, bs // t, d, t * bits // 32)
     np.testing.assert_array_equal(layout.value_logical_from_pages(vp, bits), c)
-    # value page word w of dim j holds tokens w*per .. w*per+per-1 of that dim, low bits first
+    # value tile word w of dim j holds tokens w*per .. w*per+per-1 of that tile and dim, low bits first
     per = 32 // bits
     from oracle.affine import unpack_codes
 
     q = unpack_codes(c, bits)  # [nb, bs, hkv, d]
-    assert (vp[1, 1, 5, 0] & ((1 << bits) - 1)) == q[1, 0, 1, 5]
-    assert (int(vp[1, 1, 5, 0]) >> (bits * (per - 1))) == q[1, per - 1, 1, 5]
+    assert (vp[1, 1, 0, 5, 0] & ((1 << bits) - 1)) == q[1, 0, 1, 5]
+    assert (int(vp[1, 1, 0, 5, 0]) >> (bits * (per - 1))) == q[1, per - 1, 1, 5]
+    if bs // t > 1:
+        assert (vp[2, 0, 1, 7, 1] & ((1 << bits) - 1)) == q[2, t + per, 0, 7]
     sp = layout.params_pages_from_logical(s)
     assert sp.shape == (nb, hkv, d // gs, bs) and sp[2, 1, 1, 7] == s[2, 7, 1, 1]
     np.testing.assert_array_equal(layout.params_logical_from_pages(sp), s)
