@@ -12,9 +12,13 @@
 //   two-stage pipeline (the loads of item i+1 are in flight while item i
 //   computes).  All Hq/Hkv query heads of the GQA group are served from one
 //   read of each K/V byte.  A unit that lies inside one wave's range is written
-//   straight to the output; a unit cut by range boundaries leaves one fp32
-//   partial per wave (slot wave + unit, unique because ranges are monotone)
-//   that decode_merge_d128 combines -- no cross-workgroup fences anywhere.
+//   straight to the output.  A unit cut by range boundaries leaves one fp32
+//   partial per wave (slot wave + unit, unique because ranges are monotone),
+//   written with device-coherent (SC1) vector stores; once they are complete
+//   the wave bumps the unit's arrival counter, and the wave that arrives last
+//   reads the partials back with SC1 loads, merges them (page_attention.py:
+//   2006-2059) and resets the counter.  One launch, and no cache write-back or
+//   invalidate fences: only the partials travel device-coherently.
 //
 // Per iteration (lane l: col = l%16, jj = l/16)
 //   QK^T : NT/16 token sub-tiles x 4 k-slices of v_mfma_f32_16x16x32_f16.
@@ -47,9 +51,10 @@ struct DecodeArgs {
   const int32_t* block_tables;  // [S, max_blocks]
   const int32_t* kv_lens;       // [S]
   h16* out;                   // [S, Hq, 128]
+  int* ws_cnt;                // [kMaxUnits] per-unit arrival counters: zero before and after every launch
+  int* ws_cnt_grp;            // [kMaxUnits + kMaxWaves] per-group arrival counters (indexed by slot), likewise
   float* ws_o;                // [num_waves + S*Hkv, HG, 128] partial accumulators, slot = wave + unit
   float* ws_ml;               // [num_waves + S*Hkv, HG, 2]   partial (max, sum)
-  int* ws_cum;                // [S + 1] live-item prefix written by the decode kernel for the merge
   int S, Hq, Hkv, bs, nb, max_blocks;
   float scale_log2;           // softmax_scale * log2(e)
   int window;                 // sliding window, 0 = off
@@ -57,7 +62,9 @@ struct DecodeArgs {
   int nt;                     // tokens per work item (64 at 4-bit, 32 at 8-bit)
 };
 
-constexpr int kMaxSeqs = 2048;  // per-sequence table held in LDS by both kernels
+constexpr int kMaxSeqs = 2048;    // per-sequence table held in LDS
+constexpr int kMaxUnits = 65536;  // (sequence, kv_head) units with an arrival counter
+constexpr int kMaxWaves = 4096;   // waves of the persistent grid
 
 // DPP row_ror:N -- rotate within each row of 16 lanes.
 template <int N>
@@ -327,6 +334,132 @@ __device__ __forceinline__ int wave_of_item(long long g, long long I, int NW) {
   return w;
 }
 
+constexpr int kCoherent = 16;  // cache policy SC1: device-coherent access
+constexpr int kGroup = 8;       // pieces merged together at the first level ...
+constexpr int kSingle = 16;     // ... when a unit has more pieces than this
+
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Store 16 bytes as two 8-byte stores.  A VALU write to the data VGPRs of a
+// wider vector-memory store right after its issue has been seen (gfx950, as
+// scheduled by this compiler) to corrupt the stored data.
+__device__ __forceinline__ void store_f32x4(const f32x4 v, const __amdgpu_buffer_rsrc_t r, const int voff,
+                                            const int soff) {
+  __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, f32x2{v[0], v[1]}), r, voff, soff, kCoherent);
+  __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, f32x2{v[2], v[3]}), r, voff + 8, soff, kCoherent);
+}
+
+// Combine `count` partials (slots first, first + stride, ...) of one unit:
+// O = sum_p 2^(m_p - M) o_p, L = sum_p 2^(m_p - M) l_p, M = max_p m_p.  To the
+// fp16 output (out != nullptr: O / L) or back into slot `dst` as a partial.
+// Lane owns float4 f = lane + 64k of the unit's HG*D values (head 4f/128).
+template <int HG>
+__device__ __forceinline__ void merge_range(const __amdgpu_buffer_rsrc_t ro, const __amdgpu_buffer_rsrc_t rm,
+                                            const int first, const int count, const int stride, h16* out,
+                                            const int dst, const int lane) {
+  constexpr int D = 128;
+  constexpr int NF4 = HG * D / 4;
+  constexpr int PL = (NF4 + 63) / 64;
+#pragma unroll
+  for (int k = 0; k < PL; ++k) {
+    const int f = lane + 64 * k;
+    if (NF4 % 64 != 0 && f >= NF4) break;
+    const int h = 4 * f / D;
+    float M = -INFINITY, L = 0.f;
+    f32x4 O = {0.f, 0.f, 0.f, 0.f};
+    for (int p0 = 0; p0 < count; p0 += 4) {
+      f32x4 o[4];
+      f32x2 ml[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {  // four partials' loads in flight together
+        const int p = first + min(p0 + c, count - 1) * stride;
+        o[c] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(ro, f * 16, p * HG * D * 4, kCoherent));
+        ml[c] = __builtin_bit_cast(f32x2, __builtin_amdgcn_raw_buffer_load_b64(rm, h * 8, p * HG * 8, kCoherent));
+      }
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        if (p0 + c >= count || ml[c].x == -INFINITY) continue;  // a piece may hold no live token (invalid pages)
+        const float Mn = fmaxf(M, ml[c].x);
+        const float fo = __builtin_amdgcn_exp2f(M - Mn);  // 0 while M is -inf
+        const float fp = __builtin_amdgcn_exp2f(ml[c].x - Mn);
+        O = O * fo + o[c] * fp;
+        L = L * fo + ml[c].y * fp;
+        M = Mn;
+      }
+    }
+    if (out != nullptr) {
+      const float inv = L > 0.f ? 1.f / L : 0.f;
+      typedef h16 h16x4 __attribute__((ext_vector_type(4)));
+      *reinterpret_cast<h16x4*>(out + 4 * f) = h16x4{(h16)(O[0] * inv), (h16)(O[1] * inv), (h16)(O[2] * inv),
+                                                      (h16)(O[3] * inv)};
+    } else {
+      store_f32x4(O, ro, f * 16, dst * HG * D * 4);
+      if ((4 * f) % D == 0)
+        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, f32x2{M, L}), rm, h * 8, dst * HG * 8,
+                                              kCoherent);
+    }
+  }
+}
+
+// Count one arrival on a counter (lane 0); true on the `expected`-th arrival.
+__device__ __forceinline__ bool arrive_last(int* cnt, const int expected, const int lane) {
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's stores are complete before it is counted
+  int old = 0;
+  if (lane == 0) old = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  old = __builtin_amdgcn_readfirstlane(old);
+  if (old != expected - 1) return false;
+  if (lane == 0) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // zero for the next call
+  return true;
+}
+
+// Wave W finished its piece of unit u (items [unit_first, unit_first + n) of the
+// I items split over NW waves; pieces k = W - wf of np).  It stores its partial
+// (o = acc + pbs, m, l) in slot wf + u + k.  Pieces are merged in groups of
+// kGroup by the last arrival of each group (counter per group, indexed by the
+// group's first slot); with more than one group, the group result replaces the
+// group's first partial and the last group to finish merges the groups into the
+// fp16 output (counter per unit).  The reduce of page_attention.py:2006-2059.
+template <int GS, int HG>
+__device__ __forceinline__ void merge_piece(const DecodeArgs& a, const int W, const int u, const long long unit_first,
+                                            const int n, const long long I, const int NW, const int s, const int kvh,
+                                            const f32x4 (&acc)[8], const float pbs, const float m_run, const float l,
+                                            const bool col_ok, const int gg, const int jj, const int hh,
+                                            const int lane) {
+  constexpr int D = 128;
+  const int wf = wave_of_item(unit_first, I, NW);
+  const int wl = wave_of_item(unit_first + n - 1, I, NW);
+  const int np = wl - wf + 1;
+  const int slot0 = wf + u;  // the pieces of unit u sit in slots wf+u .. wl+u
+  const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc((void*)(a.ws_o + (size_t)slot0 * (HG * D)),
+                                                                      (short)0, np * HG * D * 4, kRsrcFlags);
+  const __amdgpu_buffer_rsrc_t rm = __builtin_amdgcn_make_buffer_rsrc((void*)(a.ws_ml + (size_t)slot0 * (HG * 2)),
+                                                                      (short)0, np * HG * 2 * 4, kRsrcFlags);
+  const int me = W - wf;
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt) {  // lane (hh, gg, jj) owns dims 16*dt + 4*jj .. +3 when they lie in group gg
+    const int d = 16 * dt + 4 * jj;
+    if (col_ok && d / GS == gg) store_f32x4(acc[dt] * kTwo24 + pbs, ro, (hh * D + d) * 4, me * HG * D * 4);
+  }
+  if (col_ok && gg == 0 && jj == 0)
+    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, f32x2{m_run, l}), rm, hh * 8, me * HG * 8,
+                                          kCoherent);
+
+  // one level up to kSingle pieces; beyond, groups of kGroup first
+  const int gsz = np <= kSingle ? np : kGroup;
+  const int grp = me / gsz, ngrp = (np + gsz - 1) / gsz;
+  const int gfirst = grp * gsz, gcount = min(gsz, np - gfirst);
+  if (!arrive_last(a.ws_cnt_grp + slot0 + gfirst, gcount, lane)) return;
+  h16* out = a.out + ((size_t)s * a.Hq + (size_t)kvh * HG) * D;
+  if (ngrp == 1) {
+    merge_range<HG>(ro, rm, 0, np, 1, out, 0, lane);
+    return;
+  }
+  merge_range<HG>(ro, rm, gfirst, gcount, 1, nullptr, gfirst, lane);
+  if (!arrive_last(a.ws_cnt + u, ngrp, lane)) return;
+  merge_range<HG>(ro, rm, 0, ngrp, gsz, out, 0, lane);
+}
+
 template <int BITS, int GS, int HG>
 __global__ __launch_bounds__(256, 2) void decode_affine_d128(DecodeArgs a) {
   using C = DecodeCfg<BITS, GS, HG>;
@@ -344,8 +477,13 @@ __global__ __launch_bounds__(256, 2) void decode_affine_d128(DecodeArgs a) {
   __shared__ int kvl[kMaxSeqs];
   __shared__ __attribute__((aligned(16))) h16 stage_all[4][C::SHALVES];
   seq_table(a, cum, kvl);
-  if (blockIdx.x == 0)
-    for (int i = threadIdx.x; i <= a.S; i += 256) a.ws_cum[i] = cum[i];
+  {  // sequences without a live token produce zeros (the reference's l == 0 case)
+    const int per_seq = a.Hq * D / 8;
+    for (int i = blockIdx.x * 256 + threadIdx.x; i < a.S * per_seq; i += gridDim.x * 256) {
+      const int si = i / per_seq;
+      if (cum[si + 1] == cum[si]) reinterpret_cast<u32x4*>(a.out)[i] = u32x4{0u, 0u, 0u, 0u};
+    }
+  }
 
   const int S = a.S, Hkv = a.Hkv;
   const long long I = (long long)Hkv * cum[S];
@@ -512,19 +650,7 @@ __global__ __launch_bounds__(256, 2) void decode_affine_d128(DecodeArgs a) {
             if (col_ok && d / GS == gg) out[d] = (h16)((acc[dt][r] * kTwo24 + pbs) * inv);
           }
       } else {
-        const size_t slot = (size_t)W + u;
-        float* wo = a.ws_o + slot * (HG * D) + hh * D;
-#pragma unroll
-        for (int dt = 0; dt < 8; ++dt)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int d = 16 * dt + 4 * jj + r;
-            if (col_ok && d / GS == gg) wo[d] = acc[dt][r] * kTwo24 + pbs;
-          }
-        if (col_ok && gg == 0 && jj == 0) {
-          a.ws_ml[slot * (HG * 2) + 2 * hh] = m_run;
-          a.ws_ml[slot * (HG * 2) + 2 * hh + 1] = l;
-        }
+        merge_piece<GS, HG>(a, W, u, unit_first, n_s, I, NW, s, kvh, acc, pbs, m_run, l, col_ok, gg, jj, hh, lane);
       }
       m_run = -INFINITY;
       l_part = 0.f;
@@ -555,77 +681,6 @@ __global__ __launch_bounds__(256, 2) void decode_affine_d128(DecodeArgs a) {
     step(bufA, bufB, g);
     if (g + 1 >= g1) break;
     step(bufB, bufA, g + 1);
-  }
-}
-
-// Merge the partials of every (seq, kv_head) cut by wave-range boundaries (the
-// reduce pass of page_attention.py:2006-2059): out = sum_p 2^(m_p - M) o_p /
-// sum_p 2^(m_p - M) l_p.  One workgroup per unit; launched after
-// decode_affine_d128 on the same stream.  Units with no live token get zeros.
-template <int HG>
-__global__ __launch_bounds__(256) void decode_merge_d128(DecodeArgs a) {
-  constexpr int D = 128;
-  constexpr int PER = (HG * D + 255) / 256;  // outputs per thread
-  constexpr int CH = 8;                      // partials whose loads are in flight together
-  const int u = blockIdx.x;
-  const int kvh = u % a.Hkv;
-  const int s = u / a.Hkv;
-  const int c0 = a.ws_cum[s], c1 = a.ws_cum[s + 1], cS = a.ws_cum[a.S];
-  const int n = c1 - c0;
-  h16* out = a.out + ((size_t)s * a.Hq + (size_t)kvh * HG) * D;
-  if (n == 0) {
-    for (int i = threadIdx.x; i < HG * D; i += 256) out[i] = (h16)0.0f;
-    return;
-  }
-  const long long I = (long long)a.Hkv * cS;
-  const int NW = (int)min((long long)a.num_waves, I);
-  const long long P = (long long)a.Hkv * c0 + (long long)kvh * n;
-  const int w0 = wave_of_item(P, I, NW);
-  const int w1 = wave_of_item(P + n - 1, I, NW);
-  if (w0 == w1) return;  // one wave owned the whole unit and wrote it
-  const int np = w1 - w0 + 1;
-  const float* po = a.ws_o + ((size_t)w0 + u) * (HG * D);
-  const float* pml = a.ws_ml + ((size_t)w0 + u) * (HG * 2);
-
-  // online combine per output element: (M, L, O) <- (m_p, l_p, o_p)
-  float M[PER], L[PER], O[PER];
-#pragma unroll
-  for (int e = 0; e < PER; ++e) {
-    M[e] = -INFINITY;
-    L[e] = 0.f;
-    O[e] = 0.f;
-  }
-  for (int base = 0; base < np; base += CH) {
-    float ov[CH][PER], mv[CH][PER], lv[CH][PER];
-#pragma unroll
-    for (int c = 0; c < CH; ++c)
-#pragma unroll
-      for (int e = 0; e < PER; ++e) {
-        const int i = threadIdx.x + 256 * e;
-        const bool ok = base + c < np && i < HG * D;
-        const size_t pp = (size_t)(base + c);
-        const int h = i / D;
-        ov[c][e] = ok ? po[pp * HG * D + i] : 0.f;
-        mv[c][e] = ok ? pml[pp * HG * 2 + 2 * h] : -INFINITY;
-        lv[c][e] = ok ? pml[pp * HG * 2 + 2 * h + 1] : 0.f;
-      }
-#pragma unroll
-    for (int c = 0; c < CH; ++c)
-#pragma unroll
-      for (int e = 0; e < PER; ++e) {
-        if (mv[c][e] == -INFINITY) continue;
-        const float Mn = fmaxf(M[e], mv[c][e]);
-        const float fo = __builtin_amdgcn_exp2f(M[e] - Mn);  // 0 while M is -inf
-        const float fp = __builtin_amdgcn_exp2f(mv[c][e] - Mn);
-        O[e] = O[e] * fo + ov[c][e] * fp;
-        L[e] = L[e] * fo + lv[c][e] * fp;
-        M[e] = Mn;
-      }
-  }
-#pragma unroll
-  for (int e = 0; e < PER; ++e) {
-    const int i = threadIdx.x + 256 * e;
-    if (i < HG * D) out[i] = (h16)(L[e] > 0.f ? O[e] / L[e] : 0.f);
   }
 }
 

@@ -58,6 +58,9 @@ int device_cus() {
 
 int decode_num_waves() { return device_cus() * 4 * decode_waves_per_simd(); }
 
+// Unit counters, then per-group counters indexed by partial slot (< kMaxWaves + kMaxUnits).
+constexpr size_t kCounterInts = 2 * (size_t)emx::kMaxUnits + emx::kMaxWaves;
+
 bool decode_fast_path(int head_dim, int page_size, int bits, int group_size, int hg, int num_seqs) {
   if (head_dim != 128 || page_size % 128 != 0 || num_seqs > emx::kMaxSeqs) return false;
   if (bits != 4 && bits != 8) return false;
@@ -77,17 +80,6 @@ DecodeFn pick_decode_hg(int hg) {
     case 4: return emx::decode_affine_d128<BITS, GS, 4>;
     case 8: if constexpr (8 * G <= 16) return emx::decode_affine_d128<BITS, GS, 8>; else return nullptr;
     case 16: if constexpr (16 * G <= 16) return emx::decode_affine_d128<BITS, GS, 16>; else return nullptr;
-  }
-  return nullptr;
-}
-
-DecodeFn pick_merge(int hg) {
-  switch (hg) {
-    case 1: return emx::decode_merge_d128<1>;
-    case 2: return emx::decode_merge_d128<2>;
-    case 4: return emx::decode_merge_d128<4>;
-    case 8: return emx::decode_merge_d128<8>;
-    case 16: return emx::decode_merge_d128<16>;
   }
   return nullptr;
 }
@@ -207,11 +199,14 @@ int emx_affine_cache_write(const void* keys, const void* values, const int32_t* 
 size_t emx_paged_workspace_bytes(int num_seqs, int num_q_heads, int num_kv_heads, int head_dim,
                                  int max_blocks_per_seq, int page_size) {
   if (num_seqs <= 0 || num_kv_heads <= 0 || num_q_heads <= 0 || max_blocks_per_seq <= 0 || page_size <= 0 ||
-      head_dim != 128 || page_size % 128 != 0 || num_seqs > emx::kMaxSeqs)
+      head_dim != 128 || page_size % 128 != 0 || num_seqs > emx::kMaxSeqs ||
+      (long)num_seqs * num_kv_heads > emx::kMaxUnits)
     return 0;
   const int hg = num_q_heads / num_kv_heads;
   const size_t slots = (size_t)decode_num_waves() + (size_t)num_seqs * num_kv_heads;
-  return slots * hg * (head_dim + 2) * sizeof(float) + (num_seqs + 1) * sizeof(int);  // partials + prefix
+  if (decode_num_waves() > emx::kMaxWaves) return 0;
+  // arrival counters at a fixed offset (so every call finds them zeroed), then the partials
+  return kCounterInts * sizeof(int) + slots * hg * (head_dim + 2) * sizeof(float);
 }
 
 int emx_paged_attention_affine(const void* queries, int num_tokens, int num_q_heads, int head_dim,
@@ -242,12 +237,12 @@ int emx_paged_attention_affine(const void* queries, int num_tokens, int num_q_he
   const float scale_log2 = softmax_scale * emx::kLog2e;
   const int window = sliding_window > 0 ? sliding_window : 0;
 
-  if (single_token_decode && decode_fast_path(head_dim, page_size, bits, group_size, hg, num_seqs)) {
+  const size_t need =
+      emx_paged_workspace_bytes(num_seqs, num_q_heads, num_kv_heads, head_dim, max_blocks_per_seq, page_size);
+  if (single_token_decode && need > 0 && decode_fast_path(head_dim, page_size, bits, group_size, hg, num_seqs)) {
     if (!aligned16(queries) || !aligned16(k_codes) || !aligned16(v_codes) || !aligned16(k_scales) ||
         !aligned16(k_biases) || !aligned16(v_scales) || !aligned16(v_biases))
       return fail(EMX_ERR_INVALID, "queries and cache tensors must be 16-byte aligned");
-    const size_t need =
-        emx_paged_workspace_bytes(num_seqs, num_q_heads, num_kv_heads, head_dim, max_blocks_per_seq, page_size);
     if (workspace == nullptr || workspace_bytes < need)
       return fail(EMX_ERR_INVALID, "workspace too small: need %zu bytes, got %zu", need, workspace_bytes);
     const int nw = decode_num_waves();
@@ -263,9 +258,10 @@ int emx_paged_attention_affine(const void* queries, int num_tokens, int num_q_he
     a.kv_lens = kv_lens;
     a.out = reinterpret_cast<emx::h16*>(out);
     const size_t slots = (size_t)nw + (size_t)num_seqs * num_kv_heads;
-    a.ws_o = reinterpret_cast<float*>(workspace);
+    a.ws_cnt = reinterpret_cast<int*>(workspace);
+    a.ws_cnt_grp = a.ws_cnt + emx::kMaxUnits;
+    a.ws_o = reinterpret_cast<float*>(a.ws_cnt + kCounterInts);
     a.ws_ml = a.ws_o + slots * hg * head_dim;
-    a.ws_cum = reinterpret_cast<int*>(a.ws_ml + slots * hg * 2);
     a.S = num_seqs;
     a.Hq = num_q_heads;
     a.Hkv = num_kv_heads;
@@ -277,13 +273,10 @@ int emx_paged_attention_affine(const void* queries, int num_tokens, int num_q_he
     a.num_waves = nw;
     a.nt = bits == 4 ? 64 : 32;
     DecodeFn fn = bits == 4 ? pick_decode_gs<4>(group_size, hg) : pick_decode_gs<8>(group_size, hg);
-    DecodeFn merge = pick_merge(hg);
-    if (!fn || !merge)
+    if (!fn)
       return fail(EMX_ERR_UNSUPPORTED, "no decode kernel for bits=%d group_size=%d gqa=%d", bits, group_size, hg);
     hipLaunchKernelGGL(fn, dim3((unsigned)(nw / 4)), dim3(256), 0, st, a);
-    if (int r = check_launch("decode_affine_d128")) return r;
-    hipLaunchKernelGGL(merge, dim3((unsigned)(num_seqs * num_kv_heads)), dim3(256), 0, st, a);
-    return check_launch("decode_merge_d128");
+    return check_launch("decode_affine_d128");
   }
 
   if (queries && !aligned16(queries)) return fail(EMX_ERR_INVALID, "queries must be 16-byte aligned");

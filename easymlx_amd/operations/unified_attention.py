@@ -96,10 +96,11 @@ _ws_cache: dict[tuple[int, int], torch.Tensor] = {}
 
 
 def _workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor | None:
-    """Split-K partials buffer shared by the launches of one stream (grow-only).
+    """Split-K workspace shared by the launches of one stream (grow-only).
 
     Launches on one stream are serialised, so one buffer per (device, stream)
-    is race-free; its contents need no initialisation.
+    is race-free.  It is zero-filled when allocated: the library keeps its
+    arrival counters zero between calls.
     """
     if nbytes == 0:
         return None
@@ -109,7 +110,7 @@ def _workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor |
         if ws is None or ws.numel() < nbytes:
             if ws is not None:
                 torch.cuda.current_stream(device).synchronize()  # the old buffer may still be in use
-            ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
+            ws = torch.zeros(nbytes, dtype=torch.uint8, device=device)
             _ws_cache[key] = ws
         return ws
 

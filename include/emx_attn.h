@@ -68,8 +68,11 @@ int emx_affine_cache_write(const void* keys, const void* values, const int32_t* 
 
 /*
  * Bytes of device workspace emx_paged_attention_affine needs for split-K
- * partial results (0 if the call needs none).  Its contents need no
- * initialisation; calls sharing one workspace must be ordered (same stream).
+ * partial results and arrival counters (0 if the call needs none).  The
+ * workspace must be zero-filled before its first use; every call leaves its
+ * counter region zeroed again, so one workspace serves any sequence of calls
+ * (of any shape) that are ordered on one stream.  Calls sharing a workspace
+ * must not overlap.
  * No direct reference counterpart: replaces the tmp_out/exp_sums/max_logits
  * allocation of lib/python/easymlx/operations/kernels/page_attention.py:2205-2272.
  */
