@@ -119,6 +119,16 @@ __device__ __forceinline__ TileRsrc make_tile_rsrc(const DecodeArgs& a, const in
   return rs;
 }
 
+// Descriptors of zero size: loads through them return zeros and read nothing.
+__device__ __forceinline__ TileRsrc empty_tile_rsrc() {
+  TileRsrc rs;
+  rs.k = __builtin_amdgcn_make_buffer_rsrc(nullptr, (short)0, 0, kRsrcFlags);
+  rs.v = rs.k;
+#pragma unroll
+  for (int arr = 0; arr < 4; ++arr) rs.s[arr] = rs.k;
+  return rs;
+}
+
 // Register image of one iteration's loads.
 template <int BITS, int GS, int HG>
 struct IterLoads {
@@ -620,9 +630,14 @@ __global__ __launch_bounds__(256, 2) void decode_affine_d128(DecodeArgs a) {
       blk1 = __builtin_amdgcn_readfirstlane(__builtin_amdgcn_readlane(blkv, k1 & 63));
       if (s1 != s || kvh1 != kvh || (tb1 >> 7) != (tb >> 7))
         rs_nxt = make_tile_rsrc<BITS, GS, HG>(a, (unsigned)blk1 < (unsigned)a.nb ? blk1 : 0, kvh1, (tb1 & ~127) % a.bs);
-      issue_loads(nxt, rs_nxt, RW, (tb1 & 127) / NT, lk, lv, ls);
-      if (unit_end) issue_q(s1, kvh1);
+    } else {
+      rs_nxt = empty_tile_rsrc();
     }
+    // Issued on every path (an empty descriptor returns zeros without touching
+    // memory): the compiler's wait before this item's compute then counts these
+    // loads as younger and leaves them in flight, instead of draining them.
+    issue_loads(nxt, rs_nxt, RW, (tb1 & 127) / NT, lk, lv, ls);
+    if (has_next && unit_end) issue_q(s1, kvh1);
 
     // ---- compute the current item (an invalid page is skipped like the reference's Metal kernel)
     if ((unsigned)blk < (unsigned)a.nb) {
