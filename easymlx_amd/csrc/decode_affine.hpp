@@ -50,7 +50,8 @@ struct DecodeArgs {
   const h16* vb;              // [nb, Hkv, G, bs]
   const int32_t* block_tables;  // [S, max_blocks]
   const int32_t* kv_lens;       // [S]
-  h16* out;                   // [S, Hq, 128]
+  const int32_t* qsl;           // [S + 1] query rows of a mixed batch, or null: row s is sequence s
+  h16* out;                   // [rows, Hq, 128]
   int* ws_cnt;                // [kMaxUnits] per-unit arrival counters: zero before and after every launch
   int* ws_cnt_grp;            // [kMaxUnits + kMaxWaves] per-group arrival counters (indexed by slot), likewise
   float* ws_o;                // [num_waves + S*Hkv, HG, 128] partial accumulators, slot = wave + unit
@@ -290,7 +291,7 @@ __device__ __forceinline__ void compute_iteration(IterLoads<BITS, GS, HG>& L, co
 
 // Block-wide exclusive prefix of per-sequence live item counts into LDS.
 // cum[s] = sum_{s' < s} n(s'), cum[S] = total; kvl[s] = clamped kv_len.
-__device__ __forceinline__ void seq_table(const DecodeArgs& a, int* cum, int* kvl) {
+__device__ __forceinline__ void seq_table(const DecodeArgs& a, int* cum, int* kvl, int* qrw) {
   const int S = a.S;
   const int ch = (S + 255) / 256;
   const int s0 = threadIdx.x * ch;
@@ -300,9 +301,12 @@ __device__ __forceinline__ void seq_table(const DecodeArgs& a, int* cum, int* kv
     if (s < S) {
       int kl = min(a.kv_lens[s], a.max_blocks * a.bs);
       kl = max(kl, 0);
-      kvl[s] = kl;
+      // in a mixed batch only sequences with exactly one query token are decoded here
+      const bool dec = a.qsl == nullptr || a.qsl[s + 1] - a.qsl[s] == 1;
+      qrw[s] = a.qsl == nullptr ? s : a.qsl[s];
+      kvl[s] = dec ? kl : -1;
       int n = 0;
-      if (kl > 0) {
+      if (dec && kl > 0) {
         const int start_k = a.window > 0 ? max(0, kl - a.window) : 0;
         n = (kl - 1) / a.nt - start_k / a.nt + 1;
       }
@@ -432,7 +436,7 @@ __device__ __forceinline__ bool arrive_last(int* cnt, const int expected, const 
 // fp16 output (counter per unit).  The reduce of page_attention.py:2006-2059.
 template <int GS, int HG>
 __device__ __forceinline__ void merge_piece(const DecodeArgs& a, const int W, const int u, const long long unit_first,
-                                            const int n, const long long I, const int NW, const int s, const int kvh,
+                                            const int n, const long long I, const int NW, const int row, const int kvh,
                                             const f32x4 (&acc)[8], const float pbs, const float m_run, const float l,
                                             const bool col_ok, const int gg, const int jj, const int hh,
                                             const int lane) {
@@ -460,7 +464,7 @@ __device__ __forceinline__ void merge_piece(const DecodeArgs& a, const int W, co
   const int grp = me / gsz, ngrp = (np + gsz - 1) / gsz;
   const int gfirst = grp * gsz, gcount = min(gsz, np - gfirst);
   if (!arrive_last(a.ws_cnt_grp + slot0 + gfirst, gcount, lane)) return;
-  h16* out = a.out + ((size_t)s * a.Hq + (size_t)kvh * HG) * D;
+  h16* out = a.out + ((size_t)row * a.Hq + (size_t)kvh * HG) * D;
   if (ngrp == 1) {
     merge_range<HG>(ro, rm, 0, np, 1, out, 0, lane);
     return;
@@ -485,13 +489,15 @@ __global__ __launch_bounds__(256, 2) void decode_affine_d128(DecodeArgs a) {
 
   __shared__ int cum[kMaxSeqs + 1];
   __shared__ int kvl[kMaxSeqs];
+  __shared__ int qrw[kMaxSeqs];
   __shared__ __attribute__((aligned(16))) h16 stage_all[4][C::SHALVES];
-  seq_table(a, cum, kvl);
-  {  // sequences without a live token produce zeros (the reference's l == 0 case)
+  seq_table(a, cum, kvl, qrw);
+  {  // decoded sequences without a live token produce zeros (the reference's l == 0 case)
     const int per_seq = a.Hq * D / 8;
     for (int i = blockIdx.x * 256 + threadIdx.x; i < a.S * per_seq; i += gridDim.x * 256) {
       const int si = i / per_seq;
-      if (cum[si + 1] == cum[si]) reinterpret_cast<u32x4*>(a.out)[i] = u32x4{0u, 0u, 0u, 0u};
+      if (kvl[si] >= 0 && cum[si + 1] == cum[si])
+        reinterpret_cast<u32x4*>(a.out)[(size_t)qrw[si] * per_seq + i % per_seq] = u32x4{0u, 0u, 0u, 0u};
     }
   }
 
@@ -535,7 +541,7 @@ __global__ __launch_bounds__(256, 2) void decode_affine_d128(DecodeArgs a) {
   u32x4 qraw[4];
   auto issue_q = [&](int seq, int kh) {
     const u32x4* qp = reinterpret_cast<const u32x4*>(
-        a.q + ((size_t)seq * a.Hq + (size_t)kh * HG + (col_ok ? hh : 0)) * D + 32 * jj);
+        a.q + ((size_t)qrw[seq] * a.Hq + (size_t)kh * HG + (col_ok ? hh : 0)) * D + 32 * jj);
 #pragma unroll
     for (int i = 0; i < 4; ++i) qraw[i] = qp[i];
   };
@@ -655,7 +661,7 @@ __global__ __launch_bounds__(256, 2) void decode_affine_d128(DecodeArgs a) {
       const bool whole = unit_first >= g0 && unit_first + n_s <= g1;
       const int u = s * Hkv + kvh;
       if (whole) {
-        h16* out = a.out + ((size_t)s * a.Hq + (size_t)kvh * HG + hh) * D;
+        h16* out = a.out + ((size_t)qrw[s] * a.Hq + (size_t)kvh * HG + hh) * D;
         const float inv = l > 0.f ? 1.f / l : 0.f;
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt)
@@ -665,7 +671,8 @@ __global__ __launch_bounds__(256, 2) void decode_affine_d128(DecodeArgs a) {
             if (col_ok && d / GS == gg) out[d] = (h16)((acc[dt][r] * kTwo24 + pbs) * inv);
           }
       } else {
-        merge_piece<GS, HG>(a, W, u, unit_first, n_s, I, NW, s, kvh, acc, pbs, m_run, l, col_ok, gg, jj, hh, lane);
+        merge_piece<GS, HG>(a, W, u, unit_first, n_s, I, NW, qrw[s], kvh, acc, pbs, m_run, l, col_ok, gg, jj, hh,
+                            lane);
       }
       m_run = -INFINITY;
       l_part = 0.f;

@@ -12,6 +12,7 @@
 #include "../../include/emx_attn.h"
 #include "decode_affine.hpp"
 #include "paged_generic.hpp"
+#include "prefill_affine.hpp"
 #include "quantize.hpp"
 
 namespace {
@@ -90,6 +91,32 @@ DecodeFn pick_decode_gs(int gs, int hg) {
     case 32: return pick_decode_hg<BITS, 32>(hg);
     case 64: return pick_decode_hg<BITS, 64>(hg);
     case 128: return pick_decode_hg<BITS, 128>(hg);
+  }
+  return nullptr;
+}
+
+bool prefill_fast_path(int hg) { return hg == 1 || hg == 2 || hg == 4 || hg == 8 || hg == 16; }
+
+typedef void (*PrefillFn)(emx::PrefillArgs);
+
+template <int BITS, int GS>
+PrefillFn pick_prefill_hg(int hg) {
+  switch (hg) {
+    case 1: return emx::prefill_affine_d128<BITS, GS, 1>;
+    case 2: return emx::prefill_affine_d128<BITS, GS, 2>;
+    case 4: return emx::prefill_affine_d128<BITS, GS, 4>;
+    case 8: return emx::prefill_affine_d128<BITS, GS, 8>;
+    case 16: return emx::prefill_affine_d128<BITS, GS, 16>;
+  }
+  return nullptr;
+}
+
+template <int BITS>
+PrefillFn pick_prefill_gs(int gs, int hg) {
+  switch (gs) {
+    case 32: return pick_prefill_hg<BITS, 32>(hg);
+    case 64: return pick_prefill_hg<BITS, 64>(hg);
+    case 128: return pick_prefill_hg<BITS, 128>(hg);
   }
   return nullptr;
 }
@@ -239,12 +266,45 @@ int emx_paged_attention_affine(const void* queries, int num_tokens, int num_q_he
 
   const size_t need =
       emx_paged_workspace_bytes(num_seqs, num_q_heads, num_kv_heads, head_dim, max_blocks_per_seq, page_size);
-  if (single_token_decode && need > 0 && decode_fast_path(head_dim, page_size, bits, group_size, hg, num_seqs)) {
+  // MFMA paths: decode rows (one query token) on the split-K decode kernel, rows of
+  // longer queries on the prefill kernel; anything else on the generic kernel.
+  if (need > 0 && decode_fast_path(head_dim, page_size, bits, group_size, hg, num_seqs) &&
+      (single_token_decode || prefill_fast_path(hg))) {
     if (!aligned16(queries) || !aligned16(k_codes) || !aligned16(v_codes) || !aligned16(k_scales) ||
         !aligned16(k_biases) || !aligned16(v_scales) || !aligned16(v_biases))
       return fail(EMX_ERR_INVALID, "queries and cache tensors must be 16-byte aligned");
     if (workspace == nullptr || workspace_bytes < need)
       return fail(EMX_ERR_INVALID, "workspace too small: need %zu bytes, got %zu", need, workspace_bytes);
+    if (!single_token_decode) {
+      emx::PrefillArgs p;
+      p.q = reinterpret_cast<const emx::h16*>(queries);
+      p.kc = k_codes;
+      p.ks = reinterpret_cast<const emx::h16*>(k_scales);
+      p.kb = reinterpret_cast<const emx::h16*>(k_biases);
+      p.vc = v_codes;
+      p.vs = reinterpret_cast<const emx::h16*>(v_scales);
+      p.vb = reinterpret_cast<const emx::h16*>(v_biases);
+      p.block_tables = block_tables;
+      p.kv_lens = kv_lens;
+      p.qsl = query_start_loc;
+      p.out = reinterpret_cast<emx::h16*>(out);
+      p.S = num_seqs;
+      p.Hq = num_q_heads;
+      p.Hkv = num_kv_heads;
+      p.bs = page_size;
+      p.nb = num_blocks;
+      p.max_blocks = max_blocks_per_seq;
+      p.scale_log2 = scale_log2;
+      p.window = window;
+      PrefillFn pf = bits == 4 ? pick_prefill_gs<4>(group_size, hg) : pick_prefill_gs<8>(group_size, hg);
+      if (!pf)
+        return fail(EMX_ERR_UNSUPPORTED, "no prefill kernel for bits=%d group_size=%d gqa=%d", bits, group_size, hg);
+      // tiles of 128/hg query tokens: at most num_tokens/tile + num_seqs of them per kv head
+      const int tokb = 128 / hg;
+      const long grid = (long)((num_tokens + tokb - 1) / tokb + num_seqs) * num_kv_heads;
+      hipLaunchKernelGGL(pf, dim3((unsigned)grid), dim3(256), 0, st, p);
+      if (int r = check_launch("prefill_affine_d128")) return r;
+    }
     const int nw = decode_num_waves();
     emx::DecodeArgs a;
     a.q = reinterpret_cast<const emx::h16*>(queries);
@@ -256,6 +316,7 @@ int emx_paged_attention_affine(const void* queries, int num_tokens, int num_q_he
     a.vb = reinterpret_cast<const emx::h16*>(v_biases);
     a.block_tables = block_tables;
     a.kv_lens = kv_lens;
+    a.qsl = single_token_decode ? nullptr : query_start_loc;
     a.out = reinterpret_cast<emx::h16*>(out);
     const size_t slots = (size_t)nw + (size_t)num_seqs * num_kv_heads;
     a.ws_cnt = reinterpret_cast<int*>(workspace);

@@ -183,7 +183,7 @@ def paged_attention(
         if queries.dtype != torch.float16:
             raise NotImplementedError("affine paged attention takes fp16 queries")
         nb, hkv, bs = int(key_cache.shape[0]), int(key_cache.shape[1]), int(key_cache.shape[2])
-        need = int(lib.emx_paged_workspace_bytes(S, hq, hkv, d, max_blocks, bs)) if single_token_decode else 0
+        need = int(lib.emx_paged_workspace_bytes(S, hq, hkv, d, max_blocks, bs))
         if need and workspace is None:
             workspace = _workspace(dev, stream, need)
         ws_ptr = workspace.data_ptr() if workspace is not None else None
