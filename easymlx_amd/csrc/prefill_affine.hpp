@@ -329,17 +329,18 @@ __global__ __launch_bounds__(256, 2) void prefill_affine_d128(PrefillArgs a) {
     }
 #pragma unroll
     for (int w = 0; w < NWS; ++w) {
-      // V codes of this lane's 8 keys (TPL*jj + 8w ..) for every dim tile
-      uint32_t vw[8][2];
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt) {
-        typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
-        const u32x2v x = *reinterpret_cast<const u32x2v*>(Vl + (16 * dt + col) * 8 + TPL * jj * BITS / 32);
-        vw[dt][0] = x[0];
-        vw[dt][1] = x[1];
-      }
 #pragma unroll
       for (int g = 0; g < G; ++g) {
+        // V codes of this lane's 8 keys (TPL*jj + 8w ..) for the dim tiles of group g
+        constexpr int DTG = 8 / G;  // dim tiles per quantization group
+        h16x8 Av[DTG];
+#pragma unroll
+        for (int e = 0; e < DTG; ++e) {
+          const int dt = g * DTG + e;
+          typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
+          const u32x2v x = *reinterpret_cast<const u32x2v*>(Vl + (16 * dt + col) * 8 + TPL * jj * BITS / 32);
+          Av[e] = BITS == 4 ? unpack4(w == 0 ? x[0] : x[1]) : unpack8(x[0], x[1]);
+        }
         const h16x8 vs8 = *reinterpret_cast<const h16x8*>(Sl + (2 * G + g) * NT + TPL * jj + 8 * w);
         const h16x8 vb8 = *reinterpret_cast<const h16x8*>(Sl + (3 * G + g) * NT + TPL * jj + 8 * w);
 #pragma unroll
@@ -353,11 +354,7 @@ __global__ __launch_bounds__(256, 2) void prefill_affine_d128(PrefillArgs a) {
             pb[ct][g] = fmaf(p, (float)vb8[slot_perm<BITS>(i)], pb[ct][g]);
           }
 #pragma unroll
-          for (int dt = 0; dt < 8; ++dt) {
-            if ((16 * dt) / GS != g) continue;
-            const h16x8 A = BITS == 4 ? unpack4(vw[dt][w]) : unpack8(vw[dt][0], vw[dt][1]);
-            acc[ct][dt] = mfma16x16x32(A, pB, acc[ct][dt]);
-          }
+          for (int e = 0; e < DTG; ++e) acc[ct][g * DTG + e] = mfma16x16x32(Av[e], pB, acc[ct][g * DTG + e]);
         }
       }
     }
