@@ -213,13 +213,24 @@ int emx_affine_cache_write(const void* keys, const void* values, const int32_t* 
   a.gs = group_size;
   a.bs = page_size;
   a.nb = num_blocks;
-  const long n = (long)num_tokens * num_kv_heads * (head_dim / group_size) * 2;
-  const int blocks = (int)((n + 255) / 256);
+  if (head_dim / group_size > emx::kWriteMaxGroups || head_dim > emx::kWriteMaxDim)
+    return fail(EMX_ERR_UNSUPPORTED, "head_dim %d above %d or more than %d quantization groups per head", head_dim,
+                emx::kWriteMaxDim, emx::kWriteMaxGroups);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (num_tokens <= emx::kSmallWrite && head_dim % 16 == 0 && group_size % 16 == 0 &&
+      group_size <= emx::kSmallMaxGroup) {
+    const dim3 sgrid((unsigned)num_kv_heads, (unsigned)(head_dim / 16));
+    if (bits == 4)
+      hipLaunchKernelGGL(emx::affine_cache_write_small<4>, sgrid, dim3(256), 0, st, a);
+    else
+      hipLaunchKernelGGL(emx::affine_cache_write_small<8>, sgrid, dim3(256), 0, st, a);
+    return check_launch("affine_cache_write_small");
+  }
+  const dim3 grid((unsigned)((num_tokens + emx::kWriteTokens - 1) / emx::kWriteTokens), (unsigned)num_kv_heads);
   if (bits == 4)
-    hipLaunchKernelGGL(emx::affine_cache_write<4>, dim3(blocks), dim3(256), 0, st, a);
+    hipLaunchKernelGGL(emx::affine_cache_write<4>, grid, dim3(256), 0, st, a);
   else
-    hipLaunchKernelGGL(emx::affine_cache_write<8>, dim3(blocks), dim3(256), 0, st, a);
+    hipLaunchKernelGGL(emx::affine_cache_write<8>, grid, dim3(256), 0, st, a);
   return check_launch("affine_cache_write");
 }
 

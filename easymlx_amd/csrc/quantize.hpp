@@ -55,6 +55,21 @@ __device__ __forceinline__ void group_minmax(const h16* src, int gs, float& wmin
   }
 }
 
+// min / max of gs contiguous fp16 values held in LDS.
+__device__ __forceinline__ void lds_minmax(const h16* src, int gs, float& wmin, float& wmax) {
+  wmin = INFINITY;
+  wmax = -INFINITY;
+  for (int i = 0; i < gs; i += 8) {
+    const h16x8 x = *reinterpret_cast<const h16x8*>(src + i);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const float v = (float)x[k];
+      wmin = fminf(wmin, v);
+      wmax = fmaxf(wmax, v);
+    }
+  }
+}
+
 // x [rows, D] fp16 -> codes [rows, D*b/32] u32, scales/biases [rows, D/gs] fp16 (MLX layout).
 // One thread per (row, group).
 template <int BITS>
@@ -93,57 +108,226 @@ struct WriteArgs {
   int T, Hkv, D, gs, bs, nb;
 };
 
-// One thread per (token, kv_head, group, {K, V}).
+// One workgroup per (32 consecutive tokens, kv head):
+//   1. per (token, group, K|V): min/max -> scale/bias (kept in LDS, stored as fp16);
+//   2. K codes: one 32-bit word per (token, 32/BITS dims), plain stores;
+//   3. V codes: 4-bit words hold 8 tokens of one dim.  When the 8 tokens of an
+//      aligned octet have consecutive slots starting at a word boundary (a
+//      prefill chunk), the word is written whole; otherwise (decode appends,
+//      chunk edges) each token updates its nibble atomically.  8-bit codes are
+//      single bytes and are stored directly.
+constexpr int kWriteTokens = 32;
+constexpr int kWriteMaxGroups = 32;
+constexpr int kWriteMaxDim = 256;
+
 template <int BITS>
 __global__ __launch_bounds__(256) void affine_cache_write(WriteArgs a) {
-  const long gid = (long)blockIdx.x * blockDim.x + threadIdx.x;
-  const int G = a.D / a.gs;
-  const long per_tok = (long)a.Hkv * G * 2;
-  if (gid >= (long)a.T * per_tok) return;
-  const int t = (int)(gid / per_tok);
-  int rem = (int)(gid % per_tok);
-  const int is_v = rem & 1;
-  rem >>= 1;
-  const int h = rem / G;
-  const int g = rem % G;
-  const int slot = a.slot_mapping[t];
-  if (slot < 0) return;
-  const int blk = slot / a.bs;
-  const int off = slot % a.bs;
-  if (blk >= a.nb) return;
-
-  const float n_bins = (float)((1 << BITS) - 1);
-  const h16* src = (is_v ? a.values : a.keys) + ((size_t)t * a.Hkv + h) * a.D + (size_t)g * a.gs;
-  float wmin, wmax, scale, bias;
-  group_minmax(src, a.gs, wmin, wmax);
-  affine_params(wmin, wmax, n_bins, scale, bias);
-  const size_t ph = (size_t)blk * a.Hkv + h;
-  const size_t si = (ph * G + g) * a.bs + off;
+  constexpr int TW = kWriteTokens;
   constexpr int PW = 32 / BITS;
-  if (!is_v) {
-    uint32_t* dst = a.kc + (ph * a.bs + off) * (a.D / PW) + (size_t)g * (a.gs / PW);
-    for (int w = 0; w < a.gs / PW; ++w) {
-      uint32_t word = 0;
-#pragma unroll
-      for (int k = 0; k < PW; ++k) word |= affine_code((float)src[w * PW + k], scale, bias, n_bins) << (k * BITS);
-      dst[w] = word;
+  const int tid = threadIdx.x;
+  const int t0 = blockIdx.x * TW;
+  const int h = blockIdx.y;
+  const int nt = min(TW, a.T - t0);
+  const int G = a.D / a.gs;
+  const float n_bins = (float)((1 << BITS) - 1);
+
+  __shared__ float sp[2][TW][kWriteMaxGroups][2];  // [K|V][token][group] -> (scale, bias)
+  __shared__ int sslot[TW];
+  __shared__ __attribute__((aligned(16))) h16 sval[2][TW][kWriteMaxDim];  // this head's K / V rows
+  if (tid < TW) {
+    int sl = tid < nt ? a.slot_mapping[t0 + tid] : -1;
+    if (sl >= 0 && sl / a.bs >= a.nb) sl = -1;  // page out of range: not written
+    sslot[tid] = sl;
+  }
+  {  // one cooperative load of every value the block quantizes (16 bytes per piece)
+    const int per_row = a.D / 8;
+    for (int i = tid; i < 2 * nt * per_row; i += 256) {
+      const int kv = i / (nt * per_row), r = i % (nt * per_row);
+      const int t = r / per_row, c = r % per_row;
+      const h16* src = (kv ? a.values : a.keys) + ((size_t)(t0 + t) * a.Hkv + h) * a.D + 8 * c;
+      *reinterpret_cast<u32x4*>(&sval[kv][t][8 * c]) = *reinterpret_cast<const u32x4*>(src);
     }
-    a.ks[si] = (h16)scale;
-    a.kb[si] = (h16)bias;
-  } else {
-    for (int i = 0; i < a.gs; ++i) {
-      const uint32_t code = affine_code((float)src[i], scale, bias, n_bins);
-      uint32_t* wp = a.vc + v_word_index<BITS>(ph, off, g * a.gs + i, a.D, a.bs);
-      if constexpr (BITS == 8) {
-        reinterpret_cast<uint8_t*>(wp)[off % PW] = (uint8_t)code;
+  }
+  __syncthreads();
+
+  // ---- 1. scale / bias of every (K|V, token, group)
+  for (int task = tid; task < 2 * TW * G; task += 256) {
+    const int kv = task / (TW * G), rem = task % (TW * G);
+    const int t = rem / G, g = rem % G;
+    const int sl = t < nt ? sslot[t] : -1;
+    if (sl < 0) continue;
+    float wmin, wmax, scale, bias;
+    lds_minmax(&sval[kv][t][g * a.gs], a.gs, wmin, wmax);
+    affine_params(wmin, wmax, n_bins, scale, bias);
+    sp[kv][t][g][0] = scale;
+    sp[kv][t][g][1] = bias;
+    const size_t ph = (size_t)(sl / a.bs) * a.Hkv + h;
+    const size_t si = (ph * G + g) * a.bs + sl % a.bs;
+    (kv ? a.vs : a.ks)[si] = (h16)scale;
+    (kv ? a.vb : a.kb)[si] = (h16)bias;
+  }
+  __syncthreads();
+
+  // ---- 2. K codes: token-major words
+  const int KW = a.D / PW;
+  for (int task = tid; task < TW * KW; task += 256) {
+    const int t = task / KW, w = task % KW;
+    const int sl = t < nt ? sslot[t] : -1;
+    if (sl < 0) continue;
+    const int g = (w * PW) / a.gs;
+    const float sc = sp[0][t][g][0], bi = sp[0][t][g][1];
+    const h16* src = &sval[0][t][w * PW];
+    uint32_t word = 0;
+#pragma unroll
+    for (int k = 0; k < PW; ++k) word |= affine_code((float)src[k], sc, bi, n_bins) << (k * BITS);
+    const size_t ph = (size_t)(sl / a.bs) * a.Hkv + h;
+    a.kc[(ph * a.bs + sl % a.bs) * KW + w] = word;
+  }
+
+  // ---- 3. V codes
+  if constexpr (BITS == 4) {
+    for (int task = tid; task < (TW / 8) * a.D; task += 256) {
+      const int o = task / a.D, d = task % a.D;
+      const int g = d / a.gs;
+      const int tb = 8 * o;
+      const int s0 = tb < nt ? sslot[tb] : -1;
+      bool whole = s0 >= 0 && s0 % 8 == 0 && tb + 8 <= nt;
+#pragma unroll
+      for (int k = 1; k < 8; ++k) whole = whole && sslot[tb + k] == s0 + k;
+      if (whole) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const float v = (float)sval[1][tb + k][d];
+          word |= affine_code(v, sp[1][tb + k][g][0], sp[1][tb + k][g][1], n_bins) << (4 * k);
+        }
+        const size_t ph = (size_t)(s0 / a.bs) * a.Hkv + h;
+        a.vc[v_word_index<4>(ph, s0 % a.bs, d, a.D, a.bs)] = word;
       } else {
-        const int sh = (off % PW) * BITS;
-        atomicAnd(wp, ~(0xFu << sh));
-        atomicOr(wp, code << sh);
+        for (int k = 0; k < 8; ++k) {
+          const int t = tb + k;
+          const int sl = t < nt ? sslot[t] : -1;
+          if (sl < 0) continue;
+          const float v = (float)sval[1][t][d];
+          const uint32_t code = affine_code(v, sp[1][t][g][0], sp[1][t][g][1], n_bins);
+          const size_t ph = (size_t)(sl / a.bs) * a.Hkv + h;
+          uint32_t* wp = a.vc + v_word_index<4>(ph, sl % a.bs, d, a.D, a.bs);
+          const int sh = (sl % 8) * 4;
+          atomicAnd(wp, ~(0xFu << sh));
+          atomicOr(wp, code << sh);
+        }
       }
     }
-    a.vs[si] = (h16)scale;
-    a.vb[si] = (h16)bias;
+  } else {
+    for (int task = tid; task < TW * a.D; task += 256) {
+      const int t = task / a.D, d = task % a.D;
+      const int sl = t < nt ? sslot[t] : -1;
+      if (sl < 0) continue;
+      const int g = d / a.gs;
+      const float v = (float)sval[1][t][d];
+      const uint32_t code = affine_code(v, sp[1][t][g][0], sp[1][t][g][1], n_bins);
+      const size_t ph = (size_t)(sl / a.bs) * a.Hkv + h;
+      uint32_t* wp = a.vc + v_word_index<8>(ph, sl % a.bs, d, a.D, a.bs);
+      reinterpret_cast<uint8_t*>(wp)[sl % 4] = (uint8_t)code;
+    }
+  }
+}
+
+// Small writes (decode appends, T <= kSmallWrite tokens): one workgroup per
+// (kv head, 16-dim block) sees every token, so each value word has a single
+// writing workgroup.  A token alone in its 8-token word (always the case for
+// one token per sequence) updates its nibble with a plain read-modify-write;
+// tokens sharing a word in this call fall back to atomics.  Scales, biases
+// and K codes of the head are written by the workgroup of dim block 0 / by the
+// owner of each K word.
+constexpr int kSmallWrite = 128;
+constexpr int kSmallMaxGroup = 64;
+
+template <int BITS>
+__global__ __launch_bounds__(256) void affine_cache_write_small(WriteArgs a) {
+  constexpr int PW = 32 / BITS;
+  constexpr int DB = 16;  // dims per workgroup
+  const int tid = threadIdx.x;
+  const int h = blockIdx.x;
+  const int d0 = blockIdx.y * DB;
+  const int T = a.T;
+  const int G = a.D / a.gs;
+  const float n_bins = (float)((1 << BITS) - 1);
+  __shared__ float sp[2][kSmallWrite][2];  // [K|V][token] -> (scale, bias) of this block's group
+  __shared__ __attribute__((aligned(16))) h16 sgrp[2][kSmallWrite][kSmallMaxGroup];  // group values
+  __shared__ int sslot[kSmallWrite];
+  __shared__ int salone[kSmallWrite];
+  for (int t = tid; t < T; t += 256) {
+    int sl = a.slot_mapping[t];
+    if (sl >= 0 && sl / a.bs >= a.nb) sl = -1;
+    sslot[t] = sl;
+  }
+  __syncthreads();
+  for (int t = tid; t < T; t += 256) {  // alone: no other token of the call in the same 32/BITS-token word
+    const int sl = sslot[t];
+    bool alone = true;
+    for (int u = 0; u < T && sl >= 0; ++u)
+      if (u != t && sslot[u] >= 0 && sslot[u] / PW == sl / PW) alone = false;
+    salone[t] = alone;
+  }
+  // the quantization group holding this dim block, for every token: one cooperative load
+  const int g = d0 / a.gs;
+  for (int i = tid; i < 2 * T * (a.gs / 8); i += 256) {
+    const int kv = i / (T * (a.gs / 8)), r = i % (T * (a.gs / 8));
+    const int t = r / (a.gs / 8), c = r % (a.gs / 8);
+    const h16* src = (kv ? a.values : a.keys) + ((size_t)t * a.Hkv + h) * a.D + (size_t)g * a.gs + 8 * c;
+    *reinterpret_cast<u32x4*>(&sgrp[kv][t][8 * c]) = *reinterpret_cast<const u32x4*>(src);
+  }
+  __syncthreads();
+  // scale / bias (the first dim block of each group stores them)
+  for (int task = tid; task < 2 * T; task += 256) {
+    const int kv = task / T, t = task % T;
+    const int sl = sslot[t];
+    if (sl < 0) continue;
+    float wmin, wmax, scale, bias;
+    lds_minmax(&sgrp[kv][t][0], a.gs, wmin, wmax);
+    affine_params(wmin, wmax, n_bins, scale, bias);
+    sp[kv][t][0] = scale;
+    sp[kv][t][1] = bias;
+    if (d0 % a.gs == 0) {
+      const size_t ph = (size_t)(sl / a.bs) * a.Hkv + h;
+      const size_t si = (ph * G + g) * a.bs + sl % a.bs;
+      (kv ? a.vs : a.ks)[si] = (h16)scale;
+      (kv ? a.vb : a.kb)[si] = (h16)bias;
+    }
+  }
+  __syncthreads();
+  // K words of this block: DB / PW per token
+  for (int task = tid; task < T * (DB / PW); task += 256) {
+    const int t = task / (DB / PW), w = d0 / PW + task % (DB / PW);
+    const int sl = sslot[t];
+    if (sl < 0) continue;
+    const h16* src = &sgrp[0][t][w * PW - g * a.gs];
+    uint32_t word = 0;
+#pragma unroll
+    for (int k = 0; k < PW; ++k) word |= affine_code((float)src[k], sp[0][t][0], sp[0][t][1], n_bins) << (k * BITS);
+    const size_t ph = (size_t)(sl / a.bs) * a.Hkv + h;
+    a.kc[(ph * a.bs + sl % a.bs) * (a.D / PW) + w] = word;
+  }
+  // V codes: one value per (token, dim)
+  for (int task = tid; task < T * DB; task += 256) {
+    const int t = task / DB, d = d0 + task % DB;
+    const int sl = sslot[t];
+    if (sl < 0) continue;
+    const float v = (float)sgrp[1][t][d - g * a.gs];
+    const uint32_t code = affine_code(v, sp[1][t][0], sp[1][t][1], n_bins);
+    const size_t ph = (size_t)(sl / a.bs) * a.Hkv + h;
+    uint32_t* wp = a.vc + v_word_index<BITS>(ph, sl % a.bs, d, a.D, a.bs);
+    const int sh = (sl % PW) * BITS;
+    constexpr uint32_t M = (1u << BITS) - 1u;
+    if (BITS == 8) {
+      reinterpret_cast<uint8_t*>(wp)[sl % 4] = (uint8_t)code;
+    } else if (salone[t]) {
+      *wp = (*wp & ~(M << sh)) | (code << sh);  // the word's only writer in this call
+    } else {
+      atomicAnd(wp, ~(M << sh));
+      atomicOr(wp, code << sh);
+    }
   }
 }
 

@@ -84,3 +84,42 @@ def test_cache_write_overwrite_and_skip(cuda):
         for sl in (wl.slot[5], wl.slot[17]):
             keep[sl // wl.block_size, sl % wl.block_size] = False
         np.testing.assert_array_equal(after[name][0][keep], before[name][0][keep])
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("chunks", [(100, 29), (20,), ()], ids=["large-write", "small-shared", "appends-only"])
+def test_cache_write_appends_and_unaligned_chunks(cuda, bits, chunks):
+    """Decode appends (one token per sequence into a partly filled page) and prefill chunks that
+    start mid-word: whole-word stores and per-token nibble updates must give the same bit-exact
+    pages as the oracle, and leave every other slot untouched."""
+    print(f"[cache write appends/chunks bits={bits} chunks={chunks}]", flush=True)
+    wl = decode_workload(seed=31 + bits, num_seqs=5, ctx_range=(300, 600), bits=bits, pool_pages=32)
+    view = gpu_cache(wl, cuda)
+    before = gpu_pages_to_logical(view)
+    rng = np.random.default_rng(77 + bits)
+    bs = wl.block_size
+    # slots: one append per sequence (the next free position), then a 100-token chunk starting at offset 5
+    # of a fresh page, then a 29-token chunk at offset 37 of another page
+    appends = [int(wl.block_tables[s, wl.kv_lens[s] // bs]) * bs + int(wl.kv_lens[s]) % bs
+               for s in range(5) if wl.kv_lens[s] % bs]  # sequences whose last page has room
+    free = sorted(set(range(wl.num_blocks)) - set(int(x) for x in (wl.slot // bs)))
+    assert len(free) >= 2, "workload pool has no spare page"
+    starts = (5, 37)
+    chunk_slots = [free[c] * bs + starts[c] + i for c, n in enumerate(chunks) for i in range(n)]
+    slots = np.array(appends + chunk_slots, np.int32)
+    n = len(slots)
+    k2 = (rng.standard_normal((n, wl.num_kv_heads, wl.head_dim)) * 3).astype(np.float16)
+    v2 = (rng.standard_normal((n, wl.num_kv_heads, wl.head_dim)) * 3).astype(np.float16)
+    view.write_slots(torch.from_numpy(k2).to(cuda), torch.from_numpy(v2).to(cuda), torch.from_numpy(slots).to(cuda))
+    after = gpu_pages_to_logical(view)
+    written = np.zeros((wl.num_blocks, bs), bool)
+    written[slots // bs, slots % bs] = True
+    for name, src in (("k", k2), ("v", v2)):
+        ec, es, eb = affine_quantize(src, wl.group_size, bits)
+        b, o = slots // bs, slots % bs
+        np.testing.assert_array_equal(after[name][0][b, o], ec, err_msg=f"{name} codes")
+        np.testing.assert_array_equal(after[name][1][b, o].view(np.uint16), es.view(np.uint16))
+        np.testing.assert_array_equal(after[name][2][b, o].view(np.uint16), eb.view(np.uint16))
+        for i in range(3):
+            np.testing.assert_array_equal(after[name][i][~written], before[name][i][~written],
+                                          err_msg=f"{name} array {i}: unwritten slots changed")
