@@ -11,6 +11,10 @@ public operator's result on every pool.
 
 Prints one JSON line.  ``value`` = achieved HBM GB/s on algorithmic bytes
 (K/V codes + scales + biases of every live token) over the timed steps.
+Auxiliary fields (not the headline), each over its own rotated pools: the
+ragged unified step (c3: four 512-token prefill chunks + 28 decode rows), the
+long-context decode (c4: 8 x 32768 tokens, Hq 64) and the fused
+quantize-on-write (one appended token per c2 sequence; four 512-token chunks).
 """
 
 from __future__ import annotations
@@ -29,6 +33,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0
 
 
 def parse():
@@ -38,6 +43,7 @@ def parse():
     p.add_argument("--warmup", type=int, default=40)
     p.add_argument("--pool-gib", type=float, default=1.5, help="total size of the rotated page pools")
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-aux", action="store_true", help="skip the c3 / c4 / quantize-on-write measurements")
     p.add_argument("--cpu-seqs", type=int, default=0, help="sequences in the CPU baseline sample (0 = auto)")
     p.add_argument("--copy-probe-mib", type=int, default=0,
                    help="after the timed region, run 5 plain device copies of this size (counter calibration)")
@@ -108,6 +114,186 @@ def measured_traffic():
     return None, None
 
 
+class Setup:
+    """Rotated copies of one workload's page pool and prepared C-ABI attention calls over them.
+
+    The calls go straight through the C ABI (the drop-in boundary) with argument
+    lists prepared here: the Python wrapper's host cost per call (validation,
+    conversions) exceeds one ~30 us decode call and would otherwise be what is
+    timed.  Each prepared call is checked to reproduce the public operator's
+    output bit for bit.
+    """
+
+    def __init__(self, wl, pool_gib, dev, min_pools=4):
+        import torch
+
+        from easymlx_amd import _native, paged_attention
+        from easymlx_amd.caching import affine_pool
+
+        self.wl = wl
+        mk = dict(num_blocks=wl.num_blocks, num_kv_heads=wl.num_kv_heads, head_dim=wl.head_dim,
+                  block_size=wl.block_size, bits=wl.bits, group_size=wl.group_size)
+        base = affine_pool(**mk, block_tables=torch.from_numpy(wl.block_tables).to(dev),
+                           kv_lens=torch.from_numpy(wl.kv_lens).to(dev))
+        base.write_slots(torch.from_numpy(wl.k).to(dev), torch.from_numpy(wl.v).to(dev),
+                         torch.from_numpy(wl.slot.astype(np.int32)).to(dev))
+        names = ("k_codes", "v_codes", "k_scales", "k_biases", "v_scales", "v_biases")
+        self.pool_bytes = sum(getattr(base, n).numel() * getattr(base, n).element_size() for n in names)
+        self.n_pools = max(min_pools, math.ceil(pool_gib * 2**30 / self.pool_bytes))
+        self.pools = [base]
+        for _ in range(self.n_pools - 1):
+            p = affine_pool(**mk, block_tables=base.block_tables, kv_lens=base.kv_lens)
+            for n in names:
+                getattr(p, n).copy_(getattr(base, n))
+            self.pools.append(p)
+        q = torch.from_numpy(wl.q).to(dev)
+        qsl = torch.from_numpy(wl.query_start_loc).to(dev)
+        self.out = out = torch.empty_like(q)
+        self._keep = (q, qsl)
+        paged_attention(q, base.k_codes, base.v_codes, base.block_tables, base.kv_lens, qsl,
+                        k_scales=base.k_scales, k_biases=base.k_biases, v_scales=base.v_scales,
+                        v_biases=base.v_biases, bits=wl.bits, group_size=wl.group_size,
+                        single_token_decode=bool(wl.single_token_decode), out=out)
+        torch.cuda.synchronize()
+        assert torch.isfinite(out).all(), f"non-finite attention output ({wl.name})"
+        eager = out.clone()
+
+        lib = _native.load()
+        self._fn = lib.emx_paged_attention_affine
+        self._check = _native.check
+        T, hq, d = (int(x) for x in q.shape)
+        S = int(wl.block_tables.shape[0])
+        self.ws = torch.zeros(lib.emx_paged_workspace_bytes(S, hq, wl.num_kv_heads, d, wl.block_tables.shape[1],
+                                                            wl.block_size), dtype=torch.uint8, device=dev)
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        self.args = [
+            (q.data_ptr(), T, hq, d, p.k_codes.data_ptr(), p.k_scales.data_ptr(), p.k_biases.data_ptr(),
+             p.v_codes.data_ptr(), p.v_scales.data_ptr(), p.v_biases.data_ptr(), wl.num_blocks, wl.block_size,
+             wl.num_kv_heads, wl.bits, wl.group_size, p.block_tables.data_ptr(), S, wl.block_tables.shape[1],
+             p.kv_lens.data_ptr(), qsl.data_ptr(), 1.0 / math.sqrt(d), 0, int(wl.single_token_decode),
+             self.ws.data_ptr(), self.ws.numel(), out.data_ptr(), stream)
+            for p in self.pools
+        ]
+        for i in range(self.n_pools):  # same result as the public operator, on every pool
+            out.zero_()
+            self.call(i)
+            torch.cuda.synchronize()
+            assert torch.equal(out, eager), f"C-ABI call differs from paged_attention ({wl.name})"
+
+    def call(self, i):
+        rc = self._fn(*self.args[i % self.n_pools])
+        if rc:
+            self._check(rc)
+
+
+def warm(fn, seconds):
+    """Clocks ramp up under sustained load: keep calling for about `seconds` before timing."""
+    import torch
+
+    t_end = time.perf_counter() + seconds
+    i = 0
+    while time.perf_counter() < t_end:
+        for _ in range(32):
+            fn(i)
+            i += 1
+        torch.cuda.synchronize()
+
+
+def event_us(fn, n):
+    """Per-call times (us) from HIP events recorded on the launch stream around each call."""
+    import torch
+
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+    for i, (a, b) in enumerate(evs):
+        a.record()
+        fn(i)
+        b.record()
+    torch.cuda.synchronize()
+    return np.array([a.elapsed_time(b) for a, b in evs]) * 1e3
+
+
+def aux_c3(dev):
+    """c3: ragged unified step, prefill rows on the MFMA prefill kernel and single-token rows on split-K."""
+    from easymlx_amd.workloads import config
+
+    wl = config("c3")
+    st = Setup(wl, 1.0, dev)
+    warm(st.call, 0.5)
+    us = float(np.median(event_us(st.call, 100)))
+    qlens = np.diff(wl.query_start_loc)
+    pre = qlens > 1
+    visible = 0  # keys seen by the prefill rows (causal: row j of a chunk after p cached tokens sees p + j + 1)
+    for p, n in zip(wl.kv_lens[pre] - qlens[pre], qlens[pre]):
+        visible += int(n * p + n * (n + 1) // 2)
+    flops = 4 * wl.head_dim * wl.num_q_heads * visible
+    nbytes = wl.kv_bytes()
+    return {
+        "workload": "c3: 4 prefill chunks x 512 (prior U[0,2048]) + 28 decode rows (ctx U[256,4096]), 4-bit, "
+                    "Hq 32 / Hkv 8, D 128, page 128, group 64 (seed 3)",
+        "us_p50": round(us, 2),
+        "prefill_gflop": round(flops / 1e9, 3),
+        "kv_bytes": int(nbytes),
+        "prefill_tflops": round(flops / (us * 1e-6) / 1e12, 1),
+        "kv_GBs": round(nbytes / (us * 1e3), 1),
+    }
+
+
+def aux_c4(dev):
+    """c4: long-context decode, 8 sequences x 32768 tokens, Hq 64 / Hkv 8 (KV bytes exceed the 256 MB cache)."""
+    from easymlx_amd.workloads import config
+
+    wl = config("c4")
+    st = Setup(wl, 0.0, dev, min_pools=2)
+    warm(st.call, 0.5)
+    us = float(np.median(event_us(st.call, 100)))
+    nbytes = wl.kv_bytes()
+    return {"workload": "c4: 8 seqs x 32768 tokens, 4-bit, Hq 64 / Hkv 8, D 128, page 128, group 64 (seed 4)",
+            "us_p50": round(us, 2), "kv_bytes": int(nbytes), "kv_GBs": round(nbytes / (us * 1e3), 1),
+            "frac": round(nbytes / (us * 1e3) / HBM_PEAK_GBS, 4)}
+
+
+def aux_quantize_on_write(dev):
+    """Fused quantize-on-write (4-bit, group 64): one appended token per c2 sequence; 4 x 512-token chunks."""
+    import torch
+
+    from easymlx_amd import _native
+    from easymlx_amd.caching import affine_pool
+    from easymlx_amd.workloads import config
+
+    wl = config("c2")
+    bs, hkv, d = wl.block_size, wl.num_kv_heads, wl.head_dim
+    nb = wl.num_blocks + 16
+    view = affine_pool(num_blocks=nb, num_kv_heads=hkv, head_dim=d, block_size=bs, bits=4, group_size=64,
+                       block_tables=torch.from_numpy(wl.block_tables).to(dev),
+                       kv_lens=torch.from_numpy(wl.kv_lens).to(dev))
+    fn = _native.load().emx_affine_cache_write
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    width = wl.block_tables.shape[1]
+    appends = [int(wl.block_tables[s, min(int(wl.kv_lens[s]) // bs, width - 1)]) * bs + int(wl.kv_lens[s]) % bs
+               for s in range(wl.num_seqs)]
+    chunks = [(wl.num_blocks + 4 * c) * bs + i for c in range(4) for i in range(512)]
+    res = {}
+    for name, slots in (("append_1_token_x32_seqs", appends), ("prefill_4x512_tokens", chunks)):
+        n = len(slots)
+        k = torch.randn(n, hkv, d, device=dev).half()
+        v = torch.randn(n, hkv, d, device=dev).half()
+        s = torch.tensor(slots, dtype=torch.int32, device=dev)
+        args = (k.data_ptr(), v.data_ptr(), s.data_ptr(), n, hkv, d, 64, 4, bs, nb, view.k_codes.data_ptr(),
+                view.k_scales.data_ptr(), view.k_biases.data_ptr(), view.v_codes.data_ptr(),
+                view.v_scales.data_ptr(), view.v_biases.data_ptr(), stream)
+
+        def call(i, args=args):
+            rc = fn(*args)
+            if rc:
+                _native.check(rc)
+
+        warm(call, 0.3)
+        us = float(np.median(event_us(call, 200)))
+        moved = n * hkv * (2 * d * 2 + 2 * (d // 2 + 4 * (d // 64)))  # fp16 K,V in; codes + scale/bias out
+        res[name] = {"tokens": n, "us_p50": round(us, 2), "GBs_in_plus_out": round(moved / (us * 1e3), 1)}
+    return res
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -116,105 +302,27 @@ def main():
 
     import torch
 
-    from easymlx_amd import _native, paged_attention
-    from easymlx_amd.caching import affine_pool
     from easymlx_amd.workloads import config
 
     dev = torch.device("cuda", 0)
     wl = config("c2")
     bytes_per_step = wl.kv_bytes()
-
-    base = affine_pool(num_blocks=wl.num_blocks, num_kv_heads=wl.num_kv_heads, head_dim=wl.head_dim,
-                       block_size=wl.block_size, bits=wl.bits, group_size=wl.group_size,
-                       block_tables=torch.from_numpy(wl.block_tables).to(dev),
-                       kv_lens=torch.from_numpy(wl.kv_lens).to(dev))
-    base.write_slots(torch.from_numpy(wl.k).to(dev), torch.from_numpy(wl.v).to(dev),
-                     torch.from_numpy(wl.slot.astype(np.int32)).to(dev))
-    pool_bytes = sum(t.numel() * t.element_size() for t in
-                     (base.k_codes, base.v_codes, base.k_scales, base.k_biases, base.v_scales, base.v_biases))
-    n_pools = max(4, math.ceil(args.pool_gib * 2**30 / pool_bytes))
-    pools = [base] + [
-        affine_pool(num_blocks=wl.num_blocks, num_kv_heads=wl.num_kv_heads, head_dim=wl.head_dim,
-                    block_size=wl.block_size, bits=wl.bits, group_size=wl.group_size,
-                    block_tables=base.block_tables, kv_lens=base.kv_lens)
-        for _ in range(n_pools - 1)
-    ]
-    for p in pools[1:]:
-        for dst, src in ((p.k_codes, base.k_codes), (p.v_codes, base.v_codes), (p.k_scales, base.k_scales),
-                         (p.k_biases, base.k_biases), (p.v_scales, base.v_scales), (p.v_biases, base.v_biases)):
-            dst.copy_(src)
-    q = torch.from_numpy(wl.q).to(dev)
-    qsl = torch.from_numpy(wl.query_start_loc).to(dev)
-    out = torch.empty_like(q)
-
-    def step(i):
-        p = pools[i % n_pools]
-        paged_attention(q, p.k_codes, p.v_codes, p.block_tables, p.kv_lens, qsl, k_scales=p.k_scales,
-                        k_biases=p.k_biases, v_scales=p.v_scales, v_biases=p.v_biases, bits=wl.bits,
-                        group_size=wl.group_size, single_token_decode=True, out=out)
-
+    st = Setup(wl, args.pool_gib, dev)
     for i in range(args.warmup):
-        step(i)
-    torch.cuda.synchronize()
-    assert torch.isfinite(out).all(), "non-finite decode output"
-    eager = out.clone()
-
-    # Timed calls go straight through the C ABI (the drop-in boundary) with their argument
-    # lists prepared here: the Python wrapper's host cost per call (validation, conversions)
-    # exceeds one ~30 us call and would otherwise be what is timed.
-    lib = _native.load()
-    fn = lib.emx_paged_attention_affine
-    S, hq, d = (int(x) for x in q.shape)
-    ws = torch.zeros(lib.emx_paged_workspace_bytes(S, hq, wl.num_kv_heads, d, wl.block_tables.shape[1],
-                                                   wl.block_size), dtype=torch.uint8, device=dev)
-    stream = torch.cuda.current_stream(dev).cuda_stream
-    call_args = [
-        (q.data_ptr(), S, hq, d, p.k_codes.data_ptr(), p.k_scales.data_ptr(), p.k_biases.data_ptr(),
-         p.v_codes.data_ptr(), p.v_scales.data_ptr(), p.v_biases.data_ptr(), wl.num_blocks, wl.block_size,
-         wl.num_kv_heads, wl.bits, wl.group_size, p.block_tables.data_ptr(), S, wl.block_tables.shape[1],
-         p.kv_lens.data_ptr(), qsl.data_ptr(), 1.0 / math.sqrt(d), 0, 1, ws.data_ptr(), ws.numel(), out.data_ptr(),
-         stream)
-        for p in pools
-    ]
-
-    def call(i):
-        rc = fn(*call_args[i % n_pools])
-        if rc:
-            _native.check(rc)
-
-    for i in range(n_pools):                                      # same result as the public op, every pool
-        out.zero_()
-        call(i)
-        torch.cuda.synchronize()
-        assert torch.equal(out, eager), "C-ABI call differs from paged_attention"
-
-    # clocks ramp up under sustained load: keep calling for ~1 s before timing
-    t_end = time.perf_counter() + 1.0
-    i = 0
-    while time.perf_counter() < t_end:
-        for _ in range(64):
-            call(i)
-            i += 1
-        torch.cuda.synchronize()
+        st.call(i)
+    warm(st.call, 1.0)
 
     # ---- timed region: exactly `steps` decode calls
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
-        call(i)
+        st.call(i)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     ms_per_step = elapsed / args.steps * 1e3
 
     # ---- per-call time with HIP events on the launch stream
-    n_ev = min(args.steps, 200)
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n_ev)]
-    for i, (a, b) in enumerate(evs):
-        a.record()
-        call(i)
-        b.record()
-    torch.cuda.synchronize()
-    kt = np.array([a.elapsed_time(b) for a, b in evs]) * 1e3  # us
+    kt = event_us(st.call, min(args.steps, 200))
     k_avg_us = float(kt.mean())
     achieved = bytes_per_step / (k_avg_us * 1e-6) / 1e9
 
@@ -227,6 +335,17 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
+
+    n_pools, pool_bytes = st.n_pools, st.pool_bytes
+    del st
+    aux = None
+    if not args.no_aux:
+        torch.cuda.empty_cache()
+        aux = {"c3_unified": aux_c3(dev)}
+        torch.cuda.empty_cache()
+        aux["c4_long_context"] = aux_c4(dev)
+        torch.cuda.empty_cache()
+        aux["quantize_on_write"] = aux_quantize_on_write(dev)
 
     value = bytes_per_step / (ms_per_step * 1e-3) / 1e9
     traffic, traffic_src = measured_traffic()
@@ -266,9 +385,10 @@ def main():
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
             "traffic_source": traffic_src,
-            "kernel": "emx::decode_affine_d128<4,64,4> + emx::decode_merge_d128<4> (one decode call)",
+            "kernel": "emx::decode_affine_d128<4,64,4> (one launch per decode call; split-K merge fused)",
         },
         "cpu_baseline": cpu,
+        "aux": aux,
     }
     print(json.dumps(line))
 
