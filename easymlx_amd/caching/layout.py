@@ -50,18 +50,29 @@ def value_tile(block_size: int, bits: int) -> int:
     return min(block_size, 256 // bits)
 
 
+# 4-bit value words interleave their eight tokens: token k sits at nibble
+# (k >> 1) | ((k & 1) << 2), i.e. nibble n holds token _V4_TOKEN_AT[n].
+_V4_TOKEN_AT = np.array([0, 2, 4, 6, 1, 3, 5, 7])
+_V4_NIBBLE_OF = np.array([0, 4, 1, 5, 2, 6, 3, 7])
+
+
 def value_pages_from_logical(codes: np.ndarray, bits: int) -> np.ndarray:
-    """``[nb, bs, Hkv, W]`` -> ``[nb, Hkv, bs/T, D, T*bits/32]`` (tokens packed per word)."""
+    """``[nb, bs, Hkv, W]`` -> ``[nb, Hkv, bs/T, D, T*bits/32]`` (tokens packed per word;
+    4-bit words in the interleaved token order above, 8-bit words in byte order)."""
     q = _unpack(np.asarray(codes, dtype=np.uint32), bits)  # [nb, bs, Hkv, D]
     nb, bs, hkv, d = q.shape
     t = value_tile(bs, bits)
     q = q.reshape(nb, bs // t, t, hkv, d).transpose(0, 3, 1, 4, 2)  # [nb, Hkv, bs/T, D, T]
+    if bits == 4:
+        q = q.reshape(*q.shape[:-1], t // 8, 8)[..., _V4_TOKEN_AT].reshape(q.shape)
     return np.ascontiguousarray(_pack(q, bits))
 
 
 def value_logical_from_pages(pages: np.ndarray, bits: int) -> np.ndarray:
     q = _unpack(np.asarray(pages).view(np.uint32), bits)  # [nb, Hkv, bs/T, D, T]
     nb, hkv, nt, d, t = q.shape
+    if bits == 4:
+        q = q.reshape(*q.shape[:-1], t // 8, 8)[..., _V4_NIBBLE_OF].reshape(q.shape)
     q = q.transpose(0, 2, 4, 1, 3).reshape(nb, nt * t, hkv, d)  # [nb, bs, Hkv, D]
     return np.ascontiguousarray(_pack(q, bits))
 

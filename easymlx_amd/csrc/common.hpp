@@ -62,6 +62,16 @@ __device__ __forceinline__ void from_f32(float f, h16* p) { *p = (h16)f; }
 __device__ __forceinline__ void from_f32(float f, float* p) { *p = f; }
 __device__ __forceinline__ void from_f32(float f, uint16_t* p) { *p = f32_to_bf16(f); }
 
+// Bit offset of token k inside its value word.  4-bit value words interleave
+// their eight tokens, token k at nibble (k >> 1) | ((k & 1) << 2), so that
+// masking a word with 0x000F000F / 0x00F000F0 (and the same after >> 8) yields
+// the token pairs (0,1), (2,3), (4,5), (6,7) as fp16 subnormals (the second
+// and fourth pair scaled by 16).  8-bit value words hold tokens in byte order.
+template <int BITS>
+__host__ __device__ __forceinline__ constexpr int v_shift(int k) {
+  return BITS == 4 ? 4 * (((k & 7) >> 1) | ((k & 1) << 2)) : 8 * (k & 3);
+}
+
 // Value pages are stored in tiles of T = min(page_size, 256/BITS) tokens; inside a
 // tile they are dim-major with T*BITS/32 words per dim (32 bytes when the page
 // holds a whole tile), so one decode iteration's value codes are one contiguous

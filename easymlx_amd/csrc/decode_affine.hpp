@@ -96,6 +96,17 @@ struct DecodeCfg {
 constexpr int kRsrcFlags = 0x00020000;  // raw 32-bit buffer, gfx9 family
 constexpr int kLoadAux = 0;             // default cache policy
 
+// Raw buffer descriptor of `bytes` bytes at p, built from wave-uniform values
+// moved to SGPRs (a descriptor the compiler keeps in VGPRs makes it wrap every
+// load through it in a per-lane loop).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t uniform_rsrc(const void* p, const int bytes) {
+  const uint64_t x = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)x);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(x >> 32));
+  return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(((uint64_t)hi << 32) | lo), (short)0,
+                                           __builtin_amdgcn_readfirstlane(bytes), kRsrcFlags);
+}
+
 // Buffer resources of one 128-token tile of one (page, kv_head), held in SGPRs:
 // every per-lane address is then a single 32-bit offset.
 struct TileRsrc {
@@ -108,15 +119,11 @@ __device__ __forceinline__ TileRsrc make_tile_rsrc(const DecodeArgs& a, const in
   const int RW = a.bs * BITS / 32;
   const size_t ph = (size_t)blk * a.Hkv + kvh;
   TileRsrc rs;
-  rs.k = __builtin_amdgcn_make_buffer_rsrc((void*)(a.kc + (ph * a.bs + off) * C::W), (short)0, 128 * C::W * 4,
-                                           kRsrcFlags);
-  rs.v = __builtin_amdgcn_make_buffer_rsrc((void*)(a.vc + ph * C::D * RW + (off / C::NT) * C::D * 8), (short)0,
-                                           (C::D * RW - (off / C::NT) * C::D * 8) * 4, kRsrcFlags);
+  rs.k = uniform_rsrc(a.kc + (ph * a.bs + off) * C::W, 128 * C::W * 4);
+  rs.v = uniform_rsrc(a.vc + ph * C::D * RW + (off / C::NT) * C::D * 8, (C::D * RW - (off / C::NT) * C::D * 8) * 4);
   const h16* sp[4] = {a.ks, a.kb, a.vs, a.vb};
 #pragma unroll
-  for (int arr = 0; arr < 4; ++arr)
-    rs.s[arr] = __builtin_amdgcn_make_buffer_rsrc((void*)(sp[arr] + ph * C::G * a.bs + off), (short)0,
-                                                  (C::G * a.bs - off) * 2, kRsrcFlags);
+  for (int arr = 0; arr < 4; ++arr) rs.s[arr] = uniform_rsrc(sp[arr] + ph * C::G * a.bs + off, (C::G * a.bs - off) * 2);
   return rs;
 }
 
@@ -276,10 +283,10 @@ __device__ __forceinline__ void compute_iteration(IterLoads<BITS, GS, HG>& L, co
     h16x8 pB;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const int j = 8 * w + slot_perm<BITS>(i);
+      const int j = 8 * w + i;  // unpacked value element i is token i of the word
       const float p = sc[j >> 2][j & 3];
-      pB[i] = col_ok ? (h16)(p * (float)vs8[slot_perm<BITS>(i)]) : (h16)0.0f;
-      pb = fmaf(p, (float)vb8[slot_perm<BITS>(i)], pb);
+      pB[i] = col_ok ? (h16)(p * (float)vs8[i]) : (h16)0.0f;
+      pb = fmaf(p, (float)vb8[i], pb);
     }
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) {
@@ -340,11 +347,16 @@ __device__ __forceinline__ void seq_table(const DecodeArgs& a, int* cum, int* kv
   __syncthreads();
 }
 
-// Wave containing item g of I items split over NW waves as [w*I/NW, (w+1)*I/NW).
+// Wave containing item g of I items split over NW waves as [w*I/NW, (w+1)*I/NW):
+// the w with start(w) <= g < start(w+1), start(w) = floor(w*I/NW).  A float
+// estimate corrected with multiplications only (64-bit division is a long
+// software sequence): start(w) <= g  <=>  w*I < (g+1)*NW.
 __device__ __forceinline__ int wave_of_item(long long g, long long I, int NW) {
-  int w = (int)((g * NW) / I);
-  while (w + 1 < NW && ((long long)(w + 1) * I) / NW <= g) ++w;
-  while (w > 0 && ((long long)w * I) / NW > g) --w;
+  int w = (int)((float)g * ((float)NW / (float)I));
+  w = min(max(w, 0), NW - 1);
+  const long long lim = (g + 1) * (long long)NW;
+  while (w + 1 < NW && (long long)(w + 1) * I < lim) ++w;
+  while (w > 0 && (long long)w * I >= lim) --w;
   return w;
 }
 
@@ -427,13 +439,64 @@ __device__ __forceinline__ bool arrive_last(int* cnt, const int expected, const 
   return true;
 }
 
-// Wave W finished its piece of unit u (items [unit_first, unit_first + n) of the
-// I items split over NW waves; pieces k = W - wf of np).  It stores its partial
-// (o = acc + pbs, m, l) in slot wf + u + k.  Pieces are merged in groups of
-// kGroup by the last arrival of each group (counter per group, indexed by the
-// group's first slot); with more than one group, the group result replaces the
-// group's first partial and the last group to finish merges the groups into the
-// fp16 output (counter per unit).  The reduce of page_attention.py:2006-2059.
+// Pieces of unit u (items [unit_first, unit_first + n) of the I items split
+// over NW waves): np pieces, partial slots slot0 .. slot0 + np - 1, wave W's
+// piece is `me`; ro / rm address the pieces' accumulators and (max, sum) pairs.
+struct PieceInfo {
+  int slot0, np, me;
+  __amdgpu_buffer_rsrc_t ro, rm;
+};
+
+// Number of pieces of a unit (lane-local: callers may pass per-lane units).
+__device__ __forceinline__ int piece_count(const long long unit_first, const int n, const long long I, const int NW) {
+  return wave_of_item(unit_first + n - 1, I, NW) - wave_of_item(unit_first, I, NW) + 1;
+}
+
+// Wave-uniform arguments only.
+template <int HG>
+__device__ __forceinline__ PieceInfo piece_info(const DecodeArgs& a, const int W, const int u,
+                                                const long long unit_first, const int n, const long long I,
+                                                const int NW) {
+  constexpr int D = 128;
+  PieceInfo pi;
+  const int wf = wave_of_item(unit_first, I, NW);
+  const int wl = wave_of_item(unit_first + n - 1, I, NW);
+  // wave-uniform by construction; readfirstlane keeps the descriptors in SGPRs
+  pi.np = __builtin_amdgcn_readfirstlane(wl - wf + 1);
+  pi.slot0 = __builtin_amdgcn_readfirstlane(wf + u);  // the pieces of unit u sit in slots wf+u .. wl+u
+  pi.me = __builtin_amdgcn_readfirstlane(W - wf);
+  pi.ro = uniform_rsrc(a.ws_o + (size_t)pi.slot0 * (HG * D), pi.np * HG * D * 4);
+  pi.rm = uniform_rsrc(a.ws_ml + (size_t)pi.slot0 * (HG * 2), pi.np * HG * 2 * 4);
+  return pi;
+}
+
+// After storing its partial (o = unnormalized accumulator, m, l) in piece slot
+// `me` with device-coherent stores: pieces are merged in groups of kGroup by
+// the last arrival of each group (counter per group, indexed by the group's
+// first slot); with more than one group, the group result replaces the group's
+// first partial and the last group to finish merges the groups into the fp16
+// output (counter per unit).  The reduce of page_attention.py:2006-2059.
+template <int HG>
+__device__ __forceinline__ void merge_pieces(const DecodeArgs& a, const PieceInfo& pi, const int u, const int row,
+                                             const int kvh, const int lane) {
+  constexpr int D = 128;
+  const int np = pi.np;
+  // one level up to kSingle pieces; beyond, groups of kGroup first
+  const int gsz = np <= kSingle ? np : kGroup;
+  const int grp = pi.me / gsz, ngrp = (np + gsz - 1) / gsz;
+  const int gfirst = grp * gsz, gcount = min(gsz, np - gfirst);
+  if (!arrive_last(a.ws_cnt_grp + pi.slot0 + gfirst, gcount, lane)) return;
+  h16* out = a.out + ((size_t)row * a.Hq + (size_t)kvh * HG) * D;
+  if (ngrp == 1) {
+    merge_range<HG>(pi.ro, pi.rm, 0, np, 1, out, 0, lane);
+    return;
+  }
+  merge_range<HG>(pi.ro, pi.rm, gfirst, gcount, 1, nullptr, gfirst, lane);
+  if (!arrive_last(a.ws_cnt + u, ngrp, lane)) return;
+  merge_range<HG>(pi.ro, pi.rm, 0, ngrp, gsz, out, 0, lane);
+}
+
+// Wave W finished its piece of unit u: store its partial, then merge.
 template <int GS, int HG>
 __device__ __forceinline__ void merge_piece(const DecodeArgs& a, const int W, const int u, const long long unit_first,
                                             const int n, const long long I, const int NW, const int row, const int kvh,
@@ -441,37 +504,16 @@ __device__ __forceinline__ void merge_piece(const DecodeArgs& a, const int W, co
                                             const bool col_ok, const int gg, const int jj, const int hh,
                                             const int lane) {
   constexpr int D = 128;
-  const int wf = wave_of_item(unit_first, I, NW);
-  const int wl = wave_of_item(unit_first + n - 1, I, NW);
-  const int np = wl - wf + 1;
-  const int slot0 = wf + u;  // the pieces of unit u sit in slots wf+u .. wl+u
-  const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc((void*)(a.ws_o + (size_t)slot0 * (HG * D)),
-                                                                      (short)0, np * HG * D * 4, kRsrcFlags);
-  const __amdgpu_buffer_rsrc_t rm = __builtin_amdgcn_make_buffer_rsrc((void*)(a.ws_ml + (size_t)slot0 * (HG * 2)),
-                                                                      (short)0, np * HG * 2 * 4, kRsrcFlags);
-  const int me = W - wf;
+  const PieceInfo pi = piece_info<HG>(a, W, u, unit_first, n, I, NW);
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt) {  // lane (hh, gg, jj) owns dims 16*dt + 4*jj .. +3 when they lie in group gg
     const int d = 16 * dt + 4 * jj;
-    if (col_ok && d / GS == gg) store_f32x4(acc[dt] * kTwo24 + pbs, ro, (hh * D + d) * 4, me * HG * D * 4);
+    if (col_ok && d / GS == gg) store_f32x4(acc[dt] * kTwo24 + pbs, pi.ro, (hh * D + d) * 4, pi.me * HG * D * 4);
   }
   if (col_ok && gg == 0 && jj == 0)
-    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, f32x2{m_run, l}), rm, hh * 8, me * HG * 8,
-                                          kCoherent);
-
-  // one level up to kSingle pieces; beyond, groups of kGroup first
-  const int gsz = np <= kSingle ? np : kGroup;
-  const int grp = me / gsz, ngrp = (np + gsz - 1) / gsz;
-  const int gfirst = grp * gsz, gcount = min(gsz, np - gfirst);
-  if (!arrive_last(a.ws_cnt_grp + slot0 + gfirst, gcount, lane)) return;
-  h16* out = a.out + ((size_t)row * a.Hq + (size_t)kvh * HG) * D;
-  if (ngrp == 1) {
-    merge_range<HG>(ro, rm, 0, np, 1, out, 0, lane);
-    return;
-  }
-  merge_range<HG>(ro, rm, gfirst, gcount, 1, nullptr, gfirst, lane);
-  if (!arrive_last(a.ws_cnt + u, ngrp, lane)) return;
-  merge_range<HG>(ro, rm, 0, ngrp, gsz, out, 0, lane);
+    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, f32x2{m_run, l}), pi.rm, hh * 8,
+                                          pi.me * HG * 8, kCoherent);
+  merge_pieces<HG>(a, pi, u, row, kvh, lane);
 }
 
 template <int BITS, int GS, int HG>
@@ -530,7 +572,7 @@ __global__ __launch_bounds__(256, 2) void decode_affine_d128(DecodeArgs a) {
     if (g < g1) {
       const int si = seq_of(g, s);
       const int n = cum[si + 1] - cum[si];
-      const int jn = (int)((g - (long long)Hkv * cum[si]) % n);
+      const int jn = (int)(g - (long long)Hkv * cum[si]) % n;
       b = a.block_tables[(size_t)si * a.max_blocks + ((lo_of(si) + jn) * NT) / a.bs];
     }
     return b;

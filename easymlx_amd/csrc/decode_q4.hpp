@@ -1,0 +1,729 @@
+// Single-token paged decode over 4-bit affine pages, head_dim 128, on the
+// 16-block 4x4x4 MFMA (v_mfma_f32_4x4x4_16b_f16), group size 64 or 128.
+//
+// Replaces the reference's per-(seq, q_head) serial key loop
+// (lib/python/easymlx/operations/kernels/unified_attention.py:467-609) and its
+// split-K variant (page_attention.py:1718-2059) for int4 pages.  Work
+// decomposition, split-K partials and the in-kernel merge are those of
+// decode_affine_d128 (decode_affine.hpp); only the per-item math differs.
+//
+// Per item (64 tokens of one (sequence, kv_head); lane L = 0..63):
+//   QK^T : A = K codes, lane L holds token L's row (MFMA row = token),
+//          B = query, column = head (4 heads of a head quad), broadcast to all
+//          16 blocks from one 16-lane group (blgp 4..7), so 8 VGPR pairs hold
+//          the query operands of all 32 k-steps.  Output: lane L holds head
+//          L%4 of tokens 4*(L/4) .. +3, every output element a live score.
+//          One accumulator per quantization group; the affine scale and bias
+//          are applied per (token, group) after the MFMAs:
+//            s = sum_g scale[t,g] * C_g + bias[t,g] * sum_{d in g} q_d
+//   softmax: online, base 2, fp32; the per-head max and sum run over the 16
+//          lanes of a head (DPP row rotations, then two cross-row shuffles).
+//   PV   : A = P' = p * v_scale[t, g] in fp16, lane layout exactly as the QK
+//          output; block tau of A is broadcast to all blocks (cbsz 4, abid
+//          tau), so no transpose is needed.  B = V codes, lane L holds dims L
+//          and 64 + L (one group half each).  Output: lane L holds dims L and
+//          64 + L of the 4 heads.  sum_t p_t * v_bias[t, g] is kept in fp32.
+//
+// Codes enter the MFMA as exact fp16 subnormals: for a word x of eight 4-bit
+// codes, x & 0x000F000F and x & 0x00F000F0 (and the same for x >> 8) are the
+// code pairs of nibbles (0,4), (1,5)*16, (2,6), (3,7)*16.  The factor 16 is
+// taken out of the other operand (query / P' elements 2, 3 of each k-step).
+// Value words interleave tokens (token k at nibble (k >> 1) | ((k & 1) << 2)),
+// so each k-step of PV covers 4 consecutive tokens, the token quad of one QK
+// output block.
+#pragma once
+
+#include <utility>
+
+#include "decode_affine.hpp"
+
+namespace emx {
+
+typedef h16 h16x4 __attribute__((ext_vector_type(4)));
+
+template <int CBSZ, int ABID, int BLGP>
+__device__ __forceinline__ f32x4 mfma4(const h16x4 a, const h16x4 b, const f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_4x4x4f16(a, b, c, CBSZ, ABID, BLGP);
+}
+
+template <class F, int... Is>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, Is...>) {
+  (f(std::integral_constant<int, Is>{}), ...);
+}
+// f(std::integral_constant<int, i>) for i = 0 .. N-1, with i usable as a constant.
+template <int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+// Code pairs (nibbles 0,4) and (1,5)*16 of x as one 4-element MFMA operand.
+__device__ __forceinline__ h16x4 nib_pairs(const uint32_t x) {
+  return __builtin_bit_cast(h16x4, u32x2{x & 0x000F000Fu, x & 0x00F000F0u});
+}
+
+__device__ __forceinline__ float half_of(const uint32_t (&w)[2], const int i) {
+  const uint32_t x = w[i >> 1];
+  return (float)__builtin_bit_cast(h16, (uint16_t)((i & 1) ? (x >> 16) : (x & 0xFFFFu)));
+}
+
+template <int GS, int HQ>
+struct Q4Cfg {
+  static constexpr int D = 128;
+  static constexpr int G = D / GS;  // quantization groups per head
+  static constexpr int NT = 64;     // tokens per work item
+  static constexpr int W = 16;      // K code words per token
+  static_assert(GS == 64 || GS == 128, "a value half (64 dims) must lie in one quantization group");
+};
+
+// Register image of one item's loads.
+template <int GS, int HQ>
+struct Q4Loads {
+  static constexpr int G = Q4Cfg<GS, HQ>::G;
+  uint32_t k[16];       // K codes of token L (128 dims)
+  uint32_t v[2][8];     // V codes of dims L and 64 + L, 64 tokens
+  uint32_t s[4][G][2];  // k_scale, k_bias, v_scale, v_bias of tokens 4*(L/4) .. +3, per group
+};
+
+template <int GS, int HQ>
+__device__ __forceinline__ void q4_issue_loads(Q4Loads<GS, HQ>& L, const TileRsrc& rs, const int it, const int lane,
+                                               const int bs) {
+  constexpr int G = Q4Cfg<GS, HQ>::G;
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(rs.k, lane * 64 + 16 * v, it * 64 * 64, kLoadAux);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) L.k[4 * v + e] = x[e];
+  }
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+#pragma unroll
+    for (int v = 0; v < 2; ++v) {
+      const u32x4 x =
+          __builtin_amdgcn_raw_buffer_load_b128(rs.v, (64 * c + lane) * 32 + 16 * v, it * 128 * 8 * 4, kLoadAux);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) L.v[c][4 * v + e] = x[e];
+    }
+  }
+  const int ls = (lane >> 2) * 8;
+#pragma unroll
+  for (int arr = 0; arr < 4; ++arr) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const u32x2 x = __builtin_amdgcn_raw_buffer_load_b64(rs.s[arr], ls + g * bs * 2, it * 64 * 2, kLoadAux);
+      L.s[arr][g][0] = x[0];
+      L.s[arr][g][1] = x[1];
+    }
+  }
+}
+
+// Per-lane softmax / accumulator state of one head quad.
+struct Q4State {
+  f32x4 o[2];   // dims L, 64 + L of the quad's 4 heads (2^-24 units)
+  float m;      // running max of this lane's head (scaled log2 units)
+  float l;      // this lane's share of the softmax denominator
+  float pb[2];  // this lane's share of sum_t p_t * v_bias[t, g]
+};
+
+// Reduce over the 16 lanes holding one head (lanes L, L^4, L^8, ... within
+// rows of 16, then across rows).
+__device__ __forceinline__ float head_sum(float v) {
+  v += row_ror<4>(v);
+  v += row_ror<8>(v);
+  v += __shfl_xor(v, 16, 64);
+  v += __shfl_xor(v, 32, 64);
+  return v;
+}
+
+__device__ __forceinline__ float head_max(float v) {
+  v = fmaxf(v, row_ror<4>(v));
+  v = fmaxf(v, row_ror<8>(v));
+  v = fmaxf(v, __shfl_xor(v, 16, 64));
+  v = fmaxf(v, __shfl_xor(v, 32, 64));
+  return v;
+}
+
+// One 64-token item.  `full`: every token of the item is inside [start_k, kv_len).
+template <int GS, int HQ>
+__device__ __forceinline__ void q4_compute(Q4Loads<GS, HQ>& L, const bool full, const int lane, const int tok_base,
+                                           const int start_k, const int kv_len, const h16x4 (&qB)[HQ][8],
+                                           const float (&qs)[HQ][2], const float sc_l2, Q4State (&st)[HQ]) {
+  constexpr int G = Q4Cfg<GS, HQ>::G;
+
+  // ---- S = K Q^T, one accumulator per (head quad, group)
+  f32x4 acc[HQ][G];
+#pragma unroll
+  for (int hq = 0; hq < HQ; ++hq)
+#pragma unroll
+    for (int g = 0; g < G; ++g) acc[hq][g] = f32x4{0.f, 0.f, 0.f, 0.f};
+  static_for<16>([&](auto M) {
+    constexpr int m = decltype(M)::value;  // K word m = dims 8m .. 8m+7
+    constexpr int g = (8 * m) / GS;
+    const uint32_t x = L.k[m];
+    const h16x4 a0 = nib_pairs(x), a1 = nib_pairs(x >> 8);
+#pragma unroll
+    for (int hq = 0; hq < HQ; ++hq) {
+      acc[hq][g] = mfma4<0, 0, 4 + (2 * m) % 4>(a0, qB[hq][(2 * m) / 4], acc[hq][g]);
+      acc[hq][g] = mfma4<0, 0, 4 + (2 * m + 1) % 4>(a1, qB[hq][(2 * m + 1) / 4], acc[hq][g]);
+    }
+  });
+
+  // ---- dead tokens (outside [start_k, kv_len)): score -inf, value scale / bias 0
+  const int t0 = tok_base + 4 * (lane >> 2);
+  bool live[4] = {true, true, true, true};
+  if (!full) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) live[i] = t0 + i >= start_k && t0 + i < kv_len;
+#pragma unroll
+    for (int w = 0; w < 2; ++w) {
+      const uint32_t keep = (live[2 * w] ? 0x0000FFFFu : 0u) | (live[2 * w + 1] ? 0xFFFF0000u : 0u);
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        L.s[2][g][w] &= keep;
+        L.s[3][g][w] &= keep;
+      }
+    }
+  }
+
+#pragma unroll
+  for (int hq = 0; hq < HQ; ++hq) {
+    float sc[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float v = 0.f;
+#pragma unroll
+      for (int g = 0; g < G; ++g) v = fmaf(acc[hq][g][i], half_of(L.s[0][g], i), fmaf(half_of(L.s[1][g], i), qs[hq][g], v));
+      sc[i] = live[i] ? v : -INFINITY;
+    }
+    // ---- online softmax in base 2 (scores scaled by sc_l2 = softmax_scale * log2(e) * 2^24)
+    const float tmax = head_max(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])));
+    const float m_new = fmaxf(st[hq].m, tmax * sc_l2);
+    if (__any(m_new != st[hq].m)) {
+      const float alpha = __builtin_amdgcn_exp2f(st[hq].m - m_new);  // lane's head; 0 while m is -inf
+      st[hq].l *= alpha;
+      st[hq].pb[0] *= alpha;
+      st[hq].pb[1] *= alpha;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {  // lane i holds head i of the quad
+        const float ai = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, alpha), i));
+        st[hq].o[0][i] *= ai;
+        st[hq].o[1][i] *= ai;
+      }
+      st[hq].m = m_new;
+    }
+    float p[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      p[i] = __builtin_amdgcn_exp2f(fmaf(sc[i], sc_l2, -st[hq].m));
+      st[hq].l += p[i];
+    }
+    // ---- O += P' V, P' = p * v_scale (elements 2, 3 of each quad / 16: their codes enter * 16)
+    h16x4 pv[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        st[hq].pb[g] = fmaf(p[i], half_of(L.s[3][g], i), st[hq].pb[g]);
+        pv[g][i] = (h16)((i < 2 ? p[i] : p[i] * 0.0625f) * half_of(L.s[2][g], i));
+      }
+    }
+    static_for<8>([&](auto Wd) {
+      constexpr int w = decltype(Wd)::value;  // V word w = tokens 8w .. 8w+7 of the item
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const uint32_t x = L.v[c][w];
+        const int g = (64 * c) / GS;
+        st[hq].o[c] = mfma4<4, 2 * w, 0>(pv[g], nib_pairs(x), st[hq].o[c]);
+        st[hq].o[c] = mfma4<4, 2 * w + 1, 0>(pv[g], nib_pairs(x >> 8), st[hq].o[c]);
+      }
+    });
+  }
+}
+
+#ifdef EMX_TIMELINE
+// Diagnostic build only: per-wave timestamps (100 MHz s_memrealtime) of the
+// decode phases, slot layout [wave][kTraceSlots].
+constexpr int kTraceSlots = 48;
+__device__ unsigned long long emx_trace[4096 * kTraceSlots];
+#define EMX_TS(slot)                                                                                \
+  do {                                                                                              \
+    const unsigned long long t_ = __builtin_amdgcn_s_memrealtime();                                 \
+    if (lane == 0 && W < 4096 && (slot) < kTraceSlots) emx_trace[W * kTraceSlots + (slot)] = t_;    \
+  } while (0)
+#else
+#define EMX_TS(slot) \
+  do {               \
+  } while (0)
+#endif
+
+// Work decomposition of decode_q4_d128.  The unit of work is a workgroup of
+// four waves; a workgroup item is TW = 64 * 4 / HQ consecutive tokens of one
+// (sequence, kv_head) unit, wave k taking head quad k % HQ of the 64-token
+// slice k / HQ.  Items are ordered unit-major; workgroup w of NWG takes the
+// contiguous range [w*I/NWG, (w+1)*I/NWG), so only the first and the last unit
+// of a range can be shared with other workgroups.
+//   * unit end: the waves' (o, m, l) of the unit are combined in LDS (one
+//     barrier); a unit inside the range is written to the output directly;
+//   * a shared unit leaves one fp32 partial per workgroup (slot = w + unit),
+//     written with device-coherent (SC1) stores; at the end of its range the
+//     workgroup waits for its stores, counts its arrival on the unit's
+//     counter, and the workgroup that arrives last merges the partials
+//     (page_attention.py:2006-2059) and resets the counter.
+template <int HG>
+struct Q4Geom {
+  static constexpr int HQ = (HG + 3) / 4;  // head quads (4 heads each, padded)
+  static constexpr int NSL = 4 / HQ;       // 64-token slices per workgroup item
+  static constexpr int TW = 64 * NSL;      // tokens per workgroup item
+  static_assert(HQ == 1 || HQ == 2 || HQ == 4, "GQA ratio 1, 2, 4, 8 or 16");
+};
+
+constexpr int kTableCache = 4096;  // block-table entries a workgroup keeps in LDS
+
+template <int GS, int HG>
+__global__ __launch_bounds__(256, 2) void decode_q4_d128(DecodeArgs a) {
+  using Geo = Q4Geom<HG>;
+  constexpr int HQ = Geo::HQ, NSL = Geo::NSL, TW = Geo::TW;
+  constexpr int D = 128, G = Q4Cfg<GS, 1>::G;
+#ifdef EMX_TIMELINE
+  const unsigned long long t_start = __builtin_amdgcn_s_memrealtime();
+#endif
+
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int quad = wv % HQ, slice = wv / HQ;
+  const int hl = 4 * quad + (lane & 3);  // head of this lane's query operand and scores
+
+  __shared__ int cum[kMaxSeqs + 1];
+  __shared__ int kvl[kMaxSeqs];
+  __shared__ int qrw[kMaxSeqs];
+  __shared__ float so[4][4][D];  // per wave: o * 2^24 + bias term of its 4 heads
+  __shared__ float sml[4][4][2];  // per wave: (m, l) of its 4 heads
+  __shared__ int slast[2];
+  // Block tables of up to kTableCache entries are read into LDS together with
+  // kv_lens (one memory round trip for both), larger ones from global memory.
+  __shared__ int sbt[kTableCache];
+  const int nbt = a.S * a.max_blocks;
+  const bool bt_lds = nbt <= kTableCache;
+  int btv[kTableCache / 256];
+  if (bt_lds) {
+#pragma unroll
+    for (int k = 0; k < kTableCache / 256; ++k) {
+      const int i = threadIdx.x + 256 * k;
+      btv[k] = i < nbt ? a.block_tables[i] : -1;
+    }
+  }
+  seq_table(a, cum, kvl, qrw);
+  if (bt_lds) {
+#pragma unroll
+    for (int k = 0; k < kTableCache / 256; ++k) sbt[threadIdx.x + 256 * k] = btv[k];
+    __syncthreads();
+  }
+  {  // decoded sequences without a live token produce zeros (the reference's l == 0 case)
+    const int per_seq = a.Hq * D / 8;
+    for (int i = blockIdx.x * 256 + threadIdx.x; i < a.S * per_seq; i += gridDim.x * 256) {
+      const int si = i / per_seq;
+      if (kvl[si] >= 0 && cum[si + 1] == cum[si])
+        reinterpret_cast<u32x4*>(a.out)[(size_t)qrw[si] * per_seq + i % per_seq] = u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+
+  const int S = a.S, Hkv = a.Hkv;
+  const long long I = (long long)Hkv * cum[S];
+  const int NWG = (int)min((long long)gridDim.x, I);  // every range non-empty
+  const int wg = blockIdx.x;
+  if (wg >= NWG) return;
+  const long long g0 = ((long long)wg * I) / NWG;
+  const long long g1 = ((long long)(wg + 1) * I) / NWG;
+#ifdef EMX_TIMELINE
+  const int W = wg * 4 + wv;
+  if (lane == 0 && W < 4096) emx_trace[W * kTraceSlots + 0] = t_start;
+  EMX_TS(1);
+  int n_step = 0;
+  int npend_dbg = 0;  // unit ends seen (the first one is stamped in detail)
+#endif
+
+  // ---- item g -> (sequence, kv_head, item j of the unit)
+  auto seq_of = [&](long long g, int s_from) {  // first s >= s_from with Hkv*cum[s+1] > g
+    int si = s_from;
+    while (si + 1 < S && (long long)Hkv * cum[si + 1] <= g) ++si;
+    return si;
+  };
+  auto lo_of = [&](int si) { return (a.window > 0 ? max(0, kvl[si] - a.window) : 0) / TW; };
+  int s = 0;
+  for (int c = 0; c < S; c += 64) {
+    const int si = c + lane;
+    s += __builtin_popcountll(__ballot(si < S && (long long)Hkv * cum[si + 1] <= g0));
+  }
+  s = __builtin_amdgcn_readfirstlane(s);
+
+  // ---- page of this wave's slice for every item of the range, one item per lane
+  // (64 items per chunk); -1 where the slice holds no token below kv_len
+  auto blk_chunk = [&](long long gb) {
+    const long long g = gb + lane;
+    int b = -1;
+    if (g < g1) {
+      const int si = seq_of(g, s);
+      const int n = cum[si + 1] - cum[si];
+      const int jn = (int)(g - (long long)Hkv * cum[si]) % n;
+      const int t = (lo_of(si) + jn) * TW + 64 * slice;
+      if (t < kvl[si]) {
+        const size_t bi = (size_t)si * a.max_blocks + t / a.bs;
+        b = bt_lds ? sbt[bi] : a.block_tables[bi];
+      }
+    }
+    return b;
+  };
+  int blkv = blk_chunk(g0);
+
+  // ---- query operand of a unit (this wave's head quad).  Lane L (head 4*quad + L%4,
+  // 16-lane group n = L/16) holds, in VGPR pair r, the operand of k-step 4r + n: K word
+  // m = 2r + n/2, dims 8m + (n even ? {0,4,1,5} : {2,6,3,7}), the last two / 16.
+  const int n16 = lane >> 4;
+  const int qhalf = n16 & 1;
+  uint32_t qraw[8][2];
+  auto issue_q = [&](int seq, int kh) {
+    const uint32_t* qp = reinterpret_cast<const uint32_t*>(
+        a.q + ((size_t)qrw[seq] * a.Hq + (size_t)kh * HG + (hl < HG ? hl : 0)) * D);
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      const int m = 2 * r + (n16 >> 1);
+      qraw[r][0] = qp[4 * m + qhalf];      // dims 8m + 2*qhalf + {0, 1}
+      qraw[r][1] = qp[4 * m + qhalf + 2];  // dims 8m + 2*qhalf + {4, 5}
+    }
+  };
+  h16x4 qB[1][8];
+  float qs[1][2];
+  auto build_q = [&]() {
+    const bool ok = hl < HG;
+    float gsum[2] = {0.f, 0.f};
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      const int m = 2 * r + (n16 >> 1);
+      const h16 d0 = __builtin_bit_cast(h16, (uint16_t)(qraw[r][0] & 0xFFFFu));
+      const h16 d1 = __builtin_bit_cast(h16, (uint16_t)(qraw[r][0] >> 16));
+      const h16 d4 = __builtin_bit_cast(h16, (uint16_t)(qraw[r][1] & 0xFFFFu));
+      const h16 d5 = __builtin_bit_cast(h16, (uint16_t)(qraw[r][1] >> 16));
+      // element order (nibble 0,4 | 1,5) of the word pair; with qhalf the dims are offset by 2
+      const h16x4 v = {d0, d4, (h16)((float)d1 * 0.0625f), (h16)((float)d5 * 0.0625f)};
+      qB[0][r] = ok ? v : h16x4{(h16)0.f, (h16)0.f, (h16)0.f, (h16)0.f};
+      const float sum = ok ? ((float)d0 + (float)d1) + ((float)d4 + (float)d5) : 0.f;
+      if (G == 1 || (8 * m) / GS == 0)
+        gsum[0] += sum;
+      else
+        gsum[1] += sum;
+    }
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      float x = gsum[g];
+      x += __shfl_xor(x, 16, 64);
+      x += __shfl_xor(x, 32, 64);
+      qs[0][g] = x * (1.0f / kTwo24);  // bias term in the 2^-24 units of the MFMA output
+    }
+  };
+
+  int n_s = cum[s + 1] - cum[s];
+  int kvh, j;
+  {
+    const int r = (int)(g0 - (long long)Hkv * cum[s]);
+    kvh = r / n_s;
+    j = r % n_s;
+  }
+  issue_q(s, kvh);
+  int kv_len = kvl[s];
+  int start_k = a.window > 0 ? max(0, kv_len - a.window) : 0;
+  int it_lo = start_k / TW;
+  const float sc_l2 = a.scale_log2 * kTwo24;
+
+  // descriptors of this wave's slice at token t of page b (zero-size, reading nothing, when b is invalid)
+  auto tile_of = [&](int b, int kh, int t) {
+    const bool ok = (unsigned)b < (unsigned)a.nb;
+    const int off = (t & ~127) % a.bs;
+    const size_t ph = (size_t)(ok ? b : 0) * a.Hkv + kh;
+    const int RW = a.bs * 4 / 32;
+    TileRsrc r;
+    r.k = uniform_rsrc(a.kc + (ph * a.bs + off) * 16, ok ? 128 * 16 * 4 : 0);
+    r.v = uniform_rsrc(a.vc + ph * D * RW + (off / 64) * D * 8, ok ? (D * RW - (off / 64) * D * 8) * 4 : 0);
+    const h16* sp[4] = {a.ks, a.kb, a.vs, a.vb};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r.s[i] = uniform_rsrc(sp[i] + ph * G * a.bs + off, ok ? (G * a.bs - off) * 2 : 0);
+    return r;
+  };
+
+  // ---- first item's loads (its query is already in flight)
+  int tb = (it_lo + j) * TW + 64 * slice;
+  int blk = __builtin_amdgcn_readfirstlane(__builtin_amdgcn_readlane(blkv, 0));
+  Q4Loads<GS, 1> bufA, bufB;
+  q4_issue_loads(bufA, tile_of(blk, kvh, tb), (tb & 127) / 64, lane, a.bs);
+  build_q();
+
+  Q4State st[1];
+  auto reset = [&]() {
+    st[0].o[0] = f32x4{0.f, 0.f, 0.f, 0.f};
+    st[0].o[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    st[0].m = -INFINITY;
+    st[0].l = 0.f;
+    st[0].pb[0] = 0.f;
+    st[0].pb[1] = 0.f;
+  };
+  reset();
+  long long unit_first = (long long)Hkv * cum[s] + (long long)kvh * n_s;  // first item of the current unit
+
+  // shared units awaiting their arrival (at most the range's first and last unit)
+  int npend = 0;
+  int pend_u[2], pend_row[2], pend_kvh[2], pend_n[2];
+  long long pend_first[2];
+
+  auto step = [&](Q4Loads<GS, 1>& cur, Q4Loads<GS, 1>& nxt, const long long g) {
+    // ---- next item
+    int s1 = s, kvh1 = kvh, j1 = j + 1, n1 = n_s, kl1 = kv_len, lo1 = it_lo;
+    if (j1 == n_s) {
+      j1 = 0;
+      if (++kvh1 == Hkv) {
+        kvh1 = 0;
+        do {
+          ++s1;
+        } while (s1 < S && cum[s1 + 1] == cum[s1]);
+        if (s1 < S) {
+          n1 = cum[s1 + 1] - cum[s1];
+          kl1 = kvl[s1];
+          lo1 = (a.window > 0 ? max(0, kl1 - a.window) : 0) / TW;
+        }
+      }
+    }
+    const bool has_next = g + 1 < g1;
+    const bool unit_end = !has_next || s1 != s || kvh1 != kvh;
+    int blk1 = -1;
+    const int tb1 = (lo1 + j1) * TW + 64 * slice;
+    if (has_next) {
+      const int k1 = (int)(g + 1 - g0);
+      if ((k1 & 63) == 0) blkv = blk_chunk(g + 1);
+      blk1 = __builtin_amdgcn_readfirstlane(__builtin_amdgcn_readlane(blkv, k1 & 63));
+    }
+    // The next unit's query first: loads return in order, so building its
+    // operand at this unit's end does not wait for the next item's pages.
+    if (has_next && unit_end) issue_q(s1, kvh1);
+    // Issued on every path (an empty descriptor returns zeros without touching
+    // memory), so the wait before this item's compute leaves them in flight.
+    q4_issue_loads(nxt, tile_of(blk1, kvh1, tb1), (tb1 & 127) / 64, lane, a.bs);
+
+    // ---- compute this wave's slice of the item (skipped when it holds no live
+    // token, or its page is invalid, like the reference's Metal kernel)
+#ifdef EMX_TIMELINE
+    if (n_step == 0) EMX_TS(2);
+    __builtin_amdgcn_s_waitcnt(0x4F70);  // vmcnt(16): this item's loads done
+    EMX_TS(3 + 3 * min(n_step, 14));
+#endif
+    if ((unsigned)blk < (unsigned)a.nb && tb + 64 > start_k) {
+      const bool full = tb >= start_k && tb + 64 <= kv_len;
+      q4_compute<GS, 1>(cur, full, lane, tb, start_k, kv_len, qB, qs, sc_l2, st);
+    }
+#ifdef EMX_TIMELINE
+    EMX_TS(4 + 3 * min(n_step, 14));
+#endif
+
+    // ---- unit finished (or range ends): combine the waves in LDS, then output / partial
+    if (unit_end) {
+      const bool whole = unit_first >= g0 && unit_first + n_s <= g1;
+      const int u = s * Hkv + kvh;
+      {
+        const float l = head_sum(st[0].l);
+        float pbs[2];
+#pragma unroll
+        for (int g = 0; g < G; ++g) pbs[g] = head_sum(st[0].pb[g]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {  // lane i holds head i's sums
+#pragma unroll
+          for (int c = 0; c < 2; ++c) {
+            const float pbi =
+                __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pbs[(64 * c) / GS]), i));
+            so[wv][i][64 * c + lane] = st[0].o[c][i] * kTwo24 + pbi;
+          }
+        }
+        if (lane < 4) {
+          sml[wv][lane][0] = st[0].m;
+          sml[wv][lane][1] = l;
+        }
+      }
+#ifdef EMX_TIMELINE
+      if (npend_dbg == 0) EMX_TS(20);
+#endif
+      __syncthreads();
+#ifdef EMX_TIMELINE
+      if (npend_dbg == 0) EMX_TS(21);
+#endif
+      PieceInfo pi;
+      if (!whole) pi = piece_info<HG>(a, wg, u, unit_first, n_s, I, NWG);
+      const int row = qrw[s];
+      for (int e = threadIdx.x; e < HG * D; e += 256) {
+        const int h = e / D, d = e % D, q = h / 4, i = h % 4;
+        float M = -INFINITY;
+#pragma unroll
+        for (int sl = 0; sl < NSL; ++sl) M = fmaxf(M, sml[q + HQ * sl][i][0]);
+        float O = 0.f, L = 0.f;
+#pragma unroll
+        for (int sl = 0; sl < NSL; ++sl) {
+          const float m = sml[q + HQ * sl][i][0];
+          const float f = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - M);
+          O = fmaf(f, so[q + HQ * sl][i][d], O);
+          L = fmaf(f, sml[q + HQ * sl][i][1], L);
+        }
+        if (whole) {
+          a.out[((size_t)row * a.Hq + (size_t)kvh * HG + h) * D + d] = (h16)(L > 0.f ? O / L : 0.f);
+        } else {
+          __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, O), pi.ro, (h * D + d) * 4,
+                                                pi.me * HG * D * 4, kCoherent);
+          if (d == 0)
+            __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, f32x2{M, L}), pi.rm, h * 8,
+                                                  pi.me * HG * 8, kCoherent);
+        }
+      }
+#ifdef EMX_TIMELINE
+      if (npend_dbg == 0) EMX_TS(22);
+#endif
+      __syncthreads();  // the LDS slots are rewritten at the next unit end
+#ifdef EMX_TIMELINE
+      if (npend_dbg == 0) EMX_TS(23);
+#endif
+      if (!whole) {
+        pend_u[npend] = u;
+        pend_row[npend] = row;
+        pend_kvh[npend] = kvh;
+        pend_n[npend] = n_s;
+        pend_first[npend] = unit_first;
+        ++npend;
+      }
+#ifdef EMX_TIMELINE
+      EMX_TS(5 + 3 * min(n_step, 14));
+#endif
+      reset();
+      if (has_next) {
+        unit_first = g + 1;
+        build_q();
+#ifdef EMX_TIMELINE
+        if (npend_dbg == 0) EMX_TS(24);
+#endif
+      }
+#ifdef EMX_TIMELINE
+      ++npend_dbg;
+#endif
+    }
+
+    // ---- advance
+    if (s1 != s) {
+      kv_len = kl1;
+      start_k = a.window > 0 ? max(0, kv_len - a.window) : 0;
+    }
+    s = s1;
+    kvh = kvh1;
+    j = j1;
+    n_s = n1;
+    it_lo = lo1;
+    tb = tb1;
+    blk = blk1;
+#ifdef EMX_TIMELINE
+    ++n_step;
+#endif
+  };
+  for (long long g = g0; g < g1; g += 2) {
+    step(bufA, bufB, g);
+    if (g + 1 >= g1) break;
+    step(bufB, bufA, g + 1);
+  }
+
+  // ---- arrivals of the shared units; the last workgroup to arrive merges
+  if (npend > 0) {
+    __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores are complete ...
+#ifdef EMX_TIMELINE
+    EMX_TS(40);
+#endif
+    __syncthreads();                // ... and so are the workgroup's
+#ifdef EMX_TIMELINE
+    EMX_TS(41);
+#endif
+    if (threadIdx.x < npend) {  // one thread per shared unit: both arrivals in flight together
+      const int p = threadIdx.x;
+      const int np = piece_count(pend_first[p], pend_n[p], I, NWG);
+      const int old = __hip_atomic_fetch_add(a.ws_cnt + pend_u[p], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const bool last = old == np - 1;
+      if (last) __hip_atomic_store(a.ws_cnt + pend_u[p], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      slast[p] = last;
+    }
+    __syncthreads();
+#ifdef EMX_TIMELINE
+    EMX_TS(42);
+    if (lane == 0 && W < 4096) emx_trace[W * kTraceSlots + 43] = (unsigned long long)(npend * 10 + slast[0] + 2 * (npend > 1 ? slast[1] : 0));
+#endif
+    // Merge: thread t owns outputs e = t + 256k of the unit's HG*D values; the
+    // loads of both units and of a batch of MB pieces are in flight together.
+    constexpr int KS = (HG * D + 255) / 256;
+    constexpr int MB = HG <= 4 ? 8 : (HG == 8 ? 4 : 2);
+    bool mg[2] = {slast[0] != 0, npend > 1 && slast[1] != 0};
+    PieceInfo pm[2];
+    int nbat[2] = {0, 0};
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      if (mg[p]) {
+        pm[p] = piece_info<HG>(a, wg, pend_u[p], pend_first[p], pend_n[p], I, NWG);
+        nbat[p] = (pm[p].np + MB - 1) / MB;
+      }
+    }
+    float M[2][KS], L[2][KS], O[2][KS];
+#pragma unroll
+    for (int p = 0; p < 2; ++p)
+#pragma unroll
+      for (int k = 0; k < KS; ++k) M[p][k] = -INFINITY, L[p][k] = 0.f, O[p][k] = 0.f;
+    for (int b = 0; b < max(nbat[0], nbat[1]); ++b) {
+      float o[2][KS][MB];
+      f32x2 ml[2][KS][MB];
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        if (b >= nbat[p]) continue;
+#pragma unroll
+        for (int k = 0; k < KS; ++k) {
+          const int e = min((int)threadIdx.x + 256 * k, HG * D - 1);
+#pragma unroll
+          for (int c = 0; c < MB; ++c) {
+            const int pc = min(b * MB + c, pm[p].np - 1);
+            o[p][k][c] = __builtin_bit_cast(
+                float, __builtin_amdgcn_raw_buffer_load_b32(pm[p].ro, e * 4, pc * HG * D * 4, kCoherent));
+            ml[p][k][c] = __builtin_bit_cast(
+                f32x2, __builtin_amdgcn_raw_buffer_load_b64(pm[p].rm, (e / D) * 8, pc * HG * 8, kCoherent));
+          }
+        }
+      }
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        if (b >= nbat[p]) continue;
+#pragma unroll
+        for (int k = 0; k < KS; ++k) {
+#pragma unroll
+          for (int c = 0; c < MB; ++c) {
+            const f32x2 x = ml[p][k][c];
+            if (b * MB + c >= pm[p].np || x.x == -INFINITY) continue;  // a piece may hold no live token
+            const float Mn = fmaxf(M[p][k], x.x);
+            const float fo = __builtin_amdgcn_exp2f(M[p][k] - Mn);  // 0 while M is -inf
+            const float fp = __builtin_amdgcn_exp2f(x.x - Mn);
+            O[p][k] = O[p][k] * fo + o[p][k][c] * fp;
+            L[p][k] = L[p][k] * fo + x.y * fp;
+            M[p][k] = Mn;
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      if (!mg[p]) continue;
+      h16* out = a.out + ((size_t)pend_row[p] * a.Hq + (size_t)pend_kvh[p] * HG) * D;
+#pragma unroll
+      for (int k = 0; k < KS; ++k) {
+        const int e = threadIdx.x + 256 * k;
+        if (e < HG * D) out[e] = (h16)(L[p][k] > 0.f ? O[p][k] / L[p][k] : 0.f);
+      }
+    }
+  }
+#ifdef EMX_TIMELINE
+  EMX_TS(47);
+  if (lane == 0 && W < 4096) emx_trace[W * kTraceSlots + 46] = (unsigned long long)n_step;
+#endif
+}
+
+}  // namespace emx

@@ -13,6 +13,7 @@
 #include "decode_affine.hpp"
 #include "paged_generic.hpp"
 #include "prefill_affine.hpp"
+#include "decode_q4.hpp"
 #include "quantize.hpp"
 
 namespace {
@@ -58,6 +59,10 @@ int device_cus() {
 }
 
 int decode_num_waves() { return device_cus() * 4 * decode_waves_per_simd(); }
+// The 4-bit kernel runs two four-wave workgroups per CU.
+int decode_q4_num_waves() { return device_cus() * 8; }
+// Partial slots are sized for the larger of the two persistent grids.
+int decode_max_waves() { return std::max(decode_num_waves(), decode_q4_num_waves()); }
 
 // Unit counters, then per-group counters indexed by partial slot (< kMaxWaves + kMaxUnits).
 constexpr size_t kCounterInts = 2 * (size_t)emx::kMaxUnits + emx::kMaxWaves;
@@ -82,6 +87,31 @@ DecodeFn pick_decode_hg(int hg) {
     case 8: if constexpr (8 * G <= 16) return emx::decode_affine_d128<BITS, GS, 8>; else return nullptr;
     case 16: if constexpr (16 * G <= 16) return emx::decode_affine_d128<BITS, GS, 16>; else return nullptr;
   }
+  return nullptr;
+}
+
+// 4-bit pages, group 64 / 128, GQA ratio 1, 2, 4 or 16: the 4x4x4 MFMA decode kernel.
+// EMX_DECODE_16X16=1 selects the 16x16x32 kernel instead (comparisons).
+template <int GS>
+DecodeFn pick_decode_q4_hg(int hg) {
+  switch (hg) {
+    case 1: return emx::decode_q4_d128<GS, 1>;
+    case 2: return emx::decode_q4_d128<GS, 2>;
+    case 4: return emx::decode_q4_d128<GS, 4>;
+    // GQA 8 with groups of 64 fills all 16 columns of the 16x16x32 kernel, which is faster there
+    case 16: return emx::decode_q4_d128<GS, 16>;
+  }
+  return nullptr;
+}
+
+DecodeFn pick_decode_q4(int gs, int hg) {
+  static const bool off = [] {
+    const char* e = std::getenv("EMX_DECODE_16X16");
+    return e && std::atoi(e) == 1;
+  }();
+  if (off) return nullptr;
+  if (gs == 64) return pick_decode_q4_hg<64>(hg);
+  if (gs == 128) return pick_decode_q4_hg<128>(hg);
   return nullptr;
 }
 
@@ -241,8 +271,8 @@ size_t emx_paged_workspace_bytes(int num_seqs, int num_q_heads, int num_kv_heads
       (long)num_seqs * num_kv_heads > emx::kMaxUnits)
     return 0;
   const int hg = num_q_heads / num_kv_heads;
-  const size_t slots = (size_t)decode_num_waves() + (size_t)num_seqs * num_kv_heads;
-  if (decode_num_waves() > emx::kMaxWaves) return 0;
+  const size_t slots = (size_t)decode_max_waves() + (size_t)num_seqs * num_kv_heads;
+  if (decode_max_waves() > emx::kMaxWaves) return 0;
   // arrival counters at a fixed offset (so every call finds them zeroed), then the partials
   return kCounterInts * sizeof(int) + slots * hg * (head_dim + 2) * sizeof(float);
 }
@@ -316,7 +346,12 @@ int emx_paged_attention_affine(const void* queries, int num_tokens, int num_q_he
       hipLaunchKernelGGL(pf, dim3((unsigned)grid), dim3(256), 0, st, p);
       if (int r = check_launch("prefill_affine_d128")) return r;
     }
-    const int nw = decode_num_waves();
+    DecodeFn fn = bits == 4 ? pick_decode_q4(group_size, hg) : nullptr;
+    const bool q4 = fn != nullptr;
+    const int nw = q4 ? decode_q4_num_waves() : decode_num_waves();
+    if (!fn) fn = bits == 4 ? pick_decode_gs<4>(group_size, hg) : pick_decode_gs<8>(group_size, hg);
+    if (!fn)
+      return fail(EMX_ERR_UNSUPPORTED, "no decode kernel for bits=%d group_size=%d gqa=%d", bits, group_size, hg);
     emx::DecodeArgs a;
     a.q = reinterpret_cast<const emx::h16*>(queries);
     a.kc = k_codes;
@@ -329,7 +364,7 @@ int emx_paged_attention_affine(const void* queries, int num_tokens, int num_q_he
     a.kv_lens = kv_lens;
     a.qsl = single_token_decode ? nullptr : query_start_loc;
     a.out = reinterpret_cast<emx::h16*>(out);
-    const size_t slots = (size_t)nw + (size_t)num_seqs * num_kv_heads;
+    const size_t slots = (size_t)decode_max_waves() + (size_t)num_seqs * num_kv_heads;
     a.ws_cnt = reinterpret_cast<int*>(workspace);
     a.ws_cnt_grp = a.ws_cnt + emx::kMaxUnits;
     a.ws_o = reinterpret_cast<float*>(a.ws_cnt + kCounterInts);
@@ -343,10 +378,8 @@ int emx_paged_attention_affine(const void* queries, int num_tokens, int num_q_he
     a.scale_log2 = scale_log2;
     a.window = window;
     a.num_waves = nw;
-    a.nt = bits == 4 ? 64 : 32;
-    DecodeFn fn = bits == 4 ? pick_decode_gs<4>(group_size, hg) : pick_decode_gs<8>(group_size, hg);
-    if (!fn)
-      return fail(EMX_ERR_UNSUPPORTED, "no decode kernel for bits=%d group_size=%d gqa=%d", bits, group_size, hg);
+    // tokens per work item: per wave (16x16 kernel) or per workgroup (4-bit kernel)
+    a.nt = q4 ? 64 * (4 / ((hg + 3) / 4)) : bits == 4 ? 64 : 32;
     hipLaunchKernelGGL(fn, dim3((unsigned)(nw / 4)), dim3(256), 0, st, a);
     return check_launch("decode_affine_d128");
   }
@@ -446,3 +479,13 @@ int emx_paged_attention_dense(const void* queries, int num_tokens, int num_q_hea
 }
 
 }  // extern "C"
+
+#ifdef EMX_TIMELINE
+extern "C" int emx_trace_read(void* host, size_t bytes) {
+  return hipMemcpyFromSymbol(host, HIP_SYMBOL(emx::emx_trace), bytes) == hipSuccess ? 0 : 1;
+}
+extern "C" int emx_trace_clear() {
+  static unsigned long long zeros[4096 * emx::kTraceSlots];
+  return hipMemcpyToSymbol(HIP_SYMBOL(emx::emx_trace), zeros, sizeof(zeros)) == hipSuccess ? 0 : 1;
+}
+#endif

@@ -66,7 +66,7 @@ struct AffineKV {
     constexpr int PW = 32 / BITS;
     const size_t ph = (size_t)blk * Hkv + h;
     const uint32_t w = vc[v_word_index<BITS>(ph, off, d, D, bs)];
-    const float q = (float)((w >> ((off % PW) * BITS)) & ((1u << BITS) - 1u));
+    const float q = (float)((w >> v_shift<BITS>(off % PW)) & ((1u << BITS) - 1u));
     const size_t si = (ph * (D / gs) + d / gs) * bs + off;
     return (float)vs[si] * q + (float)vb[si];
   }

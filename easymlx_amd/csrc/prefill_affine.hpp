@@ -348,10 +348,10 @@ __global__ __launch_bounds__(256, 2) void prefill_affine_d128(PrefillArgs a) {
           h16x8 pB;
 #pragma unroll
           for (int i = 0; i < 8; ++i) {
-            const int j = 8 * w + slot_perm<BITS>(i);
+            const int j = 8 * w + i;  // unpacked value element i is token i of the word
             const float p = sc[ct][j >> 2][j & 3];
-            pB[i] = (h16)(p * (float)vs8[slot_perm<BITS>(i)]);
-            pb[ct][g] = fmaf(p, (float)vb8[slot_perm<BITS>(i)], pb[ct][g]);
+            pB[i] = (h16)(p * (float)vs8[i]);
+            pb[ct][g] = fmaf(p, (float)vb8[i], pb[ct][g]);
           }
 #pragma unroll
           for (int e = 0; e < DTG; ++e) acc[ct][g * DTG + e] = mfma16x16x32(Av[e], pB, acc[ct][g * DTG + e]);

@@ -199,7 +199,7 @@ __global__ __launch_bounds__(256) void affine_cache_write(WriteArgs a) {
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
           const float v = (float)sval[1][tb + k][d];
-          word |= affine_code(v, sp[1][tb + k][g][0], sp[1][tb + k][g][1], n_bins) << (4 * k);
+          word |= affine_code(v, sp[1][tb + k][g][0], sp[1][tb + k][g][1], n_bins) << v_shift<4>(k);
         }
         const size_t ph = (size_t)(s0 / a.bs) * a.Hkv + h;
         a.vc[v_word_index<4>(ph, s0 % a.bs, d, a.D, a.bs)] = word;
@@ -212,7 +212,7 @@ __global__ __launch_bounds__(256) void affine_cache_write(WriteArgs a) {
           const uint32_t code = affine_code(v, sp[1][t][g][0], sp[1][t][g][1], n_bins);
           const size_t ph = (size_t)(sl / a.bs) * a.Hkv + h;
           uint32_t* wp = a.vc + v_word_index<4>(ph, sl % a.bs, d, a.D, a.bs);
-          const int sh = (sl % 8) * 4;
+          const int sh = v_shift<4>(sl % 8);
           atomicAnd(wp, ~(0xFu << sh));
           atomicOr(wp, code << sh);
         }
@@ -318,7 +318,7 @@ __global__ __launch_bounds__(256) void affine_cache_write_small(WriteArgs a) {
     const uint32_t code = affine_code(v, sp[1][t][0], sp[1][t][1], n_bins);
     const size_t ph = (size_t)(sl / a.bs) * a.Hkv + h;
     uint32_t* wp = a.vc + v_word_index<BITS>(ph, sl % a.bs, d, a.D, a.bs);
-    const int sh = (sl % PW) * BITS;
+    const int sh = v_shift<BITS>(sl % PW);
     constexpr uint32_t M = (1u << BITS) - 1u;
     if (BITS == 8) {
       reinterpret_cast<uint8_t*>(wp)[sl % 4] = (uint8_t)code;

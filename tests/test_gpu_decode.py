@@ -32,6 +32,12 @@ CASES = [
     (8, 128, 16, 16, (1, 300), 4),
     (4, 64, 64, 8, (3000, 5000), 2),
     (8, 32, 8, 2, (129, 129), 3),
+    # 4-bit on the 4x4x4 kernel: GQA 1, 2, 16 and groups 64 / 128
+    (4, 64, 8, 8, (1, 700), 4),
+    (4, 128, 16, 8, (60, 3000), 5),
+    (4, 64, 64, 4, (200, 2500), 3),
+    # many short sequences: workgroup ranges spanning many whole units
+    (4, 64, 32, 8, (1, 300), 96),
 ]
 
 

@@ -97,15 +97,21 @@ def test_layout_round_trips(bits):
     t = min(bs, 256 // bits)
     assert vp.shape == (nb, hkv, bs // t, d, t * bits // 32)
     np.testing.assert_array_equal(layout.value_logical_from_pages(vp, bits), c)
-    # value tile word w of dim j holds tokens w*per .. w*per+per-1 of that tile and dim, low bits first
+    # value tile word w of dim j holds tokens w*per .. w*per+per-1 of that tile and dim:
+    # 8-bit in byte order, 4-bit with token k at nibble (k >> 1) | ((k & 1) << 2)
     per = 32 // bits
     from oracle.affine import unpack_codes
 
     q = unpack_codes(c, bits)  # [nb, bs, hkv, d]
-    assert (vp[1, 1, 0, 5, 0] & ((1 << bits) - 1)) == q[1, 0, 1, 5]
-    assert (int(vp[1, 1, 0, 5, 0]) >> (bits * (per - 1))) == q[1, per - 1, 1, 5]
+    shift = (lambda k: 4 * ((k >> 1) | ((k & 1) << 2))) if bits == 4 else (lambda k: 8 * k)
+    m = (1 << bits) - 1
+    for k in range(per):
+        assert (int(vp[1, 1, 0, 5, 0]) >> shift(k)) & m == q[1, k, 1, 5]
+    if bits == 4:
+        assert (int(vp[1, 1, 0, 5, 0]) >> 4) & m == q[1, 2, 1, 5]   # nibble 1 holds token 2
+        assert (int(vp[1, 1, 0, 5, 0]) >> 16) & m == q[1, 1, 1, 5]  # nibble 4 holds token 1
     if bs // t > 1:
-        assert (vp[2, 0, 1, 7, 1] & ((1 << bits) - 1)) == q[2, t + per, 0, 7]
+        assert (vp[2, 0, 1, 7, 1] & m) == q[2, t + per, 0, 7]
     sp = layout.params_pages_from_logical(s)
     assert sp.shape == (nb, hkv, d // gs, bs) and sp[2, 1, 1, 7] == s[2, 7, 1, 1]
     np.testing.assert_array_equal(layout.params_logical_from_pages(sp), s)
