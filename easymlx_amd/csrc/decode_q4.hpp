@@ -88,12 +88,17 @@ template <int GS, int HQ>
 __device__ __forceinline__ void q4_issue_loads(Q4Loads<GS, HQ>& L, const TileRsrc& rs, const int it, const int lane,
                                                const int bs) {
   constexpr int G = Q4Cfg<GS, HQ>::G;
+#ifndef EMX_EXP_NOK
 #pragma unroll
   for (int v = 0; v < 4; ++v) {
     const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(rs.k, lane * 64 + 16 * v, it * 64 * 64, kLoadAux);
 #pragma unroll
     for (int e = 0; e < 4; ++e) L.k[4 * v + e] = x[e];
   }
+#else
+  for (int v = 0; v < 16; ++v) L.k[v] = lane * v;
+#endif
+#ifndef EMX_EXP_NOV
 #pragma unroll
   for (int c = 0; c < 2; ++c) {
 #pragma unroll
@@ -104,6 +109,32 @@ __device__ __forceinline__ void q4_issue_loads(Q4Loads<GS, HQ>& L, const TileRsr
       for (int e = 0; e < 4; ++e) L.v[c][4 * v + e] = x[e];
     }
   }
+#else
+  for (int c = 0; c < 2; ++c)
+    for (int v = 0; v < 8; ++v) L.v[c][v] = lane * v + c;
+#endif
+#ifdef EMX_EXP_NOSCALE
+  for (int arr = 0; arr < 4; ++arr)
+    for (int g = 0; g < G; ++g) L.s[arr][g][0] = L.s[arr][g][1] = 0x3c003c00u;
+  return;
+#endif
+#ifdef EMX_EXP_SCALE1  // timing experiment: one 16-byte load per lane for all scales
+  {
+    const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(rs.s[0], lane * 16, it * 64 * 2, kLoadAux);
+    for (int arr = 0; arr < 4; ++arr)
+      for (int g = 0; g < G; ++g) { L.s[arr][g][0] = x[(arr + g) & 3]; L.s[arr][g][1] = x[(arr + g + 1) & 3]; }
+    return;
+  }
+#endif
+#ifdef EMX_EXP_SCALE4  // timing experiment: four 16-byte loads per lane
+  {
+    for (int arr = 0; arr < 4; ++arr) {
+      const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(rs.s[arr], (lane >> 2) * 16, it * 64 * 2, kLoadAux);
+      for (int g = 0; g < G; ++g) { L.s[arr][g][0] = x[2 * g]; L.s[arr][g][1] = x[2 * g + 1]; }
+    }
+    return;
+  }
+#endif
   const int ls = (lane >> 2) * 8;
 #pragma unroll
   for (int arr = 0; arr < 4; ++arr) {
@@ -295,8 +326,15 @@ __global__ __launch_bounds__(256, 2) void decode_q4_d128(DecodeArgs a) {
   __shared__ int cum[kMaxSeqs + 1];
   __shared__ int kvl[kMaxSeqs];
   __shared__ int qrw[kMaxSeqs];
-  __shared__ float so[4][4][D];  // per wave: o * 2^24 + bias term of its 4 heads
-  __shared__ float sml[4][4][2];  // per wave: (m, l) of its 4 heads
+  __shared__ float so[2][4][4][D];  // two slot sets; per wave: o * 2^24 + bias term of its 4 heads
+  __shared__ float sml[2][4][4][2];  // per wave: (m, l) of its 4 heads
+  __shared__ int scnt[2];            // waves arrived at the set's current unit end
+  __shared__ int sgen[2];            // last unit end whose combine on the set completed
+  if (threadIdx.x == 0) {
+    scnt[0] = scnt[1] = 0;
+    sgen[0] = -2;
+    sgen[1] = -1;
+  }
   __shared__ int slast[2];
   // Block tables of up to kTableCache entries are read into LDS together with
   // kv_lens (one memory round trip for both), larger ones from global memory.
@@ -327,7 +365,10 @@ __global__ __launch_bounds__(256, 2) void decode_q4_d128(DecodeArgs a) {
   }
 
   const int S = a.S, Hkv = a.Hkv;
-  const long long I = (long long)Hkv * cum[S];
+  // LDS table entries read at a wave-uniform index are moved to SGPRs (uru), so the
+  // per-item scheduling arithmetic stays scalar
+  auto uru = [](int v) { return __builtin_amdgcn_readfirstlane(v); };
+  const long long I = (long long)Hkv * uru(cum[S]);
   const int NWG = (int)min((long long)gridDim.x, I);  // every range non-empty
   const int wg = blockIdx.x;
   if (wg >= NWG) return;
@@ -340,6 +381,8 @@ __global__ __launch_bounds__(256, 2) void decode_q4_d128(DecodeArgs a) {
   int n_step = 0;
   int npend_dbg = 0;  // unit ends seen (the first one is stamped in detail)
 #endif
+
+  const int bs_log2 = __builtin_ctz(a.bs);
 
   // ---- item g -> (sequence, kv_head, item j of the unit)
   auto seq_of = [&](long long g, int s_from) {  // first s >= s_from with Hkv*cum[s+1] > g
@@ -366,13 +409,16 @@ __global__ __launch_bounds__(256, 2) void decode_q4_d128(DecodeArgs a) {
       const int jn = (int)(g - (long long)Hkv * cum[si]) % n;
       const int t = (lo_of(si) + jn) * TW + 64 * slice;
       if (t < kvl[si]) {
-        const size_t bi = (size_t)si * a.max_blocks + t / a.bs;
+        const size_t bi = (size_t)si * a.max_blocks + (t >> bs_log2);
         b = bt_lds ? sbt[bi] : a.block_tables[bi];
       }
     }
     return b;
   };
   int blkv = blk_chunk(g0);
+#ifdef EMX_TIMELINE
+  EMX_TS(25);
+#endif
 
   // ---- query operand of a unit (this wave's head quad).  Lane L (head 4*quad + L%4,
   // 16-lane group n = L/16) holds, in VGPR pair r, the operand of k-step 4r + n: K word
@@ -382,7 +428,7 @@ __global__ __launch_bounds__(256, 2) void decode_q4_d128(DecodeArgs a) {
   uint32_t qraw[8][2];
   auto issue_q = [&](int seq, int kh) {
     const uint32_t* qp = reinterpret_cast<const uint32_t*>(
-        a.q + ((size_t)qrw[seq] * a.Hq + (size_t)kh * HG + (hl < HG ? hl : 0)) * D);
+        a.q + ((size_t)uru(qrw[seq]) * a.Hq + (size_t)kh * HG + (hl < HG ? hl : 0)) * D);
 #pragma unroll
     for (int r = 0; r < 8; ++r) {
       const int m = 2 * r + (n16 >> 1);
@@ -420,15 +466,15 @@ __global__ __launch_bounds__(256, 2) void decode_q4_d128(DecodeArgs a) {
     }
   };
 
-  int n_s = cum[s + 1] - cum[s];
+  int n_s = uru(cum[s + 1]) - uru(cum[s]);
   int kvh, j;
   {
-    const int r = (int)(g0 - (long long)Hkv * cum[s]);
+    const int r = (int)(g0 - (long long)Hkv * uru(cum[s]));
     kvh = r / n_s;
     j = r % n_s;
   }
   issue_q(s, kvh);
-  int kv_len = kvl[s];
+  int kv_len = uru(kvl[s]);
   int start_k = a.window > 0 ? max(0, kv_len - a.window) : 0;
   int it_lo = start_k / TW;
   const float sc_l2 = a.scale_log2 * kTwo24;
@@ -436,7 +482,7 @@ __global__ __launch_bounds__(256, 2) void decode_q4_d128(DecodeArgs a) {
   // descriptors of this wave's slice at token t of page b (zero-size, reading nothing, when b is invalid)
   auto tile_of = [&](int b, int kh, int t) {
     const bool ok = (unsigned)b < (unsigned)a.nb;
-    const int off = (t & ~127) % a.bs;
+    const int off = t & (a.bs - 1) & ~127;  // page sizes are powers of two here
     const size_t ph = (size_t)(ok ? b : 0) * a.Hkv + kh;
     const int RW = a.bs * 4 / 32;
     TileRsrc r;
@@ -453,7 +499,13 @@ __global__ __launch_bounds__(256, 2) void decode_q4_d128(DecodeArgs a) {
   int blk = __builtin_amdgcn_readfirstlane(__builtin_amdgcn_readlane(blkv, 0));
   Q4Loads<GS, 1> bufA, bufB;
   q4_issue_loads(bufA, tile_of(blk, kvh, tb), (tb & 127) / 64, lane, a.bs);
+#ifdef EMX_TIMELINE
+  EMX_TS(26);
+#endif
   build_q();
+#ifdef EMX_TIMELINE
+  EMX_TS(27);
+#endif
 
   Q4State st[1];
   auto reset = [&]() {
@@ -469,6 +521,7 @@ __global__ __launch_bounds__(256, 2) void decode_q4_d128(DecodeArgs a) {
 
   // shared units awaiting their arrival (at most the range's first and last unit)
   int npend = 0;
+  int nue = 0;  // unit ends passed (uniform across the workgroup)
   int pend_u[2], pend_row[2], pend_kvh[2], pend_n[2];
   long long pend_first[2];
 
@@ -481,10 +534,10 @@ __global__ __launch_bounds__(256, 2) void decode_q4_d128(DecodeArgs a) {
         kvh1 = 0;
         do {
           ++s1;
-        } while (s1 < S && cum[s1 + 1] == cum[s1]);
+        } while (s1 < S && uru(cum[s1 + 1]) == uru(cum[s1]));
         if (s1 < S) {
-          n1 = cum[s1 + 1] - cum[s1];
-          kl1 = kvl[s1];
+          n1 = uru(cum[s1 + 1]) - uru(cum[s1]);
+          kl1 = uru(kvl[s1]);
           lo1 = (a.window > 0 ? max(0, kl1 - a.window) : 0) / TW;
         }
       }
@@ -520,10 +573,20 @@ __global__ __launch_bounds__(256, 2) void decode_q4_d128(DecodeArgs a) {
     EMX_TS(4 + 3 * min(n_step, 14));
 #endif
 
-    // ---- unit finished (or range ends): combine the waves in LDS, then output / partial
+    // ---- unit finished (or range ends): the waves' (o, m, l) meet in LDS; the last
+    // wave to arrive combines them into the output or the workgroup's partial while
+    // the others go on.  Unit ends alternate between two slot sets; a wave reusing a
+    // set first waits for the combine of two unit ends back (done by a sibling wave
+    // that waits on nothing, so the wait ends).
     if (unit_end) {
       const bool whole = unit_first >= g0 && unit_first + n_s <= g1;
       const int u = s * Hkv + kvh;
+      const int par = nue & 1;
+      const int row = uru(qrw[s]);
+      if (nue >= 2) {
+        while (__hip_atomic_load(&sgen[par], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < nue - 2)
+          __builtin_amdgcn_s_sleep(1);
+      }
       {
         const float l = head_sum(st[0].l);
         float pbs[2];
@@ -535,54 +598,105 @@ __global__ __launch_bounds__(256, 2) void decode_q4_d128(DecodeArgs a) {
           for (int c = 0; c < 2; ++c) {
             const float pbi =
                 __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pbs[(64 * c) / GS]), i));
-            so[wv][i][64 * c + lane] = st[0].o[c][i] * kTwo24 + pbi;
+            so[par][wv][i][64 * c + lane] = st[0].o[c][i] * kTwo24 + pbi;
           }
         }
         if (lane < 4) {
-          sml[wv][lane][0] = st[0].m;
-          sml[wv][lane][1] = l;
+          sml[par][wv][lane][0] = st[0].m;
+          sml[par][wv][lane][1] = l;
         }
       }
 #ifdef EMX_TIMELINE
       if (npend_dbg == 0) EMX_TS(20);
 #endif
-      __syncthreads();
-#ifdef EMX_TIMELINE
-      if (npend_dbg == 0) EMX_TS(21);
-#endif
-      PieceInfo pi;
-      if (!whole) pi = piece_info<HG>(a, wg, u, unit_first, n_s, I, NWG);
-      const int row = qrw[s];
-      for (int e = threadIdx.x; e < HG * D; e += 256) {
-        const int h = e / D, d = e % D, q = h / 4, i = h % 4;
-        float M = -INFINITY;
+      int arrived = 0;
+      if (has_next) {
+        if (lane == 0) arrived = __hip_atomic_fetch_add(&scnt[par], 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
+        arrived = __builtin_amdgcn_readfirstlane(arrived);
+      } else {
+        // the range's last unit: every wave is done, so all four combine it together
+        __syncthreads();
+        PieceInfo pi;
+        if (!whole) pi = piece_info<HG>(a, wg, u, unit_first, n_s, I, NWG);
+        for (int e = threadIdx.x; e < HG * D; e += 256) {
+          const int h = e / D, d = e % D, q = h / 4, i = h % 4;
+          float M = -INFINITY;
 #pragma unroll
-        for (int sl = 0; sl < NSL; ++sl) M = fmaxf(M, sml[q + HQ * sl][i][0]);
-        float O = 0.f, L = 0.f;
+          for (int sl = 0; sl < NSL; ++sl) M = fmaxf(M, sml[par][q + HQ * sl][i][0]);
+          float O = 0.f, L = 0.f;
 #pragma unroll
-        for (int sl = 0; sl < NSL; ++sl) {
-          const float m = sml[q + HQ * sl][i][0];
-          const float f = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - M);
-          O = fmaf(f, so[q + HQ * sl][i][d], O);
-          L = fmaf(f, sml[q + HQ * sl][i][1], L);
-        }
-        if (whole) {
-          a.out[((size_t)row * a.Hq + (size_t)kvh * HG + h) * D + d] = (h16)(L > 0.f ? O / L : 0.f);
-        } else {
-          __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, O), pi.ro, (h * D + d) * 4,
-                                                pi.me * HG * D * 4, kCoherent);
-          if (d == 0)
-            __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, f32x2{M, L}), pi.rm, h * 8,
-                                                  pi.me * HG * 8, kCoherent);
+          for (int sl = 0; sl < NSL; ++sl) {
+            const float m = sml[par][q + HQ * sl][i][0];
+            const float f = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - M);
+            O = fmaf(f, so[par][q + HQ * sl][i][d], O);
+            L = fmaf(f, sml[par][q + HQ * sl][i][1], L);
+          }
+          if (whole) {
+            a.out[((size_t)row * a.Hq + (size_t)kvh * HG + h) * D + d] = (h16)(L > 0.f ? O / L : 0.f);
+          } else {
+            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, O), pi.ro, (h * D + d) * 4,
+                                                  pi.me * HG * D * 4, kCoherent);
+            if (d == 0)
+              __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, f32x2{M, L}), pi.rm, h * 8,
+                                                    pi.me * HG * 8, kCoherent);
+          }
         }
       }
 #ifdef EMX_TIMELINE
-      if (npend_dbg == 0) EMX_TS(22);
+      if (npend_dbg == 0) EMX_TS(21);
 #endif
-      __syncthreads();  // the LDS slots are rewritten at the next unit end
+      if (arrived == 3) {  // last of the four waves: combine
+        if (lane == 0) __hip_atomic_store(&scnt[par], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        PieceInfo pi;
+        if (!whole) pi = piece_info<HG>(a, wg, u, unit_first, n_s, I, NWG);
+        // per-head weights of the slices: lane h (< HG) computes them, every lane reads them back
+        float fw[NSL], Lh = 0.f, Mh = -INFINITY;
+        {
+          const int h = lane < HG ? lane : 0, q = h / 4, i = h % 4;
+#pragma unroll
+          for (int sl = 0; sl < NSL; ++sl) Mh = fmaxf(Mh, sml[par][q + HQ * sl][i][0]);
+#pragma unroll
+          for (int sl = 0; sl < NSL; ++sl) {
+            const float m = sml[par][q + HQ * sl][i][0];
+            fw[sl] = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - Mh);
+            Lh = fmaf(fw[sl], sml[par][q + HQ * sl][i][1], Lh);
+          }
+        }
+#pragma unroll
+        for (int h = 0; h < HG; ++h) {
+          const int q = h / 4, i = h % 4;
+          const float L = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, Lh), h));
+          const float M = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, Mh), h));
+          const float inv = L > 0.f ? 1.f / L : 0.f;
+#pragma unroll
+          for (int c = 0; c < 2; ++c) {
+            const int d = 64 * c + lane;
+            float O = 0.f;
+#pragma unroll
+            for (int sl = 0; sl < NSL; ++sl) {
+              const float f = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, fw[sl]), h));
+              O = fmaf(f, so[par][q + HQ * sl][i][d], O);
+            }
+            if (whole) {
+              a.out[((size_t)row * a.Hq + (size_t)kvh * HG + h) * D + d] = (h16)(O * inv);
+            } else {
+              __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, O), pi.ro, (h * D + d) * 4,
+                                                    pi.me * HG * D * 4, kCoherent);
+            }
+          }
+          if (!whole && lane == 0)
+            __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, f32x2{M, L}), pi.rm, h * 8,
+                                                  pi.me * HG * 8, kCoherent);
+        }
+        // the slot set may be rewritten once every lane's reads above are done
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+        if (lane == 0) __hip_atomic_store(&sgen[par], nue, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+      }
 #ifdef EMX_TIMELINE
+      if (npend_dbg == 0) EMX_TS(22);
       if (npend_dbg == 0) EMX_TS(23);
 #endif
+      ++nue;
       if (!whole) {
         pend_u[npend] = u;
         pend_row[npend] = row;

@@ -346,7 +346,8 @@ int emx_paged_attention_affine(const void* queries, int num_tokens, int num_q_he
       hipLaunchKernelGGL(pf, dim3((unsigned)grid), dim3(256), 0, st, p);
       if (int r = check_launch("prefill_affine_d128")) return r;
     }
-    DecodeFn fn = bits == 4 ? pick_decode_q4(group_size, hg) : nullptr;
+    // the 4-bit kernel addresses pages with shifts: power-of-two page sizes
+    DecodeFn fn = bits == 4 && (page_size & (page_size - 1)) == 0 ? pick_decode_q4(group_size, hg) : nullptr;
     const bool q4 = fn != nullptr;
     const int nw = q4 ? decode_q4_num_waves() : decode_num_waves();
     if (!fn) fn = bits == 4 ? pick_decode_gs<4>(group_size, hg) : pick_decode_gs<8>(group_size, hg);
