@@ -104,7 +104,7 @@ def cpu_baseline(wl, n_seqs: int | None):
 
 def measured_traffic():
     """HBM bytes per decode call from the committed counter summary (two rocprofv3 --pmc passes)."""
-    path = os.path.join(ROOT, "profiles", "decode_affine_c2_hbm_traffic.md")
+    path = os.path.join(ROOT, "profiles", "decode_q4_c2_hbm_traffic.md")
     try:
         for line in open(path):
             if line.startswith("TRAFFIC_BYTES_PER_CALL:"):
@@ -312,19 +312,23 @@ def main():
         st.call(i)
     warm(st.call, 1.0)
 
-    # ---- timed region: exactly `steps` decode calls
+    # ---- timed region: exactly `steps` decode calls, bracketed by HIP events on the launch stream
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
+    ev0.record()
     for i in range(args.steps):
         st.call(i)
+    ev1.record()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     ms_per_step = elapsed / args.steps * 1e3
+    call_us = ev0.elapsed_time(ev1) * 1e3 / args.steps  # device time per call, back to back
+    achieved = bytes_per_step / (call_us * 1e-6) / 1e9
 
-    # ---- per-call time with HIP events on the launch stream
+    # ---- per-call times with events around each call (includes each launch's dispatch gap)
     kt = event_us(st.call, min(args.steps, 200))
     k_avg_us = float(kt.mean())
-    achieved = bytes_per_step / (k_avg_us * 1e-6) / 1e9
 
     if args.copy_probe_mib:
         n = args.copy_probe_mib << 20
@@ -375,6 +379,7 @@ def main():
         "tokens_per_s_per_layer": round(wl.num_seqs / (ms_per_step * 1e-3), 1),
         "tokens_per_s_attention_32_layers": round(wl.num_seqs / (ms_per_step * 1e-3 * 32), 1),
         "us_per_layer_step": round(ms_per_step * 1e3, 3),
+        "call_us_back_to_back": round(call_us, 3),
         "kernel_us": {"mean": round(k_avg_us, 3), "p10": round(float(np.percentile(kt, 10)), 3),
                       "p50": round(float(np.percentile(kt, 50)), 3), "p90": round(float(np.percentile(kt, 90)), 3)},
         "roofline": {
@@ -385,7 +390,7 @@ def main():
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
             "traffic_source": traffic_src,
-            "kernel": "emx::decode_affine_d128<4,64,4> (one launch per decode call; split-K merge fused)",
+            "kernel": "emx::decode_q4_d128<64,4> (one launch per decode call; split-K merge fused)",
         },
         "cpu_baseline": cpu,
         "aux": aux,
