@@ -5,7 +5,7 @@
 // (lib/python/easymlx/operations/kernels/unified_attention.py:290-465, causal
 // limit :357-361, sliding window :369-376) and the single-sequence causal path
 // (page_attention.py:84-133).  Decode rows (one query token) of the same batch
-// go to decode_affine_d128.
+// go to the decode kernels (decode_q4_d128 / decode_affine_d128).
 //
 // Work: one workgroup (4 waves) per (sequence, kv_head, tile of 128/HG query
 // tokens); a wave owns 32 query columns = (token, head) pairs, head fastest.

@@ -10,12 +10,14 @@
  *   key codes    uint32 [num_blocks, Hkv, page_size, head_dim*bits/32]  token-major
  *   value codes  uint32 [num_blocks, Hkv, page_size/T, head_dim, T*bits/32]
  *                with T = min(page_size, 256/bits) tokens per tile, dim-major inside
- *                a tile (a word packs 32/bits consecutive tokens of one dim);
+ *                a tile (a word packs 32/bits consecutive tokens of one dim: 8-bit in
+ *                byte order, 4-bit with token k at nibble (k >> 1) | ((k & 1) << 2));
  *                page_size must be a multiple of T
  *   k/v scales   fp16   [num_blocks, Hkv, G, page_size]
  *   k/v biases   fp16   [num_blocks, Hkv, G, page_size]
- * Codes are packed little-endian (element j of a word at bits [j*bits,(j+1)*bits)),
- * value w = scale * code + bias, as produced by mlx.core.quantize(mode="affine").
+ * Key words are packed as MLX packs them (element j of a word at bits
+ * [j*bits,(j+1)*bits)); value w = scale * code + bias, with the codes, scales and
+ * biases of mlx.core.quantize(mode="affine").
  */
 #ifndef EMX_ATTN_H_
 #define EMX_ATTN_H_
