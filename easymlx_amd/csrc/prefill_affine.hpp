@@ -9,19 +9,24 @@
 //
 // Work: one workgroup (4 waves) per (sequence, kv_head, tile of 128/HG query
 // tokens); a wave owns 32 query columns = (token, head) pairs, head fastest.
-// Keys are walked in NT-token steps (64 at 4-bit, 32 at 8-bit) up to the tile's
-// causal limit; each step's K/V codes and scales are loaded once per workgroup
-// into LDS (double-buffered) and shared by the four waves.
-//
-// Arithmetic is exact in the codes, like the decode kernel: codes enter
-// v_mfma_f32_16x16x32_f16 as fp16 subnormals (code * 2^-24) and the affine
-// scale / bias are applied in fp32 afterwards.
-//   S^T: A = K codes (rows = keys; row rho of sub-tile a is key
-//        TPL*(rho/4) + 4a + rho%4), B = queries; MFMA w spans dims
-//        [32w, 32w+32), so each quantization group accumulates separately:
+// Keys are walked in NT-token steps (64 at 4-bit, 32 at 8-bit) up to the
+// tile's causal limit.  Per step, once per workgroup:
+//   * K/V codes and scales arrive in LDS (the next step's loads are in flight
+//     in registers meanwhile);
+//   * K codes are expanded into LDS as exact fp16 subnormals (code * 2^-24),
+//     K scales / biases converted to fp32;
+//   * V is dequantized into LDS as fp16 (v_scale * code + v_bias), dim-major,
+//     with the keys of each 32-key block in the order the PV B operand holds
+//     them.
+// Then each wave, on v_mfma_f32_16x16x32_f16:
+//   S^T: A = expanded K (rows = keys), B = queries; MFMA w spans dims
+//        [32w, 32w+32), so each quantization group accumulates separately and
+//        the scores stay exact in the codes:
 //          s = 2^24 * sum_g ks[t,g] C_g[t,c] + sum_g kb[t,g] * sum_{d in g} q[c,d]
-//   PV : A = V codes (rows = dims), B = p * vs[t, g] in fp16 for the dims of
-//        group g; sum_t p * vb[t, g] is accumulated in fp32.
+//   online softmax per column (base 2, fp32);
+//   O^T += V^T P^T with P in fp16.
+// Only V is rounded to fp16 before use; its error is relative to |v| and
+// stays inside the relative tolerance, while a rounded K would move scores.
 #pragma once
 
 #include "common.hpp"
@@ -46,19 +51,22 @@ struct PrefillArgs {
 
 template <int BITS, int GS, int HG>
 struct PrefillCfg {
-  using C = DecodeCfg<BITS, GS, 1>;
-  static constexpr int D = 128, G = C::G, NT = C::NT, TPL = C::TPL, NA = C::NA, NWS = C::NWS, W = C::W;
+  static constexpr int D = 128, G = D / GS;
+  static constexpr int NT = 256 / BITS;            // keys per step (64 at 4-bit, 32 at 8-bit)
+  static constexpr int NA = NT / 16;               // 16-key S^T sub-tiles per step
+  static constexpr int NKS = NT / 32;              // 32-key PV k-steps per step
+  static constexpr int W = D * BITS / 32;          // code words per key
   static constexpr int COLS = 32;                  // query columns per wave
   static constexpr int TOKW = COLS / HG;           // query tokens per wave
   static constexpr int TOKB = 4 * TOKW;            // query tokens per workgroup
-  static constexpr int KROW = W + 4;               // LDS words per key row (padded)
-  static constexpr int KBYTES = NT * KROW * 4;     // K codes of one step
-  static constexpr int VBYTES = 4096;              // V tile of one step
-  static constexpr int SBYTES = 4 * G * NT * 2;    // ks, kb, vs, vb of one step
-  static constexpr int BUF = KBYTES + VBYTES + SBYTES;
+  static constexpr int KSTR = D + 8;               // halves per expanded key row (padded)
+  static constexpr int VSTR = NT + 8;              // halves per dequantized value dim (padded)
+  static constexpr int RAWV = 4096;                // bytes of the step's V tile
+  static constexpr int RAWS = 4 * G * NT * 2;      // bytes of the step's ks, kb, vs, vb
   static constexpr int SEGS = 4 * G;               // contiguous scale segments per step
   static constexpr int SEGB = NT * 2;              // bytes per segment
   static_assert(COLS % HG == 0, "query columns per wave must hold whole tokens");
+  static_assert(W * NT == 1024, "a step's K codes are 4 KiB: one 16-byte piece per thread");
 };
 
 // Number of query-token tiles of sequence s (0 for decode rows and empty rows).
@@ -67,11 +75,15 @@ __device__ __forceinline__ int prefill_tiles(const PrefillArgs& a, const int s, 
   return ql > 1 ? (ql + tokb - 1) / tokb : 0;
 }
 
+// Position, inside its 32-key block, at which the dequantized value of key k
+// (0..31 within the block) is stored: the PV B operand of lane (col, kg) holds
+// keys kg*4 + {0..3} and 16 + kg*4 + {0..3} of the block, in that order.
+__device__ __forceinline__ constexpr int pv_slot(int k) { return 8 * ((k & 15) >> 2) + 4 * (k >> 4) + (k & 3); }
+
 template <int BITS, int GS, int HG>
 __global__ __launch_bounds__(256, 2) void prefill_affine_d128(PrefillArgs a) {
   using P = PrefillCfg<BITS, GS, HG>;
-  constexpr int D = P::D, G = P::G, NT = P::NT, TPL = P::TPL, NA = P::NA, NWS = P::NWS, W = P::W;
-  constexpr int KW = BITS;  // K words a lane reads per sub-tile (4 MFMAs x 32 dims)
+  constexpr int D = P::D, G = P::G, NT = P::NT, NA = P::NA, NKS = P::NKS, W = P::W;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -96,8 +108,9 @@ __global__ __launch_bounds__(256, 2) void prefill_affine_d128(PrefillArgs a) {
   const int kvh = blockIdx.x % a.Hkv;
   int s = 0;
   while (tcum[s + 1] <= item) ++s;
+  s = __builtin_amdgcn_readfirstlane(s);
   const int nt_s = tcum[s + 1] - tcum[s];
-  const int tile = nt_s - 1 - (item - tcum[s]);  // last tile first
+  const int tile = __builtin_amdgcn_readfirstlane(nt_s - 1 - (item - tcum[s]));  // last tile first
   const int q0 = a.qsl[s];
   const int qlen = a.qsl[s + 1] - q0;
   const int kv_len = min(max(a.kv_lens[s], 0), a.max_blocks * a.bs);
@@ -123,7 +136,8 @@ __global__ __launch_bounds__(256, 2) void prefill_affine_d128(PrefillArgs a) {
   const int k_lo = a.window > 0 ? max(0, past + t_first - a.window + 1) : 0;
   const int step_lo = k_lo / NT, step_hi = k_hi >= 0 ? k_hi / NT : -1;
 
-  // ---- query operands: MFMA w spans dims [32w, 32w + 32); lane group jj holds dims 32w + 8jj + slot(i)
+  // ---- query operands: MFMA w spans dims [32w, 32w + 32); lane group jj holds dims
+  // 32w + 8jj + i in the element order of the expanded keys (unpack4 / unpack8 order)
   h16x8 qB[2][4];
   float qs[2][G];  // per-group sum of the query, in the 2^-24 units of the MFMA output
 #pragma unroll
@@ -149,11 +163,15 @@ __global__ __launch_bounds__(256, 2) void prefill_affine_d128(PrefillArgs a) {
     }
   }
 
-  // ---- LDS: two step buffers [K rows (padded, MFMA order) | V tile | scales]
-  __shared__ __attribute__((aligned(16))) uint8_t lds[2][P::BUF];
+  // ---- LDS: the step's raw V tile and scales, then the expanded K, dequantized V and fp32 K scales
+  __shared__ __attribute__((aligned(16))) uint8_t raw_v[P::RAWV];
+  __shared__ __attribute__((aligned(16))) h16 raw_s[4 * G * NT];   // [arr][g][NT]
+  __shared__ __attribute__((aligned(16))) h16 ke[NT * P::KSTR];    // [key][dims, unpack order]
+  __shared__ __attribute__((aligned(16))) h16 ve[D * P::VSTR];     // [dim][keys, pv_slot order]
+  __shared__ __attribute__((aligned(16))) float ksf[2][G][NT];    // k_scale, k_bias in fp32
 
   // Cooperative load of one step into registers: thread owns one 16-byte piece of K and of V,
-  // and (threads < 8*G*... ) one piece of the scales.
+  // and (threads < SEGS * SEGB / 16) one piece of the scales.
   u32x4 rk, rv, rsc;
   auto load_step = [&](const int st) {
     const int pos0 = st * NT;
@@ -185,177 +203,177 @@ __global__ __launch_bounds__(256, 2) void prefill_affine_d128(PrefillArgs a) {
       }
     }
   };
-  auto store_step = [&](const int buf) {
-    uint8_t* L = lds[buf];
-    // K: word w' of the row goes to position 4*jj + w for w' = 4w + jj (4-bit), so a lane's
-    // four MFMA words are contiguous; 8-bit keeps word pairs: w' = 8w + 2jj + e -> 8jj + 2w + e
+
+  // Expansion, part 1 (from registers): K codes -> exact fp16 subnormals; raw V and scales -> LDS.
+  auto expand_k = [&]() {
     const int krow = tid / (W / 4), kq = tid % (W / 4);
-    uint32_t* kr = reinterpret_cast<uint32_t*>(L) + krow * P::KROW;
+    h16* kr = ke + krow * P::KSTR;
+    if constexpr (BITS == 4) {
+      // words 4kq .. 4kq+3 hold dims 32kq .. 32kq+31: one MFMA k-step, lane group e of it
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int wp = 4 * kq + e;
-      int pos;
-      if constexpr (BITS == 4) {
-        pos = 4 * (wp % 4) + wp / 4;
-      } else {
-        pos = 8 * ((wp % 8) / 2) + 2 * (wp / 8) + wp % 2;
-      }
-      kr[pos] = rk[e];
+      for (int e = 0; e < 4; ++e)
+        *reinterpret_cast<h16x8*>(kr + 32 * kq + 8 * e) = unpack4(rk[e]);
+    } else {
+      // words 4kq .. 4kq+3 hold dims 16kq .. 16kq+15: half of k-step kq/2, lane groups 2(kq%2), +1
+#pragma unroll
+      for (int e = 0; e < 2; ++e)
+        *reinterpret_cast<h16x8*>(kr + 16 * kq + 8 * e) = unpack8(rk[2 * e], rk[2 * e + 1]);
     }
-    reinterpret_cast<u32x4*>(L + P::KBYTES)[tid] = rv;
+    reinterpret_cast<u32x4*>(raw_v)[tid] = rv;
     constexpr int PER = P::SEGB / 16;
-    if (tid < P::SEGS * PER) reinterpret_cast<u32x4*>(L + P::KBYTES + P::VBYTES)[tid] = rsc;
+    if (tid < P::SEGS * PER) reinterpret_cast<u32x4*>(raw_s)[tid] = rsc;
+  };
+
+  // Expansion, part 2 (from LDS): V -> fp16 v_scale * code + v_bias; K scales -> fp32.
+  // Thread -> dim, TPT consecutive keys of the step (a whole 32-key block at 4-bit,
+  // half of one at 8-bit); keys go to their pv_slot positions in runs of 4.
+  auto expand_v = [&]() {
+    constexpr int TPT = NT * D / 256;  // values per thread (32 at 4-bit, 16 at 8-bit)
+    constexpr int PW = 32 / BITS;      // keys per word
+    const int dim = tid * TPT / NT;
+    const int k0 = (tid * TPT) % NT;   // first key (multiple of 16)
+    const int g = dim / GS;
+    const uint32_t* vw = reinterpret_cast<const uint32_t*>(raw_v) + dim * 8 + k0 / PW;
+    const h16* vsp = raw_s + (2 * G + g) * NT + k0;
+    const h16* vbp = raw_s + (3 * G + g) * NT + k0;
+    h16* vd = ve + dim * P::VSTR + 32 * (k0 >> 5);
+    typedef h16 h16x4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+    for (int q4 = 0; q4 < TPT / 4; ++q4) {  // keys k0 + 4q4 .. +3 (consecutive slots)
+      const int kk = (k0 & 31) + 4 * q4;     // key within its 32-key block
+      h16x4 o;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int e = 4 * q4 + r;  // value index of the thread
+        const uint32_t x = vw[e / PW];
+        const float c = (float)((x >> v_shift<BITS>(e % PW)) & ((1u << BITS) - 1u));
+        o[r] = (h16)fmaf((float)vsp[e], c, (float)vbp[e]);
+      }
+      *reinterpret_cast<h16x4*>(vd + pv_slot(kk)) = o;
+    }
+    // K scales / biases of the step in fp32
+    for (int i = tid; i < 2 * G * NT; i += 256) ksf[i / (G * NT)][(i / NT) % G][i % NT] = (float)raw_s[i];
   };
 
   float m_run[2] = {-INFINITY, -INFINITY}, l_part[2] = {0.f, 0.f};
-  float pb[2][G];
   f32x4 acc[2][8];
 #pragma unroll
-  for (int ct = 0; ct < 2; ++ct) {
-#pragma unroll
-    for (int g = 0; g < G; ++g) pb[ct][g] = 0.f;
+  for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc[ct][i] = f32x4{0.f, 0.f, 0.f, 0.f};
-  }
   const float sc_l2 = a.scale_log2 * kTwo24;
 
   if (step_lo <= step_hi) load_step(step_lo);
   for (int st = step_lo; st <= step_hi; ++st) {
-    const int buf = (st - step_lo) & 1;
-    __syncthreads();  // buffer `buf` is no longer read (step st - 2)
-    store_step(buf);
+    __syncthreads();  // the previous step's expanded tiles are no longer read
+    expand_k();
     __syncthreads();
     if (st + 1 <= step_hi) load_step(st + 1);
+    expand_v();
+    __syncthreads();
     const int pos0 = st * NT;
     const int blk_i = a.block_tables[(size_t)s * a.max_blocks + pos0 / a.bs];
     if ((unsigned)blk_i >= (unsigned)a.nb) continue;  // an invalid page is skipped
-    const uint8_t* L = lds[buf];
-    const uint32_t* Kl = reinterpret_cast<const uint32_t*>(L);
-    const uint32_t* Vl = reinterpret_cast<const uint32_t*>(L + P::KBYTES);
-    const h16* Sl = reinterpret_cast<const h16*>(L + P::KBYTES + P::VBYTES);  // [arr][g][NT]
 
-    // ---- S^T per sub-tile a and query tile ct, per quantization group
-    float sc[2][NA][4];
+    // The step in halves of 32 keys (sub-tiles 2h, 2h + 1): scores, softmax, then PV,
+    // which keeps one half's scores and operand reads live at a time.
 #pragma unroll
-    for (int at = 0; at < NA; ++at) {
-      const int row = TPL * (col >> 2) + 4 * at + (col & 3);
-      uint32_t kw[KW];
+    for (int h = 0; h < NKS; ++h) {
+      // ---- S^T per query tile ct and key sub-tile, per quantization group
+      float sc[2][2][4];  // [ct][sub-tile 2h + t][r]: key 32h + 16t + 4jj + r of the step
 #pragma unroll
-      for (int v = 0; v < KW / 4; ++v) {
-        const u32x4 x = *reinterpret_cast<const u32x4*>(Kl + row * P::KROW + KW * jj + 4 * v);
+      for (int ct = 0; ct < 2; ++ct) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) kw[4 * v + e] = x[e];
+        for (int t = 0; t < 2; ++t) {
+          const int at = 2 * h + t;
+          const h16* kr = ke + (16 * at + col) * P::KSTR + 8 * jj;
+          f32x4 cg[G];
+#pragma unroll
+          for (int g = 0; g < G; ++g) cg[g] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+            const h16x8 A = *reinterpret_cast<const h16x8*>(kr + 32 * w);
+            cg[(32 * w) / GS] = mfma16x16x32(A, qB[ct][w], cg[(32 * w) / GS]);
+          }
+          float v[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int g = 0; g < G; ++g) {
+            const f32x4 ks4 = *reinterpret_cast<const f32x4*>(&ksf[0][g][16 * at + 4 * jj]);
+            const f32x4 kb4 = *reinterpret_cast<const f32x4*>(&ksf[1][g][16 * at + 4 * jj]);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) v[r] = fmaf(cg[g][r], ks4[r], fmaf(kb4[r], qs[ct][g], v[r]));
+          }
+#pragma unroll
+          for (int r = 0; r < 4; ++r) sc[ct][t][r] = v[r];
+        }
       }
-      f32x4 cg[2][G];
+
+      // ---- mask (causal / window / kv_len) where the half is not fully visible to every column
+      const int kpos0 = pos0 + 32 * h;
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct) {
+        const bool full = kpos0 >= start[ct] && kpos0 + 31 <= limit[ct];
+        if (!full) {
+#pragma unroll
+          for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int p = kpos0 + 16 * t + 4 * jj + r;
+              if (p < start[ct] || p > limit[ct]) sc[ct][t][r] = -INFINITY;
+            }
+        }
+      }
+
+      // ---- online softmax per column (base 2)
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct) {
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) tmax = fmaxf(tmax, sc[ct][t][r]);
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+        const float m_new = fmaxf(m_run[ct], tmax * sc_l2);
+        if (m_new == -INFINITY) {  // nothing visible yet for this column
+#pragma unroll
+          for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) sc[ct][t][r] = 0.f;
+        } else {
+          if (__any(m_new != m_run[ct])) {
+            const float alpha = __builtin_amdgcn_exp2f(m_run[ct] - m_new);
+            l_part[ct] *= alpha;
+#pragma unroll
+            for (int dt = 0; dt < 8; ++dt) acc[ct][dt] *= alpha;
+            m_run[ct] = m_new;
+          }
+#pragma unroll
+          for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const float p = __builtin_amdgcn_exp2f(fmaf(sc[ct][t][r], sc_l2, -m_run[ct]));
+              sc[ct][t][r] = p;
+              l_part[ct] += p;
+            }
+        }
+      }
+
+      // ---- O^T += V^T P^T over the half's 32 keys: lane (col, jj) holds keys
+      // 32h + 4jj + r (sub-tile 2h) and 32h + 16 + 4jj + r (sub-tile 2h + 1)
+      h16x8 pB[2];
 #pragma unroll
       for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
-        for (int g = 0; g < G; ++g) cg[ct][g] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        const h16x8 A = BITS == 4 ? unpack4(kw[w]) : unpack8(kw[2 * w], kw[2 * w + 1]);
-        const int g = (32 * w) / GS;
-#pragma unroll
-        for (int ct = 0; ct < 2; ++ct) cg[ct][g] = mfma16x16x32(A, qB[ct][w], cg[ct][g]);
-      }
-      // lane holds keys TPL*jj + 4*at + r (r = 0..3) of the step
-      typedef h16 h16x4 __attribute__((ext_vector_type(4)));
-#pragma unroll
-      for (int ct = 0; ct < 2; ++ct)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) sc[ct][at][r] = 0.f;
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        const h16x4 ks4 = *reinterpret_cast<const h16x4*>(Sl + (0 * G + g) * NT + TPL * jj + 4 * at);
-        const h16x4 kb4 = *reinterpret_cast<const h16x4*>(Sl + (1 * G + g) * NT + TPL * jj + 4 * at);
-#pragma unroll
-        for (int ct = 0; ct < 2; ++ct)
-#pragma unroll
-          for (int r = 0; r < 4; ++r)
-            sc[ct][at][r] = fmaf(cg[ct][g][r], (float)ks4[r], fmaf((float)kb4[r], qs[ct][g], sc[ct][at][r]));
-      }
-    }
-
-    // ---- mask (causal / window / kv_len) where the step is not fully visible to every column
-#pragma unroll
-    for (int ct = 0; ct < 2; ++ct) {
-      const bool full = pos0 >= start[ct] && pos0 + NT - 1 <= limit[ct];
-      if (!full) {
-#pragma unroll
-        for (int at = 0; at < NA; ++at)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int p = pos0 + TPL * jj + 4 * at + r;
-            if (p < start[ct] || p > limit[ct]) sc[ct][at][r] = -INFINITY;
-          }
-      }
-    }
-
-    // ---- online softmax per column (base 2), then O += P V per quantization group of dims
-#pragma unroll
-    for (int ct = 0; ct < 2; ++ct) {
-      float tmax = -INFINITY;
-#pragma unroll
-      for (int at = 0; at < NA; ++at)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) tmax = fmaxf(tmax, sc[ct][at][r]);
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-      const float m_new = fmaxf(m_run[ct], tmax * sc_l2);
-      if (m_new == -INFINITY) {  // nothing visible yet for this column
-#pragma unroll
-        for (int at = 0; at < NA; ++at)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) sc[ct][at][r] = 0.f;
-      } else {
-        if (__any(m_new != m_run[ct])) {
-          const float alpha = __builtin_amdgcn_exp2f(m_run[ct] - m_new);
-          l_part[ct] *= alpha;
-#pragma unroll
-          for (int g = 0; g < G; ++g) pb[ct][g] *= alpha;
-#pragma unroll
-          for (int dt = 0; dt < 8; ++dt) acc[ct][dt] *= alpha;
-          m_run[ct] = m_new;
+        for (int r = 0; r < 4; ++r) {
+          pB[ct][r] = (h16)sc[ct][0][r];
+          pB[ct][4 + r] = (h16)sc[ct][1][r];
         }
 #pragma unroll
-        for (int at = 0; at < NA; ++at)
+      for (int dt = 0; dt < 8; ++dt) {
+        const h16x8 Av = *reinterpret_cast<const h16x8*>(ve + (16 * dt + col) * P::VSTR + 32 * h + 8 * jj);
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const float p = __builtin_amdgcn_exp2f(fmaf(sc[ct][at][r], sc_l2, -m_run[ct]));
-            sc[ct][at][r] = p;
-            l_part[ct] += p;
-          }
-      }
-    }
-#pragma unroll
-    for (int w = 0; w < NWS; ++w) {
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        // V codes of this lane's 8 keys (TPL*jj + 8w ..) for the dim tiles of group g
-        constexpr int DTG = 8 / G;  // dim tiles per quantization group
-        h16x8 Av[DTG];
-#pragma unroll
-        for (int e = 0; e < DTG; ++e) {
-          const int dt = g * DTG + e;
-          typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
-          const u32x2v x = *reinterpret_cast<const u32x2v*>(Vl + (16 * dt + col) * 8 + TPL * jj * BITS / 32);
-          Av[e] = BITS == 4 ? unpack4(w == 0 ? x[0] : x[1]) : unpack8(x[0], x[1]);
-        }
-        const h16x8 vs8 = *reinterpret_cast<const h16x8*>(Sl + (2 * G + g) * NT + TPL * jj + 8 * w);
-        const h16x8 vb8 = *reinterpret_cast<const h16x8*>(Sl + (3 * G + g) * NT + TPL * jj + 8 * w);
-#pragma unroll
-        for (int ct = 0; ct < 2; ++ct) {
-          h16x8 pB;
-#pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            const int j = 8 * w + i;  // unpacked value element i is token i of the word
-            const float p = sc[ct][j >> 2][j & 3];
-            pB[i] = (h16)(p * (float)vs8[i]);
-            pb[ct][g] = fmaf(p, (float)vb8[i], pb[ct][g]);
-          }
-#pragma unroll
-          for (int e = 0; e < DTG; ++e) acc[ct][g * DTG + e] = mfma16x16x32(Av[e], pB, acc[ct][g * DTG + e]);
-        }
+        for (int ct = 0; ct < 2; ++ct) acc[ct][dt] = mfma16x16x32(Av, pB[ct], acc[ct][dt]);
       }
     }
   }
@@ -365,12 +383,6 @@ __global__ __launch_bounds__(256, 2) void prefill_affine_d128(PrefillArgs a) {
   for (int ct = 0; ct < 2; ++ct) {
     float l = l_part[ct] + __shfl_xor(l_part[ct], 16, 64);
     l += __shfl_xor(l, 32, 64);
-    float pbs[G];
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      float x = pb[ct][g] + __shfl_xor(pb[ct][g], 16, 64);
-      pbs[g] = x + __shfl_xor(x, 32, 64);
-    }
     if (!cvalid[ct]) continue;
     const float inv = l > 0.f ? 1.f / l : 0.f;
     h16* op = a.out + ((size_t)(q0 + ctok[ct]) * a.Hq + (size_t)kvh * HG + chead[ct]) * D;
@@ -378,11 +390,8 @@ __global__ __launch_bounds__(256, 2) void prefill_affine_d128(PrefillArgs a) {
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) {
       const int d = 16 * dt + 4 * jj;
-      const float b = pbs[d / GS];
-      *reinterpret_cast<h16x4*>(op + d) = h16x4{(h16)((acc[ct][dt][0] * kTwo24 + b) * inv),
-                                                (h16)((acc[ct][dt][1] * kTwo24 + b) * inv),
-                                                (h16)((acc[ct][dt][2] * kTwo24 + b) * inv),
-                                                (h16)((acc[ct][dt][3] * kTwo24 + b) * inv)};
+      *reinterpret_cast<h16x4*>(op + d) = h16x4{(h16)(acc[ct][dt][0] * inv), (h16)(acc[ct][dt][1] * inv),
+                                                (h16)(acc[ct][dt][2] * inv), (h16)(acc[ct][dt][3] * inv)};
     }
   }
 }
