@@ -79,26 +79,69 @@ struct Q4Cfg {
 template <int GS, int HQ>
 struct Q4Loads {
   static constexpr int G = Q4Cfg<GS, HQ>::G;
+  static constexpr int NSEG = 4 * G;                 // (array, group) segments of 64 tokens, 128 B each
+  static constexpr int SNI = NSEG * 8 > 64 ? NSEG * 8 / 64 : 1;  // 16-byte scale pieces per lane
   uint32_t k[16];       // K codes of token L (128 dims)
   uint32_t v[2][8];     // V codes of dims L and 64 + L, 64 tokens
-  uint32_t s[4][G][2];  // k_scale, k_bias, v_scale, v_bias of tokens 4*(L/4) .. +3, per group
+  u32x4 sraw[SNI];      // scale pieces as loaded: piece 64i + L = segment (64i + L) / 8, tokens 8 * ((64i + L) % 8) ..
+  uint32_t s[4][G][2];  // after staging: k_scale, k_bias, v_scale, v_bias of tokens 4*(L/4) .. +3, per group
 };
 
+// Per-lane base pointers of the scale pieces: piece P = 64i + L is segment
+// seg = P / 8 = (array seg / G, group seg % G), tokens 8 * (P % 8) .. + 7.
+template <int GS>
+struct Q4ScalePtrs {
+  static constexpr int G = 128 / GS, NSEG = 4 * G, SNI = NSEG * 8 > 64 ? NSEG * 8 / 64 : 1;
+  const h16* p[SNI];
+};
+
+template <int GS>
+__device__ __forceinline__ Q4ScalePtrs<GS> q4_scale_ptrs(const DecodeArgs& a, const int lane) {
+  using SP = Q4ScalePtrs<GS>;
+  SP r;
+#pragma unroll
+  for (int i = 0; i < SP::SNI; ++i) {
+    const int P = (64 * i + lane) % (SP::NSEG * 8);  // G = 1: lanes 32..63 repeat 0..31
+    const int seg = P / 8, arr = seg / SP::G, g = seg % SP::G;
+    const h16* base = arr == 0 ? a.ks : arr == 1 ? a.kb : arr == 2 ? a.vs : a.vb;
+    r.p[i] = base + (size_t)g * a.bs + 8 * (P % 8);
+  }
+  return r;
+}
+
+// Scale pieces -> per-lane token-quad values, through this wave's LDS region
+// [16 quads][NSEG] of 8 bytes.
 template <int GS, int HQ>
-__device__ __forceinline__ void q4_issue_loads(Q4Loads<GS, HQ>& L, const TileRsrc& rs, const int it, const int lane,
-                                               const int bs) {
+__device__ __forceinline__ void q4_stage_scales(Q4Loads<GS, HQ>& L, u32x2* region, const int lane) {
+  using LD = Q4Loads<GS, HQ>;
+  constexpr int G = LD::G, NSEG = LD::NSEG;
+#pragma unroll
+  for (int i = 0; i < LD::SNI; ++i) {
+    const int P = 64 * i + lane;
+    if (NSEG * 8 >= 64 || P < NSEG * 8) {
+      const int seg = P / 8, pc = P % 8;
+      region[(2 * pc) * NSEG + seg] = u32x2{L.sraw[i][0], L.sraw[i][1]};
+      region[(2 * pc + 1) * NSEG + seg] = u32x2{L.sraw[i][2], L.sraw[i][3]};
+    }
+  }
+#pragma unroll
+  for (int seg = 0; seg < NSEG; ++seg) {
+    const u32x2 y = region[(lane >> 2) * NSEG + seg];
+    L.s[seg / G][seg % G][0] = y[0];
+    L.s[seg / G][seg % G][1] = y[1];
+  }
+}
+
+template <int GS, int HQ>
+__device__ __forceinline__ void q4_issue_loads(Q4Loads<GS, HQ>& L, const TileRsrc& rs, const Q4ScalePtrs<GS>& sp,
+                                               const size_t soff, const int it, const int lane, const int bs) {
   constexpr int G = Q4Cfg<GS, HQ>::G;
-#ifndef EMX_EXP_NOK
 #pragma unroll
   for (int v = 0; v < 4; ++v) {
     const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(rs.k, lane * 64 + 16 * v, it * 64 * 64, kLoadAux);
 #pragma unroll
     for (int e = 0; e < 4; ++e) L.k[4 * v + e] = x[e];
   }
-#else
-  for (int v = 0; v < 16; ++v) L.k[v] = lane * v;
-#endif
-#ifndef EMX_EXP_NOV
 #pragma unroll
   for (int c = 0; c < 2; ++c) {
 #pragma unroll
@@ -109,42 +152,10 @@ __device__ __forceinline__ void q4_issue_loads(Q4Loads<GS, HQ>& L, const TileRsr
       for (int e = 0; e < 4; ++e) L.v[c][4 * v + e] = x[e];
     }
   }
-#else
-  for (int c = 0; c < 2; ++c)
-    for (int v = 0; v < 8; ++v) L.v[c][v] = lane * v + c;
-#endif
-#ifdef EMX_EXP_NOSCALE
-  for (int arr = 0; arr < 4; ++arr)
-    for (int g = 0; g < G; ++g) L.s[arr][g][0] = L.s[arr][g][1] = 0x3c003c00u;
-  return;
-#endif
-#ifdef EMX_EXP_SCALE1  // timing experiment: one 16-byte load per lane for all scales
-  {
-    const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(rs.s[0], lane * 16, it * 64 * 2, kLoadAux);
-    for (int arr = 0; arr < 4; ++arr)
-      for (int g = 0; g < G; ++g) { L.s[arr][g][0] = x[(arr + g) & 3]; L.s[arr][g][1] = x[(arr + g + 1) & 3]; }
-    return;
-  }
-#endif
-#ifdef EMX_EXP_SCALE4  // timing experiment: four 16-byte loads per lane
-  {
-    for (int arr = 0; arr < 4; ++arr) {
-      const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(rs.s[arr], (lane >> 2) * 16, it * 64 * 2, kLoadAux);
-      for (int g = 0; g < G; ++g) { L.s[arr][g][0] = x[2 * g]; L.s[arr][g][1] = x[2 * g + 1]; }
-    }
-    return;
-  }
-#endif
-  const int ls = (lane >> 2) * 8;
+  (void)bs;
 #pragma unroll
-  for (int arr = 0; arr < 4; ++arr) {
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const u32x2 x = __builtin_amdgcn_raw_buffer_load_b64(rs.s[arr], ls + g * bs * 2, it * 64 * 2, kLoadAux);
-      L.s[arr][g][0] = x[0];
-      L.s[arr][g][1] = x[1];
-    }
-  }
+  for (int i = 0; i < Q4Loads<GS, HQ>::SNI; ++i)
+    L.sraw[i] = *reinterpret_cast<const u32x4*>(sp.p[i] + soff + it * 64);
 }
 
 // Per-lane softmax / accumulator state of one head quad.
@@ -479,8 +490,9 @@ __global__ __launch_bounds__(256, 2) void decode_q4_d128(DecodeArgs a) {
   int it_lo = start_k / TW;
   const float sc_l2 = a.scale_log2 * kTwo24;
 
-  // descriptors of this wave's slice at token t of page b (zero-size, reading nothing, when b is invalid)
-  auto tile_of = [&](int b, int kh, int t) {
+  // descriptors of this wave's slice at token t of page b (zero-size, reading nothing, when b is
+  // invalid), and the element offset of the page-head's scales (page 0 when b is invalid)
+  auto tile_of = [&](int b, int kh, int t, size_t& soff) {
     const bool ok = (unsigned)b < (unsigned)a.nb;
     const int off = t & (a.bs - 1) & ~127;  // page sizes are powers of two here
     const size_t ph = (size_t)(ok ? b : 0) * a.Hkv + kh;
@@ -488,17 +500,19 @@ __global__ __launch_bounds__(256, 2) void decode_q4_d128(DecodeArgs a) {
     TileRsrc r;
     r.k = uniform_rsrc(a.kc + (ph * a.bs + off) * 16, ok ? 128 * 16 * 4 : 0);
     r.v = uniform_rsrc(a.vc + ph * D * RW + (off / 64) * D * 8, ok ? (D * RW - (off / 64) * D * 8) * 4 : 0);
-    const h16* sp[4] = {a.ks, a.kb, a.vs, a.vb};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) r.s[i] = uniform_rsrc(sp[i] + ph * G * a.bs + off, ok ? (G * a.bs - off) * 2 : 0);
+    soff = ph * G * a.bs + off;
     return r;
   };
+  const Q4ScalePtrs<GS> sptr = q4_scale_ptrs<GS>(a, lane);
+  __shared__ u32x2 sst[4][16 * 4 * G];  // per wave: scale staging [16 quads][4 * G segments]
 
   // ---- first item's loads (its query is already in flight)
   int tb = (it_lo + j) * TW + 64 * slice;
   int blk = __builtin_amdgcn_readfirstlane(__builtin_amdgcn_readlane(blkv, 0));
   Q4Loads<GS, 1> bufA, bufB;
-  q4_issue_loads(bufA, tile_of(blk, kvh, tb), (tb & 127) / 64, lane, a.bs);
+  size_t soff0;
+  const TileRsrc rs0 = tile_of(blk, kvh, tb, soff0);
+  q4_issue_loads(bufA, rs0, sptr, soff0, (tb & 127) / 64, lane, a.bs);
 #ifdef EMX_TIMELINE
   EMX_TS(26);
 #endif
@@ -556,7 +570,9 @@ __global__ __launch_bounds__(256, 2) void decode_q4_d128(DecodeArgs a) {
     if (has_next && unit_end) issue_q(s1, kvh1);
     // Issued on every path (an empty descriptor returns zeros without touching
     // memory), so the wait before this item's compute leaves them in flight.
-    q4_issue_loads(nxt, tile_of(blk1, kvh1, tb1), (tb1 & 127) / 64, lane, a.bs);
+    size_t soff1;
+    const TileRsrc rs1 = tile_of(blk1, kvh1, tb1, soff1);
+    q4_issue_loads(nxt, rs1, sptr, soff1, (tb1 & 127) / 64, lane, a.bs);
 
     // ---- compute this wave's slice of the item (skipped when it holds no live
     // token, or its page is invalid, like the reference's Metal kernel)
@@ -566,6 +582,7 @@ __global__ __launch_bounds__(256, 2) void decode_q4_d128(DecodeArgs a) {
     EMX_TS(3 + 3 * min(n_step, 14));
 #endif
     if ((unsigned)blk < (unsigned)a.nb && tb + 64 > start_k) {
+      q4_stage_scales<GS, 1>(cur, sst[wv], lane);
       const bool full = tb >= start_k && tb + 64 <= kv_len;
       q4_compute<GS, 1>(cur, full, lane, tb, start_k, kv_len, qB, qs, sc_l2, st);
     }
