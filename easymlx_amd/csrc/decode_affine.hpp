@@ -114,26 +114,19 @@ struct TileRsrc {
 };
 
 template <int BITS, int GS, int HG>
-__device__ __forceinline__ TileRsrc make_tile_rsrc(const DecodeArgs& a, const int blk, const int kvh, const int off) {
+__device__ __forceinline__ TileRsrc make_tile_rsrc(const DecodeArgs& a, const int blk, const int kvh, const int off,
+                                                   const bool live = true) {
   using C = DecodeCfg<BITS, GS, HG>;
   const int RW = a.bs * BITS / 32;
   const size_t ph = (size_t)blk * a.Hkv + kvh;
-  TileRsrc rs;
-  rs.k = uniform_rsrc(a.kc + (ph * a.bs + off) * C::W, 128 * C::W * 4);
-  rs.v = uniform_rsrc(a.vc + ph * C::D * RW + (off / C::NT) * C::D * 8, (C::D * RW - (off / C::NT) * C::D * 8) * 4);
+  TileRsrc rs;  // live = false: zero-size descriptors (loads read nothing and return zeros)
+  rs.k = uniform_rsrc(a.kc + (ph * a.bs + off) * C::W, live ? 128 * C::W * 4 : 0);
+  rs.v = uniform_rsrc(a.vc + ph * C::D * RW + (off / C::NT) * C::D * 8,
+                      live ? (C::D * RW - (off / C::NT) * C::D * 8) * 4 : 0);
   const h16* sp[4] = {a.ks, a.kb, a.vs, a.vb};
 #pragma unroll
-  for (int arr = 0; arr < 4; ++arr) rs.s[arr] = uniform_rsrc(sp[arr] + ph * C::G * a.bs + off, (C::G * a.bs - off) * 2);
-  return rs;
-}
-
-// Descriptors of zero size: loads through them return zeros and read nothing.
-__device__ __forceinline__ TileRsrc empty_tile_rsrc() {
-  TileRsrc rs;
-  rs.k = __builtin_amdgcn_make_buffer_rsrc(nullptr, (short)0, 0, kRsrcFlags);
-  rs.v = rs.k;
-#pragma unroll
-  for (int arr = 0; arr < 4; ++arr) rs.s[arr] = rs.k;
+  for (int arr = 0; arr < 4; ++arr)
+    rs.s[arr] = uniform_rsrc(sp[arr] + ph * C::G * a.bs + off, live ? (C::G * a.bs - off) * 2 : 0);
   return rs;
 }
 
@@ -148,8 +141,9 @@ struct IterLoads {
 
 template <int BITS, int GS, int HG>
 __device__ __forceinline__ void issue_loads(IterLoads<BITS, GS, HG>& L, const TileRsrc& rs, const int RW,
-                                            const int it, const int lk, const int lv, const int (&ls)[2]) {
+                                            const int it_, const int lk, const int lv, const int (&ls)[2]) {
   using C = DecodeCfg<BITS, GS, HG>;
+  const int it = __builtin_amdgcn_readfirstlane(it_);  // wave-uniform: the loads' scalar offsets
 #pragma unroll
   for (int at = 0; at < C::NA; ++at) {
 #pragma unroll
@@ -544,7 +538,10 @@ __global__ __launch_bounds__(256, 2) void decode_affine_d128(DecodeArgs a) {
   }
 
   const int S = a.S, Hkv = a.Hkv;
-  const long long I = (long long)Hkv * cum[S];
+  // LDS table entries read at a wave-uniform index are moved to SGPRs (uru), so the
+  // per-item scheduling arithmetic and the load offsets stay scalar
+  auto uru = [](int v) { return __builtin_amdgcn_readfirstlane(v); };
+  const long long I = (long long)Hkv * uru(cum[S]);
   const int NW = (int)min((long long)a.num_waves, I);  // every wave range non-empty
   const int W = blockIdx.x * 4 + wv;
   if (W >= NW) return;
@@ -608,15 +605,15 @@ __global__ __launch_bounds__(256, 2) void decode_affine_d128(DecodeArgs a) {
     qs = qsum * (1.0f / kTwo24);  // bias term in the 2^-24 units of the MFMA output
   };
 
-  int n_s = cum[s + 1] - cum[s];
+  int n_s = uru(cum[s + 1]) - uru(cum[s]);
   int kvh, j;
   {
-    const int r = (int)(g0 - (long long)Hkv * cum[s]);
+    const int r = (int)(g0 - (long long)Hkv * uru(cum[s]));
     kvh = r / n_s;
     j = r % n_s;
   }
   issue_q(s, kvh);
-  int kv_len = kvl[s];
+  int kv_len = uru(kvl[s]);
   int start_k = a.window > 0 ? max(0, kv_len - a.window) : 0;
   int it_lo = start_k / NT;
 
@@ -638,11 +635,12 @@ __global__ __launch_bounds__(256, 2) void decode_affine_d128(DecodeArgs a) {
   // ---- first item's loads (its query is already in flight)
   int tb = (it_lo + j) * NT;
   int blk = __builtin_amdgcn_readfirstlane(__builtin_amdgcn_readlane(blkv, 0));
-  TileRsrc rs_cur = make_tile_rsrc<BITS, GS, HG>(a, (unsigned)blk < (unsigned)a.nb ? blk : 0, kvh, (tb & ~127) % a.bs);
+  const TileRsrc rs_first =
+      make_tile_rsrc<BITS, GS, HG>(a, (unsigned)blk < (unsigned)a.nb ? blk : 0, kvh, (tb & ~127) % a.bs);
   // two load buffers used alternately, so the wait before an item's compute
   // never covers the following item's loads
   IterLoads<BITS, GS, HG> bufA, bufB;
-  issue_loads(bufA, rs_cur, RW, (tb & 127) / NT, lk, lv, ls);
+  issue_loads(bufA, rs_first, RW, (tb & 127) / NT, lk, lv, ls);
   build_q();
 
   float m_run = -INFINITY, l_part = 0.f, pb = 0.f;
@@ -660,27 +658,26 @@ __global__ __launch_bounds__(256, 2) void decode_affine_d128(DecodeArgs a) {
         kvh1 = 0;
         do {
           ++s1;
-        } while (s1 < S && cum[s1 + 1] == cum[s1]);
+        } while (s1 < S && uru(cum[s1 + 1]) == uru(cum[s1]));
         if (s1 < S) {
-          n1 = cum[s1 + 1] - cum[s1];
-          kl1 = kvl[s1];
+          n1 = uru(cum[s1 + 1]) - uru(cum[s1]);
+          kl1 = uru(kvl[s1]);
           lo1 = (a.window > 0 ? max(0, kl1 - a.window) : 0) / NT;
         }
       }
     }
     const bool has_next = g + 1 < g1;
     const bool unit_end = !has_next || s1 != s || kvh1 != kvh;
-    TileRsrc rs_nxt = rs_cur;
     int blk1 = blk, tb1 = (lo1 + j1) * NT;
     if (has_next) {
       const int k1 = (int)(g + 1 - g0);
       if ((k1 & 63) == 0) blkv = blk_chunk(g + 1);
       blk1 = __builtin_amdgcn_readfirstlane(__builtin_amdgcn_readlane(blkv, k1 & 63));
-      if (s1 != s || kvh1 != kvh || (tb1 >> 7) != (tb >> 7))
-        rs_nxt = make_tile_rsrc<BITS, GS, HG>(a, (unsigned)blk1 < (unsigned)a.nb ? blk1 : 0, kvh1, (tb1 & ~127) % a.bs);
-    } else {
-      rs_nxt = empty_tile_rsrc();
     }
+    // built from scalar inputs every step (a descriptor carried or selected between
+    // steps ends up in VGPRs, which wraps each load in a per-lane loop)
+    const TileRsrc rs_nxt = make_tile_rsrc<BITS, GS, HG>(a, (unsigned)blk1 < (unsigned)a.nb ? blk1 : 0, kvh1,
+                                                         (tb1 & ~127) % a.bs, has_next);
     // Issued on every path (an empty descriptor returns zeros without touching
     // memory): the compiler's wait before this item's compute then counts these
     // loads as younger and leaves them in flight, instead of draining them.
@@ -728,7 +725,6 @@ __global__ __launch_bounds__(256, 2) void decode_affine_d128(DecodeArgs a) {
     }
 
     // ---- advance
-    rs_cur = rs_nxt;
     if (s1 != s) {
       kv_len = kl1;
       start_k = a.window > 0 ? max(0, kv_len - a.window) : 0;
