@@ -783,71 +783,48 @@ __global__ __launch_bounds__(256, 2) void decode_q4_d128(DecodeArgs a) {
     EMX_TS(42);
     if (lane == 0 && W < 4096) emx_trace[W * kTraceSlots + 43] = (unsigned long long)(npend * 10 + slast[0] + 2 * (npend > 1 ? slast[1] : 0));
 #endif
-    // Merge: thread t owns outputs e = t + 256k of the unit's HG*D values; the
-    // loads of both units and of a batch of MB pieces are in flight together.
-    constexpr int KS = (HG * D + 255) / 256;
-    constexpr int MB = HG <= 4 ? 8 : (HG == 8 ? 4 : 2);
-    bool mg[2] = {slast[0] != 0, npend > 1 && slast[1] != 0};
-    PieceInfo pm[2];
-    int nbat[2] = {0, 0};
-#pragma unroll
-    for (int p = 0; p < 2; ++p) {
-      if (mg[p]) {
-        pm[p] = piece_info<HG>(a, wg, pend_u[p], pend_first[p], pend_n[p], I, NWG);
-        nbat[p] = (pm[p].np + MB - 1) / MB;
-      }
-    }
-    float M[2][KS], L[2][KS], O[2][KS];
-#pragma unroll
-    for (int p = 0; p < 2; ++p)
-#pragma unroll
-      for (int k = 0; k < KS; ++k) M[p][k] = -INFINITY, L[p][k] = 0.f, O[p][k] = 0.f;
-    for (int b = 0; b < max(nbat[0], nbat[1]); ++b) {
-      float o[2][KS][MB];
-      f32x2 ml[2][KS][MB];
-#pragma unroll
-      for (int p = 0; p < 2; ++p) {
-        if (b >= nbat[p]) continue;
-#pragma unroll
-        for (int k = 0; k < KS; ++k) {
-          const int e = min((int)threadIdx.x + 256 * k, HG * D - 1);
-#pragma unroll
-          for (int c = 0; c < MB; ++c) {
-            const int pc = min(b * MB + c, pm[p].np - 1);
-            o[p][k][c] = __builtin_bit_cast(
-                float, __builtin_amdgcn_raw_buffer_load_b32(pm[p].ro, e * 4, pc * HG * D * 4, kCoherent));
-            ml[p][k][c] = __builtin_bit_cast(
-                f32x2, __builtin_amdgcn_raw_buffer_load_b64(pm[p].rm, (e / D) * 8, pc * HG * 8, kCoherent));
-          }
-        }
-      }
-#pragma unroll
-      for (int p = 0; p < 2; ++p) {
-        if (b >= nbat[p]) continue;
-#pragma unroll
-        for (int k = 0; k < KS; ++k) {
-#pragma unroll
-          for (int c = 0; c < MB; ++c) {
-            const f32x2 x = ml[p][k][c];
-            if (b * MB + c >= pm[p].np || x.x == -INFINITY) continue;  // a piece may hold no live token
-            const float Mn = fmaxf(M[p][k], x.x);
-            const float fo = __builtin_amdgcn_exp2f(M[p][k] - Mn);  // 0 while M is -inf
-            const float fp = __builtin_amdgcn_exp2f(x.x - Mn);
-            O[p][k] = O[p][k] * fo + o[p][k][c] * fp;
-            L[p][k] = L[p][k] * fo + x.y * fp;
-            M[p][k] = Mn;
-          }
-        }
-      }
-    }
-#pragma unroll
-    for (int p = 0; p < 2; ++p) {
-      if (!mg[p]) continue;
+    // Merge (page_attention.py:2006-2059): with two units to merge, waves 0-1 take
+    // the first and waves 2-3 the second, so both units' loads are in flight
+    // together; a thread owns float4 f of the unit's HG*D values and loads only
+    // the pieces that exist, up to eight at once.
+    const bool mg0 = slast[0] != 0, mg1 = npend > 1 && slast[1] != 0;
+    if (mg0 || mg1) {
+      const int T = mg0 && mg1 ? 128 : 256;
+      const int p = mg0 && mg1 ? (wv >> 1) : (mg0 ? 0 : 1);
+      const int t = threadIdx.x & (T - 1);
+      const PieceInfo pi = piece_info<HG>(a, wg, pend_u[p], pend_first[p], pend_n[p], I, NWG);
       h16* out = a.out + ((size_t)pend_row[p] * a.Hq + (size_t)pend_kvh[p] * HG) * D;
+      constexpr int NF4 = HG * D / 4;
+      for (int f = t; f < NF4; f += T) {
+        const int h = 4 * f / D;
+        float M = -INFINITY, L = 0.f;
+        f32x4 O = {0.f, 0.f, 0.f, 0.f};
+        for (int p0 = 0; p0 < pi.np; p0 += 8) {
+          f32x4 o[8];
+          f32x2 ml[8];
 #pragma unroll
-      for (int k = 0; k < KS; ++k) {
-        const int e = threadIdx.x + 256 * k;
-        if (e < HG * D) out[e] = (h16)(L[p][k] > 0.f ? O[p][k] / L[p][k] : 0.f);
+          for (int c = 0; c < 8; ++c) {
+            if (p0 + c < pi.np) {
+              o[c] = __builtin_bit_cast(
+                  f32x4, __builtin_amdgcn_raw_buffer_load_b128(pi.ro, f * 16, (p0 + c) * HG * D * 4, kCoherent));
+              ml[c] = __builtin_bit_cast(
+                  f32x2, __builtin_amdgcn_raw_buffer_load_b64(pi.rm, h * 8, (p0 + c) * HG * 8, kCoherent));
+            }
+          }
+#pragma unroll
+          for (int c = 0; c < 8; ++c) {
+            if (p0 + c >= pi.np || ml[c].x == -INFINITY) continue;  // a piece may hold no live token
+            const float Mn = fmaxf(M, ml[c].x);
+            const float fo = __builtin_amdgcn_exp2f(M - Mn);  // 0 while M is -inf
+            const float fp = __builtin_amdgcn_exp2f(ml[c].x - Mn);
+            O = O * fo + o[c] * fp;
+            L = L * fo + ml[c].y * fp;
+            M = Mn;
+          }
+        }
+        const float inv = L > 0.f ? 1.f / L : 0.f;
+        const h16x4 r = {(h16)(O[0] * inv), (h16)(O[1] * inv), (h16)(O[2] * inv), (h16)(O[3] * inv)};
+        *reinterpret_cast<u32x2*>(out + 4 * f) = __builtin_bit_cast(u32x2, r);
       }
     }
   }
