@@ -1,5 +1,5 @@
-"""Paged KV caches (dense and affine-quantized)."""
+"""Paged KV caches (dense, FP8 E4M3 and affine-quantized)."""
 
-from .paged import AffinePageCacheView, PageCacheView, PageMetadata, affine_pool, build_query_start_loc
+from .paged import AffinePageCacheView, Fp8PageCacheView, PageCacheView, PageMetadata, affine_pool, build_query_start_loc
 
-__all__ = ("AffinePageCacheView", "PageCacheView", "PageMetadata", "affine_pool", "build_query_start_loc")
+__all__ = ("AffinePageCacheView", "Fp8PageCacheView", "PageCacheView", "PageMetadata", "affine_pool", "build_query_start_loc")

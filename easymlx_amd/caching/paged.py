@@ -278,6 +278,87 @@ class PageCacheView:
         self.value_cache[ids] = 0
 
 
+class Fp8PageCacheView(PageCacheView):
+    """FP8 (E4M3) page cache with per-page fp32 scales (``cache.py:770-797, 1171-1184``).
+
+    ``key_cache/value_cache [num_blocks, block_size, Hkv, D]`` uint8 codes and
+    ``k_scales/v_scales [num_blocks]`` float32 (zero at allocation), as the
+    reference's FP8 cache.  Writes go through ``emx_fp8_cache_write``: one scale
+    per call (``max|x| / 240``), codes ``enc(x / scale)``, and each written page's
+    scale raised to ``max(page scale, call scale)`` without requantizing the
+    page's earlier codes -- the reference's rule (``cache.py:1181-1184``).
+    """
+
+    cache_dtype_is_fp8 = True
+
+    def __init__(self, *, key_cache, value_cache, k_scales, v_scales, block_tables, kv_lens, block_size,
+                 num_kv_heads, head_dim):
+        super().__init__(key_cache=key_cache, value_cache=value_cache, block_tables=block_tables, kv_lens=kv_lens,
+                         block_size=block_size, num_kv_heads=num_kv_heads, head_dim=head_dim)
+        self.k_scales = k_scales
+        self.v_scales = v_scales
+        self._ws: torch.Tensor | None = None
+
+    @classmethod
+    def init(
+        cls,
+        *,
+        num_seqs: int,
+        max_seq_len: int,
+        num_kv_heads: int,
+        head_dim: int,
+        block_size: int = 16,
+        dtype: torch.dtype = torch.uint8,
+        device: tp.Any = "cuda",
+    ) -> "Fp8PageCacheView":
+        if dtype != torch.uint8:
+            raise ValueError("an FP8 cache stores uint8 codes")
+        base = PageCacheView.init(num_seqs=num_seqs, max_seq_len=max_seq_len, num_kv_heads=num_kv_heads,
+                                  head_dim=head_dim, block_size=block_size, dtype=torch.uint8, device=device)
+        nb = int(base.key_cache.shape[0])
+        return cls(key_cache=base.key_cache, value_cache=base.value_cache,
+                   k_scales=torch.zeros((nb,), dtype=torch.float32, device=device),
+                   v_scales=torch.zeros((nb,), dtype=torch.float32, device=device),
+                   block_tables=base.block_tables, kv_lens=base.kv_lens, block_size=block_size,
+                   num_kv_heads=num_kv_heads, head_dim=head_dim)
+
+    allocate = init
+
+    def _write(self, keys, values, slot_mapping):
+        from .._native import DTYPE_BF16, DTYPE_F16, DTYPE_F32, check, load
+
+        codes = {torch.float16: DTYPE_F16, torch.bfloat16: DTYPE_BF16, torch.float32: DTYPE_F32}
+        if keys.dtype not in codes or values.dtype != keys.dtype:
+            raise NotImplementedError(f"FP8 cache writes take fp16/bf16/fp32 keys and values, got {keys.dtype}")
+        lib = load()
+        if self._ws is None:
+            self._ws = torch.empty(int(lib.emx_fp8_write_workspace_bytes()), dtype=torch.uint8,
+                                   device=self.key_cache.device)
+        keys = keys.contiguous()
+        values = values.contiguous()
+        slot_mapping = slot_mapping.to(device=keys.device, dtype=torch.int32).contiguous()
+        check(
+            lib.emx_fp8_cache_write(
+                keys.data_ptr(), values.data_ptr(), codes[keys.dtype], slot_mapping.data_ptr(), int(keys.shape[0]),
+                self.num_kv_heads, self.head_dim, self.block_size, self.num_blocks,
+                self.key_cache.data_ptr(), self.value_cache.data_ptr(), self.k_scales.data_ptr(),
+                self.v_scales.data_ptr(), self._ws.data_ptr(), self._ws.numel(), _stream_ptr(keys.device),
+            )
+        )
+
+    def write_slots(self, keys: torch.Tensor, values: torch.Tensor, slot_mapping: torch.Tensor) -> None:
+        """Write tokens to explicit slots (``block * block_size + offset``; -1 skips)."""
+        if keys.shape != values.shape or keys.ndim != 3:
+            raise ValueError("keys/values must be [num_tokens, num_kv_heads, head_dim] of one shape")
+        if keys.shape[0]:
+            self._write(keys, values, slot_mapping)
+
+    def _zero_blocks(self, ids: torch.Tensor) -> None:
+        super()._zero_blocks(ids)
+        self.k_scales[ids] = 0
+        self.v_scales[ids] = 0
+
+
 class AffinePageCacheView(PageCacheView):
     """Affine int4/int8 KV pages with fused quantize-on-write.
 

@@ -83,6 +83,48 @@ __host__ __device__ __forceinline__ size_t v_word_index(size_t ph, int off, int 
   return ((ph * (size_t)(bs / T) + (size_t)(off / T)) * D + d) * (size_t)(T * BITS / 32) + (off % T) / (32 / BITS);
 }
 
+// FP8 E4M3 code -> float, as the reference's kernels decode it
+// (lib/python/easymlx/operations/kernels/unified_attention.py:1275-1285): no NaN
+// code, exponent 15 with mantissa 7 is (1 + 7/8) * 2^8.
+__device__ __forceinline__ float e4m3_to_f32(uint32_t c) {
+  const uint32_t e = (c >> 3) & 0xFu, m = c & 0x7u;
+  const float v = e == 0 ? (float)m * 0.001953125f : __uint_as_float(((e + 120u) << 23) | (m << 20));
+  return (c & 0x80u) ? -v : v;
+}
+
+// float -> FP8 E4M3 code with the reference's encoder
+// (lib/python/easymlx/operations/kernels/_metal_header.py:339-419): round to
+// nearest even for exponents 1..14, round half up through its sub-normal
+// branch otherwise (which also takes 240 < |x| <= 448 and keeps only the low
+// mantissa bits there), |x| > 448 and infinities to 448, NaN to 0x7F.
+__device__ __forceinline__ uint32_t f32_to_e4m3(float f) {
+  const uint32_t bits = __float_as_uint(f), s = bits >> 31, ab = bits & 0x7FFFFFFFu;
+  if (ab > 0x7F800000u) return 0x7Fu;
+  if (ab == 0x7F800000u || ab > 0x43E00000u) return (s << 7) | 0x7Eu;  // 0x43E00000 = 448.0f
+  const int e8 = (int)((ab >> 23) & 0xFFu) - 120;
+  const uint32_t m = ab & 0x7FFFFFu;
+  uint32_t r;
+  if (e8 >= 1 && e8 <= 14) {
+    uint32_t mant = m >> 20;
+    const uint32_t lsb = mant & 1u, rnd = (m >> 19) & 1u, sticky = (m & 0x7FFFFu) != 0u;
+    mant += rnd & (sticky | lsb);
+    int ee = e8;
+    if (mant >> 3) {
+      mant = 0;
+      if (++ee > 14) return (s << 7) | (0xFu << 3);
+    }
+    r = (s << 7) | ((uint32_t)ee << 3) | (mant & 0x7u);
+  } else {
+    if (e8 < -2) return s << 7;
+    const int rshift = (1 - e8) + 20;
+    const uint32_t rounded = ((0x800000u | m) + (1u << (rshift - 1))) >> rshift;
+    if (rounded == 0) return s << 7;
+    r = (s << 7) | (rounded & 0x7u);
+  }
+  if (((r >> 3) & 0xFu) == 0xFu && (r & 0x7u) == 0x7u) r = (s << 7) | 0x7Eu;
+  return r;
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));

@@ -15,6 +15,7 @@
 #include "prefill_affine.hpp"
 #include "decode_q4.hpp"
 #include "quantize.hpp"
+#include "fp8.hpp"
 
 namespace {
 
@@ -477,6 +478,100 @@ int emx_paged_attention_dense(const void* queries, int num_tokens, int num_q_hea
     }
   }
   return fail(EMX_ERR_UNSUPPORTED, "unknown dtype code %d", dtype);
+}
+
+size_t emx_fp8_write_workspace_bytes(void) { return sizeof(float) * 2 * emx::kFp8Parts; }
+
+int emx_fp8_cache_write(const void* keys, const void* values, int dtype, const int32_t* slot_mapping, int num_tokens,
+                        int num_kv_heads, int head_dim, int page_size, int num_blocks, uint8_t* key_cache,
+                        uint8_t* value_cache, float* k_scales, float* v_scales, void* workspace,
+                        size_t workspace_bytes, void* stream) {
+  if (num_tokens < 0) return fail(EMX_ERR_INVALID, "num_tokens must be >= 0");
+  if (num_kv_heads <= 0 || head_dim <= 0 || page_size <= 0 || num_blocks <= 0)
+    return fail(EMX_ERR_INVALID, "num_kv_heads, head_dim, page_size, num_blocks must be positive");
+  if (head_dim % 4 != 0) return fail(EMX_ERR_UNSUPPORTED, "head_dim %d must be a multiple of 4", head_dim);
+  if (dtype != EMX_DTYPE_F16 && dtype != EMX_DTYPE_BF16 && dtype != EMX_DTYPE_F32)
+    return fail(EMX_ERR_INVALID, "unknown dtype %d", dtype);
+  if (num_tokens == 0) return EMX_OK;
+  if (!keys || !values || !slot_mapping || !key_cache || !value_cache || !k_scales || !v_scales || !workspace)
+    return fail(EMX_ERR_INVALID, "null pointer");
+  if (workspace_bytes < emx_fp8_write_workspace_bytes())
+    return fail(EMX_ERR_INVALID, "workspace of %zu bytes, %zu needed", workspace_bytes, emx_fp8_write_workspace_bytes());
+  if ((reinterpret_cast<uintptr_t>(key_cache) | reinterpret_cast<uintptr_t>(value_cache)) & 3)
+    return fail(EMX_ERR_INVALID, "key/value cache must be 4-byte aligned");
+  emx::Fp8WriteArgs a;
+  a.k = keys;
+  a.v = values;
+  a.slot = slot_mapping;
+  a.T = num_tokens;
+  a.Hkv = num_kv_heads;
+  a.D = head_dim;
+  a.bs = page_size;
+  a.nb = num_blocks;
+  a.kc = key_cache;
+  a.vc = value_cache;
+  a.ks = k_scales;
+  a.vs = v_scales;
+  a.part = reinterpret_cast<float*>(workspace);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const size_t n = (size_t)num_tokens * num_kv_heads * head_dim;
+  const int nparts = (int)std::min<size_t>(emx::kFp8Parts, (n + 255) / 256);
+  const int nwrite = (int)std::min<size_t>(1024, (n / 4 + 255) / 256);
+  switch (dtype) {
+    case EMX_DTYPE_F16:
+      hipLaunchKernelGGL(emx::fp8_amax<emx::F16>, dim3(nparts), dim3(256), 0, st, a);
+      hipLaunchKernelGGL(emx::fp8_write<emx::F16>, dim3(nwrite), dim3(256), 0, st, a, nparts);
+      break;
+    case EMX_DTYPE_BF16:
+      hipLaunchKernelGGL(emx::fp8_amax<emx::BF16>, dim3(nparts), dim3(256), 0, st, a);
+      hipLaunchKernelGGL(emx::fp8_write<emx::BF16>, dim3(nwrite), dim3(256), 0, st, a, nparts);
+      break;
+    default:
+      hipLaunchKernelGGL(emx::fp8_amax<emx::F32>, dim3(nparts), dim3(256), 0, st, a);
+      hipLaunchKernelGGL(emx::fp8_write<emx::F32>, dim3(nwrite), dim3(256), 0, st, a, nparts);
+      break;
+  }
+  return check_launch("fp8_cache_write");
+}
+
+int emx_paged_attention_fp8(const void* queries, int num_tokens, int num_q_heads, int head_dim, int dtype,
+                            const uint8_t* key_cache, const uint8_t* value_cache, const float* k_scale,
+                            const float* v_scale, int num_blocks, int page_size, int num_kv_heads,
+                            const int32_t* block_tables, int num_seqs, int max_blocks_per_seq, const int32_t* kv_lens,
+                            const int32_t* query_start_loc, float softmax_scale, int sliding_window,
+                            int single_token_decode, void* out, void* stream) {
+  int rc = validate_common(queries, num_tokens, num_q_heads, head_dim, num_kv_heads, num_blocks, page_size,
+                           block_tables, num_seqs, max_blocks_per_seq, kv_lens, query_start_loc, single_token_decode,
+                           out);
+  if (rc) return rc;
+  if (!std::isfinite(softmax_scale)) return fail(EMX_ERR_INVALID, "softmax_scale must be finite");
+  if (num_tokens == 0) return EMX_OK;
+  if (!key_cache || !value_cache || !k_scale || !v_scale) return fail(EMX_ERR_INVALID, "null cache or scale pointer");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  emx::GenericArgs ga;
+  ga.q = queries;
+  ga.out = out;
+  ga.block_tables = block_tables;
+  ga.kv_lens = kv_lens;
+  ga.qsl = query_start_loc;
+  ga.T = num_tokens;
+  ga.S = num_seqs;
+  ga.Hq = num_q_heads;
+  ga.Hkv = num_kv_heads;
+  ga.D = head_dim;
+  ga.bs = page_size;
+  ga.nb = num_blocks;
+  ga.max_blocks = max_blocks_per_seq;
+  ga.scale_log2 = softmax_scale * emx::kLog2e;
+  ga.window = sliding_window > 0 ? sliding_window : 0;
+  ga.decode = single_token_decode ? 1 : 0;
+  const emx::Fp8KV kv{key_cache, value_cache, k_scale, v_scale, num_kv_heads, head_dim, page_size};
+  switch (dtype) {
+    case EMX_DTYPE_F16: return launch_generic<emx::h16>(ga, kv, st);
+    case EMX_DTYPE_BF16: return launch_generic<uint16_t>(ga, kv, st);
+    case EMX_DTYPE_F32: return launch_generic<float>(ga, kv, st);
+  }
+  return fail(EMX_ERR_INVALID, "unknown dtype %d", dtype);
 }
 
 }  // extern "C"

@@ -1,0 +1,105 @@
+// FP8 (E4M3) quantize-on-write into a page cache [nb, bs, Hkv, D] uint8 with one
+// fp32 scale per page, as the reference's PageCacheView.concatenate_to_cache
+// writes an FP8 cache (lib/python/easymlx/caching/paged/cache.py:1171-1184):
+//   * one scale per call for K and one for V: max|x| / 240 over the written
+//     tokens (_KV_SCALE_UPDATE_SOURCE :195-239, compute_kv_scales :430-463);
+//   * codes enc(x / max(scale, 1e-12)) with the reference's E4M3 encoder
+//     (_fp8_quantize :466-478; encoder _metal_header.py:339-419);
+//   * each written page's scale raised to max(page_scale, scale); the page's
+//     earlier codes are not requantized (the reference's rule).
+// Two launches: per-workgroup maxima into a small workspace, then every
+// workgroup reduces them and quantizes its share (4 values per thread).
+#pragma once
+
+#include "common.hpp"
+
+namespace emx {
+
+constexpr int kFp8Parts = 256;  // workgroups of the max pass (partials in the workspace)
+
+struct Fp8WriteArgs {
+  const void* k;         // [T, Hkv, D] in the input dtype
+  const void* v;
+  const int32_t* slot;   // [T] block * bs + offset, -1 skips the token
+  int T, Hkv, D, bs, nb;
+  uint8_t* kc;           // [nb, bs, Hkv, D]
+  uint8_t* vc;
+  float* ks;             // [nb]
+  float* vs;
+  float* part;           // [2][kFp8Parts] per-workgroup maxima
+};
+
+template <typename Tag>
+__global__ __launch_bounds__(256) void fp8_amax(Fp8WriteArgs a) {
+  typedef typename Tag::T T;
+  const T* k = reinterpret_cast<const T*>(a.k);
+  const T* v = reinterpret_cast<const T*>(a.v);
+  const size_t row = (size_t)a.Hkv * a.D, n = (size_t)a.T * row;
+  float mk = 0.f, mv = 0.f;
+  for (size_t e = (size_t)blockIdx.x * 256 + threadIdx.x; e < n; e += (size_t)gridDim.x * 256) {
+    if (a.slot[e / row] < 0) continue;
+    mk = fmaxf(mk, fabsf(to_f32(k[e])));
+    mv = fmaxf(mv, fabsf(to_f32(v[e])));
+  }
+  mk = wave_max(mk);
+  mv = wave_max(mv);
+  __shared__ float sm[2][4];
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    sm[0][w] = mk;
+    sm[1][w] = mv;
+  }
+  __syncthreads();
+  if (threadIdx.x < 2) {
+    const float* x = sm[threadIdx.x];
+    a.part[threadIdx.x * kFp8Parts + blockIdx.x] = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+  }
+}
+
+template <typename Tag>
+__global__ __launch_bounds__(256) void fp8_write(Fp8WriteArgs a, int nparts) {
+  typedef typename Tag::T T;
+  __shared__ float sc[2];
+  if (threadIdx.x < 64) {
+    float mk = 0.f, mv = 0.f;
+    for (int i = threadIdx.x; i < nparts; i += 64) {
+      mk = fmaxf(mk, a.part[i]);
+      mv = fmaxf(mv, a.part[kFp8Parts + i]);
+    }
+    mk = wave_max(mk);
+    mv = wave_max(mv);
+    if (threadIdx.x == 0) {
+      sc[0] = mk / 240.0f;
+      sc[1] = mv / 240.0f;
+    }
+  }
+  __syncthreads();
+  const float ksc = sc[0], vsc = sc[1];
+  const float kq = fmaxf(ksc, 1e-12f), vq = fmaxf(vsc, 1e-12f);
+  const T* k = reinterpret_cast<const T*>(a.k);
+  const T* v = reinterpret_cast<const T*>(a.v);
+  const int row4 = a.Hkv * a.D / 4;
+  const size_t n4 = (size_t)a.T * row4;
+  for (size_t e = (size_t)blockIdx.x * 256 + threadIdx.x; e < n4; e += (size_t)gridDim.x * 256) {
+    const int t = (int)(e / row4), r = (int)(e % row4);
+    const int slot = a.slot[t];
+    if (slot < 0) continue;
+    const int blk = slot / a.bs, off = slot % a.bs;
+    if (blk >= a.nb) continue;
+    uint32_t ck = 0, cv = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      ck |= f32_to_e4m3(to_f32(k[4 * e + j]) / kq) << (8 * j);
+      cv |= f32_to_e4m3(to_f32(v[4 * e + j]) / vq) << (8 * j);
+    }
+    const size_t dst = ((size_t)blk * a.bs + off) * (size_t)row4 + r;  // [nb, bs, Hkv*D/4] words
+    reinterpret_cast<uint32_t*>(a.kc)[dst] = ck;
+    reinterpret_cast<uint32_t*>(a.vc)[dst] = cv;
+    if (r == 0) {  // once per written token: the page keeps the larger scale (scales are >= 0)
+      atomicMax(reinterpret_cast<unsigned int*>(a.ks) + blk, __float_as_uint(ksc));
+      atomicMax(reinterpret_cast<unsigned int*>(a.vs) + blk, __float_as_uint(vsc));
+    }
+  }
+}
+
+}  // namespace emx

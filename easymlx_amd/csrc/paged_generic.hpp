@@ -72,6 +72,22 @@ struct AffineKV {
   }
 };
 
+// FP8 E4M3 cache in the reference layout [nb, bs, Hkv, D] uint8 with one fp32
+// scale per page for K and V (unified_attention.py:892-939: dec(code) * scale[block]).
+struct Fp8KV {
+  const uint8_t* k;
+  const uint8_t* v;
+  const float* ks;
+  const float* vs;
+  int Hkv, D, bs;
+  __device__ __forceinline__ float key(int blk, int off, int h, int d) const {
+    return e4m3_to_f32(k[(((size_t)blk * bs + off) * Hkv + h) * D + d]) * ks[blk];
+  }
+  __device__ __forceinline__ float val(int blk, int off, int h, int d) const {
+    return e4m3_to_f32(v[(((size_t)blk * bs + off) * Hkv + h) * D + d]) * vs[blk];
+  }
+};
+
 template <typename QT, typename KV>
 __global__ __launch_bounds__(64) void paged_generic(GenericArgs a, KV kv) {
   constexpr int MAXH = 16;

@@ -3,9 +3,9 @@
 Drop-in counterpart of the reference's default attention operation:
 
 * ``paged_attention(...)`` -- ``lib/python/easymlx/operations/kernels/unified_attention.py:1377-1512``
-  (same positional arguments and keyword meaning; the FP8 ``k_scale/v_scale``
-  per-block scales generalise to affine ``k_scales/k_biases/v_scales/v_biases``
-  with ``bits`` and ``group_size``).
+  (same positional arguments and keyword meaning).  An FP8 (E4M3) cache takes
+  the reference's per-page ``k_scale/v_scale``; affine pages take
+  ``k_scales/k_biases/v_scales/v_biases`` with ``bits`` and ``group_size``.
 * ``UnifiedAttention`` -- ``unified_attention.py:1515-1684``, registered under
   the same names, with ``forward_native(query=, key=, value=, cache_metadata=,
   cache_view=, scale=, ...) -> AttentionOutput``.
@@ -25,7 +25,7 @@ from dataclasses import dataclass
 import torch
 
 from .. import _native
-from ..caching.paged import AffinePageCacheView, PageCacheView, PageMetadata
+from ..caching.paged import AffinePageCacheView, Fp8PageCacheView, PageCacheView, PageMetadata
 from ._base_operation import (
     AttentionOutput,
     BaseOperation,
@@ -132,6 +132,8 @@ def paged_attention(
     softmax_scale: float | None = None,
     sliding_window: int | None = None,
     single_token_decode: bool | None = None,
+    k_scale: torch.Tensor | None = None,
+    v_scale: torch.Tensor | None = None,
     k_scales: torch.Tensor | None = None,
     k_biases: torch.Tensor | None = None,
     v_scales: torch.Tensor | None = None,
@@ -143,7 +145,9 @@ def paged_attention(
 ) -> torch.Tensor:
     """Execute paged attention over block-tabled KV caches.
 
-    Dense caches use the reference layout ``[num_blocks, block_size, Hkv, D]``.
+    Dense caches use the reference layout ``[num_blocks, block_size, Hkv, D]``;
+    an FP8 (E4M3) cache is that layout in ``uint8`` with per-page fp32 scales
+    ``k_scale/v_scale [num_blocks]`` (``unified_attention.py:1431``).
     Affine caches (``k_scales`` given) use the page layout of
     :class:`~easymlx_amd.caching.paged.AffinePageCacheView`:
     ``key_cache [nb, Hkv, bs, D*bits/32]``, ``value_cache [nb, Hkv, bs/T, D, T*bits/32]``
@@ -204,6 +208,29 @@ def paged_attention(
         )
         return out
 
+    if queries.dtype not in _DTYPE_CODE:
+        raise NotImplementedError(f"unsupported dtype {queries.dtype}")
+    fp8 = key_cache.dtype == torch.uint8 and k_scale is not None and v_scale is not None
+    if fp8:
+        if value_cache.dtype != torch.uint8:
+            raise ValueError("an FP8 cache needs uint8 key and value caches")
+        key_cache = key_cache.contiguous()
+        value_cache = value_cache.contiguous()
+        nb, bs, hkv = int(key_cache.shape[0]), int(key_cache.shape[1]), int(key_cache.shape[2])
+        k_scale = k_scale.to(device=dev, dtype=torch.float32).contiguous()
+        v_scale = v_scale.to(device=dev, dtype=torch.float32).contiguous()
+        if k_scale.numel() != nb or v_scale.numel() != nb:
+            raise ValueError("k_scale/v_scale must hold one scale per block: [num_blocks]")
+        _native.check(
+            lib.emx_paged_attention_fp8(
+                queries.data_ptr(), total, hq, d, _DTYPE_CODE[queries.dtype],
+                key_cache.data_ptr(), value_cache.data_ptr(), k_scale.data_ptr(), v_scale.data_ptr(),
+                nb, bs, hkv, block_tables.data_ptr(), S, max_blocks, kv_lens.data_ptr(), query_start_loc.data_ptr(),
+                float(softmax_scale), int(sliding_window), int(bool(single_token_decode)),
+                out.data_ptr(), stream,
+            )
+        )
+        return out
     if key_cache.dtype != queries.dtype or value_cache.dtype != queries.dtype:
         raise NotImplementedError("dense paged attention needs the cache in the queries' dtype")
     if queries.dtype not in _DTYPE_CODE:
@@ -279,8 +306,13 @@ class UnifiedAttention(BaseOperation):
                 bits=cache_view.bits,
                 group_size=cache_view.group_size,
             )
+        elif cache_view is not None and getattr(cache_view, "cache_dtype_is_fp8", False) and key.dtype == torch.uint8:
+            # unified_attention.py:1633-1656: the view's per-page scales
+            kwargs.update(k_scale=cache_view.k_scales, v_scale=cache_view.v_scales)
         elif key.dtype == torch.int32:
             raise ValueError("affine KV pages require an AffinePageCacheView as cache_view")
+        elif key.dtype == torch.uint8:
+            raise ValueError("an FP8 cache requires a cache_view with per-page k_scales/v_scales")
         outputs = paged_attention(
             query,
             key,

@@ -111,6 +111,47 @@ int emx_paged_attention_dense(const void* queries, int num_tokens, int num_q_hea
                               const int32_t* kv_lens, const int32_t* query_start_loc, float softmax_scale,
                               int sliding_window, int single_token_decode, void* out, void* stream);
 
+/*
+ * Bytes of device workspace emx_fp8_cache_write needs (per-workgroup maxima;
+ * no zero fill needed).  Calls sharing a workspace must not overlap.
+ * No direct reference counterpart (the reference reduces into an MLX output
+ * array, lib/python/easymlx/caching/paged/cache.py:430-463).
+ */
+size_t emx_fp8_write_workspace_bytes(void);
+
+/*
+ * FP8 (E4M3) quantize-on-write into a page cache key/value [num_blocks,
+ * page_size, Hkv, head_dim] uint8 with one fp32 scale per page (k_scales,
+ * v_scales [num_blocks], zero-filled at allocation).  keys/values [num_tokens,
+ * Hkv, head_dim] in dtype (EMX_DTYPE_*); slot_mapping int32 [num_tokens]
+ * (block * page_size + offset, -1 to skip).  One scale per call,
+ * max|x| / 240 over the written tokens; codes enc(x / max(scale, 1e-12));
+ * each written page's scale becomes max(page scale, call scale).
+ * Replaces the FP8 branch of PageCacheView.concatenate_to_cache
+ *   lib/python/easymlx/caching/paged/cache.py:1171-1184 (compute_kv_scales
+ *   :430-463, _fp8_quantize :466-478, encoder
+ *   lib/python/easymlx/operations/kernels/_metal_header.py:339-419).
+ */
+int emx_fp8_cache_write(const void* keys, const void* values, int dtype, const int32_t* slot_mapping, int num_tokens,
+                        int num_kv_heads, int head_dim, int page_size, int num_blocks, uint8_t* key_cache,
+                        uint8_t* value_cache, float* k_scales, float* v_scales, void* workspace,
+                        size_t workspace_bytes, void* stream);
+
+/*
+ * Paged attention over an FP8 (E4M3) cache key/value [num_blocks, page_size,
+ * Hkv, head_dim] uint8 with per-page fp32 scales k_scale/v_scale [num_blocks]:
+ * K = dec(code) * k_scale[page].  queries/out in dtype (EMX_DTYPE_*).
+ * Replaces: paged_attention(..., k_scale=, v_scale=)
+ *   lib/python/easymlx/operations/kernels/unified_attention.py:1377-1512 with the
+ *   FP8 kernels :776-1268 (decoder :1275-1285).
+ */
+int emx_paged_attention_fp8(const void* queries, int num_tokens, int num_q_heads, int head_dim, int dtype,
+                            const uint8_t* key_cache, const uint8_t* value_cache, const float* k_scale,
+                            const float* v_scale, int num_blocks, int page_size, int num_kv_heads,
+                            const int32_t* block_tables, int num_seqs, int max_blocks_per_seq, const int32_t* kv_lens,
+                            const int32_t* query_start_loc, float softmax_scale, int sliding_window,
+                            int single_token_decode, void* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

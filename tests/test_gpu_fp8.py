@@ -1,0 +1,152 @@
+"""FP8 (E4M3) cache: GPU write bit-exact vs the oracle; attention over it vs the oracle."""
+
+import numpy as np
+import pytest
+import torch
+
+from easymlx_amd import Fp8PageCacheView, UnifiedAttention, paged_attention
+from easymlx_amd.caching.paged import PageMetadata
+from easymlx_amd.workloads import decode_workload, unified_workload
+from oracle import fp8
+from oracle.paged_attention import paged_attention as oracle_attention
+from tests.helpers import assert_attention_close
+
+pytestmark = pytest.mark.gpu
+
+
+def _view(wl, device):
+    nb = wl.num_blocks
+    shape = (nb, wl.block_size, wl.num_kv_heads, wl.head_dim)
+    return Fp8PageCacheView(
+        key_cache=torch.zeros(shape, dtype=torch.uint8, device=device),
+        value_cache=torch.zeros(shape, dtype=torch.uint8, device=device),
+        k_scales=torch.zeros((nb,), dtype=torch.float32, device=device),
+        v_scales=torch.zeros((nb,), dtype=torch.float32, device=device),
+        block_tables=torch.from_numpy(wl.block_tables).to(device),
+        kv_lens=torch.from_numpy(wl.kv_lens).to(device),
+        block_size=wl.block_size,
+        num_kv_heads=wl.num_kv_heads,
+        head_dim=wl.head_dim,
+    )
+
+
+def _write_per_sequence(wl, view, dtype, hold_last: bool):
+    """One write call per sequence (each its own scale); the oracle replays the same calls.
+
+    hold_last: the last token of every sequence is held back and written in one
+    final call for all sequences (a decode step), which raises page scales.
+    """
+    shape = (wl.num_blocks, wl.block_size, wl.num_kv_heads, wl.head_dim)
+    kc, vc = np.zeros(shape, np.uint8), np.zeros(shape, np.uint8)
+    ks, vs = np.zeros(wl.num_blocks, np.float32), np.zeros(wl.num_blocks, np.float32)
+    bounds = np.concatenate([[0], np.cumsum(wl.kv_lens)])
+    last = []
+    dev = view.key_cache.device
+    tdt = {"f16": torch.float16, "bf16": torch.bfloat16, "f32": torch.float32}[dtype]
+
+    def call(idx):
+        k = torch.from_numpy(wl.k[idx]).to(dev).to(tdt)
+        v = torch.from_numpy(wl.v[idx]).to(dev).to(tdt)
+        slot = wl.slot[idx].astype(np.int32)
+        view.write_slots(k, v, torch.from_numpy(slot).to(dev))
+        # the oracle sees exactly the values the GPU converted
+        fp8.fp8_write(k.float().cpu().numpy(), v.float().cpu().numpy(), slot, kc, vc, ks, vs)
+
+    for s in range(len(wl.kv_lens)):
+        lo, hi = int(bounds[s]), int(bounds[s + 1])
+        if hi == lo:
+            continue
+        if hold_last:
+            last.append(hi - 1)
+            hi -= 1
+        if hi > lo:
+            call(np.arange(lo, hi))
+    if last:
+        call(np.array(last))
+    return kc, vc, ks, vs
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16", "f32"])
+def test_fp8_write_bit_exact(cuda, dtype):
+    print(f"[fp8 write {dtype}]", flush=True)
+    wl = decode_workload(seed=21, num_seqs=6, num_q_heads=8, num_kv_heads=2, head_dim=64, ctx_range=(5, 300),
+                         block_size=32, bits=None)
+    view = _view(wl, cuda)
+    kc, vc, ks, vs = _write_per_sequence(wl, view, dtype, hold_last=True)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(view.key_cache.cpu().numpy(), kc)
+    np.testing.assert_array_equal(view.value_cache.cpu().numpy(), vc)
+    np.testing.assert_array_equal(view.k_scales.cpu().numpy(), ks)
+    np.testing.assert_array_equal(view.v_scales.cpu().numpy(), vs)
+
+
+def test_fp8_write_skips_and_large_batch(cuda):
+    """A 4096-token write (several workgroups in the max pass) with skipped slots."""
+    print("[fp8 write large]", flush=True)
+    rng = np.random.default_rng(3)
+    nb, bs, hkv, d, t = 64, 128, 4, 128, 4096
+    k = (rng.standard_normal((t, hkv, d)) * rng.uniform(0.1, 8.0, (1, hkv, d))).astype(np.float16)
+    v = rng.standard_normal((t, hkv, d)).astype(np.float16)
+    slot = rng.permutation(nb * bs)[:t].astype(np.int32)
+    slot[rng.random(t) < 0.1] = -1
+    shape = (nb, bs, hkv, d)
+    view = Fp8PageCacheView(key_cache=torch.zeros(shape, dtype=torch.uint8, device=cuda),
+                            value_cache=torch.zeros(shape, dtype=torch.uint8, device=cuda),
+                            k_scales=torch.zeros(nb, device=cuda), v_scales=torch.zeros(nb, device=cuda),
+                            block_tables=torch.zeros((1, 1), dtype=torch.int32, device=cuda),
+                            kv_lens=torch.zeros(1, dtype=torch.int32, device=cuda), block_size=bs,
+                            num_kv_heads=hkv, head_dim=d)
+    view.write_slots(torch.from_numpy(k).to(cuda), torch.from_numpy(v).to(cuda), torch.from_numpy(slot).to(cuda))
+    kc, vc = np.zeros(shape, np.uint8), np.zeros(shape, np.uint8)
+    ks, vs = np.zeros(nb, np.float32), np.zeros(nb, np.float32)
+    fp8.fp8_write(k.astype(np.float32), v.astype(np.float32), slot, kc, vc, ks, vs)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(view.key_cache.cpu().numpy(), kc)
+    np.testing.assert_array_equal(view.value_cache.cpu().numpy(), vc)
+    np.testing.assert_array_equal(view.k_scales.cpu().numpy(), ks)
+    np.testing.assert_array_equal(view.v_scales.cpu().numpy(), vs)
+
+
+def _attention_case(cuda, wl, hold_last, sliding_window=0):
+    view = _view(wl, cuda)
+    kc, vc, ks, vs = _write_per_sequence(wl, view, "f16", hold_last=hold_last)
+    q = torch.from_numpy(wl.q).to(cuda)
+    out = paged_attention(q, view.key_cache, view.value_cache, view.block_tables, view.kv_lens,
+                          torch.from_numpy(wl.query_start_loc).to(cuda), k_scale=view.k_scales,
+                          v_scale=view.v_scales, sliding_window=sliding_window or None)
+    torch.cuda.synchronize()
+    exp = oracle_attention(wl.q.astype(np.float32), fp8.fp8_dequant_cache(kc, ks), fp8.fp8_dequant_cache(vc, vs),
+                           wl.block_tables, wl.kv_lens, wl.query_start_loc, sliding_window=sliding_window,
+                           compute_dtype=np.float64)
+    return out, exp, view
+
+
+def test_fp8_decode_vs_oracle(cuda):
+    print("[fp8 decode]", flush=True)
+    wl = decode_workload(seed=22, num_seqs=16, ctx_range=(1, 1500), bits=None)
+    out, exp, _ = _attention_case(cuda, wl, hold_last=True)
+    assert_attention_close(out.float().cpu().numpy(), exp, "fp8 decode")
+
+
+def test_fp8_unified_vs_oracle(cuda):
+    print("[fp8 unified]", flush=True)
+    wl = unified_workload("fp8u", seed=23, num_prefill=2, chunk=96, prior_range=(0, 300), num_decode=5,
+                          decode_ctx=(1, 700), bits=None)
+    out, exp, _ = _attention_case(cuda, wl, hold_last=False)
+    assert_attention_close(out.float().cpu().numpy(), exp, "fp8 unified")
+    out, exp, _ = _attention_case(cuda, wl, hold_last=False, sliding_window=64)
+    assert_attention_close(out.float().cpu().numpy(), exp, "fp8 unified window")
+
+
+def test_fp8_registered_op(cuda):
+    """UnifiedAttention routes an FP8 cache view to the per-page scales (unified_attention.py:1633-1656)."""
+    print("[fp8 op]", flush=True)
+    wl = decode_workload(seed=24, num_seqs=8, ctx_range=(16, 900), bits=None)
+    out_ref, exp, view = _attention_case(cuda, wl, hold_last=True)
+    md = PageMetadata(query_start_loc=torch.from_numpy(wl.query_start_loc).to(cuda), block_tables=view.block_tables,
+                      kv_lens=view.kv_lens, block_size=wl.block_size, is_single_token_decode=True)
+    res = UnifiedAttention().forward_native(query=torch.from_numpy(wl.q).to(cuda), key=view.key_cache,
+                                            value=view.value_cache, cache_metadata=md, cache_view=view)
+    torch.cuda.synchronize()
+    assert torch.equal(res.attention_outputs, out_ref)
+    assert_attention_close(res.attention_outputs.float().cpu().numpy(), exp, "fp8 op")
