@@ -142,6 +142,17 @@ PrefillFn pick_prefill_hg(int hg) {
   return nullptr;
 }
 
+PrefillFn pick_prefill_fp8(int hg) {
+  switch (hg) {
+    case 1: return emx::prefill_affine_d128<8, 128, 1, true>;
+    case 2: return emx::prefill_affine_d128<8, 128, 2, true>;
+    case 4: return emx::prefill_affine_d128<8, 128, 4, true>;
+    case 8: return emx::prefill_affine_d128<8, 128, 8, true>;
+    case 16: return emx::prefill_affine_d128<8, 128, 16, true>;
+  }
+  return nullptr;
+}
+
 template <int BITS>
 PrefillFn pick_prefill_gs(int gs, int hg) {
   switch (gs) {
@@ -338,6 +349,7 @@ int emx_paged_attention_affine(const void* queries, int num_tokens, int num_q_he
       p.max_blocks = max_blocks_per_seq;
       p.scale_log2 = scale_log2;
       p.window = window;
+      p.min_q = 2;
       PrefillFn pf = bits == 4 ? pick_prefill_gs<4>(group_size, hg) : pick_prefill_gs<8>(group_size, hg);
       if (!pf)
         return fail(EMX_ERR_UNSUPPORTED, "no prefill kernel for bits=%d group_size=%d gqa=%d", bits, group_size, hg);
@@ -565,6 +577,36 @@ int emx_paged_attention_fp8(const void* queries, int num_tokens, int num_q_heads
   ga.scale_log2 = softmax_scale * emx::kLog2e;
   ga.window = sliding_window > 0 ? sliding_window : 0;
   ga.decode = single_token_decode ? 1 : 0;
+  // head_dim 128, fp16 queries: the MFMA kernel over every row (a decode row is a
+  // tile of one query token); other shapes run on the generic kernel
+  const int hg = num_q_heads / num_kv_heads;
+  const PrefillFn pf = pick_prefill_fp8(hg);
+  if (pf && dtype == EMX_DTYPE_F16 && head_dim == 128 && page_size % 32 == 0 && query_start_loc &&
+      num_seqs <= emx::kMaxSeqs && aligned16(key_cache) && aligned16(value_cache)) {
+    emx::PrefillArgs p{};
+    p.q = reinterpret_cast<const emx::h16*>(queries);
+    p.block_tables = block_tables;
+    p.kv_lens = kv_lens;
+    p.qsl = query_start_loc;
+    p.out = reinterpret_cast<emx::h16*>(out);
+    p.S = num_seqs;
+    p.Hq = num_q_heads;
+    p.Hkv = num_kv_heads;
+    p.bs = page_size;
+    p.nb = num_blocks;
+    p.max_blocks = max_blocks_per_seq;
+    p.scale_log2 = ga.scale_log2;
+    p.window = ga.window;
+    p.min_q = 1;
+    p.k8 = key_cache;
+    p.v8 = value_cache;
+    p.kps = k_scale;
+    p.vps = v_scale;
+    const int tokb = 128 / hg;
+    const long grid = (long)((num_tokens + tokb - 1) / tokb + num_seqs) * num_kv_heads;
+    hipLaunchKernelGGL(pf, dim3((unsigned)grid), dim3(256), 0, st, p);
+    return check_launch("prefill_affine_d128 (fp8)");
+  }
   const emx::Fp8KV kv{key_cache, value_cache, k_scale, v_scale, num_kv_heads, head_dim, page_size};
   switch (dtype) {
     case EMX_DTYPE_F16: return launch_generic<emx::h16>(ga, kv, st);

@@ -47,6 +47,13 @@ struct PrefillArgs {
   int S, Hq, Hkv, bs, nb, max_blocks;
   float scale_log2;             // softmax_scale * log2(e)
   int window;                   // sliding window, 0 = off
+  int min_q;                    // rows with fewer query tokens go to the decode kernels (2), or none (1)
+  // FP8 (E4M3) cache instead of affine pages: key/value [nb, bs, Hkv, 128]
+  // uint8 with one fp32 scale per page (unified_attention.py:892-939)
+  const uint8_t* k8;
+  const uint8_t* v8;
+  const float* kps;             // [nb]
+  const float* vps;             // [nb]
 };
 
 template <int BITS, int GS, int HG>
@@ -72,7 +79,7 @@ struct PrefillCfg {
 // Number of query-token tiles of sequence s (0 for decode rows and empty rows).
 __device__ __forceinline__ int prefill_tiles(const PrefillArgs& a, const int s, const int tokb) {
   const int ql = a.qsl[s + 1] - a.qsl[s];
-  return ql > 1 ? (ql + tokb - 1) / tokb : 0;
+  return ql >= a.min_q ? (ql + tokb - 1) / tokb : 0;
 }
 
 // Position, inside its 32-key block, at which the dequantized value of key k
@@ -80,8 +87,12 @@ __device__ __forceinline__ int prefill_tiles(const PrefillArgs& a, const int s, 
 // keys kg*4 + {0..3} and 16 + kg*4 + {0..3} of the block, in that order.
 __device__ __forceinline__ constexpr int pv_slot(int k) { return 8 * ((k & 15) >> 2) + 4 * (k >> 4) + (k & 3); }
 
-template <int BITS, int GS, int HG>
+// FP8: the same kernel over an FP8 cache (BITS 8, one group): K expands to its
+// exact fp16 values with the page scale * 2^-24 as the key scale (so the scores
+// keep the affine formula with zero biases), V dequantizes to dec(code) * scale.
+template <int BITS, int GS, int HG, bool FP8 = false>
 __global__ __launch_bounds__(256, 2) void prefill_affine_d128(PrefillArgs a) {
+  static_assert(!FP8 || (BITS == 8 && GS == 128), "the FP8 cache runs as 8-bit codes in one group");
   using P = PrefillCfg<BITS, GS, HG>;
   constexpr int D = P::D, G = P::G, NT = P::NT, NA = P::NA, NKS = P::NKS, W = P::W;
 
@@ -173,11 +184,23 @@ __global__ __launch_bounds__(256, 2) void prefill_affine_d128(PrefillArgs a) {
   // Cooperative load of one step into registers: thread owns one 16-byte piece of K and of V,
   // and (threads < SEGS * SEGB / 16) one piece of the scales.
   u32x4 rk, rv, rsc;
+  float psk = 0.f, psv = 0.f;  // FP8: the loaded step's page scales
+  float vsc = 0.f;             // FP8: the expanded step's value scale
   auto load_step = [&](const int st) {
     const int pos0 = st * NT;
     const int blk_i = a.block_tables[(size_t)s * a.max_blocks + pos0 / a.bs];
     const int blk = (unsigned)blk_i < (unsigned)a.nb ? blk_i : 0;
     const int off = pos0 % a.bs;
+    if constexpr (FP8) {
+      // 32 key rows of 128 bytes, 1 KiB apart per head: thread -> row tid / 8, bytes 16 * (tid % 8) ..
+      const size_t rowb = (size_t)a.Hkv * D;
+      const size_t base = ((size_t)blk * a.bs + off + (tid >> 3)) * rowb + (size_t)kvh * D + 16 * (tid & 7);
+      rk = *reinterpret_cast<const u32x4*>(a.k8 + base);
+      rv = *reinterpret_cast<const u32x4*>(a.v8 + base);
+      psk = a.kps[blk];
+      psv = a.vps[blk];
+      return;
+    }
     const size_t ph = (size_t)blk * a.Hkv + kvh;
     // K: NT rows x W words = 4 KiB; piece tid -> row tid / (W/4), words 4*(tid % (W/4)) ..
     const int krow = tid / (W / 4), kq = tid % (W / 4);
@@ -213,6 +236,23 @@ __global__ __launch_bounds__(256, 2) void prefill_affine_d128(PrefillArgs a) {
 #pragma unroll
       for (int e = 0; e < 4; ++e)
         *reinterpret_cast<h16x8*>(kr + 32 * kq + 8 * e) = unpack4(rk[e]);
+    } else if constexpr (FP8) {
+      // the 16 codes of dims 16kq .. 16kq+15 as their exact fp16 values
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        h16x8 o;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[i] = (h16)e4m3_to_f32((rk[2 * e + (i >> 2)] >> (8 * (i & 3))) & 0xFFu);
+        *reinterpret_cast<h16x8*>(kr + 16 * kq + 8 * e) = o;
+      }
+      // scores keep the affine formula: key scale = page scale * 2^-24, biases 0
+      if (tid < NT) {
+        ksf[0][0][tid] = psk * (1.0f / kTwo24);
+        ksf[1][0][tid] = 0.f;
+      }
+      vsc = psv;
+      reinterpret_cast<u32x4*>(raw_v)[tid] = rv;  // [32 keys][128 bytes]
+      return;
     } else {
       // words 4kq .. 4kq+3 hold dims 16kq .. 16kq+15: half of k-step kq/2, lane groups 2(kq%2), +1
 #pragma unroll
@@ -233,11 +273,23 @@ __global__ __launch_bounds__(256, 2) void prefill_affine_d128(PrefillArgs a) {
     const int dim = tid * TPT / NT;
     const int k0 = (tid * TPT) % NT;   // first key (multiple of 16)
     const int g = dim / GS;
+    typedef h16 h16x4 __attribute__((ext_vector_type(4)));
+    if constexpr (FP8) {  // token-major raw tile: key k's code of dim d at byte 128k + d
+      h16* vd = ve + dim * P::VSTR + 32 * (k0 >> 5);
+#pragma unroll
+      for (int q4 = 0; q4 < TPT / 4; ++q4) {
+        const int kk = (k0 & 31) + 4 * q4;
+        h16x4 o;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o[r] = (h16)(e4m3_to_f32(raw_v[(k0 + 4 * q4 + r) * D + dim]) * vsc);
+        *reinterpret_cast<h16x4*>(vd + pv_slot(kk)) = o;
+      }
+      return;
+    }
     const uint32_t* vw = reinterpret_cast<const uint32_t*>(raw_v) + dim * 8 + k0 / PW;
     const h16* vsp = raw_s + (2 * G + g) * NT + k0;
     const h16* vbp = raw_s + (3 * G + g) * NT + k0;
     h16* vd = ve + dim * P::VSTR + 32 * (k0 >> 5);
-    typedef h16 h16x4 __attribute__((ext_vector_type(4)));
 #pragma unroll
     for (int q4 = 0; q4 < TPT / 4; ++q4) {  // keys k0 + 4q4 .. +3 (consecutive slots)
       const int kk = (k0 & 31) + 4 * q4;     // key within its 32-key block
