@@ -252,6 +252,48 @@ def aux_c4(dev):
             "frac": round(nbytes / (us * 1e3) / HBM_PEAK_GBS, 4)}
 
 
+def aux_fp8(dev):
+    """FP8 (E4M3, per-page scale) cache: c2-shaped decode (batch 32, ctx U[512,4096]) and a 32-token write.
+
+    One pool (fits the 256 MB cache: an upper bound on the rate), HIP events per call.
+    """
+    import torch
+
+    from easymlx_amd import Fp8PageCacheView, paged_attention
+    from easymlx_amd.workloads import decode_workload
+
+    wl = decode_workload(seed=2, bits=None)
+    nb = wl.num_blocks
+    shape = (nb, wl.block_size, wl.num_kv_heads, wl.head_dim)
+    view = Fp8PageCacheView(key_cache=torch.zeros(shape, dtype=torch.uint8, device=dev),
+                            value_cache=torch.zeros(shape, dtype=torch.uint8, device=dev),
+                            k_scales=torch.zeros(nb, device=dev), v_scales=torch.zeros(nb, device=dev),
+                            block_tables=torch.from_numpy(wl.block_tables).to(dev),
+                            kv_lens=torch.from_numpy(wl.kv_lens).to(dev), block_size=wl.block_size,
+                            num_kv_heads=wl.num_kv_heads, head_dim=wl.head_dim)
+    view.write_slots(torch.from_numpy(wl.k).to(dev), torch.from_numpy(wl.v).to(dev),
+                     torch.from_numpy(wl.slot.astype(np.int32)).to(dev))
+    q = torch.from_numpy(wl.q).to(dev)
+    qsl = torch.from_numpy(wl.query_start_loc).to(dev)
+    out = torch.empty_like(q)
+
+    def call(i=0):
+        paged_attention(q, view.key_cache, view.value_cache, view.block_tables, view.kv_lens, qsl,
+                        k_scale=view.k_scales, v_scale=view.v_scales, single_token_decode=True, out=out)
+
+    warm(call, 0.3)
+    us = float(np.median(event_us(call, 50)))
+    nbytes = int(wl.kv_lens.astype(np.int64).sum()) * wl.num_kv_heads * 2 * wl.head_dim
+    kk = torch.randn(wl.num_seqs, wl.num_kv_heads, wl.head_dim, device=dev).half()
+    slot = torch.from_numpy((wl.block_tables[:, 0] * wl.block_size).astype(np.int32)).to(dev)
+    w = lambda i=0: view.write_slots(kk, kk, slot)  # noqa: E731
+    warm(w, 0.2)
+    wus = float(np.median(event_us(w, 100)))
+    return {"workload": "fp8 e4m3 cache, c2 shape: batch 32, Hq 32 / Hkv 8, D 128, page 128, ctx U[512,4096] (seed 2)",
+            "decode_us_p50": round(us, 2), "kv_bytes": nbytes, "kv_GBs": round(nbytes / (us * 1e3), 1),
+            "write_32_tokens_us_p50": round(wus, 2)}
+
+
 def aux_quantize_on_write(dev):
     """Fused quantize-on-write (4-bit, group 64): one appended token per c2 sequence; 4 x 512-token chunks."""
     import torch
@@ -350,6 +392,7 @@ def main():
         aux["c4_long_context"] = aux_c4(dev)
         torch.cuda.empty_cache()
         aux["quantize_on_write"] = aux_quantize_on_write(dev)
+        aux["fp8_cache"] = aux_fp8(dev)
 
     value = bytes_per_step / (ms_per_step * 1e-3) / 1e9
     traffic, traffic_src = measured_traffic()
