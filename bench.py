@@ -291,7 +291,7 @@ def aux_fp8(dev):
     wus = float(np.median(event_us(w, 100)))
     return {"workload": "fp8 e4m3 cache, c2 shape: batch 32, Hq 32 / Hkv 8, D 128, page 128, ctx U[512,4096] (seed 2)",
             "decode_us_p50": round(us, 2), "kv_bytes": nbytes, "kv_GBs": round(nbytes / (us * 1e3), 1),
-            "write_32_tokens_us_p50": round(wus, 2)}
+            "frac": round(nbytes / (us * 1e3) / HBM_PEAK_GBS, 4), "write_32_tokens_us_p50": round(wus, 2)}
 
 
 def aux_quantize_on_write(dev):

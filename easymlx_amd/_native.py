@@ -48,7 +48,7 @@ SIGNATURES: dict[str, tuple] = {
     "emx_fp8_cache_write": (_I, [_P, _P, _I, _P, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _SZ, _P]),
     "emx_paged_attention_fp8": (
         _I,
-        [_P, _I, _I, _I, _I, _P, _P, _P, _P, _I, _I, _I, _P, _I, _I, _P, _P, _F, _I, _I, _P, _P],
+        [_P, _I, _I, _I, _I, _P, _P, _P, _P, _I, _I, _I, _P, _I, _I, _P, _P, _F, _I, _I, _P, _SZ, _P, _P],
     ),
 }
 

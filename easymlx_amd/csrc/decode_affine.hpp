@@ -60,7 +60,9 @@ struct DecodeArgs {
   float scale_log2;           // softmax_scale * log2(e)
   int window;                 // sliding window, 0 = off
   int num_waves;              // waves of the persistent decode grid
-  int nt;                     // tokens per work item (64 at 4-bit, 32 at 8-bit)
+  int nt;                     // tokens per work item (64 at 4-bit, 32 at 8-bit and FP8)
+  const float* kps;           // FP8 pages only: key / value scale per page [nb]
+  const float* vps;
 };
 
 constexpr int kMaxSeqs = 2048;    // per-sequence table held in LDS
@@ -374,6 +376,8 @@ __device__ __forceinline__ void store_f32x4(const f32x4 v, const __amdgpu_buffer
 // O = sum_p 2^(m_p - M) o_p, L = sum_p 2^(m_p - M) l_p, M = max_p m_p.  To the
 // fp16 output (out != nullptr: O / L) or back into slot `dst` as a partial.
 // Lane owns float4 f = lane + 64k of the unit's HG*D values (head 4f/128).
+// The loads of NB pieces (all of a lane's float4s) are in flight together:
+// each batch costs one round trip to the coherent cache.
 template <int HG>
 __device__ __forceinline__ void merge_range(const __amdgpu_buffer_rsrc_t ro, const __amdgpu_buffer_rsrc_t rm,
                                             const int first, const int count, const int stride, h16* out,
@@ -381,43 +385,66 @@ __device__ __forceinline__ void merge_range(const __amdgpu_buffer_rsrc_t ro, con
   constexpr int D = 128;
   constexpr int NF4 = HG * D / 4;
   constexpr int PL = (NF4 + 63) / 64;
+  constexpr int KC = PL <= 2 ? PL : 2;  // float4s per lane merged together
+  constexpr int NB = 8 / KC / (PL <= 2 ? 1 : 2);  // pieces per batch (fewer with more values: no spills)
+  // lanes past the unit's values (HG = 1) read inside the buffer and write nothing
+  auto fidx = [&](int k) { return NF4 % 64 == 0 ? lane + 64 * k : min(lane + 64 * k, NF4 - 1); };
+#pragma unroll 1
+  for (int k0 = 0; k0 < PL; k0 += KC) {
+    float M[KC], L[KC];
+    f32x4 O[KC];
 #pragma unroll
-  for (int k = 0; k < PL; ++k) {
-    const int f = lane + 64 * k;
-    if (NF4 % 64 != 0 && f >= NF4) break;
-    const int h = 4 * f / D;
-    float M = -INFINITY, L = 0.f;
-    f32x4 O = {0.f, 0.f, 0.f, 0.f};
-    for (int p0 = 0; p0 < count; p0 += 4) {
-      f32x4 o[4];
-      f32x2 ml[4];
+    for (int k = 0; k < KC; ++k) {
+      M[k] = -INFINITY;
+      L[k] = 0.f;
+      O[k] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    for (int p0 = 0; p0 < count; p0 += NB) {
+      f32x4 o[NB][KC];
+      f32x2 ml[NB][KC];
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {  // four partials' loads in flight together
+      for (int c = 0; c < NB; ++c) {
         const int p = first + min(p0 + c, count - 1) * stride;
-        o[c] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(ro, f * 16, p * HG * D * 4, kCoherent));
-        ml[c] = __builtin_bit_cast(f32x2, __builtin_amdgcn_raw_buffer_load_b64(rm, h * 8, p * HG * 8, kCoherent));
+#pragma unroll
+        for (int k = 0; k < KC; ++k) {
+          const int f = fidx(k0 + k), h = 4 * f / D;
+          o[c][k] = __builtin_bit_cast(f32x4,
+                                       __builtin_amdgcn_raw_buffer_load_b128(ro, f * 16, p * HG * D * 4, kCoherent));
+          ml[c][k] =
+              __builtin_bit_cast(f32x2, __builtin_amdgcn_raw_buffer_load_b64(rm, h * 8, p * HG * 8, kCoherent));
+        }
       }
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        if (p0 + c >= count || ml[c].x == -INFINITY) continue;  // a piece may hold no live token (invalid pages)
-        const float Mn = fmaxf(M, ml[c].x);
-        const float fo = __builtin_amdgcn_exp2f(M - Mn);  // 0 while M is -inf
-        const float fp = __builtin_amdgcn_exp2f(ml[c].x - Mn);
-        O = O * fo + o[c] * fp;
-        L = L * fo + ml[c].y * fp;
-        M = Mn;
+      for (int c = 0; c < NB; ++c) {
+        if (p0 + c >= count) break;
+#pragma unroll
+        for (int k = 0; k < KC; ++k) {
+          if (ml[c][k].x == -INFINITY) continue;  // a piece may hold no live token (invalid pages)
+          const float Mn = fmaxf(M[k], ml[c][k].x);
+          const float fo = __builtin_amdgcn_exp2f(M[k] - Mn);  // 0 while M is -inf
+          const float fp = __builtin_amdgcn_exp2f(ml[c][k].x - Mn);
+          O[k] = O[k] * fo + o[c][k] * fp;
+          L[k] = L[k] * fo + ml[c][k].y * fp;
+          M[k] = Mn;
+        }
       }
     }
-    if (out != nullptr) {
-      const float inv = L > 0.f ? 1.f / L : 0.f;
-      typedef h16 h16x4 __attribute__((ext_vector_type(4)));
-      *reinterpret_cast<h16x4*>(out + 4 * f) = h16x4{(h16)(O[0] * inv), (h16)(O[1] * inv), (h16)(O[2] * inv),
-                                                      (h16)(O[3] * inv)};
-    } else {
-      store_f32x4(O, ro, f * 16, dst * HG * D * 4);
-      if ((4 * f) % D == 0)
-        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, f32x2{M, L}), rm, h * 8, dst * HG * 8,
-                                              kCoherent);
+#pragma unroll
+    for (int k = 0; k < KC; ++k) {
+      const int f = lane + 64 * (k0 + k);
+      if (NF4 % 64 != 0 && f >= NF4) break;
+      const int h = 4 * f / D;
+      if (out != nullptr) {
+        const float inv = L[k] > 0.f ? 1.f / L[k] : 0.f;
+        typedef h16 h16x4 __attribute__((ext_vector_type(4)));
+        *reinterpret_cast<h16x4*>(out + 4 * f) = h16x4{(h16)(O[k][0] * inv), (h16)(O[k][1] * inv),
+                                                        (h16)(O[k][2] * inv), (h16)(O[k][3] * inv)};
+      } else {
+        store_f32x4(O[k], ro, f * 16, dst * HG * D * 4);
+        if ((4 * f) % D == 0)
+          __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, f32x2{M[k], L[k]}), rm, h * 8,
+                                                dst * HG * 8, kCoherent);
+      }
     }
   }
 }

@@ -16,6 +16,7 @@
 #include "decode_q4.hpp"
 #include "quantize.hpp"
 #include "fp8.hpp"
+#include "decode_fp8.hpp"
 
 namespace {
 
@@ -153,6 +154,17 @@ PrefillFn pick_prefill_fp8(int hg) {
   return nullptr;
 }
 
+DecodeFn pick_decode_fp8(int hg) {
+  switch (hg) {
+    case 1: return emx::decode_fp8_d128<1>;
+    case 2: return emx::decode_fp8_d128<2>;
+    case 4: return emx::decode_fp8_d128<4>;
+    case 8: return emx::decode_fp8_d128<8>;
+    case 16: return emx::decode_fp8_d128<16>;
+  }
+  return nullptr;
+}
+
 template <int BITS>
 PrefillFn pick_prefill_gs(int gs, int hg) {
   switch (gs) {
@@ -279,7 +291,7 @@ int emx_affine_cache_write(const void* keys, const void* values, const int32_t* 
 size_t emx_paged_workspace_bytes(int num_seqs, int num_q_heads, int num_kv_heads, int head_dim,
                                  int max_blocks_per_seq, int page_size) {
   if (num_seqs <= 0 || num_kv_heads <= 0 || num_q_heads <= 0 || max_blocks_per_seq <= 0 || page_size <= 0 ||
-      head_dim != 128 || page_size % 128 != 0 || num_seqs > emx::kMaxSeqs ||
+      head_dim != 128 || page_size % 32 != 0 || num_seqs > emx::kMaxSeqs ||
       (long)num_seqs * num_kv_heads > emx::kMaxUnits)
     return 0;
   const int hg = num_q_heads / num_kv_heads;
@@ -551,7 +563,8 @@ int emx_paged_attention_fp8(const void* queries, int num_tokens, int num_q_heads
                             const float* v_scale, int num_blocks, int page_size, int num_kv_heads,
                             const int32_t* block_tables, int num_seqs, int max_blocks_per_seq, const int32_t* kv_lens,
                             const int32_t* query_start_loc, float softmax_scale, int sliding_window,
-                            int single_token_decode, void* out, void* stream) {
+                            int single_token_decode, void* workspace, size_t workspace_bytes, void* out,
+                            void* stream) {
   int rc = validate_common(queries, num_tokens, num_q_heads, head_dim, num_kv_heads, num_blocks, page_size,
                            block_tables, num_seqs, max_blocks_per_seq, kv_lens, query_start_loc, single_token_decode,
                            out);
@@ -577,12 +590,15 @@ int emx_paged_attention_fp8(const void* queries, int num_tokens, int num_q_heads
   ga.scale_log2 = softmax_scale * emx::kLog2e;
   ga.window = sliding_window > 0 ? sliding_window : 0;
   ga.decode = single_token_decode ? 1 : 0;
-  // head_dim 128, fp16 queries: the MFMA kernel over every row (a decode row is a
-  // tile of one query token); other shapes run on the generic kernel
   const int hg = num_q_heads / num_kv_heads;
-  const PrefillFn pf = pick_prefill_fp8(hg);
-  if (pf && dtype == EMX_DTYPE_F16 && head_dim == 128 && page_size % 32 == 0 && query_start_loc &&
-      num_seqs <= emx::kMaxSeqs && aligned16(key_cache) && aligned16(value_cache)) {
+  const bool mfma_ok = dtype == EMX_DTYPE_F16 && head_dim == 128 && page_size % 32 == 0 &&
+                       num_seqs <= emx::kMaxSeqs && aligned16(queries) && aligned16(key_cache) &&
+                       aligned16(value_cache);
+  const size_t need =
+      emx_paged_workspace_bytes(num_seqs, num_q_heads, num_kv_heads, head_dim, max_blocks_per_seq, page_size);
+  const DecodeFn dfn = mfma_ok && need > 0 ? pick_decode_fp8(hg) : nullptr;
+  const PrefillFn pf = mfma_ok ? pick_prefill_fp8(hg) : nullptr;
+  auto launch_prefill = [&](int min_q) {
     emx::PrefillArgs p{};
     p.q = reinterpret_cast<const emx::h16*>(queries);
     p.block_tables = block_tables;
@@ -597,7 +613,7 @@ int emx_paged_attention_fp8(const void* queries, int num_tokens, int num_q_heads
     p.max_blocks = max_blocks_per_seq;
     p.scale_log2 = ga.scale_log2;
     p.window = ga.window;
-    p.min_q = 1;
+    p.min_q = min_q;
     p.k8 = key_cache;
     p.v8 = value_cache;
     p.kps = k_scale;
@@ -606,7 +622,46 @@ int emx_paged_attention_fp8(const void* queries, int num_tokens, int num_q_heads
     const long grid = (long)((num_tokens + tokb - 1) / tokb + num_seqs) * num_kv_heads;
     hipLaunchKernelGGL(pf, dim3((unsigned)grid), dim3(256), 0, st, p);
     return check_launch("prefill_affine_d128 (fp8)");
+  };
+  // head_dim 128, fp16 queries: decode rows (one query token) on the split-K FP8
+  // decode kernel, rows of longer queries on the MFMA prefill kernel
+  if (dfn && (single_token_decode || (pf && query_start_loc))) {
+    if (workspace == nullptr || workspace_bytes < need)
+      return fail(EMX_ERR_INVALID, "workspace too small: need %zu bytes, got %zu", need, workspace_bytes);
+    if (!single_token_decode)
+      if (int r = launch_prefill(2)) return r;
+    const int nw = decode_num_waves();
+    emx::DecodeArgs a{};
+    a.q = reinterpret_cast<const emx::h16*>(queries);
+    a.kc = reinterpret_cast<const uint32_t*>(key_cache);
+    a.vc = reinterpret_cast<const uint32_t*>(value_cache);
+    a.kps = k_scale;
+    a.vps = v_scale;
+    a.block_tables = block_tables;
+    a.kv_lens = kv_lens;
+    a.qsl = single_token_decode ? nullptr : query_start_loc;
+    a.out = reinterpret_cast<emx::h16*>(out);
+    const size_t slots = (size_t)decode_max_waves() + (size_t)num_seqs * num_kv_heads;
+    a.ws_cnt = reinterpret_cast<int*>(workspace);
+    a.ws_cnt_grp = a.ws_cnt + emx::kMaxUnits;
+    a.ws_o = reinterpret_cast<float*>(a.ws_cnt + kCounterInts);
+    a.ws_ml = a.ws_o + slots * hg * head_dim;
+    a.S = num_seqs;
+    a.Hq = num_q_heads;
+    a.Hkv = num_kv_heads;
+    a.bs = page_size;
+    a.nb = num_blocks;
+    a.max_blocks = max_blocks_per_seq;
+    a.scale_log2 = ga.scale_log2;
+    a.window = ga.window;
+    a.num_waves = nw;
+    a.nt = emx::kFp8DecodeNT;
+    hipLaunchKernelGGL(dfn, dim3((unsigned)(nw / 4)), dim3(256), 0, st, a);
+    return check_launch("decode_fp8_d128");
   }
+  // other GQA ratios: the MFMA prefill kernel over every row (a decode row is a
+  // tile of one query token)
+  if (pf && query_start_loc) return launch_prefill(1);
   const emx::Fp8KV kv{key_cache, value_cache, k_scale, v_scale, num_kv_heads, head_dim, page_size};
   switch (dtype) {
     case EMX_DTYPE_F16: return launch_generic<emx::h16>(ga, kv, st);

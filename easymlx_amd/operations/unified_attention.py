@@ -221,13 +221,18 @@ def paged_attention(
         v_scale = v_scale.to(device=dev, dtype=torch.float32).contiguous()
         if k_scale.numel() != nb or v_scale.numel() != nb:
             raise ValueError("k_scale/v_scale must hold one scale per block: [num_blocks]")
+        need = int(lib.emx_paged_workspace_bytes(S, hq, hkv, d, max_blocks, bs))
+        if need and workspace is None:
+            workspace = _workspace(dev, stream, need)
+        ws_ptr = workspace.data_ptr() if workspace is not None else None
+        ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
         _native.check(
             lib.emx_paged_attention_fp8(
                 queries.data_ptr(), total, hq, d, _DTYPE_CODE[queries.dtype],
                 key_cache.data_ptr(), value_cache.data_ptr(), k_scale.data_ptr(), v_scale.data_ptr(),
                 nb, bs, hkv, block_tables.data_ptr(), S, max_blocks, kv_lens.data_ptr(), query_start_loc.data_ptr(),
                 float(softmax_scale), int(sliding_window), int(bool(single_token_decode)),
-                out.data_ptr(), stream,
+                ws_ptr, ws_bytes, out.data_ptr(), stream,
             )
         )
         return out

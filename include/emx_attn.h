@@ -69,7 +69,8 @@ int emx_affine_cache_write(const void* keys, const void* values, const int32_t* 
                            void* v_biases, void* stream);
 
 /*
- * Bytes of device workspace emx_paged_attention_affine needs for split-K
+ * Bytes of device workspace emx_paged_attention_affine and
+ * emx_paged_attention_fp8 need for split-K
  * partial results and arrival counters (0 if the call needs none).  The
  * workspace must be zero-filled before its first use; every call leaves its
  * counter region zeroed again, so one workspace serves any sequence of calls
@@ -141,6 +142,10 @@ int emx_fp8_cache_write(const void* keys, const void* values, int dtype, const i
  * Paged attention over an FP8 (E4M3) cache key/value [num_blocks, page_size,
  * Hkv, head_dim] uint8 with per-page fp32 scales k_scale/v_scale [num_blocks]:
  * K = dec(code) * k_scale[page].  queries/out in dtype (EMX_DTYPE_*).
+ * With fp16 queries, head_dim 128 and page_size % 32 == 0, decode rows run on
+ * the split-K decode kernel, which needs the workspace sized by
+ * emx_paged_workspace_bytes (same rules as emx_paged_attention_affine);
+ * other calls ignore it.
  * Replaces: paged_attention(..., k_scale=, v_scale=)
  *   lib/python/easymlx/operations/kernels/unified_attention.py:1377-1512 with the
  *   FP8 kernels :776-1268 (decoder :1275-1285).
@@ -150,7 +155,8 @@ int emx_paged_attention_fp8(const void* queries, int num_tokens, int num_q_heads
                             const float* v_scale, int num_blocks, int page_size, int num_kv_heads,
                             const int32_t* block_tables, int num_seqs, int max_blocks_per_seq, const int32_t* kv_lens,
                             const int32_t* query_start_loc, float softmax_scale, int sliding_window,
-                            int single_token_decode, void* out, void* stream);
+                            int single_token_decode, void* workspace, size_t workspace_bytes, void* out,
+                            void* stream);
 
 #ifdef __cplusplus
 }

@@ -150,3 +150,24 @@ def test_fp8_registered_op(cuda):
     torch.cuda.synchronize()
     assert torch.equal(res.attention_outputs, out_ref)
     assert_attention_close(res.attention_outputs.float().cpu().numpy(), exp, "fp8 op")
+
+
+@pytest.mark.parametrize("hq,hkv,bs", [(8, 8, 32), (16, 8, 64), (64, 8, 128), (32, 2, 32)])
+def test_fp8_decode_gqa_and_page_sizes(cuda, hq, hkv, bs):
+    """Split-K FP8 decode over GQA 1/2/8/16 and pages of 32/64/128 tokens."""
+    print(f"[fp8 decode hq={hq} hkv={hkv} bs={bs}]", flush=True)
+    wl = decode_workload(seed=25 + hq + bs, num_seqs=7, num_q_heads=hq, num_kv_heads=hkv, block_size=bs,
+                         ctx_range=(1, 900), bits=None)
+    out, exp, _ = _attention_case(cuda, wl, hold_last=True)
+    assert_attention_close(out.float().cpu().numpy(), exp, f"fp8 decode {hq}/{hkv} bs {bs}")
+
+
+def test_fp8_decode_window_and_long_context(cuda):
+    """40,000-token contexts: more than 16 pieces per unit (two-level merge); then a sliding window."""
+    print("[fp8 decode long]", flush=True)
+    wl = decode_workload(seed=31, num_seqs=2, fixed_ctx=40000, bits=None)
+    out, exp, _ = _attention_case(cuda, wl, hold_last=True)
+    assert_attention_close(out.float().cpu().numpy(), exp, "fp8 decode long")
+    wl = decode_workload(seed=32, num_seqs=9, ctx_range=(1, 2000), bits=None)
+    out, exp, _ = _attention_case(cuda, wl, hold_last=True, sliding_window=200)
+    assert_attention_close(out.float().cpu().numpy(), exp, "fp8 decode window")
