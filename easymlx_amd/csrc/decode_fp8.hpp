@@ -23,7 +23,9 @@
 // Per item (lane l: i = l % 16, jj = l / 16)
 //   QK^T : 2 token sub-tiles x 4 dim slices of v_mfma_f32_16x16x32_f16.
 //          A row i of sub-tile at = token 16 at + i; lane jj holds that token's
-//          dims 32 jj .. 32 jj + 31 (two 16-byte loads).  B column h = query
+//          dims 16 jj .. 16 jj + 15 and 64 + 16 jj .. 64 + 16 jj + 15 (two
+//          16-byte loads; a load instruction reads 64 contiguous bytes of each
+//          row), slices 0-1 the first half, 2-3 the second.  B column h = query
 //          head h of the GQA group (zero beyond HG).  Output rows 4 jj + r:
 //          lane (h, jj) holds the scores of tokens 16 at + 4 jj + r.
 //   softmax: online, base 2, fp32.
@@ -76,7 +78,7 @@ __device__ __forceinline__ void fp8_issue(Fp8Loads& L, const Fp8Rsrc& rs, const 
   for (int at = 0; at < 2; ++at) {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(rs.k, lk + 16 * h, at * 16 * rs_, kLoadAux);
+      const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(rs.k, lk + 64 * h, at * 16 * rs_, kLoadAux);
 #pragma unroll
       for (int c = 0; c < 4; ++c) L.k[at][4 * h + c] = x[c];
     }
@@ -221,13 +223,13 @@ __global__ __launch_bounds__(256, 2) void decode_fp8_d128(DecodeArgs a) {
   };
   int blkv = blk_chunk(g0);
 
-  // query operand: lane (h, jj) holds dims 32 jj .. 32 jj + 31 of head h
+  // query operand: lane (h, jj) holds dims 16 jj .. 16 jj + 15 and 64 + 16 jj .. of head h
   u32x4 qraw[4];
   auto issue_q = [&](int seq, int kh) {
     const u32x4* qp = reinterpret_cast<const u32x4*>(
-        a.q + ((size_t)qrw[seq] * a.Hq + (size_t)kh * HG + (col_ok ? col : 0)) * D + 32 * jj);
+        a.q + ((size_t)qrw[seq] * a.Hq + (size_t)kh * HG + (col_ok ? col : 0)) * D + 16 * jj);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) qraw[i] = qp[i];
+    for (int i = 0; i < 4; ++i) qraw[i] = qp[(i & 1) + 8 * (i >> 1)];
   };
   h16x8 qB[4];
   auto build_q = [&]() {
@@ -248,7 +250,7 @@ __global__ __launch_bounds__(256, 2) void decode_fp8_d128(DecodeArgs a) {
   int it_lo = start_k / NT;
 
   const int RS = Hkv * D;
-  const int lk = col * RS + 32 * jj;
+  const int lk = col * RS + 16 * jj;
   const int lv = 4 * jj * RS + 8 * col;
   const float kl2 = a.scale_log2 * 256.0f;
 

@@ -40,13 +40,15 @@ int check_launch(const char* what) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// Waves per SIMD the persistent decode grid is sized for (its launch bounds
-// allow 2); EMX_DECODE_WAVES_PER_SIMD overrides it for tuning (1..2).
+// Waves per SIMD the persistent 16x16 / FP8 decode grid is sized for (launch
+// bounds allow 2; one measured faster: these kernels are latency-bound, and more
+// waves add split-K pieces rather than bandwidth); EMX_DECODE_WAVES_PER_SIMD
+// overrides it for tuning (1..2).
 int decode_waves_per_simd() {
   static const int v = [] {
     const char* e = std::getenv("EMX_DECODE_WAVES_PER_SIMD");
-    const int x = e ? std::atoi(e) : 2;
-    return x >= 1 && x <= 2 ? x : 2;
+    const int x = e ? std::atoi(e) : 1;
+    return x >= 1 && x <= 2 ? x : 1;
   }();
   return v;
 }
@@ -60,7 +62,15 @@ int device_cus() {
   return cus;
 }
 
-int decode_num_waves() { return device_cus() * 4 * decode_waves_per_simd(); }
+int decode_num_waves() {
+  // EMX_DECODE_WAVES overrides the wave count (tuning; multiple of 4, at most kMaxWaves)
+  static const int ov = [] {
+    const char* e = std::getenv("EMX_DECODE_WAVES");
+    const int x = e ? std::atoi(e) : 0;
+    return x >= 4 && x <= emx::kMaxWaves && x % 4 == 0 ? x : 0;
+  }();
+  return ov ? ov : device_cus() * 4 * decode_waves_per_simd();
+}
 // The 4-bit kernel runs two four-wave workgroups per CU.
 int decode_q4_num_waves() { return device_cus() * 8; }
 // Partial slots are sized for the larger of the two persistent grids.
