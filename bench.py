@@ -163,8 +163,10 @@ class Setup:
         self._check = _native.check
         T, hq, d = (int(x) for x in q.shape)
         S = int(wl.block_tables.shape[0])
-        self.ws = torch.zeros(lib.emx_paged_workspace_bytes(S, hq, wl.num_kv_heads, d, wl.block_tables.shape[1],
-                                                            wl.block_size), dtype=torch.uint8, device=dev)
+        nws = lib.emx_paged_workspace_bytes(S, hq, wl.num_kv_heads, d, wl.block_tables.shape[1], wl.block_size)
+        if not wl.single_token_decode:  # the prefill key split's partial states
+            nws += lib.emx_paged_prefill_workspace_bytes(T, S, hq, wl.num_kv_heads, d)
+        self.ws = torch.zeros(nws, dtype=torch.uint8, device=dev)
         stream = torch.cuda.current_stream(dev).cuda_stream
         self.args = [
             (q.data_ptr(), T, hq, d, p.k_codes.data_ptr(), p.k_scales.data_ptr(), p.k_biases.data_ptr(),

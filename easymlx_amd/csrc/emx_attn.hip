@@ -77,7 +77,32 @@ int decode_q4_num_waves() { return device_cus() * 8; }
 int decode_max_waves() { return std::max(decode_num_waves(), decode_q4_num_waves()); }
 
 // Unit counters, then per-group counters indexed by partial slot (< kMaxWaves + kMaxUnits).
-constexpr size_t kCounterInts = 2 * (size_t)emx::kMaxUnits + emx::kMaxWaves;
+// Then the prefill key-split counters.
+constexpr size_t kCounterInts = 2 * (size_t)emx::kMaxUnits + emx::kMaxWaves + emx::kPrefillCounters;
+constexpr size_t kPrefillCounterOff = 2 * (size_t)emx::kMaxUnits + emx::kMaxWaves;
+
+// Prefill tiles per kv head a call with num_tokens query rows can have: a
+// sequence with q >= 2 query tokens has ceil(q / tokb) <= q / tokb + 1 tiles.
+long prefill_max_items(int num_tokens, int num_seqs, int tokb) {
+  return (long)(num_tokens + tokb - 1) / tokb + std::min(num_seqs, num_tokens / 2);
+}
+
+// Wires the key split of the prefill kernel when the workspace holds the
+// partial states after the decode region (`need` bytes).
+void prefill_split(emx::PrefillArgs& p, int num_tokens, int num_q_heads, int num_kv_heads, void* workspace,
+                   size_t workspace_bytes, size_t need) {
+  p.nparts = 1;
+  p.max_items = 0;
+  p.ws_cnt = nullptr;
+  p.ws_part = nullptr;
+  const size_t extra = emx_paged_prefill_workspace_bytes(num_tokens, p.S, num_q_heads, num_kv_heads, 128);
+  if (extra == 0 || workspace == nullptr || workspace_bytes < need + extra) return;
+  const size_t base = (need + 255) & ~(size_t)255;
+  p.nparts = emx::kPrefillParts;
+  p.max_items = (int)prefill_max_items(num_tokens, p.S, 128 / (num_q_heads / num_kv_heads));
+  p.ws_cnt = reinterpret_cast<int*>(workspace) + kPrefillCounterOff;
+  p.ws_part = reinterpret_cast<float*>(static_cast<char*>(workspace) + base);
+}
 
 bool decode_fast_path(int head_dim, int page_size, int bits, int group_size, int hg, int num_seqs) {
   if (head_dim != 128 || page_size % 128 != 0 || num_seqs > emx::kMaxSeqs) return false;
@@ -298,6 +323,18 @@ int emx_affine_cache_write(const void* keys, const void* values, const int32_t* 
   return check_launch("affine_cache_write");
 }
 
+size_t emx_paged_prefill_workspace_bytes(int num_tokens, int num_seqs, int num_q_heads, int num_kv_heads,
+                                         int head_dim) {
+  if (num_tokens <= 0 || num_seqs <= 0 || num_kv_heads <= 0 || num_q_heads <= 0 || head_dim != 128 ||
+      num_q_heads % num_kv_heads != 0)
+    return 0;
+  const int hg = num_q_heads / num_kv_heads;
+  if (hg > 16 || (hg & (hg - 1)) != 0) return 0;
+  const long items = prefill_max_items(num_tokens, num_seqs, 128 / hg);
+  if (items * num_kv_heads * 4 > emx::kPrefillCounters) return 0;
+  return 256 + (size_t)items * num_kv_heads * emx::kPrefillParts * emx::kPrefillPartBytes;
+}
+
 size_t emx_paged_workspace_bytes(int num_seqs, int num_q_heads, int num_kv_heads, int head_dim,
                                  int max_blocks_per_seq, int page_size) {
   if (num_seqs <= 0 || num_kv_heads <= 0 || num_q_heads <= 0 || max_blocks_per_seq <= 0 || page_size <= 0 ||
@@ -372,12 +409,13 @@ int emx_paged_attention_affine(const void* queries, int num_tokens, int num_q_he
       p.scale_log2 = scale_log2;
       p.window = window;
       p.min_q = 2;
+      prefill_split(p, num_tokens, num_q_heads, num_kv_heads, workspace, workspace_bytes, need);
       PrefillFn pf = bits == 4 ? pick_prefill_gs<4>(group_size, hg) : pick_prefill_gs<8>(group_size, hg);
       if (!pf)
         return fail(EMX_ERR_UNSUPPORTED, "no prefill kernel for bits=%d group_size=%d gqa=%d", bits, group_size, hg);
       // tiles of 128/hg query tokens: at most num_tokens/tile + num_seqs of them per kv head
       const int tokb = 128 / hg;
-      const long grid = (long)((num_tokens + tokb - 1) / tokb + num_seqs) * num_kv_heads;
+      const long grid = (long)((num_tokens + tokb - 1) / tokb + num_seqs) * num_kv_heads * p.nparts;
       hipLaunchKernelGGL(pf, dim3((unsigned)grid), dim3(256), 0, st, p);
       if (int r = check_launch("prefill_affine_d128")) return r;
     }
@@ -628,8 +666,9 @@ int emx_paged_attention_fp8(const void* queries, int num_tokens, int num_q_heads
     p.v8 = value_cache;
     p.kps = k_scale;
     p.vps = v_scale;
+    prefill_split(p, num_tokens, num_q_heads, num_kv_heads, workspace, workspace_bytes, need);
     const int tokb = 128 / hg;
-    const long grid = (long)((num_tokens + tokb - 1) / tokb + num_seqs) * num_kv_heads;
+    const long grid = (long)((num_tokens + tokb - 1) / tokb + num_seqs) * num_kv_heads * p.nparts;
     hipLaunchKernelGGL(pf, dim3((unsigned)grid), dim3(256), 0, st, p);
     return check_launch("prefill_affine_d128 (fp8)");
   };

@@ -54,7 +54,20 @@ struct PrefillArgs {
   const uint8_t* v8;
   const float* kps;             // [nb]
   const float* vps;             // [nb]
+  // Key split: a tile with many key steps is cut into up to nparts parts (one
+  // workgroup each); every wave stores its part's state and the last of a
+  // wave's parts merges them.  nparts = 1: no split (ws_* unused).
+  int nparts;
+  int max_items;                // tiles the workspace holds per kv head
+  int* ws_cnt;                  // [max_items * Hkv * 4] arrival counters: zero before and after every launch
+  float* ws_part;               // [max_items * Hkv][kPrefillParts][kPrefillPartFloats]
 };
+
+constexpr int kPrefillParts = 3;          // most parts a tile is split into
+constexpr int kPrefillSplitKeys = 768;    // keys per part the split aims at
+constexpr int kPrefillPartVec = 17;       // f32x4 per lane of a stored state: acc[2][8], (m0, m1, l0, l1)
+constexpr int kPrefillPartBytes = 4 * kPrefillPartVec * 64 * 16;  // one part of one workgroup
+constexpr int kPrefillCounters = 65536;   // arrival counters (max_items * Hkv * 4 must fit)
 
 template <int BITS, int GS, int HG>
 struct PrefillCfg {
@@ -103,20 +116,46 @@ __global__ __launch_bounds__(256, 2) void prefill_affine_d128(PrefillArgs a) {
   const int jj = lane >> 4;
 
   // ---- work item: blockIdx -> (sequence, tile, kv_head); later tiles (more keys) first
+  // ---- per-sequence tile counts, scanned by the whole workgroup (one pass of
+  // global loads in parallel, not a serial walk by one thread)
   __shared__ int tcum[kMaxSeqs + 1];
-  if (tid == 0) {
-    int c = 0;
-    for (int s = 0; s < a.S; ++s) {
-      tcum[s] = c;
-      c += prefill_tiles(a, s, P::TOKB);
+  __shared__ int wred[4];
+  {
+    const int ch = (a.S + 255) / 256, s0 = tid * ch;
+    int tsum = 0;
+    for (int i = 0; i < ch; ++i) {
+      const int si = s0 + i;
+      if (si >= a.S) break;
+      const int nt = prefill_tiles(a, si, P::TOKB);
+      tcum[si] = nt;  // the count for now
+      tsum += nt;
     }
-    tcum[a.S] = c;
+    int x = tsum;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int y = __shfl_up(x, o, 64);
+      if (lane >= o) x += y;
+    }
+    if (lane == 63) wred[tid >> 6] = x;
+    __syncthreads();
+    int base = 0;
+    for (int w = 0; w < (tid >> 6); ++w) base += wred[w];
+    int run = base + x - tsum;
+    for (int i = 0; i < ch; ++i) {
+      const int si = s0 + i;
+      if (si >= a.S) break;
+      const int n = tcum[si];
+      tcum[si] = run;
+      run += n;
+    }
+    if (tid == 255) tcum[a.S] = base + x;
   }
   __syncthreads();
   const int ntiles = tcum[a.S];
-  const int item = blockIdx.x / a.Hkv;
-  if (item >= ntiles) return;
   const int kvh = blockIdx.x % a.Hkv;
+  const int part = (blockIdx.x / a.Hkv) % a.nparts;
+  const int item = blockIdx.x / a.Hkv / a.nparts;
+  if (item >= ntiles) return;
   int s = 0;
   while (tcum[s + 1] <= item) ++s;
   s = __builtin_amdgcn_readfirstlane(s);
@@ -145,7 +184,14 @@ __global__ __launch_bounds__(256, 2) void prefill_affine_d128(PrefillArgs a) {
   const int t_first = tok_lo, t_last = min(tok_lo + P::TOKB, qlen) - 1;
   const int k_hi = min(past + t_last, kv_len - 1);
   const int k_lo = a.window > 0 ? max(0, past + t_first - a.window + 1) : 0;
-  const int step_lo = k_lo / NT, step_hi = k_hi >= 0 ? k_hi / NT : -1;
+  const int steps_all = k_hi >= 0 ? max(k_hi / NT - k_lo / NT + 1, 0) : 0;
+  // parts of this tile: the steps split evenly, at most nparts, about kPrefillSplitKeys keys each
+  const int nparts = a.nparts > 1 && item < a.max_items
+                         ? max(1, min(a.nparts, (steps_all * NT + kPrefillSplitKeys - 1) / kPrefillSplitKeys))
+                         : 1;
+  if (part >= nparts) return;
+  const int step_lo = k_lo / NT + part * steps_all / nparts;
+  const int step_hi = k_lo / NT + (part + 1) * steps_all / nparts - 1;
 
   // ---- query operands: MFMA w spans dims [32w, 32w + 32); lane group jj holds dims
   // 32w + 8jj + i in the element order of the expanded keys (unpack4 / unpack8 order)
@@ -426,6 +472,50 @@ __global__ __launch_bounds__(256, 2) void prefill_affine_d128(PrefillArgs a) {
         const h16x8 Av = *reinterpret_cast<const h16x8*>(ve + (16 * dt + col) * P::VSTR + 32 * h + 8 * jj);
 #pragma unroll
         for (int ct = 0; ct < 2; ++ct) acc[ct][dt] = mfma16x16x32(Av, pB[ct], acc[ct][dt]);
+      }
+    }
+  }
+
+  // ---- split tile: store this wave's state; the wave arriving last among the parts merges
+  if (nparts > 1) {
+    const int u = item * a.Hkv + kvh;
+    const __amdgpu_buffer_rsrc_t rp =
+        uniform_rsrc(reinterpret_cast<uint8_t*>(a.ws_part) + (size_t)u * kPrefillParts * kPrefillPartBytes,
+                     kPrefillParts * kPrefillPartBytes);
+    auto vo = [&](int k) { return ((wv * kPrefillPartVec + k) * 64 + lane) * 16; };
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) store_f32x4(acc[ct][dt], rp, vo(8 * ct + dt), part * kPrefillPartBytes);
+    store_f32x4(f32x4{m_run[0], m_run[1], l_part[0], l_part[1]}, rp, vo(16), part * kPrefillPartBytes);
+    if (!arrive_last(a.ws_cnt + u * 4 + wv, nparts, lane)) return;
+    // every part (this one's too) read back in part order: the result does not
+    // depend on which part arrived last
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct) {
+      m_run[ct] = -INFINITY;
+      l_part[ct] = 0.f;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) acc[ct][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    for (int q = 0; q < nparts; ++q) {
+      f32x4 o[16];
+#pragma unroll
+      for (int k = 0; k < 16; ++k)
+        o[k] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rp, vo(k), q * kPrefillPartBytes,
+                                                                               kCoherent));
+      const f32x4 ml =
+          __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rp, vo(16), q * kPrefillPartBytes, kCoherent));
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct) {
+        const float m1 = ml[ct], l1 = ml[2 + ct];
+        const float mn = fmaxf(m_run[ct], m1);
+        const float f0 = m_run[ct] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run[ct] - mn);
+        const float f1 = m1 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m1 - mn);
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) acc[ct][dt] = acc[ct][dt] * f0 + o[8 * ct + dt] * f1;
+        l_part[ct] = l_part[ct] * f0 + l1 * f1;
+        m_run[ct] = mn;
       }
     }
   }

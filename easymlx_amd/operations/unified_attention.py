@@ -188,6 +188,8 @@ def paged_attention(
             raise NotImplementedError("affine paged attention takes fp16 queries")
         nb, hkv, bs = int(key_cache.shape[0]), int(key_cache.shape[1]), int(key_cache.shape[2])
         need = int(lib.emx_paged_workspace_bytes(S, hq, hkv, d, max_blocks, bs))
+        if need and not single_token_decode:  # room for the prefill key split
+            need += int(lib.emx_paged_prefill_workspace_bytes(total, S, hq, hkv, d))
         if need and workspace is None:
             workspace = _workspace(dev, stream, need)
         ws_ptr = workspace.data_ptr() if workspace is not None else None
@@ -222,6 +224,8 @@ def paged_attention(
         if k_scale.numel() != nb or v_scale.numel() != nb:
             raise ValueError("k_scale/v_scale must hold one scale per block: [num_blocks]")
         need = int(lib.emx_paged_workspace_bytes(S, hq, hkv, d, max_blocks, bs))
+        if need and not single_token_decode:  # room for the prefill key split
+            need += int(lib.emx_paged_prefill_workspace_bytes(total, S, hq, hkv, d))
         if need and workspace is None:
             workspace = _workspace(dev, stream, need)
         ws_ptr = workspace.data_ptr() if workspace is not None else None

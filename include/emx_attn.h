@@ -83,6 +83,19 @@ size_t emx_paged_workspace_bytes(int num_seqs, int num_q_heads, int num_kv_heads
                                  int max_blocks_per_seq, int page_size);
 
 /*
+ * Extra workspace bytes, after emx_paged_workspace_bytes(...), with which the
+ * prefill kernel of emx_paged_attention_affine / emx_paged_attention_fp8 cuts
+ * tiles of many keys into up to three parts (one workgroup each) and merges
+ * them in-kernel (0 if the shape cannot split).  A call whose workspace_bytes
+ * covers both sums splits; a smaller workspace runs every tile in one
+ * workgroup.  Same zero-fill and ordering rules as the decode workspace.
+ * No direct reference counterpart: the reference's prefill kernel runs one
+ * threadgroup per query row (unified_attention.py:290-465).
+ */
+size_t emx_paged_prefill_workspace_bytes(int num_tokens, int num_seqs, int num_q_heads, int num_kv_heads,
+                                         int head_dim);
+
+/*
  * Paged attention over affine pages; queries/out fp16 [num_tokens, Hq, head_dim].
  * block_tables int32 [num_seqs, max_blocks_per_seq]; kv_lens int32 [num_seqs];
  * query_start_loc int32 [num_seqs+1].  single_token_decode != 0 means token i

@@ -136,6 +136,11 @@ def test_fp8_unified_vs_oracle(cuda):
     assert_attention_close(out.float().cpu().numpy(), exp, "fp8 unified")
     out, exp, _ = _attention_case(cuda, wl, hold_last=False, sliding_window=64)
     assert_attention_close(out.float().cpu().numpy(), exp, "fp8 unified window")
+    # long contexts: prefill tiles split over workgroups and merged in-kernel
+    wl = unified_workload("fp8long", seed=26, num_prefill=2, chunk=100, prior_range=(1500, 2500), num_decode=3,
+                          decode_ctx=(1, 2000), bits=None)
+    out, exp, _ = _attention_case(cuda, wl, hold_last=False)
+    assert_attention_close(out.float().cpu().numpy(), exp, "fp8 unified long")
 
 
 def test_fp8_registered_op(cuda):

@@ -75,3 +75,31 @@ def test_kv_shorter_than_query_rows(cuda):
     assert_attention_close(got, exp, "short kv")
     assert np.all(got[:80] == 0)
     assert np.all(got[int(wl.query_start_loc[2])] == 0)
+
+
+@pytest.mark.parametrize("bits,window", [(4, 0), (8, 0), (4, 1000)])
+def test_prefill_key_split(cuda, bits, window):
+    """Tiles of long contexts split over up to three workgroups (merged in-kernel) vs the oracle and vs one
+    workgroup per tile (a workspace without room for the split); a repeat reuses the cleared counters."""
+    from easymlx_amd import _native
+
+    print(f"[prefill key split bits={bits} window={window}]", flush=True)
+    wl = unified_workload("split", seed=50 + bits, num_prefill=3, chunk=160, prior_range=(1500, 3000),
+                          num_decode=4, decode_ctx=(100, 3000), bits=bits)
+    view = gpu_cache(wl, cuda)
+    exp = oracle_expected(wl, sliding_window=window)
+    split = _run(wl, view, cuda, sliding_window=window)
+    assert_attention_close(split, exp, "split")
+    assert np.array_equal(_run(wl, view, cuda, sliding_window=window), split), "repeat differs"
+    lib = _native.load()
+    S, mb = wl.block_tables.shape
+    ws = torch.zeros(lib.emx_paged_workspace_bytes(S, wl.num_q_heads, wl.num_kv_heads, wl.head_dim, mb,
+                                                   wl.block_size), dtype=torch.uint8, device=cuda)
+    q = torch.from_numpy(wl.q).to(cuda)
+    whole = paged_attention(q, view.k_codes, view.v_codes, view.block_tables, view.kv_lens,
+                            torch.from_numpy(wl.query_start_loc).to(cuda), k_scales=view.k_scales,
+                            k_biases=view.k_biases, v_scales=view.v_scales, v_biases=view.v_biases, bits=wl.bits,
+                            group_size=wl.group_size, single_token_decode=False, sliding_window=window,
+                            workspace=ws).float().cpu().numpy()
+    assert_attention_close(whole, exp, "unsplit")
+    assert np.abs(whole - split).max() < 2e-3
