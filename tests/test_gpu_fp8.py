@@ -176,3 +176,25 @@ def test_fp8_decode_window_and_long_context(cuda):
     wl = decode_workload(seed=32, num_seqs=9, ctx_range=(1, 2000), bits=None)
     out, exp, _ = _attention_case(cuda, wl, hold_last=True, sliding_window=200)
     assert_attention_close(out.float().cpu().numpy(), exp, "fp8 decode window")
+
+
+def test_fp8_decode_edge_lengths_and_invalid_pages(cuda):
+    """kv_len 0 -> zeros; block id -1 / out-of-range pages are skipped like the reference's Metal kernel."""
+    print("[fp8 decode edges]", flush=True)
+    wl = decode_workload(seed=27, num_seqs=5, ctx_range=(300, 1200), bits=None)
+    view = _view(wl, cuda)
+    kc, vc, ks, vs = _write_per_sequence(wl, view, "f16", hold_last=True)
+    lens = wl.kv_lens.copy()
+    lens[1] = 0
+    tables = wl.block_tables.copy()
+    tables[2, 1] = -1
+    tables[3, 0] = wl.num_blocks + 7
+    bt = torch.from_numpy(tables).to(cuda)
+    kl = torch.from_numpy(lens).to(cuda)
+    out = paged_attention(torch.from_numpy(wl.q).to(cuda), view.key_cache, view.value_cache, bt, kl,
+                          torch.from_numpy(wl.query_start_loc).to(cuda), k_scale=view.k_scales,
+                          v_scale=view.v_scales).float().cpu().numpy()
+    exp = oracle_attention(wl.q.astype(np.float32), fp8.fp8_dequant_cache(kc, ks), fp8.fp8_dequant_cache(vc, vs),
+                           tables, lens, wl.query_start_loc, compute_dtype=np.float64)
+    assert_attention_close(out, exp, "fp8 edges")
+    assert np.all(out[1] == 0)
