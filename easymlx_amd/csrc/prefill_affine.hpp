@@ -332,22 +332,34 @@ __global__ __launch_bounds__(256, 2) void prefill_affine_d128(PrefillArgs a) {
       }
       return;
     }
+    // Two keys at a time in packed fp16: a pair of codes placed as 0x6400 | code is
+    // 1024 + code exactly; minus 1024, then one fused multiply-add with the keys'
+    // (scale, bias) pairs (single rounding to fp16, as the fp32 path rounds once).
+    typedef h16 h16x2 __attribute__((ext_vector_type(2)));
     const uint32_t* vw = reinterpret_cast<const uint32_t*>(raw_v) + dim * 8 + k0 / PW;
-    const h16* vsp = raw_s + (2 * G + g) * NT + k0;
-    const h16* vbp = raw_s + (3 * G + g) * NT + k0;
+    const uint32_t* vsp = reinterpret_cast<const uint32_t*>(raw_s + (2 * G + g) * NT + k0);
+    const uint32_t* vbp = reinterpret_cast<const uint32_t*>(raw_s + (3 * G + g) * NT + k0);
     h16* vd = ve + dim * P::VSTR + 32 * (k0 >> 5);
+    const h16x2 k1024 = {(h16)1024.0f, (h16)1024.0f};
 #pragma unroll
     for (int q4 = 0; q4 < TPT / 4; ++q4) {  // keys k0 + 4q4 .. +3 (consecutive slots)
       const int kk = (k0 & 31) + 4 * q4;     // key within its 32-key block
-      h16x4 o;
+      uint32_t o[2];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int e = 4 * q4 + r;  // value index of the thread
+      for (int hp = 0; hp < 2; ++hp) {
+        const int e = 4 * q4 + 2 * hp;  // first value index of the pair (keys e, e + 1 of the thread)
         const uint32_t x = vw[e / PW];
-        const float c = (float)((x >> v_shift<BITS>(e % PW)) & ((1u << BITS) - 1u));
-        o[r] = (h16)fmaf((float)vsp[e], c, (float)vbp[e]);
+        uint32_t pair;  // the two codes at bits 0 and 16
+        if constexpr (BITS == 4)
+          pair = (x >> (4 * ((e % PW) >> 1))) & 0x000F000Fu;  // keys 2m, 2m + 1 sit at nibbles m, m + 4
+        else
+          pair = __builtin_amdgcn_perm(0u, x, (e % PW) == 0 ? 0x0C010C00u : 0x0C030C02u);
+        const h16x2 c = __builtin_bit_cast(h16x2, pair | 0x64006400u) - k1024;
+        const h16x2 v = __builtin_elementwise_fma(c, __builtin_bit_cast(h16x2, vsp[e / 2]),
+                                                  __builtin_bit_cast(h16x2, vbp[e / 2]));
+        o[hp] = __builtin_bit_cast(uint32_t, v);
       }
-      *reinterpret_cast<h16x4*>(vd + pv_slot(kk)) = o;
+      *reinterpret_cast<u32x2*>(vd + pv_slot(kk)) = u32x2{o[0], o[1]};
     }
     // K scales / biases of the step in fp32
     for (int i = tid; i < 2 * G * NT; i += 256) ksf[i / (G * NT)][(i / NT) % G][i % NT] = (float)raw_s[i];
