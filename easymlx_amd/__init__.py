@@ -7,6 +7,7 @@ attention-operation plugin interface.
 """
 
 from .caching.paged import AffinePageCacheView, Fp8PageCacheView, PageCacheView, PageMetadata, build_query_start_loc
+from .caching.rope import RotaryEmbedding
 from .operations import AttentionOutput, BaseOperation, OperationRegistry, UnifiedAttention, paged_attention
 from .quantize import affine_quantize
 
@@ -18,6 +19,7 @@ __all__ = (
     "OperationRegistry",
     "PageCacheView",
     "PageMetadata",
+    "RotaryEmbedding",
     "UnifiedAttention",
     "affine_quantize",
     "build_query_start_loc",

@@ -149,13 +149,19 @@ class PageCacheView:
 
     # -- slot arithmetic shared by both views (cache.py:1127-1170, 1230-1261)
     def _slot_mapping(self, slot_ids, query_lens) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+        mapping, slots, base, _ = self._slot_mapping_positions(slot_ids, query_lens)
+        return mapping, slots, base
+
+    def _slot_mapping_positions(self, slot_ids, query_lens):
+        """Slot of every token, the sequences' slots and prior lengths, and every token's position."""
         dev = self.block_tables.device
         qlens = [max(0, int(q)) for q in query_lens]
         slots = torch.tensor(list(slot_ids), dtype=torch.long, device=dev)
         base = self.kv_lens.index_select(0, slots).to(torch.long)
         total = sum(qlens)
         if total == 0:
-            return torch.empty((0,), dtype=torch.int32, device=dev), slots, base
+            empty = torch.empty((0,), dtype=torch.int32, device=dev)
+            return empty, slots, base, empty
         qlen_t = torch.tensor(qlens, dtype=torch.long, device=dev)
         tok_slot = torch.repeat_interleave(slots, qlen_t, output_size=total)
         starts = [0]
@@ -169,7 +175,7 @@ class PageCacheView:
         blk = self.block_tables[tok_slot, col].to(torch.long)
         ok = (blk >= 0) & (pos // self.block_size < self.blocks_per_seq)
         mapping = torch.where(ok, blk * self.block_size + pos % self.block_size, torch.full_like(blk, -1))
-        return mapping.to(torch.int32), slots, base
+        return mapping.to(torch.int32), slots, base, pos.to(torch.int32)
 
     def _resolve(self, cache_metadata, slot_ids, query_lens, n_tokens):
         if slot_ids is None:
@@ -488,6 +494,52 @@ class AffinePageCacheView(PageCacheView):
             raise ValueError("slot_mapping must be [num_tokens]")
         if keys.shape[0]:
             self._write(keys, values, slot_mapping)
+
+    def concatenate_to_cache(self, queries, keys, values, *, cache_metadata, rope=None, slot_ids=None,
+                             query_lens=None):
+        """``PageCacheView.concatenate_to_cache`` with a :class:`RotaryEmbedding` fused in.
+
+        K turns inside the quantize-on-write kernel and Q in one launch
+        (``cache.py:1161-1166`` then ``:1186-1190``); any other ``rope`` callable
+        runs first, as in the reference, and the write follows.
+        """
+        from .rope import RotaryEmbedding
+
+        if not isinstance(rope, RotaryEmbedding) or rope.dims > self.head_dim or queries.shape[-1] != self.head_dim:
+            return super().concatenate_to_cache(queries, keys, values, cache_metadata=cache_metadata, rope=rope,
+                                                slot_ids=slot_ids, query_lens=query_lens)
+        slot_ids, qlens, single = self._resolve(cache_metadata, slot_ids, query_lens, int(queries.shape[0]))
+        slot_mapping, slots, base, positions = self._slot_mapping_positions(slot_ids, qlens)
+        lib = _native.load()
+        n = int(slot_mapping.numel())
+        q_out = queries.to(torch.float16).contiguous().clone()
+        if n:
+            keys = keys.to(torch.float16).contiguous()
+            values = values.to(torch.float16).contiguous()
+            inv = rope.inv_freq(keys.device)
+            stream = _stream_ptr(keys.device)
+            _native.check(lib.emx_rope_rows(q_out.data_ptr(), n, int(q_out.shape[1]), self.head_dim,
+                                            positions.data_ptr(), inv.data_ptr(), rope.dims, int(rope.traditional),
+                                            stream))
+            _native.check(
+                lib.emx_affine_cache_write_rope(
+                    keys.data_ptr(), values.data_ptr(), slot_mapping.data_ptr(), n, self.num_kv_heads,
+                    self.head_dim, self.group_size, self.bits, self.block_size, self.num_blocks,
+                    self.key_cache.data_ptr(), self.k_scales.data_ptr(), self.k_biases.data_ptr(),
+                    self.value_cache.data_ptr(), self.v_scales.data_ptr(), self.v_biases.data_ptr(),
+                    positions.data_ptr(), inv.data_ptr(), rope.dims, int(rope.traditional), stream,
+                )
+            )
+        if len(slot_ids):
+            add = torch.tensor(qlens, dtype=torch.int32, device=self.kv_lens.device)
+            self.kv_lens.index_copy_(0, slots, (base + add).to(torch.int32))
+        md = cache_metadata.with_cache_state(
+            block_tables=self.block_tables.index_select(0, slots) if len(slot_ids) else self.block_tables[:0],
+            kv_lens=self.kv_lens.index_select(0, slots) if len(slot_ids) else self.kv_lens[:0],
+            block_size=self.block_size,
+        )
+        md.is_single_token_decode = single
+        return q_out.to(queries.dtype), self.key_cache, self.value_cache, md
 
     def _zero_blocks(self, ids: torch.Tensor) -> None:
         for t in (self.key_cache, self.value_cache, self.k_scales, self.k_biases, self.v_scales, self.v_biases):

@@ -72,7 +72,15 @@ int decode_num_waves() {
   return ov ? ov : device_cus() * 4 * decode_waves_per_simd();
 }
 // The 4-bit kernel runs two four-wave workgroups per CU.
-int decode_q4_num_waves() { return device_cus() * 8; }
+int decode_q4_num_waves() {
+  // EMX_DECODE_Q4_WAVES overrides the wave count (tuning; multiple of 4, at most kMaxWaves)
+  static const int ov = [] {
+    const char* e = std::getenv("EMX_DECODE_Q4_WAVES");
+    const int x = e ? std::atoi(e) : 0;
+    return x >= 4 && x <= emx::kMaxWaves && x % 4 == 0 ? x : 0;
+  }();
+  return ov ? ov : device_cus() * 8;
+}
 // Partial slots are sized for the larger of the two persistent grids.
 int decode_max_waves() { return std::max(decode_num_waves(), decode_q4_num_waves()); }
 
@@ -269,10 +277,10 @@ int emx_affine_quantize(const void* x, long rows, int head_dim, int group_size, 
   return check_launch("affine_quantize");
 }
 
-int emx_affine_cache_write(const void* keys, const void* values, const int32_t* slot_mapping, int num_tokens,
-                           int num_kv_heads, int head_dim, int group_size, int bits, int page_size, int num_blocks,
-                           uint32_t* k_codes, void* k_scales, void* k_biases, uint32_t* v_codes, void* v_scales,
-                           void* v_biases, void* stream) {
+static int affine_write_impl(const void* keys, const void* values, const int32_t* slot_mapping, int num_tokens,
+                      int num_kv_heads, int head_dim, int group_size, int bits, int page_size, int num_blocks,
+                      uint32_t* k_codes, void* k_scales, void* k_biases, uint32_t* v_codes, void* v_scales,
+                      void* v_biases, const emx::RopeArgs& rope, void* stream) {
   if (num_tokens < 0) return fail(EMX_ERR_INVALID, "num_tokens must be >= 0");
   if (bits != 4 && bits != 8) return fail(EMX_ERR_UNSUPPORTED, "bits must be 4 or 8, got %d", bits);
   if (num_kv_heads <= 0 || head_dim <= 0 || page_size <= 0 || num_blocks <= 0)
@@ -305,8 +313,9 @@ int emx_affine_cache_write(const void* keys, const void* values, const int32_t* 
   if (head_dim / group_size > emx::kWriteMaxGroups || head_dim > emx::kWriteMaxDim)
     return fail(EMX_ERR_UNSUPPORTED, "head_dim %d above %d or more than %d quantization groups per head", head_dim,
                 emx::kWriteMaxDim, emx::kWriteMaxGroups);
+  a.rope = rope;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  if (num_tokens <= emx::kSmallWrite && head_dim % 16 == 0 && group_size % 16 == 0 &&
+  if (rope.inv_freq == nullptr && num_tokens <= emx::kSmallWrite && head_dim % 16 == 0 && group_size % 16 == 0 &&
       group_size <= emx::kSmallMaxGroup) {
     const dim3 sgrid((unsigned)num_kv_heads, (unsigned)(head_dim / 16));
     if (bits == 4)
@@ -321,6 +330,45 @@ int emx_affine_cache_write(const void* keys, const void* values, const int32_t* 
   else
     hipLaunchKernelGGL(emx::affine_cache_write<8>, grid, dim3(256), 0, st, a);
   return check_launch("affine_cache_write");
+}
+
+int emx_affine_cache_write(const void* keys, const void* values, const int32_t* slot_mapping, int num_tokens,
+                           int num_kv_heads, int head_dim, int group_size, int bits, int page_size, int num_blocks,
+                           uint32_t* k_codes, void* k_scales, void* k_biases, uint32_t* v_codes, void* v_scales,
+                           void* v_biases, void* stream) {
+  return affine_write_impl(keys, values, slot_mapping, num_tokens, num_kv_heads, head_dim, group_size, bits,
+                           page_size, num_blocks, k_codes, k_scales, k_biases, v_codes, v_scales, v_biases,
+                           emx::RopeArgs{nullptr, nullptr, 0, 0}, stream);
+}
+
+static bool rope_ok(const int32_t* positions, const float* inv_freq, int rot_dims, int head_dim) {
+  return positions && inv_freq && rot_dims > 0 && rot_dims % 2 == 0 && rot_dims <= head_dim;
+}
+
+int emx_affine_cache_write_rope(const void* keys, const void* values, const int32_t* slot_mapping, int num_tokens,
+                                int num_kv_heads, int head_dim, int group_size, int bits, int page_size,
+                                int num_blocks, uint32_t* k_codes, void* k_scales, void* k_biases, uint32_t* v_codes,
+                                void* v_scales, void* v_biases, const int32_t* positions, const float* inv_freq,
+                                int rot_dims, int traditional, void* stream) {
+  if (num_tokens > 0 && !rope_ok(positions, inv_freq, rot_dims, head_dim))
+    return fail(EMX_ERR_INVALID, "rope: positions and inv_freq needed, rot_dims even and in (0, head_dim]");
+  return affine_write_impl(keys, values, slot_mapping, num_tokens, num_kv_heads, head_dim, group_size, bits,
+                           page_size, num_blocks, k_codes, k_scales, k_biases, v_codes, v_scales, v_biases,
+                           emx::RopeArgs{inv_freq, positions, rot_dims, traditional ? 1 : 0}, stream);
+}
+
+int emx_rope_rows(void* x, int rows, int heads, int head_dim, const int32_t* positions, const float* inv_freq,
+                  int rot_dims, int traditional, void* stream) {
+  if (rows < 0 || heads <= 0 || head_dim <= 0) return fail(EMX_ERR_INVALID, "rows >= 0, heads and head_dim > 0");
+  if (rows == 0) return EMX_OK;
+  if (!x || !rope_ok(positions, inv_freq, rot_dims, head_dim))
+    return fail(EMX_ERR_INVALID, "rope: x, positions and inv_freq needed, rot_dims even and in (0, head_dim]");
+  const long n = (long)rows * heads * (rot_dims / 2);
+  const unsigned grid = (unsigned)std::min<long>((n + 255) / 256, 4096);
+  hipLaunchKernelGGL(emx::rope_rows, dim3(grid), dim3(256), 0, reinterpret_cast<hipStream_t>(stream),
+                     reinterpret_cast<emx::h16*>(x), rows, heads, head_dim,
+                     emx::RopeArgs{inv_freq, positions, rot_dims, traditional ? 1 : 0});
+  return check_launch("rope_rows");
 }
 
 size_t emx_paged_prefill_workspace_bytes(int num_tokens, int num_seqs, int num_q_heads, int num_kv_heads,

@@ -97,6 +97,42 @@ __global__ __launch_bounds__(256) void affine_quantize_rows(const h16* x, long r
   biases[gid] = (h16)bias;
 }
 
+// Rotary position embedding applied to K inside a fused write (and to rows by
+// rope_rows), as mlx.core.fast.rope rotates for the reference's RoPE modules
+// (nn.RoPE; Llama3RoPE / SuScaledRoPE / YarnRoPE pass their own frequencies,
+// lib/python/easymlx/layers/rotary/_rotary.py:134-221): pair i of the first
+// `rot` dims -- (i, i + rot/2), or (2i, 2i+1) when traditional -- turns by
+// theta = position * inv_freq[i]; other dims pass through.  The result is
+// rounded to fp16, the dtype the reference's rotated keys have when written.
+struct RopeArgs {
+  const float* inv_freq;       // [rot / 2], null: no rotation
+  const int32_t* positions;    // [T] position of each token
+  int rot;                     // rotated dims (even, <= D)
+  int traditional;
+};
+
+__device__ __forceinline__ void rope_pair(h16& a0, h16& a1, const float theta) {
+  float sn, cs;
+  sincosf(theta, &sn, &cs);
+  const float x0 = (float)a0, x1 = (float)a1;
+  a0 = (h16)(x0 * cs - x1 * sn);
+  a1 = (h16)(x0 * sn + x1 * cs);
+}
+
+// Rows x [rows, heads, D] fp16 rotated in place; row r is at positions[r].
+__global__ __launch_bounds__(256) void rope_rows(h16* x, int rows, int heads, int D, RopeArgs r) {
+  const int half = r.rot / 2;
+  const long n = (long)rows * heads * half;
+  for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n; i += (long)gridDim.x * 256) {
+    const int p = (int)(i % half);
+    const long rh = i / half;
+    const int row = (int)(rh / heads);
+    h16* v = x + rh * D;
+    const int i0 = r.traditional ? 2 * p : p, i1 = r.traditional ? 2 * p + 1 : p + half;
+    rope_pair(v[i0], v[i1], (float)r.positions[row] * r.inv_freq[p]);
+  }
+}
+
 struct WriteArgs {
   const h16* keys;             // [T, Hkv, D]
   const h16* values;           // [T, Hkv, D]
@@ -106,6 +142,7 @@ struct WriteArgs {
   uint32_t* vc;                // [nb, Hkv, bs/T, D, T*b/32], T = min(bs, 256/b) (v_word_index)
   h16 *vs, *vb;                // [nb, Hkv, D/gs, bs]
   int T, Hkv, D, gs, bs, nb;
+  RopeArgs rope;               // K rotation before quantizing (inv_freq null: none; block kernel only)
 };
 
 // One workgroup per (32 consecutive tokens, kv head):
@@ -149,6 +186,16 @@ __global__ __launch_bounds__(256) void affine_cache_write(WriteArgs a) {
     }
   }
   __syncthreads();
+  if (a.rope.inv_freq != nullptr) {  // fused RoPE: the K rows turn in LDS before quantizing
+    const RopeArgs& r = a.rope;
+    const int half = r.rot / 2;
+    for (int task = tid; task < nt * half; task += 256) {
+      const int t = task / half, p = task % half;
+      const int i0 = r.traditional ? 2 * p : p, i1 = r.traditional ? 2 * p + 1 : p + half;
+      rope_pair(sval[0][t][i0], sval[0][t][i1], (float)r.positions[t0 + t] * r.inv_freq[p]);
+    }
+    __syncthreads();
+  }
 
   // ---- 1. scale / bias of every (K|V, token, group)
   for (int task = tid; task < 2 * TW * G; task += 256) {

@@ -69,6 +69,32 @@ int emx_affine_cache_write(const void* keys, const void* values, const int32_t* 
                            void* v_biases, void* stream);
 
 /*
+ * emx_affine_cache_write with rotary position embedding fused in: K rows turn
+ * by theta = positions[t] * inv_freq[i] on pair i of the first rot_dims dims
+ * ((i, i + rot_dims/2), or (2i, 2i+1) when traditional != 0), are rounded to
+ * fp16 and then quantized exactly as emx_affine_cache_write does.  V is not
+ * rotated.  positions int32 [num_tokens], inv_freq float32 [rot_dims/2].
+ * Replaces the RoPE applied to keys in PageCacheView.concatenate_to_cache
+ *   lib/python/easymlx/caching/paged/cache.py:1161-1166 (multi-token :1208-1253)
+ *   followed by the write :1186-1190, with the RoPE of
+ *   lib/python/easymlx/layers/rotary/_rotary.py (mlx.core.fast.rope).
+ */
+int emx_affine_cache_write_rope(const void* keys, const void* values, const int32_t* slot_mapping, int num_tokens,
+                                int num_kv_heads, int head_dim, int group_size, int bits, int page_size,
+                                int num_blocks, uint32_t* k_codes, void* k_scales, void* k_biases, uint32_t* v_codes,
+                                void* v_scales, void* v_biases, const int32_t* positions, const float* inv_freq,
+                                int rot_dims, int traditional, void* stream);
+
+/*
+ * Rotary position embedding in place on fp16 rows x [rows, heads, head_dim]
+ * (row r at positions[r]), the same rotation as emx_affine_cache_write_rope.
+ * Replaces the RoPE applied to queries in concatenate_to_cache
+ *   lib/python/easymlx/caching/paged/cache.py:1161-1166.
+ */
+int emx_rope_rows(void* x, int rows, int heads, int head_dim, const int32_t* positions, const float* inv_freq,
+                  int rot_dims, int traditional, void* stream);
+
+/*
  * Bytes of device workspace emx_paged_attention_affine and
  * emx_paged_attention_fp8 need for split-K
  * partial results and arrival counters (0 if the call needs none).  The
