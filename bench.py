@@ -335,6 +335,31 @@ def aux_quantize_on_write(dev):
         us = float(np.median(event_us(call, 200)))
         moved = n * hkv * (2 * d * 2 + 2 * (d // 2 + 4 * (d // 64)))  # fp16 K,V in; codes + scale/bias out
         res[name] = {"tokens": n, "us_p50": round(us, 2), "GBs_in_plus_out": round(moved / (us * 1e3), 1)}
+    # a decode step's append with Llama-3 RoPE fused in: K rotated inside the write, Q (32 heads) in one launch
+    from easymlx_amd import RotaryEmbedding
+
+    lib = _native.load()
+    rope = RotaryEmbedding.llama3(d, base=500000.0)
+    inv = rope.inv_freq(dev)
+    n = len(appends)
+    k = torch.randn(n, hkv, d, device=dev).half()
+    v = torch.randn(n, hkv, d, device=dev).half()
+    q = torch.randn(n, 32, d, device=dev).half()
+    s = torch.tensor(appends, dtype=torch.int32, device=dev)
+    pos = torch.from_numpy(wl.kv_lens.astype(np.int32)).to(dev)
+
+    def call_rope(i):
+        rc = lib.emx_rope_rows(q.data_ptr(), n, 32, d, pos.data_ptr(), inv.data_ptr(), d, 0, stream)
+        rc = rc or lib.emx_affine_cache_write_rope(
+            k.data_ptr(), v.data_ptr(), s.data_ptr(), n, hkv, d, 64, 4, bs, nb, view.k_codes.data_ptr(),
+            view.k_scales.data_ptr(), view.k_biases.data_ptr(), view.v_codes.data_ptr(), view.v_scales.data_ptr(),
+            view.v_biases.data_ptr(), pos.data_ptr(), inv.data_ptr(), d, 0, stream)
+        if rc:
+            _native.check(rc)
+
+    warm(call_rope, 0.3)
+    res["append_1_token_x32_seqs_rope_q_and_k"] = {"tokens": n,
+                                                   "us_p50": round(float(np.median(event_us(call_rope, 200))), 2)}
     return res
 
 
