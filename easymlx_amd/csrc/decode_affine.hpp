@@ -517,20 +517,40 @@ __device__ __forceinline__ void merge_pieces(const DecodeArgs& a, const PieceInf
   merge_range<HG>(pi.ro, pi.rm, 0, ngrp, gsz, out, 0, lane);
 }
 
-// Wave W finished its piece of unit u: store its partial, then merge.
+// Stores a wave's partial (HG x 128 floats, head-major, already in the wave's
+// LDS slot xw) with 8-byte stores of 64 consecutive lanes: every store
+// instruction writes 512 contiguous bytes, whole lines instead of scattered pieces.
+template <int HG>
+__device__ __forceinline__ void store_partial_lds(const float* xw, const __amdgpu_buffer_rsrc_t ro, const int me,
+                                                  const int lane) {
+  constexpr int D = 128;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+  for (int b = 0; b < HG * D; b += 128) {
+    const f32x2 v = *reinterpret_cast<const f32x2*>(xw + b + 2 * lane);
+    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, v), ro, (b + 2 * lane) * 4, me * HG * D * 4,
+                                          kCoherent);
+  }
+}
+
+// Wave W finished its piece of unit u: store its partial (through the wave's
+// LDS slot xw), then merge.
 template <int GS, int HG>
 __device__ __forceinline__ void merge_piece(const DecodeArgs& a, const int W, const int u, const long long unit_first,
                                             const int n, const long long I, const int NW, const int row, const int kvh,
                                             const f32x4 (&acc)[8], const float pbs, const float m_run, const float l,
                                             const bool col_ok, const int gg, const int jj, const int hh,
-                                            const int lane) {
+                                            const int lane, float* xw) {
   constexpr int D = 128;
   const PieceInfo pi = piece_info<HG>(a, W, u, unit_first, n, I, NW);
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt) {  // lane (hh, gg, jj) owns dims 16*dt + 4*jj .. +3 when they lie in group gg
     const int d = 16 * dt + 4 * jj;
-    if (col_ok && d / GS == gg) store_f32x4(acc[dt] * kTwo24 + pbs, pi.ro, (hh * D + d) * 4, pi.me * HG * D * 4);
+    if (col_ok && d / GS == gg) *reinterpret_cast<f32x4*>(xw + hh * D + d) = acc[dt] * kTwo24 + pbs;
   }
+  store_partial_lds<HG>(xw, pi.ro, pi.me, lane);
   if (col_ok && gg == 0 && jj == 0)
     __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, f32x2{m_run, l}), pi.rm, hh * 8,
                                           pi.me * HG * 8, kCoherent);
@@ -554,6 +574,7 @@ __global__ __launch_bounds__(256, 2) void decode_affine_d128(DecodeArgs a) {
   __shared__ int kvl[kMaxSeqs];
   __shared__ int qrw[kMaxSeqs];
   __shared__ __attribute__((aligned(16))) h16 stage_all[4][C::SHALVES];
+  __shared__ __attribute__((aligned(16))) float xst[4][HG * 128];  // per wave: a partial, head-major
   seq_table(a, cum, kvl, qrw);
   {  // decoded sequences without a live token produce zeros (the reference's l == 0 case)
     const int per_seq = a.Hq * D / 8;
@@ -738,7 +759,7 @@ __global__ __launch_bounds__(256, 2) void decode_affine_d128(DecodeArgs a) {
           }
       } else {
         merge_piece<GS, HG>(a, W, u, unit_first, n_s, I, NW, qrw[s], kvh, acc, pbs, m_run, l, col_ok, gg, jj, hh,
-                            lane);
+                            lane, xst[wv]);
       }
       m_run = -INFINITY;
       l_part = 0.f;

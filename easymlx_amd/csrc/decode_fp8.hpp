@@ -177,6 +177,7 @@ __global__ __launch_bounds__(256, 2) void decode_fp8_d128(DecodeArgs a) {
   __shared__ int cum[kMaxSeqs + 1];
   __shared__ int kvl[kMaxSeqs];
   __shared__ int qrw[kMaxSeqs];
+  __shared__ __attribute__((aligned(16))) float xst[4][HG * D];  // per wave: a partial, head-major
   seq_table(a, cum, kvl, qrw);
   {  // decoded sequences without a live token produce zeros (the reference's l == 0 case)
     const int per_seq = a.Hq * D / 8;
@@ -324,17 +325,21 @@ __global__ __launch_bounds__(256, 2) void decode_fp8_d128(DecodeArgs a) {
         }
       } else {
         const PieceInfo pi = piece_info<HG>(a, W, s * Hkv + kvh, unit_first, n_s, I, NW);
+        // the partial goes through the wave's LDS slot so that every store
+        // instruction writes 512 contiguous bytes (whole lines, not scattered pieces)
+        float* xw = xst[wv];
         if (col_ok) {
 #pragma unroll
           for (int r = 0; r < 4; ++r)
 #pragma unroll
             for (int c = 0; c < 2; ++c)
-              store_f32x4(f32x4{acc[4 * c][r], acc[4 * c + 1][r], acc[4 * c + 2][r], acc[4 * c + 3][r]}, pi.ro,
-                          (col * D + 32 * jj + 8 * r + 4 * c) * 4, pi.me * HG * D * 4);
+              *reinterpret_cast<f32x4*>(xw + col * D + 32 * jj + 8 * r + 4 * c) =
+                  f32x4{acc[4 * c][r], acc[4 * c + 1][r], acc[4 * c + 2][r], acc[4 * c + 3][r]};
           if (jj == 0)
             __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, f32x2{m_run, l}), pi.rm, col * 8,
                                                   pi.me * HG * 8, kCoherent);
         }
+        store_partial_lds<HG>(xw, pi.ro, pi.me, lane);
         merge_pieces<HG>(a, pi, s * Hkv + kvh, qrw[s], kvh, lane);
       }
       m_run = -INFINITY;
