@@ -505,14 +505,15 @@ class AffinePageCacheView(PageCacheView):
         """
         from .rope import RotaryEmbedding
 
-        if not isinstance(rope, RotaryEmbedding) or rope.dims > self.head_dim or queries.shape[-1] != self.head_dim:
+        if (not isinstance(rope, RotaryEmbedding) or rope.dims > self.head_dim or queries.shape[-1] != self.head_dim
+                or queries.dtype != torch.float16):  # the rotation kernels read and write fp16 rows
             return super().concatenate_to_cache(queries, keys, values, cache_metadata=cache_metadata, rope=rope,
                                                 slot_ids=slot_ids, query_lens=query_lens)
         slot_ids, qlens, single = self._resolve(cache_metadata, slot_ids, query_lens, int(queries.shape[0]))
         slot_mapping, slots, base, positions = self._slot_mapping_positions(slot_ids, qlens)
         lib = _native.load()
         n = int(slot_mapping.numel())
-        q_out = queries.to(torch.float16).contiguous().clone()
+        q_out = queries.contiguous().clone()
         if n:
             keys = keys.to(torch.float16).contiguous()
             values = values.to(torch.float16).contiguous()
@@ -539,7 +540,7 @@ class AffinePageCacheView(PageCacheView):
             block_size=self.block_size,
         )
         md.is_single_token_decode = single
-        return q_out.to(queries.dtype), self.key_cache, self.value_cache, md
+        return q_out, self.key_cache, self.value_cache, md
 
     def _zero_blocks(self, ids: torch.Tensor) -> None:
         for t in (self.key_cache, self.value_cache, self.k_scales, self.k_biases, self.v_scales, self.v_biases):
