@@ -250,6 +250,39 @@ class PageCacheView:
         md.is_single_token_decode = single
         return queries, self.key_cache, self.value_cache, md
 
+    def _concatenate_rope_fused(self, queries, keys, values, cache_metadata, rope, slot_ids, query_lens, write,
+                                rot_multiple):
+        """The write with a :class:`RotaryEmbedding` fused into ``write`` (a cache's C entry point) and Q turned
+        by ``emx_rope_rows``; any other ``rope`` (or fp16-incompatible inputs) takes the reference's order."""
+        from .rope import RotaryEmbedding
+
+        if (not isinstance(rope, RotaryEmbedding) or rope.dims > self.head_dim or rope.dims % rot_multiple
+                or queries.shape[-1] != self.head_dim or queries.dtype != torch.float16):
+            return PageCacheView.concatenate_to_cache(self, queries, keys, values, cache_metadata=cache_metadata,
+                                                      rope=rope, slot_ids=slot_ids, query_lens=query_lens)
+        slot_ids, qlens, single = self._resolve(cache_metadata, slot_ids, query_lens, int(queries.shape[0]))
+        slot_mapping, slots, base, positions = self._slot_mapping_positions(slot_ids, qlens)
+        lib = _native.load()
+        n = int(slot_mapping.numel())
+        q_out = queries.contiguous().clone()
+        if n:
+            inv = rope.inv_freq(q_out.device)
+            stream = _stream_ptr(q_out.device)
+            _native.check(lib.emx_rope_rows(q_out.data_ptr(), n, int(q_out.shape[1]), self.head_dim,
+                                            positions.data_ptr(), inv.data_ptr(), rope.dims, int(rope.traditional),
+                                            stream))
+            _native.check(write(keys, values, slot_mapping, positions, inv, rope, stream))
+        if len(slot_ids):
+            add = torch.tensor(qlens, dtype=torch.int32, device=self.kv_lens.device)
+            self.kv_lens.index_copy_(0, slots, (base + add).to(torch.int32))
+        md = cache_metadata.with_cache_state(
+            block_tables=self.block_tables.index_select(0, slots) if len(slot_ids) else self.block_tables[:0],
+            kv_lens=self.kv_lens.index_select(0, slots) if len(slot_ids) else self.kv_lens[:0],
+            block_size=self.block_size,
+        )
+        md.is_single_token_decode = single
+        return q_out, self.key_cache, self.value_cache, md
+
     def append(self, seq_idx: int, key: torch.Tensor, value: torch.Tensor) -> None:
         """Append ``[num_tokens, Hkv, D]`` tokens to one sequence (``cache.py:834-872``)."""
         if key.shape != value.shape:
@@ -351,6 +384,32 @@ class Fp8PageCacheView(PageCacheView):
                 self.v_scales.data_ptr(), self._ws.data_ptr(), self._ws.numel(), _stream_ptr(keys.device),
             )
         )
+
+    def concatenate_to_cache(self, queries, keys, values, *, cache_metadata, rope=None, slot_ids=None,
+                             query_lens=None):
+        """With a :class:`RotaryEmbedding`, the call's K scale and codes come from the keys turned inside the
+        write kernels (``cache.py:1161-1166`` then ``:1171-1184``); Q turns in one launch."""
+        from .._native import DTYPE_BF16, DTYPE_F16, DTYPE_F32
+
+        codes = {torch.float16: DTYPE_F16, torch.bfloat16: DTYPE_BF16, torch.float32: DTYPE_F32}
+
+        def write(keys, values, slot_mapping, positions, inv, rope, stream):
+            if keys.dtype not in codes or values.dtype != keys.dtype:
+                raise NotImplementedError(f"FP8 cache writes take fp16/bf16/fp32 keys and values, got {keys.dtype}")
+            lib = _native.load()
+            if self._ws is None:
+                self._ws = torch.empty(int(lib.emx_fp8_write_workspace_bytes()), dtype=torch.uint8,
+                                       device=self.key_cache.device)
+            keys = keys.contiguous()
+            values = values.contiguous()
+            return lib.emx_fp8_cache_write_rope(
+                keys.data_ptr(), values.data_ptr(), codes[keys.dtype], slot_mapping.data_ptr(), int(keys.shape[0]),
+                self.num_kv_heads, self.head_dim, self.block_size, self.num_blocks, self.key_cache.data_ptr(),
+                self.value_cache.data_ptr(), self.k_scales.data_ptr(), self.v_scales.data_ptr(), self._ws.data_ptr(),
+                self._ws.numel(), positions.data_ptr(), inv.data_ptr(), rope.dims, int(rope.traditional), stream)
+
+        return self._concatenate_rope_fused(queries, keys, values, cache_metadata, rope, slot_ids, query_lens, write,
+                                            rot_multiple=4 if getattr(rope, "traditional", False) else 8)
 
     def write_slots(self, keys: torch.Tensor, values: torch.Tensor, slot_mapping: torch.Tensor) -> None:
         """Write tokens to explicit slots (``block * block_size + offset``; -1 skips)."""
@@ -497,50 +556,21 @@ class AffinePageCacheView(PageCacheView):
 
     def concatenate_to_cache(self, queries, keys, values, *, cache_metadata, rope=None, slot_ids=None,
                              query_lens=None):
-        """``PageCacheView.concatenate_to_cache`` with a :class:`RotaryEmbedding` fused in.
+        """``PageCacheView.concatenate_to_cache`` with a :class:`RotaryEmbedding` fused in: K turns inside the
+        quantize-on-write kernel, Q in one launch (``cache.py:1161-1166`` then ``:1186-1190``)."""
 
-        K turns inside the quantize-on-write kernel and Q in one launch
-        (``cache.py:1161-1166`` then ``:1186-1190``); any other ``rope`` callable
-        runs first, as in the reference, and the write follows.
-        """
-        from .rope import RotaryEmbedding
-
-        if (not isinstance(rope, RotaryEmbedding) or rope.dims > self.head_dim or queries.shape[-1] != self.head_dim
-                or queries.dtype != torch.float16):  # the rotation kernels read and write fp16 rows
-            return super().concatenate_to_cache(queries, keys, values, cache_metadata=cache_metadata, rope=rope,
-                                                slot_ids=slot_ids, query_lens=query_lens)
-        slot_ids, qlens, single = self._resolve(cache_metadata, slot_ids, query_lens, int(queries.shape[0]))
-        slot_mapping, slots, base, positions = self._slot_mapping_positions(slot_ids, qlens)
-        lib = _native.load()
-        n = int(slot_mapping.numel())
-        q_out = queries.contiguous().clone()
-        if n:
+        def write(keys, values, slot_mapping, positions, inv, rope, stream):
             keys = keys.to(torch.float16).contiguous()
             values = values.to(torch.float16).contiguous()
-            inv = rope.inv_freq(keys.device)
-            stream = _stream_ptr(keys.device)
-            _native.check(lib.emx_rope_rows(q_out.data_ptr(), n, int(q_out.shape[1]), self.head_dim,
-                                            positions.data_ptr(), inv.data_ptr(), rope.dims, int(rope.traditional),
-                                            stream))
-            _native.check(
-                lib.emx_affine_cache_write_rope(
-                    keys.data_ptr(), values.data_ptr(), slot_mapping.data_ptr(), n, self.num_kv_heads,
-                    self.head_dim, self.group_size, self.bits, self.block_size, self.num_blocks,
-                    self.key_cache.data_ptr(), self.k_scales.data_ptr(), self.k_biases.data_ptr(),
-                    self.value_cache.data_ptr(), self.v_scales.data_ptr(), self.v_biases.data_ptr(),
-                    positions.data_ptr(), inv.data_ptr(), rope.dims, int(rope.traditional), stream,
-                )
-            )
-        if len(slot_ids):
-            add = torch.tensor(qlens, dtype=torch.int32, device=self.kv_lens.device)
-            self.kv_lens.index_copy_(0, slots, (base + add).to(torch.int32))
-        md = cache_metadata.with_cache_state(
-            block_tables=self.block_tables.index_select(0, slots) if len(slot_ids) else self.block_tables[:0],
-            kv_lens=self.kv_lens.index_select(0, slots) if len(slot_ids) else self.kv_lens[:0],
-            block_size=self.block_size,
-        )
-        md.is_single_token_decode = single
-        return q_out, self.key_cache, self.value_cache, md
+            return _native.load().emx_affine_cache_write_rope(
+                keys.data_ptr(), values.data_ptr(), slot_mapping.data_ptr(), int(keys.shape[0]), self.num_kv_heads,
+                self.head_dim, self.group_size, self.bits, self.block_size, self.num_blocks,
+                self.key_cache.data_ptr(), self.k_scales.data_ptr(), self.k_biases.data_ptr(),
+                self.value_cache.data_ptr(), self.v_scales.data_ptr(), self.v_biases.data_ptr(),
+                positions.data_ptr(), inv.data_ptr(), rope.dims, int(rope.traditional), stream)
+
+        return self._concatenate_rope_fused(queries, keys, values, cache_metadata, rope, slot_ids, query_lens, write,
+                                            rot_multiple=2)
 
     def _zero_blocks(self, ids: torch.Tensor) -> None:
         for t in (self.key_cache, self.value_cache, self.k_scales, self.k_biases, self.v_scales, self.v_biases):

@@ -125,6 +125,27 @@ __device__ __forceinline__ uint32_t f32_to_e4m3(float f) {
   return r;
 }
 
+// Rotary position embedding as mlx.core.fast.rope rotates for the reference's
+// RoPE modules (nn.RoPE; Llama3RoPE / SuScaledRoPE / YarnRoPE pass their own
+// frequencies, lib/python/easymlx/layers/rotary/_rotary.py:134-221): pair i of
+// the first `rot` dims -- (i, i + rot/2), or (2i, 2i+1) when traditional --
+// turns by theta = position * inv_freq[i]; other dims pass through.
+struct RopeArgs {
+  const float* inv_freq;       // [rot / 2], null: no rotation
+  const int32_t* positions;    // [T] position of each token
+  int rot;                     // rotated dims (even, <= D)
+  int traditional;
+};
+
+// (y0, y1) = (x0, x1) turned by theta; fp32 products and sums rounded one by
+// one (no contraction), so every kernel that rotates gets the same bits.
+__device__ __forceinline__ void rope_rotate(const float x0, const float x1, const float theta, float& y0, float& y1) {
+  float sn, cs;
+  sincosf(theta, &sn, &cs);
+  y0 = __fsub_rn(__fmul_rn(x0, cs), __fmul_rn(x1, sn));
+  y1 = __fadd_rn(__fmul_rn(x0, sn), __fmul_rn(x1, cs));
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));

@@ -602,10 +602,10 @@ int emx_paged_attention_dense(const void* queries, int num_tokens, int num_q_hea
 
 size_t emx_fp8_write_workspace_bytes(void) { return sizeof(float) * 2 * emx::kFp8Parts; }
 
-int emx_fp8_cache_write(const void* keys, const void* values, int dtype, const int32_t* slot_mapping, int num_tokens,
-                        int num_kv_heads, int head_dim, int page_size, int num_blocks, uint8_t* key_cache,
-                        uint8_t* value_cache, float* k_scales, float* v_scales, void* workspace,
-                        size_t workspace_bytes, void* stream) {
+static int fp8_write_impl(const void* keys, const void* values, int dtype, const int32_t* slot_mapping, int num_tokens,
+                          int num_kv_heads, int head_dim, int page_size, int num_blocks, uint8_t* key_cache,
+                          uint8_t* value_cache, float* k_scales, float* v_scales, void* workspace,
+                          size_t workspace_bytes, const emx::RopeArgs& rope, void* stream) {
   if (num_tokens < 0) return fail(EMX_ERR_INVALID, "num_tokens must be >= 0");
   if (num_kv_heads <= 0 || head_dim <= 0 || page_size <= 0 || num_blocks <= 0)
     return fail(EMX_ERR_INVALID, "num_kv_heads, head_dim, page_size, num_blocks must be positive");
@@ -633,9 +633,10 @@ int emx_fp8_cache_write(const void* keys, const void* values, int dtype, const i
   a.ks = k_scales;
   a.vs = v_scales;
   a.part = reinterpret_cast<float*>(workspace);
+  a.rope = rope;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const size_t n = (size_t)num_tokens * num_kv_heads * head_dim;
-  const int nparts = (int)std::min<size_t>(emx::kFp8Parts, (n + 255) / 256);
+  const int nparts = (int)std::min<size_t>(emx::kFp8Parts, (n / 4 + 255) / 256);
   const int nwrite = (int)std::min<size_t>(1024, (n / 4 + 255) / 256);
   switch (dtype) {
     case EMX_DTYPE_F16:
@@ -652,6 +653,28 @@ int emx_fp8_cache_write(const void* keys, const void* values, int dtype, const i
       break;
   }
   return check_launch("fp8_cache_write");
+}
+
+int emx_fp8_cache_write(const void* keys, const void* values, int dtype, const int32_t* slot_mapping, int num_tokens,
+                        int num_kv_heads, int head_dim, int page_size, int num_blocks, uint8_t* key_cache,
+                        uint8_t* value_cache, float* k_scales, float* v_scales, void* workspace,
+                        size_t workspace_bytes, void* stream) {
+  return fp8_write_impl(keys, values, dtype, slot_mapping, num_tokens, num_kv_heads, head_dim, page_size, num_blocks,
+                        key_cache, value_cache, k_scales, v_scales, workspace, workspace_bytes,
+                        emx::RopeArgs{nullptr, nullptr, 0, 0}, stream);
+}
+
+int emx_fp8_cache_write_rope(const void* keys, const void* values, int dtype, const int32_t* slot_mapping,
+                             int num_tokens, int num_kv_heads, int head_dim, int page_size, int num_blocks,
+                             uint8_t* key_cache, uint8_t* value_cache, float* k_scales, float* v_scales,
+                             void* workspace, size_t workspace_bytes, const int32_t* positions, const float* inv_freq,
+                             int rot_dims, int traditional, void* stream) {
+  if (num_tokens > 0 && (!rope_ok(positions, inv_freq, rot_dims, head_dim) || rot_dims % (traditional ? 4 : 8) != 0))
+    return fail(EMX_ERR_INVALID,
+                "rope: positions and inv_freq needed, rot_dims in (0, head_dim] and a multiple of 8 (4 if traditional)");
+  return fp8_write_impl(keys, values, dtype, slot_mapping, num_tokens, num_kv_heads, head_dim, page_size, num_blocks,
+                        key_cache, value_cache, k_scales, v_scales, workspace, workspace_bytes,
+                        emx::RopeArgs{inv_freq, positions, rot_dims, traditional ? 1 : 0}, stream);
 }
 
 int emx_paged_attention_fp8(const void* queries, int num_tokens, int num_q_heads, int head_dim, int dtype,

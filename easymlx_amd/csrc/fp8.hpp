@@ -27,19 +27,67 @@ struct Fp8WriteArgs {
   float* ks;             // [nb]
   float* vs;
   float* part;           // [2][kFp8Parts] per-workgroup maxima
+  RopeArgs rope;         // K turned before the scale and the codes (inv_freq null: none)
 };
+
+__device__ __forceinline__ float round_to(float x, h16*) { return (float)(h16)x; }
+__device__ __forceinline__ float round_to(float x, uint16_t*) { return bf16_to_f32(f32_to_bf16(x)); }
+__device__ __forceinline__ float round_to(float x, float*) { return x; }
+
+// The 4 K values of word e (dims 4w .. 4w+3 of one token and head), turned by
+// the call's RoPE and rounded to the input dtype when a.rope is set (the
+// reference writes the rotated keys of the model's dtype).  Needs rot % 8 == 0
+// (non-traditional): a word and its partner word lie in one half each.
+template <typename T>
+__device__ __forceinline__ void k_word(const Fp8WriteArgs& a, const T* k, const size_t e, float (&x)[4]) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) x[j] = to_f32(k[4 * e + j]);
+  const RopeArgs& r = a.rope;
+  if (r.inv_freq == nullptr) return;
+  const int wpr = a.D / 4;  // words per head row
+  const int d0 = 4 * (int)(e % wpr);
+  if (d0 >= r.rot) return;
+  const float pos = (float)r.positions[e / ((size_t)a.Hkv * wpr)];
+  float y[4];
+  if (r.traditional) {
+#pragma unroll
+    for (int j = 0; j < 4; j += 2) rope_rotate(x[j], x[j + 1], pos * r.inv_freq[(d0 + j) >> 1], y[j], y[j + 1]);
+  } else {
+    const int half = r.rot / 2;
+    const bool lo = d0 < half;
+    const size_t pe = lo ? e + half / 4 : e - half / 4;  // the partner word
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float p = to_f32(k[4 * pe + j]);
+      float y0, y1;
+      const int i = (lo ? d0 : d0 - half) + j;
+      if (lo)
+        rope_rotate(x[j], p, pos * r.inv_freq[i], y0, y1);
+      else
+        rope_rotate(p, x[j], pos * r.inv_freq[i], y1, y0);
+      y[j] = y0;
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) x[j] = round_to(y[j], (T*)nullptr);
+}
 
 template <typename Tag>
 __global__ __launch_bounds__(256) void fp8_amax(Fp8WriteArgs a) {
   typedef typename Tag::T T;
   const T* k = reinterpret_cast<const T*>(a.k);
   const T* v = reinterpret_cast<const T*>(a.v);
-  const size_t row = (size_t)a.Hkv * a.D, n = (size_t)a.T * row;
+  const size_t row4 = (size_t)a.Hkv * a.D / 4, n4 = (size_t)a.T * row4;
   float mk = 0.f, mv = 0.f;
-  for (size_t e = (size_t)blockIdx.x * 256 + threadIdx.x; e < n; e += (size_t)gridDim.x * 256) {
-    if (a.slot[e / row] < 0) continue;
-    mk = fmaxf(mk, fabsf(to_f32(k[e])));
-    mv = fmaxf(mv, fabsf(to_f32(v[e])));
+  for (size_t e = (size_t)blockIdx.x * 256 + threadIdx.x; e < n4; e += (size_t)gridDim.x * 256) {
+    if (a.slot[e / row4] < 0) continue;
+    float x[4];
+    k_word(a, k, e, x);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      mk = fmaxf(mk, fabsf(x[j]));
+      mv = fmaxf(mv, fabsf(to_f32(v[4 * e + j])));
+    }
   }
   mk = wave_max(mk);
   mv = wave_max(mv);
@@ -86,10 +134,12 @@ __global__ __launch_bounds__(256) void fp8_write(Fp8WriteArgs a, int nparts) {
     if (slot < 0) continue;
     const int blk = slot / a.bs, off = slot % a.bs;
     if (blk >= a.nb) continue;
+    float x[4];
+    k_word(a, k, e, x);
     uint32_t ck = 0, cv = 0;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      ck |= f32_to_e4m3(to_f32(k[4 * e + j]) / kq) << (8 * j);
+      ck |= f32_to_e4m3(x[j] / kq) << (8 * j);
       cv |= f32_to_e4m3(to_f32(v[4 * e + j]) / vq) << (8 * j);
     }
     const size_t dst = ((size_t)blk * a.bs + off) * (size_t)row4 + r;  // [nb, bs, Hkv*D/4] words

@@ -97,26 +97,14 @@ __global__ __launch_bounds__(256) void affine_quantize_rows(const h16* x, long r
   biases[gid] = (h16)bias;
 }
 
-// Rotary position embedding applied to K inside a fused write (and to rows by
-// rope_rows), as mlx.core.fast.rope rotates for the reference's RoPE modules
-// (nn.RoPE; Llama3RoPE / SuScaledRoPE / YarnRoPE pass their own frequencies,
-// lib/python/easymlx/layers/rotary/_rotary.py:134-221): pair i of the first
-// `rot` dims -- (i, i + rot/2), or (2i, 2i+1) when traditional -- turns by
-// theta = position * inv_freq[i]; other dims pass through.  The result is
-// rounded to fp16, the dtype the reference's rotated keys have when written.
-struct RopeArgs {
-  const float* inv_freq;       // [rot / 2], null: no rotation
-  const int32_t* positions;    // [T] position of each token
-  int rot;                     // rotated dims (even, <= D)
-  int traditional;
-};
-
+// K rows turn (RopeArgs, common.hpp) inside a fused write and rows of Q in
+// rope_rows; the result is rounded to fp16, the dtype the reference's rotated
+// keys have when written.
 __device__ __forceinline__ void rope_pair(h16& a0, h16& a1, const float theta) {
-  float sn, cs;
-  sincosf(theta, &sn, &cs);
-  const float x0 = (float)a0, x1 = (float)a1;
-  a0 = (h16)(x0 * cs - x1 * sn);
-  a1 = (h16)(x0 * sn + x1 * cs);
+  float y0, y1;
+  rope_rotate((float)a0, (float)a1, theta, y0, y1);
+  a0 = (h16)y0;
+  a1 = (h16)y1;
 }
 
 // Rows x [rows, heads, D] fp16 rotated in place; row r is at positions[r].

@@ -178,6 +178,20 @@ int emx_fp8_cache_write(const void* keys, const void* values, int dtype, const i
                         size_t workspace_bytes, void* stream);
 
 /*
+ * emx_fp8_cache_write with rotary position embedding fused in: the call's K
+ * scale and codes are taken over the keys turned as in
+ * emx_affine_cache_write_rope and rounded to dtype.  rot_dims a multiple of 8
+ * (of 4 when traditional).
+ * Replaces the RoPE of PageCacheView.concatenate_to_cache
+ *   lib/python/easymlx/caching/paged/cache.py:1161-1166 followed by its FP8 write :1171-1184.
+ */
+int emx_fp8_cache_write_rope(const void* keys, const void* values, int dtype, const int32_t* slot_mapping,
+                             int num_tokens, int num_kv_heads, int head_dim, int page_size, int num_blocks,
+                             uint8_t* key_cache, uint8_t* value_cache, float* k_scales, float* v_scales,
+                             void* workspace, size_t workspace_bytes, const int32_t* positions, const float* inv_freq,
+                             int rot_dims, int traditional, void* stream);
+
+/*
  * Paged attention over an FP8 (E4M3) cache key/value [num_blocks, page_size,
  * Hkv, head_dim] uint8 with per-page fp32 scales k_scale/v_scale [num_blocks]:
  * K = dec(code) * k_scale[page].  queries/out in dtype (EMX_DTYPE_*).

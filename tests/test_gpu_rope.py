@@ -123,3 +123,80 @@ def test_concatenate_fused_vs_callable(cuda):
         assert np.all(np.abs(qa - qb) <= 2 * ulp + arith), f"queries differ at step {qlens}"
         assert_attention_close(oa, ob.astype(np.float64), f"fused vs callable {qlens}")
         assert views[0].kv_lens.cpu().tolist() == views[1].kv_lens.cpu().tolist()
+
+
+@pytest.mark.parametrize("traditional", [False, True])
+def test_fp8_fused_write_equals_rotate_then_write(cuda, traditional):
+    """FP8 cache: the call's scale and the codes over the turned keys, in the write kernels == emx_rope_rows on K,
+    then the plain FP8 write: every byte of the pages and every page scale."""
+    from easymlx_amd import Fp8PageCacheView
+
+    print(f"[fp8 fused rope write traditional={traditional}]", flush=True)
+    rng = np.random.default_rng(11 + traditional)
+    T, hkv, d, bs, nb = 200, 8, 128, 32, 64
+    rope = RotaryEmbedding.llama3(128, base=500000.0, traditional=traditional)
+    k = torch.from_numpy((rng.standard_normal((T, hkv, d)) * 2).astype(np.float16)).to(cuda)
+    v = torch.from_numpy((rng.standard_normal((T, hkv, d)) * 2).astype(np.float16)).to(cuda)
+    slots = torch.from_numpy(rng.permutation(nb * bs)[:T].astype(np.int32)).to(cuda)
+    pos = torch.from_numpy(rng.integers(0, 30000, T).astype(np.int32)).to(cuda)
+
+    def view():
+        shape = (nb, bs, hkv, d)
+        return Fp8PageCacheView(key_cache=torch.zeros(shape, dtype=torch.uint8, device=cuda),
+                                value_cache=torch.zeros(shape, dtype=torch.uint8, device=cuda),
+                                k_scales=torch.zeros(nb, device=cuda), v_scales=torch.zeros(nb, device=cuda),
+                                block_tables=torch.zeros((1, 1), dtype=torch.int32, device=cuda),
+                                kv_lens=torch.zeros(1, dtype=torch.int32, device=cuda), block_size=bs,
+                                num_kv_heads=hkv, head_dim=d)
+
+    a, b = view(), view()
+    lib = _native.load()
+    ws = torch.empty(int(lib.emx_fp8_write_workspace_bytes()), dtype=torch.uint8, device=cuda)
+    _native.check(lib.emx_fp8_cache_write_rope(
+        k.data_ptr(), v.data_ptr(), _native.DTYPE_F16, slots.data_ptr(), T, hkv, d, bs, nb, a.key_cache.data_ptr(),
+        a.value_cache.data_ptr(), a.k_scales.data_ptr(), a.v_scales.data_ptr(), ws.data_ptr(), ws.numel(),
+        pos.data_ptr(), rope.inv_freq(cuda).data_ptr(), rope.dims, int(traditional),
+        torch.cuda.current_stream(cuda).cuda_stream))
+    kr = k.clone()
+    _rope_rows(kr, pos, rope)
+    b.write_slots(kr, v, slots)
+    torch.cuda.synchronize()
+    for name in ("key_cache", "value_cache", "k_scales", "v_scales"):
+        assert torch.equal(getattr(a, name), getattr(b, name)), name
+
+
+def test_fp8_concatenate_fused_vs_callable(cuda):
+    """Fp8PageCacheView.concatenate_to_cache with a RotaryEmbedding vs the same RoPE as a plain callable."""
+    from easymlx_amd import Fp8PageCacheView, paged_attention
+
+    print("[fp8 concatenate fused rope]", flush=True)
+    rng = np.random.default_rng(13)
+    S, hq, hkv, d, bs, mb = 3, 32, 8, 128, 32, 16
+    rope = RotaryEmbedding(128, base=10000.0)
+    plain = lambda x, offset=0: rope(x, offset=offset)  # noqa: E731
+
+    def view():
+        nb = S * mb
+        shape = (nb, bs, hkv, d)
+        return Fp8PageCacheView(key_cache=torch.zeros(shape, dtype=torch.uint8, device=cuda),
+                                value_cache=torch.zeros(shape, dtype=torch.uint8, device=cuda),
+                                k_scales=torch.zeros(nb, device=cuda), v_scales=torch.zeros(nb, device=cuda),
+                                block_tables=torch.arange(nb, dtype=torch.int32, device=cuda).reshape(S, mb),
+                                kv_lens=torch.zeros(S, dtype=torch.int32, device=cuda), block_size=bs,
+                                num_kv_heads=hkv, head_dim=d)
+
+    views = [view(), view()]
+    for qlens in ([150, 31, 1], [1, 1, 1]):
+        T = sum(qlens)
+        q = torch.from_numpy(rng.standard_normal((T, hq, d)).astype(np.float16)).to(cuda)
+        k = torch.from_numpy((rng.standard_normal((T, hkv, d)) * 2).astype(np.float16)).to(cuda)
+        v = torch.from_numpy((rng.standard_normal((T, hkv, d)) * 2).astype(np.float16)).to(cuda)
+        outs = []
+        for vw, r in zip(views, (rope, plain)):
+            md = PageMetadata(query_start_loc=build_query_start_loc(qlens, device=cuda), slot_ids=tuple(range(S)))
+            qq, kc, vc, md = vw.concatenate_to_cache(q, k, v, cache_metadata=md, rope=r)
+            o = paged_attention(qq, kc, vc, md.block_tables, md.kv_lens, md.query_start_loc, k_scale=vw.k_scales,
+                                v_scale=vw.v_scales)
+            outs.append(o.float().cpu().numpy())
+        torch.cuda.synchronize()
+        assert_attention_close(outs[0], outs[1].astype(np.float64), f"fp8 fused vs callable {qlens}")
