@@ -315,13 +315,14 @@ static int affine_write_impl(const void* keys, const void* values, const int32_t
                 emx::kWriteMaxDim, emx::kWriteMaxGroups);
   a.rope = rope;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  if (rope.inv_freq == nullptr && num_tokens <= emx::kSmallWrite && head_dim % 16 == 0 && group_size % 16 == 0 &&
+  if (num_tokens <= emx::kSmallWrite && head_dim % 16 == 0 && group_size % 16 == 0 &&
       group_size <= emx::kSmallMaxGroup) {
     const dim3 sgrid((unsigned)num_kv_heads, (unsigned)(head_dim / 16));
-    if (bits == 4)
-      hipLaunchKernelGGL(emx::affine_cache_write_small<4>, sgrid, dim3(256), 0, st, a);
-    else
-      hipLaunchKernelGGL(emx::affine_cache_write_small<8>, sgrid, dim3(256), 0, st, a);
+    typedef void (*SmallFn)(emx::WriteArgs);
+    const bool r = rope.inv_freq != nullptr;
+    SmallFn fn = bits == 4 ? (r ? emx::affine_cache_write_small<4, true> : emx::affine_cache_write_small<4, false>)
+                           : (r ? emx::affine_cache_write_small<8, true> : emx::affine_cache_write_small<8, false>);
+    hipLaunchKernelGGL(fn, sgrid, dim3(256), 0, st, a);
     return check_launch("affine_cache_write_small");
   }
   const dim3 grid((unsigned)((num_tokens + emx::kWriteTokens - 1) / emx::kWriteTokens), (unsigned)num_kv_heads);

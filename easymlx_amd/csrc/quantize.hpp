@@ -130,7 +130,7 @@ struct WriteArgs {
   uint32_t* vc;                // [nb, Hkv, bs/T, D, T*b/32], T = min(bs, 256/b) (v_word_index)
   h16 *vs, *vb;                // [nb, Hkv, D/gs, bs]
   int T, Hkv, D, gs, bs, nb;
-  RopeArgs rope;               // K rotation before quantizing (inv_freq null: none; block kernel only)
+  RopeArgs rope;               // K rotation before quantizing (inv_freq null: none)
 };
 
 // One workgroup per (32 consecutive tokens, kv head):
@@ -278,7 +278,9 @@ __global__ __launch_bounds__(256) void affine_cache_write(WriteArgs a) {
 constexpr int kSmallWrite = 128;
 constexpr int kSmallMaxGroup = 64;
 
-template <int BITS>
+// ROPE: the K rows of every token are loaded whole, turned in LDS (pairs span
+// quantization groups), and the block's group is taken from the turned rows.
+template <int BITS, bool ROPE = false>
 __global__ __launch_bounds__(256) void affine_cache_write_small(WriteArgs a) {
   constexpr int PW = 32 / BITS;
   constexpr int DB = 16;  // dims per workgroup
@@ -307,8 +309,29 @@ __global__ __launch_bounds__(256) void affine_cache_write_small(WriteArgs a) {
   }
   // the quantization group holding this dim block, for every token: one cooperative load
   const int g = d0 / a.gs;
-  for (int i = tid; i < 2 * T * (a.gs / 8); i += 256) {
-    const int kv = i / (T * (a.gs / 8)), r = i % (T * (a.gs / 8));
+  if constexpr (ROPE) {
+    __shared__ __attribute__((aligned(16))) h16 krow[kSmallWrite][kWriteMaxDim];
+    for (int i = tid; i < T * (a.D / 8); i += 256) {
+      const int t = i / (a.D / 8), c = i % (a.D / 8);
+      *reinterpret_cast<u32x4*>(&krow[t][8 * c]) =
+          *reinterpret_cast<const u32x4*>(a.keys + ((size_t)t * a.Hkv + h) * a.D + 8 * c);
+    }
+    __syncthreads();
+    const RopeArgs& r = a.rope;
+    const int half = r.rot / 2;
+    for (int task = tid; task < T * half; task += 256) {
+      const int t = task / half, p = task % half;
+      const int i0 = r.traditional ? 2 * p : p, i1 = r.traditional ? 2 * p + 1 : p + half;
+      rope_pair(krow[t][i0], krow[t][i1], (float)r.positions[t] * r.inv_freq[p]);
+    }
+    __syncthreads();
+    for (int i = tid; i < T * (a.gs / 8); i += 256) {
+      const int t = i / (a.gs / 8), c = i % (a.gs / 8);
+      *reinterpret_cast<u32x4*>(&sgrp[0][t][8 * c]) = *reinterpret_cast<const u32x4*>(&krow[t][g * a.gs + 8 * c]);
+    }
+  }
+  for (int i = tid; i < (ROPE ? 1 : 2) * T * (a.gs / 8); i += 256) {
+    const int kv = ROPE ? 1 : i / (T * (a.gs / 8)), r = i % (T * (a.gs / 8));
     const int t = r / (a.gs / 8), c = r % (a.gs / 8);
     const h16* src = (kv ? a.values : a.keys) + ((size_t)t * a.Hkv + h) * a.D + (size_t)g * a.gs + 8 * c;
     *reinterpret_cast<u32x4*>(&sgrp[kv][t][8 * c]) = *reinterpret_cast<const u32x4*>(src);
