@@ -146,6 +146,25 @@ __device__ __forceinline__ void rope_rotate(const float x0, const float x1, cons
   y1 = __fadd_rn(__fmul_rn(x0, sn), __fmul_rn(x1, cs));
 }
 
+// Max / sum over the lanes i, i^16, i^32, i^48 (one column of the four 16-lane
+// rows, the MFMA output rows of a 16-wide tile) with gfx950's row swaps:
+// v_permlane16_swap pairs rows (0,1) and (2,3), v_permlane32_swap the halves.
+// Plain VALU, no LDS round trip (a __shfl_xor is a ds_bpermute); every lane of
+// a column gets the same bits.
+__device__ __forceinline__ float rows4_max(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
+__device__ __forceinline__ float rows4_sum(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));

@@ -248,8 +248,7 @@ __device__ __forceinline__ void compute_iteration(IterLoads<BITS, GS, HG>& L, co
 #pragma unroll
     for (int r = 0; r < 4; ++r) tmax = fmaxf(tmax, sc[at][r]);
   }
-  tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-  tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+  tmax = rows4_max(tmax);
   const float m_new = fmaxf(m_run, tmax * sc_l2);
   if (__any(m_new != m_run)) {
     const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);

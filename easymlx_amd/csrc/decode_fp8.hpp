@@ -130,8 +130,7 @@ __device__ __forceinline__ void fp8_compute(const Fp8Loads& L, const bool full, 
 #pragma unroll
     for (int r = 0; r < 4; ++r) tmax = fmaxf(tmax, sc[at][r]);
   }
-  tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-  tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+  tmax = rows4_max(tmax);
   const float m_new = fmaxf(m_run, tmax);
   if (__any(m_new != m_run)) {
     const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);

@@ -442,8 +442,7 @@ __global__ __launch_bounds__(256, 2) void prefill_affine_d128(PrefillArgs a) {
         for (int t = 0; t < 2; ++t)
 #pragma unroll
           for (int r = 0; r < 4; ++r) tmax = fmaxf(tmax, sc[ct][t][r]);
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+        tmax = rows4_max(tmax);
         const float m_new = fmaxf(m_run[ct], tmax * sc_l2);
         if (m_new == -INFINITY) {  // nothing visible yet for this column
 #pragma unroll
