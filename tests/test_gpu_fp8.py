@@ -198,3 +198,24 @@ def test_fp8_decode_edge_lengths_and_invalid_pages(cuda):
                            tables, lens, wl.query_start_loc, compute_dtype=np.float64)
     assert_attention_close(out, exp, "fp8 edges")
     assert np.all(out[1] == 0)
+
+
+@pytest.mark.parametrize("qdtype,hq,hkv,d", [("bf16", 32, 8, 128), ("f32", 12, 4, 64), ("f16", 24, 8, 128)],
+                         ids=["bf16-queries", "f32-d64", "gqa3"])
+def test_fp8_generic_shapes_vs_oracle(cuda, qdtype, hq, hkv, d):
+    """Shapes outside the MFMA paths (bf16 / fp32 queries, head_dim 64, GQA 3) on the generic kernel's FP8
+    loader: a ragged batch of prefill chunks and decode rows vs the oracle."""
+    print(f"[fp8 generic {qdtype} {hq}/{hkv} d={d}]", flush=True)
+    wl = unified_workload("fp8g", seed=28 + hq, num_prefill=2, chunk=40, prior_range=(0, 200), num_decode=4,
+                          decode_ctx=(1, 600), num_q_heads=hq, num_kv_heads=hkv, head_dim=d, bits=None)
+    view = _view(wl, cuda)
+    kc, vc, ks, vs = _write_per_sequence(wl, view, "f16", hold_last=False)
+    tdt = {"bf16": torch.bfloat16, "f32": torch.float32, "f16": torch.float16}[qdtype]
+    q = torch.from_numpy(wl.q).to(cuda).to(tdt)
+    out = paged_attention(q, view.key_cache, view.value_cache, view.block_tables, view.kv_lens,
+                          torch.from_numpy(wl.query_start_loc).to(cuda), k_scale=view.k_scales, v_scale=view.v_scales)
+    torch.cuda.synchronize()
+    assert out.dtype == tdt
+    exp = oracle_attention(q.float().cpu().numpy(), fp8.fp8_dequant_cache(kc, ks), fp8.fp8_dequant_cache(vc, vs),
+                           wl.block_tables, wl.kv_lens, wl.query_start_loc, compute_dtype=np.float64)
+    assert_attention_close(out.float().cpu().numpy(), exp, f"fp8 generic {qdtype}")
