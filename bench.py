@@ -291,7 +291,31 @@ def aux_fp8(dev):
     w = lambda i=0: view.write_slots(kk, kk, slot)  # noqa: E731
     warm(w, 0.2)
     wus = float(np.median(event_us(w, 100)))
+    # the c3-shaped unified step (4 x 512 prefill rows + 28 decode rows) over an FP8 cache
+    from easymlx_amd.workloads import unified_workload
+
+    uw = unified_workload("c3", bits=None)
+    ushape = (uw.num_blocks, uw.block_size, uw.num_kv_heads, uw.head_dim)
+    uv = Fp8PageCacheView(key_cache=torch.zeros(ushape, dtype=torch.uint8, device=dev),
+                          value_cache=torch.zeros(ushape, dtype=torch.uint8, device=dev),
+                          k_scales=torch.zeros(uw.num_blocks, device=dev), v_scales=torch.zeros(uw.num_blocks, device=dev),
+                          block_tables=torch.from_numpy(uw.block_tables).to(dev),
+                          kv_lens=torch.from_numpy(uw.kv_lens).to(dev), block_size=uw.block_size,
+                          num_kv_heads=uw.num_kv_heads, head_dim=uw.head_dim)
+    uv.write_slots(torch.from_numpy(uw.k).to(dev), torch.from_numpy(uw.v).to(dev),
+                   torch.from_numpy(uw.slot.astype(np.int32)).to(dev))
+    uq = torch.from_numpy(uw.q).to(dev)
+    uqsl = torch.from_numpy(uw.query_start_loc).to(dev)
+    uout = torch.empty_like(uq)
+
+    def ucall(i=0):
+        paged_attention(uq, uv.key_cache, uv.value_cache, uv.block_tables, uv.kv_lens, uqsl, k_scale=uv.k_scales,
+                        v_scale=uv.v_scales, out=uout)
+
+    warm(ucall, 0.3)
+    uus = float(np.median(event_us(ucall, 50)))
     return {"workload": "fp8 e4m3 cache, c2 shape: batch 32, Hq 32 / Hkv 8, D 128, page 128, ctx U[512,4096] (seed 2)",
+            "unified_c3_shape_us_p50": round(uus, 2),
             "decode_us_p50": round(us, 2), "kv_bytes": nbytes, "kv_GBs": round(nbytes / (us * 1e3), 1),
             "frac": round(nbytes / (us * 1e3) / HBM_PEAK_GBS, 4), "write_32_tokens_us_p50": round(wus, 2)}
 

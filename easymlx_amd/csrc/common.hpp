@@ -92,6 +92,13 @@ __device__ __forceinline__ float e4m3_to_f32(uint32_t c) {
   return (c & 0x80u) ? -v : v;
 }
 
+// Two E4M3 bytes at bits 0-7 and 16-23 of y (zeros elsewhere) -> two fp16 equal
+// to dec(byte) * 2^-8 exactly: the 16-bit value (b + (b & 0x80)) << 7 keeps the
+// sign and shifts exponent and mantissa up by seven bits (normals: exponent bias
+// 15 against 7; sub-normals: m * 2^-17 = m * 2^-9 * 2^-8; 0x7F gives 1.875 =
+// 480 * 2^-8, the reference decoder's value for that code).
+__device__ __forceinline__ uint32_t e4m3x2_to_h16x2(const uint32_t y) { return (y + (y & 0x00800080u)) << 7; }
+
 // float -> FP8 E4M3 code with the reference's encoder
 // (lib/python/easymlx/operations/kernels/_metal_header.py:339-419): round to
 // nearest even for exponents 1..14, round half up through its sub-normal

@@ -45,9 +45,6 @@ namespace emx {
 
 constexpr int kFp8DecodeNT = 32;  // tokens per work item
 
-// Two E4M3 bytes at bits 0-7 and 16-23 of y (zeros elsewhere) -> two fp16 equal
-// to dec(byte) * 2^-8.
-__device__ __forceinline__ uint32_t e4m3x2_to_h16x2(const uint32_t y) { return (y + (y & 0x00800080u)) << 7; }
 
 struct Fp8Loads {
   uint32_t k[2][8];  // [sub-tile][dword]: 32 bytes of one token

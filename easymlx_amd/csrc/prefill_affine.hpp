@@ -283,17 +283,19 @@ __global__ __launch_bounds__(256, 2) void prefill_affine_d128(PrefillArgs a) {
       for (int e = 0; e < 4; ++e)
         *reinterpret_cast<h16x8*>(kr + 32 * kq + 8 * e) = unpack4(rk[e]);
     } else if constexpr (FP8) {
-      // the 16 codes of dims 16kq .. 16kq+15 as their exact fp16 values
+      // the 16 codes of dims 16kq .. 16kq+15 as the exact fp16 values dec(code) * 2^-8
 #pragma unroll
       for (int e = 0; e < 2; ++e) {
-        h16x8 o;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) o[i] = (h16)e4m3_to_f32((rk[2 * e + (i >> 2)] >> (8 * (i & 3))) & 0xFFu);
-        *reinterpret_cast<h16x8*>(kr + 16 * kq + 8 * e) = o;
+        const uint32_t w0 = rk[2 * e], w1 = rk[2 * e + 1];
+        *reinterpret_cast<h16x8*>(kr + 16 * kq + 8 * e) =
+            as_h8(e4m3x2_to_h16x2(__builtin_amdgcn_perm(0u, w0, 0x0C010C00u)),
+                  e4m3x2_to_h16x2(__builtin_amdgcn_perm(0u, w0, 0x0C030C02u)),
+                  e4m3x2_to_h16x2(__builtin_amdgcn_perm(0u, w1, 0x0C010C00u)),
+                  e4m3x2_to_h16x2(__builtin_amdgcn_perm(0u, w1, 0x0C030C02u)));
       }
-      // scores keep the affine formula: key scale = page scale * 2^-24, biases 0
+      // scores keep the affine formula: key scale = page scale * 2^8 * 2^-24, biases 0
       if (tid < NT) {
-        ksf[0][0][tid] = psk * (1.0f / kTwo24);
+        ksf[0][0][tid] = psk * (256.0f / kTwo24);
         ksf[1][0][tid] = 0.f;
       }
       vsc = psv;
@@ -327,7 +329,10 @@ __global__ __launch_bounds__(256, 2) void prefill_affine_d128(PrefillArgs a) {
         const int kk = (k0 & 31) + 4 * q4;
         h16x4 o;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) o[r] = (h16)(e4m3_to_f32(raw_v[(k0 + 4 * q4 + r) * D + dim]) * vsc);
+        for (int r = 0; r < 4; ++r) {  // (dec * 2^-8) * (scale * 2^8): the same product as dec * scale
+          const uint32_t h = e4m3x2_to_h16x2(raw_v[(k0 + 4 * q4 + r) * D + dim]);
+          o[r] = (h16)((float)__builtin_bit_cast(h16, (uint16_t)h) * (vsc * 256.0f));
+        }
         *reinterpret_cast<h16x4*>(vd + pv_slot(kk)) = o;
       }
       return;
