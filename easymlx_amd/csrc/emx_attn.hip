@@ -188,11 +188,11 @@ PrefillFn pick_prefill_hg(int hg) {
 
 PrefillFn pick_prefill_fp8(int hg) {
   switch (hg) {
-    case 1: return emx::prefill_affine_d128<8, 128, 1, true>;
-    case 2: return emx::prefill_affine_d128<8, 128, 2, true>;
-    case 4: return emx::prefill_affine_d128<8, 128, 4, true>;
-    case 8: return emx::prefill_affine_d128<8, 128, 8, true>;
-    case 16: return emx::prefill_affine_d128<8, 128, 16, true>;
+    case 1: return emx::prefill_affine_d128<4, 128, 1, true>;
+    case 2: return emx::prefill_affine_d128<4, 128, 2, true>;
+    case 4: return emx::prefill_affine_d128<4, 128, 4, true>;
+    case 8: return emx::prefill_affine_d128<4, 128, 8, true>;
+    case 16: return emx::prefill_affine_d128<4, 128, 16, true>;
   }
   return nullptr;
 }
@@ -717,7 +717,8 @@ int emx_paged_attention_fp8(const void* queries, int num_tokens, int num_q_heads
   const size_t need =
       emx_paged_workspace_bytes(num_seqs, num_q_heads, num_kv_heads, head_dim, max_blocks_per_seq, page_size);
   const DecodeFn dfn = mfma_ok && need > 0 ? pick_decode_fp8(hg) : nullptr;
-  const PrefillFn pf = mfma_ok ? pick_prefill_fp8(hg) : nullptr;
+  // the FP8 prefill kernel walks 64-key steps inside one page
+  const PrefillFn pf = mfma_ok && page_size % 64 == 0 ? pick_prefill_fp8(hg) : nullptr;
   auto launch_prefill = [&](int min_q) {
     emx::PrefillArgs p{};
     p.q = reinterpret_cast<const emx::h16*>(queries);

@@ -100,12 +100,15 @@ __device__ __forceinline__ int prefill_tiles(const PrefillArgs& a, const int s, 
 // keys kg*4 + {0..3} and 16 + kg*4 + {0..3} of the block, in that order.
 __device__ __forceinline__ constexpr int pv_slot(int k) { return 8 * ((k & 15) >> 2) + 4 * (k >> 4) + (k & 3); }
 
-// FP8: the same kernel over an FP8 cache (BITS 8, one group): K expands to its
-// exact fp16 values with the page scale * 2^-24 as the key scale (so the scores
-// keep the affine formula with zero biases), V dequantizes to dec(code) * scale.
+// FP8: the same kernel over an FP8 cache, on the 64-key step geometry of BITS 4
+// with one group (two 16-byte pieces of K and of V per thread and step; pages
+// of a multiple of 64 tokens): K expands to dec(code) * 2^-8 exactly with the
+// page scale * 2^8 * 2^-24 as the key scale (so the scores keep the affine
+// formula with zero biases), V dequantizes to dec(code) * scale.
 template <int BITS, int GS, int HG, bool FP8 = false>
 __global__ __launch_bounds__(256, 2) void prefill_affine_d128(PrefillArgs a) {
-  static_assert(!FP8 || (BITS == 8 && GS == 128), "the FP8 cache runs as 8-bit codes in one group");
+  static_assert(!FP8 || (BITS == 4 && GS == 128), "the FP8 cache runs on the 64-key geometry, one group");
+  constexpr int RAWV = FP8 ? 2 * PrefillCfg<BITS, GS, HG>::RAWV : PrefillCfg<BITS, GS, HG>::RAWV;
   using P = PrefillCfg<BITS, GS, HG>;
   constexpr int D = P::D, G = P::G, NT = P::NT, NA = P::NA, NKS = P::NKS, W = P::W;
 
@@ -206,7 +209,7 @@ __global__ __launch_bounds__(256, 2) void prefill_affine_d128(PrefillArgs a) {
       const h16x8 raw = *reinterpret_cast<const h16x8*>(qp + 32 * w + 8 * jj);
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const h16 v = cvalid[ct] ? raw[slot_perm<BITS>(i)] : (h16)0.0f;
+        const h16 v = cvalid[ct] ? raw[slot_perm<FP8 ? 8 : BITS>(i)] : (h16)0.0f;
         qB[ct][w][i] = v;
         gs[(32 * w) / GS] += (float)v;
       }
@@ -221,7 +224,7 @@ __global__ __launch_bounds__(256, 2) void prefill_affine_d128(PrefillArgs a) {
   }
 
   // ---- LDS: the step's raw V tile and scales, then the expanded K, dequantized V and fp32 K scales
-  __shared__ __attribute__((aligned(16))) uint8_t raw_v[P::RAWV];
+  __shared__ __attribute__((aligned(16))) uint8_t raw_v[RAWV];
   __shared__ __attribute__((aligned(16))) h16 raw_s[4 * G * NT];   // [arr][g][NT]
   __shared__ __attribute__((aligned(16))) h16 ke[NT * P::KSTR];    // [key][dims, unpack order]
   __shared__ __attribute__((aligned(16))) h16 ve[D * P::VSTR];     // [dim][keys, pv_slot order]
@@ -229,7 +232,7 @@ __global__ __launch_bounds__(256, 2) void prefill_affine_d128(PrefillArgs a) {
 
   // Cooperative load of one step into registers: thread owns one 16-byte piece of K and of V,
   // and (threads < SEGS * SEGB / 16) one piece of the scales.
-  u32x4 rk, rv, rsc;
+  u32x4 rk, rv, rsc, rk2, rv2;  // rk2 / rv2: FP8's second pieces (key rows 32 .. 63 of the step)
   float psk = 0.f, psv = 0.f;  // FP8: the loaded step's page scales
   float vsc = 0.f;             // FP8: the expanded step's value scale
   auto load_step = [&](const int st) {
@@ -238,11 +241,14 @@ __global__ __launch_bounds__(256, 2) void prefill_affine_d128(PrefillArgs a) {
     const int blk = (unsigned)blk_i < (unsigned)a.nb ? blk_i : 0;
     const int off = pos0 % a.bs;
     if constexpr (FP8) {
-      // 32 key rows of 128 bytes, 1 KiB apart per head: thread -> row tid / 8, bytes 16 * (tid % 8) ..
+      // 64 key rows of 128 bytes, Hkv * 128 bytes apart: thread -> rows tid / 8 and 32 + tid / 8,
+      // bytes 16 * (tid % 8) ..
       const size_t rowb = (size_t)a.Hkv * D;
       const size_t base = ((size_t)blk * a.bs + off + (tid >> 3)) * rowb + (size_t)kvh * D + 16 * (tid & 7);
       rk = *reinterpret_cast<const u32x4*>(a.k8 + base);
       rv = *reinterpret_cast<const u32x4*>(a.v8 + base);
+      rk2 = *reinterpret_cast<const u32x4*>(a.k8 + base + 32 * rowb);
+      rv2 = *reinterpret_cast<const u32x4*>(a.v8 + base + 32 * rowb);
       psk = a.kps[blk];
       psv = a.vps[blk];
       return;
@@ -275,23 +281,21 @@ __global__ __launch_bounds__(256, 2) void prefill_affine_d128(PrefillArgs a) {
 
   // Expansion, part 1 (from registers): K codes -> exact fp16 subnormals; raw V and scales -> LDS.
   auto expand_k = [&]() {
-    const int krow = tid / (W / 4), kq = tid % (W / 4);
-    h16* kr = ke + krow * P::KSTR;
-    if constexpr (BITS == 4) {
-      // words 4kq .. 4kq+3 hold dims 32kq .. 32kq+31: one MFMA k-step, lane group e of it
+    if constexpr (FP8) {
+      // rows tid / 8 and 32 + tid / 8: the 16 codes of dims 16kq .. 16kq+15 as the exact fp16
+      // values dec(code) * 2^-8
+      const int kq = tid & 7;
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        *reinterpret_cast<h16x8*>(kr + 32 * kq + 8 * e) = unpack4(rk[e]);
-    } else if constexpr (FP8) {
-      // the 16 codes of dims 16kq .. 16kq+15 as the exact fp16 values dec(code) * 2^-8
+      for (int pc = 0; pc < 2; ++pc) {
+        const u32x4 w = pc ? rk2 : rk;
+        h16* kr = ke + ((tid >> 3) + 32 * pc) * P::KSTR;
 #pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        const uint32_t w0 = rk[2 * e], w1 = rk[2 * e + 1];
-        *reinterpret_cast<h16x8*>(kr + 16 * kq + 8 * e) =
-            as_h8(e4m3x2_to_h16x2(__builtin_amdgcn_perm(0u, w0, 0x0C010C00u)),
-                  e4m3x2_to_h16x2(__builtin_amdgcn_perm(0u, w0, 0x0C030C02u)),
-                  e4m3x2_to_h16x2(__builtin_amdgcn_perm(0u, w1, 0x0C010C00u)),
-                  e4m3x2_to_h16x2(__builtin_amdgcn_perm(0u, w1, 0x0C030C02u)));
+        for (int e = 0; e < 2; ++e)
+          *reinterpret_cast<h16x8*>(kr + 16 * kq + 8 * e) =
+              as_h8(e4m3x2_to_h16x2(__builtin_amdgcn_perm(0u, w[2 * e], 0x0C010C00u)),
+                    e4m3x2_to_h16x2(__builtin_amdgcn_perm(0u, w[2 * e], 0x0C030C02u)),
+                    e4m3x2_to_h16x2(__builtin_amdgcn_perm(0u, w[2 * e + 1], 0x0C010C00u)),
+                    e4m3x2_to_h16x2(__builtin_amdgcn_perm(0u, w[2 * e + 1], 0x0C030C02u)));
       }
       // scores keep the affine formula: key scale = page scale * 2^8 * 2^-24, biases 0
       if (tid < NT) {
@@ -299,8 +303,17 @@ __global__ __launch_bounds__(256, 2) void prefill_affine_d128(PrefillArgs a) {
         ksf[1][0][tid] = 0.f;
       }
       vsc = psv;
-      reinterpret_cast<u32x4*>(raw_v)[tid] = rv;  // [32 keys][128 bytes]
+      reinterpret_cast<u32x4*>(raw_v)[tid] = rv;  // [64 keys][128 bytes]
+      reinterpret_cast<u32x4*>(raw_v)[256 + tid] = rv2;
       return;
+    }
+    const int krow = tid / (W / 4), kq = tid % (W / 4);
+    h16* kr = ke + krow * P::KSTR;
+    if constexpr (BITS == 4) {
+      // words 4kq .. 4kq+3 hold dims 32kq .. 32kq+31: one MFMA k-step, lane group e of it
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        *reinterpret_cast<h16x8*>(kr + 32 * kq + 8 * e) = unpack4(rk[e]);
     } else {
       // words 4kq .. 4kq+3 hold dims 16kq .. 16kq+15: half of k-step kq/2, lane groups 2(kq%2), +1
 #pragma unroll
