@@ -244,6 +244,37 @@ def test_abi_argument_errors(lib):
     assert lib.emx_paged_workspace_bytes(32, 32, 8, 64, 32, 128) == 0
 
 
+def test_abi_rope_and_prefill_split_arguments(lib):
+    """Argument checks of the RoPE and key-split entry points run on the host (no device work)."""
+    from easymlx_amd import _native
+
+    err = _native.EMX_ERR_INVALID
+    one = ctypes.c_int32(0)
+    inv = ctypes.c_float(1.0)
+    p_one, p_inv = ctypes.addressof(one), ctypes.addressof(inv)
+    # rope_rows: zero rows is a no-op; odd or oversized rot_dims and missing tables are errors
+    assert lib.emx_rope_rows(None, 0, 8, 128, None, None, 128, 0, None) == _native.EMX_OK
+    assert lib.emx_rope_rows(p_one, 4, 8, 128, p_one, p_inv, 127, 0, None) == err
+    assert lib.emx_rope_rows(p_one, 4, 8, 128, p_one, p_inv, 130, 0, None) == err
+    assert lib.emx_rope_rows(p_one, 4, 8, 128, None, p_inv, 128, 0, None) == err
+    assert b"rope" in lib.emx_last_error()
+    # fused writes: the same checks before any pointer is touched; FP8 needs rot_dims % 8 (4 if traditional)
+    args = [p_one, p_one, p_one, 4, 8, 128, 64, 4, 128, 16] + [p_one] * 6
+    assert lib.emx_affine_cache_write_rope(*args, None, p_inv, 128, 0, None) == err
+    assert lib.emx_affine_cache_write_rope(*args, p_one, p_inv, 0, 0, None) == err
+    fargs = [p_one, p_one, _native.DTYPE_F16, p_one, 4, 8, 128, 128, 16, p_one, p_one, p_one, p_one, p_one, 2048]
+    assert lib.emx_fp8_cache_write_rope(*fargs, p_one, p_inv, 12, 0, None) == err
+    assert lib.emx_fp8_cache_write_rope(*fargs, p_one, p_inv, 10, 1, None) == err
+    # prefill key-split workspace: host arithmetic, 0 where the split cannot apply, growing with the tokens
+    c3 = lib.emx_paged_prefill_workspace_bytes(2076, 32, 32, 8, 128)
+    assert c3 > 0 and c3 % 4 == 0
+    assert lib.emx_paged_prefill_workspace_bytes(4152, 32, 32, 8, 128) > c3
+    assert lib.emx_paged_prefill_workspace_bytes(2076, 32, 32, 8, 64) == 0    # head_dim 64: no MFMA prefill
+    assert lib.emx_paged_prefill_workspace_bytes(2076, 32, 24, 8, 128) == 0   # GQA 3
+    assert lib.emx_paged_prefill_workspace_bytes(0, 32, 32, 8, 128) == 0
+    assert lib.emx_paged_prefill_workspace_bytes(10 ** 7, 32, 32, 8, 128) == 0  # counters would not fit
+
+
 def test_bench_refuses_more_than_one_gpu():
     r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True, text=True,
                        timeout=60)
