@@ -639,6 +639,15 @@ static int fp8_write_impl(const void* keys, const void* values, int dtype, const
   const size_t n = (size_t)num_tokens * num_kv_heads * head_dim;
   const int nparts = (int)std::min<size_t>(emx::kFp8Parts, (n / 4 + 255) / 256);
   const int nwrite = (int)std::min<size_t>(1024, (n / 4 + 255) / 256);
+  if (n <= (size_t)emx::kFp8SelfMax) {  // one launch: each workgroup takes the maxima itself
+    const dim3 g1((unsigned)((n / 4 + 1023) / 1024));
+    switch (dtype) {
+      case EMX_DTYPE_F16: hipLaunchKernelGGL((emx::fp8_write<emx::F16, true>), g1, dim3(1024), 0, st, a, 0); break;
+      case EMX_DTYPE_BF16: hipLaunchKernelGGL((emx::fp8_write<emx::BF16, true>), g1, dim3(1024), 0, st, a, 0); break;
+      default: hipLaunchKernelGGL((emx::fp8_write<emx::F32, true>), g1, dim3(1024), 0, st, a, 0); break;
+    }
+    return check_launch("fp8_cache_write");
+  }
   switch (dtype) {
     case EMX_DTYPE_F16:
       hipLaunchKernelGGL(emx::fp8_amax<emx::F16>, dim3(nparts), dim3(256), 0, st, a);

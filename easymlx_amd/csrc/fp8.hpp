@@ -8,14 +8,17 @@
 //   * each written page's scale raised to max(page_scale, scale); the page's
 //     earlier codes are not requantized (the reference's rule).
 // Two launches: per-workgroup maxima into a small workspace, then every
-// workgroup reduces them and quantizes its share (4 values per thread).
+// workgroup reduces them and quantizes its share (4 values per thread).  Writes
+// of up to kFp8SelfMax values per tensor (decode appends) take one launch in
+// which every workgroup computes the maxima itself.
 #pragma once
 
 #include "common.hpp"
 
 namespace emx {
 
-constexpr int kFp8Parts = 256;  // workgroups of the max pass (partials in the workspace)
+constexpr int kFp8Parts = 256;      // workgroups of the max pass (partials in the workspace)
+constexpr int kFp8SelfMax = 65536;  // values per tensor of the one-launch write
 
 struct Fp8WriteArgs {
   const void* k;         // [T, Hkv, D] in the input dtype
@@ -104,11 +107,60 @@ __global__ __launch_bounds__(256) void fp8_amax(Fp8WriteArgs a) {
   }
 }
 
-template <typename Tag>
-__global__ __launch_bounds__(256) void fp8_write(Fp8WriteArgs a, int nparts) {
+template <typename Tag, bool SELF = false>
+__global__ __launch_bounds__(SELF ? 1024 : 256) void fp8_write(Fp8WriteArgs a, int nparts) {
   typedef typename Tag::T T;
+  constexpr int NTH = SELF ? 1024 : 256;  // threads per workgroup
   __shared__ float sc[2];
-  if (threadIdx.x < 64) {
+  if constexpr (SELF) {
+    // a small write in one launch: every workgroup takes the maxima over all the
+    // written values itself (exact and order-free, so each gets the same
+    // scales); four words per thread in flight together
+    const T* k = reinterpret_cast<const T*>(a.k);
+    const T* v = reinterpret_cast<const T*>(a.v);
+    const size_t row4 = (size_t)a.Hkv * a.D / 4, n4 = (size_t)a.T * row4;
+    float mk = 0.f, mv = 0.f;
+    for (size_t e0 = threadIdx.x; e0 < n4; e0 += 4 * NTH) {
+      float x[4][4], y[4][4];
+      bool live[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const size_t e = e0 + (size_t)u * NTH;
+        live[u] = e < n4 && a.slot[e / row4] >= 0;
+        const size_t ee = e < n4 ? e : e0;
+        k_word(a, k, ee, x[u]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) y[u][j] = to_f32(v[4 * ee + j]);
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        if (!live[u]) continue;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          mk = fmaxf(mk, fabsf(x[u][j]));
+          mv = fmaxf(mv, fabsf(y[u][j]));
+        }
+      }
+    }
+    mk = wave_max(mk);
+    mv = wave_max(mv);
+    __shared__ float sm[2][NTH / 64];
+    if ((threadIdx.x & 63) == 0) {
+      sm[0][threadIdx.x >> 6] = mk;
+      sm[1][threadIdx.x >> 6] = mv;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+      for (int i = 0; i < NTH / 64; ++i) {
+        a0 = fmaxf(a0, sm[0][i]);
+        a1 = fmaxf(a1, sm[1][i]);
+      }
+      sc[0] = a0 / 240.0f;
+      sc[1] = a1 / 240.0f;
+    }
+  } else if (threadIdx.x < 64) {
     float mk = 0.f, mv = 0.f;
     for (int i = threadIdx.x; i < nparts; i += 64) {
       mk = fmaxf(mk, a.part[i]);
@@ -128,7 +180,7 @@ __global__ __launch_bounds__(256) void fp8_write(Fp8WriteArgs a, int nparts) {
   const T* v = reinterpret_cast<const T*>(a.v);
   const int row4 = a.Hkv * a.D / 4;
   const size_t n4 = (size_t)a.T * row4;
-  for (size_t e = (size_t)blockIdx.x * 256 + threadIdx.x; e < n4; e += (size_t)gridDim.x * 256) {
+  for (size_t e = (size_t)blockIdx.x * NTH + threadIdx.x; e < n4; e += (size_t)gridDim.x * NTH) {
     const int t = (int)(e / row4), r = (int)(e % row4);
     const int slot = a.slot[t];
     if (slot < 0) continue;
