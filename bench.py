@@ -359,7 +359,7 @@ def aux_quantize_on_write(dev):
         us = float(np.median(event_us(call, 200)))
         moved = n * hkv * (2 * d * 2 + 2 * (d // 2 + 4 * (d // 64)))  # fp16 K,V in; codes + scale/bias out
         res[name] = {"tokens": n, "us_p50": round(us, 2), "GBs_in_plus_out": round(moved / (us * 1e3), 1)}
-    # a decode step's append with Llama-3 RoPE fused in: K rotated inside the write, Q (32 heads) in one launch
+    # a decode step's append with Llama-3 RoPE fused in: K rotated inside the write, Q (32 heads) by the same launch
     from easymlx_amd import RotaryEmbedding
 
     lib = _native.load()
@@ -373,11 +373,10 @@ def aux_quantize_on_write(dev):
     pos = torch.from_numpy(wl.kv_lens.astype(np.int32)).to(dev)
 
     def call_rope(i):
-        rc = lib.emx_rope_rows(q.data_ptr(), n, 32, d, pos.data_ptr(), inv.data_ptr(), d, 0, stream)
-        rc = rc or lib.emx_affine_cache_write_rope(
+        rc = lib.emx_affine_cache_write_rope(
             k.data_ptr(), v.data_ptr(), s.data_ptr(), n, hkv, d, 64, 4, bs, nb, view.k_codes.data_ptr(),
             view.k_scales.data_ptr(), view.k_biases.data_ptr(), view.v_codes.data_ptr(), view.v_scales.data_ptr(),
-            view.v_biases.data_ptr(), pos.data_ptr(), inv.data_ptr(), d, 0, stream)
+            view.v_biases.data_ptr(), pos.data_ptr(), inv.data_ptr(), d, 0, q.data_ptr(), 32, stream)
         if rc:
             _native.check(rc)
 

@@ -251,7 +251,7 @@ class PageCacheView:
         return queries, self.key_cache, self.value_cache, md
 
     def _concatenate_rope_fused(self, queries, keys, values, cache_metadata, rope, slot_ids, query_lens, write,
-                                rot_multiple):
+                                rot_multiple, writes_queries=False):
         """The write with a :class:`RotaryEmbedding` fused into ``write`` (a cache's C entry point) and Q turned
         by ``emx_rope_rows``; any other ``rope`` (or fp16-incompatible inputs) takes the reference's order."""
         from .rope import RotaryEmbedding
@@ -268,10 +268,11 @@ class PageCacheView:
         if n:
             inv = rope.inv_freq(q_out.device)
             stream = _stream_ptr(q_out.device)
-            _native.check(lib.emx_rope_rows(q_out.data_ptr(), n, int(q_out.shape[1]), self.head_dim,
-                                            positions.data_ptr(), inv.data_ptr(), rope.dims, int(rope.traditional),
-                                            stream))
-            _native.check(write(keys, values, slot_mapping, positions, inv, rope, stream))
+            if not writes_queries:
+                _native.check(lib.emx_rope_rows(q_out.data_ptr(), n, int(q_out.shape[1]), self.head_dim,
+                                                positions.data_ptr(), inv.data_ptr(), rope.dims,
+                                                int(rope.traditional), stream))
+            _native.check(write(keys, values, slot_mapping, positions, inv, rope, stream, q_out))
         if len(slot_ids):
             add = torch.tensor(qlens, dtype=torch.int32, device=self.kv_lens.device)
             self.kv_lens.index_copy_(0, slots, (base + add).to(torch.int32))
@@ -393,7 +394,7 @@ class Fp8PageCacheView(PageCacheView):
 
         codes = {torch.float16: DTYPE_F16, torch.bfloat16: DTYPE_BF16, torch.float32: DTYPE_F32}
 
-        def write(keys, values, slot_mapping, positions, inv, rope, stream):
+        def write(keys, values, slot_mapping, positions, inv, rope, stream, q_out):
             if keys.dtype not in codes or values.dtype != keys.dtype:
                 raise NotImplementedError(f"FP8 cache writes take fp16/bf16/fp32 keys and values, got {keys.dtype}")
             lib = _native.load()
@@ -557,9 +558,9 @@ class AffinePageCacheView(PageCacheView):
     def concatenate_to_cache(self, queries, keys, values, *, cache_metadata, rope=None, slot_ids=None,
                              query_lens=None):
         """``PageCacheView.concatenate_to_cache`` with a :class:`RotaryEmbedding` fused in: K turns inside the
-        quantize-on-write kernel, Q in one launch (``cache.py:1161-1166`` then ``:1186-1190``)."""
+        quantize-on-write kernel and Q in the same launch (``cache.py:1161-1166`` then ``:1186-1190``)."""
 
-        def write(keys, values, slot_mapping, positions, inv, rope, stream):
+        def write(keys, values, slot_mapping, positions, inv, rope, stream, q_out):
             keys = keys.to(torch.float16).contiguous()
             values = values.to(torch.float16).contiguous()
             return _native.load().emx_affine_cache_write_rope(
@@ -567,10 +568,11 @@ class AffinePageCacheView(PageCacheView):
                 self.head_dim, self.group_size, self.bits, self.block_size, self.num_blocks,
                 self.key_cache.data_ptr(), self.k_scales.data_ptr(), self.k_biases.data_ptr(),
                 self.value_cache.data_ptr(), self.v_scales.data_ptr(), self.v_biases.data_ptr(),
-                positions.data_ptr(), inv.data_ptr(), rope.dims, int(rope.traditional), stream)
+                positions.data_ptr(), inv.data_ptr(), rope.dims, int(rope.traditional), q_out.data_ptr(),
+                int(q_out.shape[1]), stream)
 
         return self._concatenate_rope_fused(queries, keys, values, cache_metadata, rope, slot_ids, query_lens, write,
-                                            rot_multiple=2)
+                                            rot_multiple=2, writes_queries=True)
 
     def _zero_blocks(self, ids: torch.Tensor) -> None:
         for t in (self.key_cache, self.value_cache, self.k_scales, self.k_biases, self.v_scales, self.v_biases):

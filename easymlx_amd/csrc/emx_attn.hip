@@ -280,7 +280,8 @@ int emx_affine_quantize(const void* x, long rows, int head_dim, int group_size, 
 static int affine_write_impl(const void* keys, const void* values, const int32_t* slot_mapping, int num_tokens,
                       int num_kv_heads, int head_dim, int group_size, int bits, int page_size, int num_blocks,
                       uint32_t* k_codes, void* k_scales, void* k_biases, uint32_t* v_codes, void* v_scales,
-                      void* v_biases, const emx::RopeArgs& rope, void* stream) {
+                      void* v_biases, const emx::RopeArgs& rope, void* queries, int num_q_heads,
+                      void* stream) {
   if (num_tokens < 0) return fail(EMX_ERR_INVALID, "num_tokens must be >= 0");
   if (bits != 4 && bits != 8) return fail(EMX_ERR_UNSUPPORTED, "bits must be 4 or 8, got %d", bits);
   if (num_kv_heads <= 0 || head_dim <= 0 || page_size <= 0 || num_blocks <= 0)
@@ -314,12 +315,16 @@ static int affine_write_impl(const void* keys, const void* values, const int32_t
     return fail(EMX_ERR_UNSUPPORTED, "head_dim %d above %d or more than %d quantization groups per head", head_dim,
                 emx::kWriteMaxDim, emx::kWriteMaxGroups);
   a.rope = rope;
+  a.q = reinterpret_cast<emx::h16*>(queries);
+  a.Hq = num_q_heads;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (num_tokens <= emx::kSmallWrite && head_dim % 16 == 0 && group_size % 16 == 0 &&
       group_size <= emx::kSmallMaxGroup) {
-    const dim3 sgrid((unsigned)num_kv_heads, (unsigned)(head_dim / 16));
-    typedef void (*SmallFn)(emx::WriteArgs);
     const bool r = rope.inv_freq != nullptr;
+    // with RoPE and queries: kQRopeBlocks more rows of workgroups turn the queries in the same launch
+    const dim3 sgrid((unsigned)num_kv_heads,
+                     (unsigned)(head_dim / 16 + (r && queries ? emx::kQRopeBlocks : 0)));
+    typedef void (*SmallFn)(emx::WriteArgs);
     SmallFn fn = bits == 4 ? (r ? emx::affine_cache_write_small<4, true> : emx::affine_cache_write_small<4, false>)
                            : (r ? emx::affine_cache_write_small<8, true> : emx::affine_cache_write_small<8, false>);
     hipLaunchKernelGGL(fn, sgrid, dim3(256), 0, st, a);
@@ -330,7 +335,15 @@ static int affine_write_impl(const void* keys, const void* values, const int32_t
     hipLaunchKernelGGL(emx::affine_cache_write<4>, grid, dim3(256), 0, st, a);
   else
     hipLaunchKernelGGL(emx::affine_cache_write<8>, grid, dim3(256), 0, st, a);
-  return check_launch("affine_cache_write");
+  if (int rc = check_launch("affine_cache_write")) return rc;
+  if (rope.inv_freq != nullptr && queries != nullptr) {  // larger writes: the queries in their own launch
+    const long n = (long)num_tokens * num_q_heads * (rope.rot / 2);
+    const unsigned qgrid = (unsigned)std::min<long>((n + 255) / 256, 4096);
+    hipLaunchKernelGGL(emx::rope_rows, dim3(qgrid), dim3(256), 0, st, reinterpret_cast<emx::h16*>(queries),
+                       num_tokens, num_q_heads, head_dim, rope);
+    return check_launch("rope_rows");
+  }
+  return EMX_OK;
 }
 
 int emx_affine_cache_write(const void* keys, const void* values, const int32_t* slot_mapping, int num_tokens,
@@ -339,7 +352,7 @@ int emx_affine_cache_write(const void* keys, const void* values, const int32_t* 
                            void* v_biases, void* stream) {
   return affine_write_impl(keys, values, slot_mapping, num_tokens, num_kv_heads, head_dim, group_size, bits,
                            page_size, num_blocks, k_codes, k_scales, k_biases, v_codes, v_scales, v_biases,
-                           emx::RopeArgs{nullptr, nullptr, 0, 0}, stream);
+                           emx::RopeArgs{nullptr, nullptr, 0, 0}, nullptr, 0, stream);
 }
 
 static bool rope_ok(const int32_t* positions, const float* inv_freq, int rot_dims, int head_dim) {
@@ -350,12 +363,15 @@ int emx_affine_cache_write_rope(const void* keys, const void* values, const int3
                                 int num_kv_heads, int head_dim, int group_size, int bits, int page_size,
                                 int num_blocks, uint32_t* k_codes, void* k_scales, void* k_biases, uint32_t* v_codes,
                                 void* v_scales, void* v_biases, const int32_t* positions, const float* inv_freq,
-                                int rot_dims, int traditional, void* stream) {
+                                int rot_dims, int traditional, void* queries, int num_q_heads, void* stream) {
   if (num_tokens > 0 && !rope_ok(positions, inv_freq, rot_dims, head_dim))
     return fail(EMX_ERR_INVALID, "rope: positions and inv_freq needed, rot_dims even and in (0, head_dim]");
+  if (queries != nullptr && (num_q_heads <= 0 || !aligned16(queries)))
+    return fail(EMX_ERR_INVALID, "queries need num_q_heads > 0 and 16-byte alignment");
   return affine_write_impl(keys, values, slot_mapping, num_tokens, num_kv_heads, head_dim, group_size, bits,
                            page_size, num_blocks, k_codes, k_scales, k_biases, v_codes, v_scales, v_biases,
-                           emx::RopeArgs{inv_freq, positions, rot_dims, traditional ? 1 : 0}, stream);
+                           emx::RopeArgs{inv_freq, positions, rot_dims, traditional ? 1 : 0}, queries, num_q_heads,
+                           stream);
 }
 
 int emx_rope_rows(void* x, int rows, int heads, int head_dim, const int32_t* positions, const float* inv_freq,

@@ -131,7 +131,11 @@ struct WriteArgs {
   h16 *vs, *vb;                // [nb, Hkv, D/gs, bs]
   int T, Hkv, D, gs, bs, nb;
   RopeArgs rope;               // K rotation before quantizing (inv_freq null: none)
+  h16* q;                      // [T, Hq, D] queries turned in place by the same launch (null: none)
+  int Hq;
 };
+
+constexpr int kQRopeBlocks = 4;  // extra workgroup rows of the small write that turn the queries
 
 // One workgroup per (32 consecutive tokens, kv head):
 //   1. per (token, group, K|V): min/max -> scale/bias (kept in LDS, stored as fp16);
@@ -287,6 +291,25 @@ __global__ __launch_bounds__(256) void affine_cache_write_small(WriteArgs a) {
   const int tid = threadIdx.x;
   const int h = blockIdx.x;
   const int d0 = blockIdx.y * DB;
+  if constexpr (ROPE) {
+    // the extra rows of workgroups turn the queries (rows of gridDim.x * kQRopeBlocks workgroups)
+    if (d0 >= a.D) {
+      if (a.q == nullptr) return;
+      const RopeArgs& r = a.rope;
+      const int half = r.rot / 2;
+      const int nwg = gridDim.x * kQRopeBlocks;
+      const int wg = (blockIdx.y - a.D / DB) * gridDim.x + blockIdx.x;
+      const long n = (long)a.T * a.Hq * half;
+      for (long i = (long)wg * 256 + tid; i < n; i += (long)nwg * 256) {
+        const int p = (int)(i % half);
+        const long rh = i / half;
+        h16* v = a.q + rh * a.D;
+        const int i0 = r.traditional ? 2 * p : p, i1 = r.traditional ? 2 * p + 1 : p + half;
+        rope_pair(v[i0], v[i1], (float)r.positions[rh / a.Hq] * r.inv_freq[p]);
+      }
+      return;
+    }
+  }
   const int T = a.T;
   const int G = a.D / a.gs;
   const float n_bins = (float)((1 << BITS) - 1);

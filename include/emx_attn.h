@@ -74,6 +74,8 @@ int emx_affine_cache_write(const void* keys, const void* values, const int32_t* 
  * ((i, i + rot_dims/2), or (2i, 2i+1) when traditional != 0), are rounded to
  * fp16 and then quantized exactly as emx_affine_cache_write does.  V is not
  * rotated.  positions int32 [num_tokens], inv_freq float32 [rot_dims/2].
+ * queries (fp16 [num_tokens, num_q_heads, head_dim], or null) are turned in
+ * place by the same rotation, in the same launch for decode-size writes.
  * Replaces the RoPE applied to keys in PageCacheView.concatenate_to_cache
  *   lib/python/easymlx/caching/paged/cache.py:1161-1166 (multi-token :1208-1253)
  *   followed by the write :1186-1190, with the RoPE of
@@ -83,7 +85,7 @@ int emx_affine_cache_write_rope(const void* keys, const void* values, const int3
                                 int num_kv_heads, int head_dim, int group_size, int bits, int page_size,
                                 int num_blocks, uint32_t* k_codes, void* k_scales, void* k_biases, uint32_t* v_codes,
                                 void* v_scales, void* v_biases, const int32_t* positions, const float* inv_freq,
-                                int rot_dims, int traditional, void* stream);
+                                int rot_dims, int traditional, void* queries, int num_q_heads, void* stream);
 
 /*
  * Rotary position embedding in place on fp16 rows x [rows, heads, head_dim]

@@ -82,14 +82,18 @@ def test_fused_write_equals_rotate_then_write(cuda, bits, T):
     lib = _native.load()
     st = torch.cuda.current_stream(cuda).cuda_stream
     inv = rope.inv_freq(cuda)
+    q = torch.from_numpy(rng.standard_normal((T, 32, d)).astype(np.float16)).to(cuda)
+    qa = q.clone()  # turned by the write's own launch
     _native.check(lib.emx_affine_cache_write_rope(
         k.data_ptr(), v.data_ptr(), slots.data_ptr(), T, hkv, d, 64, bits, bs, nb, a.key_cache.data_ptr(),
         a.k_scales.data_ptr(), a.k_biases.data_ptr(), a.value_cache.data_ptr(), a.v_scales.data_ptr(),
-        a.v_biases.data_ptr(), pos.data_ptr(), inv.data_ptr(), rope.dims, 0, st))
-    kr = k.clone()
+        a.v_biases.data_ptr(), pos.data_ptr(), inv.data_ptr(), rope.dims, 0, qa.data_ptr(), 32, st))
+    kr, qb = k.clone(), q.clone()
     _rope_rows(kr, pos, rope)
+    _rope_rows(qb, pos, rope)
     b.write_slots(kr, v, slots)
     torch.cuda.synchronize()
+    assert torch.equal(qa, qb), "queries"
     for name in ("key_cache", "k_scales", "k_biases", "value_cache", "v_scales", "v_biases"):
         assert torch.equal(getattr(a, name), getattr(b, name)), name
 
