@@ -407,10 +407,12 @@ class Fp8PageCacheView(PageCacheView):
                 keys.data_ptr(), values.data_ptr(), codes[keys.dtype], slot_mapping.data_ptr(), int(keys.shape[0]),
                 self.num_kv_heads, self.head_dim, self.block_size, self.num_blocks, self.key_cache.data_ptr(),
                 self.value_cache.data_ptr(), self.k_scales.data_ptr(), self.v_scales.data_ptr(), self._ws.data_ptr(),
-                self._ws.numel(), positions.data_ptr(), inv.data_ptr(), rope.dims, int(rope.traditional), stream)
+                self._ws.numel(), positions.data_ptr(), inv.data_ptr(), rope.dims, int(rope.traditional),
+                q_out.data_ptr(), int(q_out.shape[1]), stream)
 
         return self._concatenate_rope_fused(queries, keys, values, cache_metadata, rope, slot_ids, query_lens, write,
-                                            rot_multiple=4 if getattr(rope, "traditional", False) else 8)
+                                            rot_multiple=4 if getattr(rope, "traditional", False) else 8,
+                                            writes_queries=True)
 
     def write_slots(self, keys: torch.Tensor, values: torch.Tensor, slot_mapping: torch.Tensor) -> None:
         """Write tokens to explicit slots (``block * block_size + offset``; -1 skips)."""

@@ -622,7 +622,8 @@ size_t emx_fp8_write_workspace_bytes(void) { return sizeof(float) * 2 * emx::kFp
 static int fp8_write_impl(const void* keys, const void* values, int dtype, const int32_t* slot_mapping, int num_tokens,
                           int num_kv_heads, int head_dim, int page_size, int num_blocks, uint8_t* key_cache,
                           uint8_t* value_cache, float* k_scales, float* v_scales, void* workspace,
-                          size_t workspace_bytes, const emx::RopeArgs& rope, void* stream) {
+                          size_t workspace_bytes, const emx::RopeArgs& rope, void* queries, int num_q_heads,
+                          void* stream) {
   if (num_tokens < 0) return fail(EMX_ERR_INVALID, "num_tokens must be >= 0");
   if (num_kv_heads <= 0 || head_dim <= 0 || page_size <= 0 || num_blocks <= 0)
     return fail(EMX_ERR_INVALID, "num_kv_heads, head_dim, page_size, num_blocks must be positive");
@@ -651,12 +652,16 @@ static int fp8_write_impl(const void* keys, const void* values, int dtype, const
   a.vs = v_scales;
   a.part = reinterpret_cast<float*>(workspace);
   a.rope = rope;
+  a.q = reinterpret_cast<emx::h16*>(queries);
+  a.Hq = num_q_heads;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const size_t n = (size_t)num_tokens * num_kv_heads * head_dim;
   const int nparts = (int)std::min<size_t>(emx::kFp8Parts, (n / 4 + 255) / 256);
   const int nwrite = (int)std::min<size_t>(1024, (n / 4 + 255) / 256);
+  const bool turn_q = rope.inv_freq != nullptr && queries != nullptr;
   if (n <= (size_t)emx::kFp8SelfMax) {  // one launch: each workgroup takes the maxima itself
-    const dim3 g1((unsigned)((n / 4 + 1023) / 1024));
+    a.nwg = (int)((n / 4 + 1023) / 1024);
+    const dim3 g1((unsigned)(a.nwg + (turn_q ? 4 : 0)));  // + workgroups that turn the queries
     switch (dtype) {
       case EMX_DTYPE_F16: hipLaunchKernelGGL((emx::fp8_write<emx::F16, true>), g1, dim3(1024), 0, st, a, 0); break;
       case EMX_DTYPE_BF16: hipLaunchKernelGGL((emx::fp8_write<emx::BF16, true>), g1, dim3(1024), 0, st, a, 0); break;
@@ -678,7 +683,14 @@ static int fp8_write_impl(const void* keys, const void* values, int dtype, const
       hipLaunchKernelGGL(emx::fp8_write<emx::F32>, dim3(nwrite), dim3(256), 0, st, a, nparts);
       break;
   }
-  return check_launch("fp8_cache_write");
+  if (int rc = check_launch("fp8_cache_write")) return rc;
+  if (turn_q) {  // larger writes: the queries in their own launch
+    const long nq = (long)num_tokens * num_q_heads * (rope.rot / 2);
+    hipLaunchKernelGGL(emx::rope_rows, dim3((unsigned)std::min<long>((nq + 255) / 256, 4096)), dim3(256), 0, st,
+                       reinterpret_cast<emx::h16*>(queries), num_tokens, num_q_heads, head_dim, rope);
+    return check_launch("rope_rows");
+  }
+  return EMX_OK;
 }
 
 int emx_fp8_cache_write(const void* keys, const void* values, int dtype, const int32_t* slot_mapping, int num_tokens,
@@ -687,20 +699,22 @@ int emx_fp8_cache_write(const void* keys, const void* values, int dtype, const i
                         size_t workspace_bytes, void* stream) {
   return fp8_write_impl(keys, values, dtype, slot_mapping, num_tokens, num_kv_heads, head_dim, page_size, num_blocks,
                         key_cache, value_cache, k_scales, v_scales, workspace, workspace_bytes,
-                        emx::RopeArgs{nullptr, nullptr, 0, 0}, stream);
+                        emx::RopeArgs{nullptr, nullptr, 0, 0}, nullptr, 0, stream);
 }
 
 int emx_fp8_cache_write_rope(const void* keys, const void* values, int dtype, const int32_t* slot_mapping,
                              int num_tokens, int num_kv_heads, int head_dim, int page_size, int num_blocks,
                              uint8_t* key_cache, uint8_t* value_cache, float* k_scales, float* v_scales,
                              void* workspace, size_t workspace_bytes, const int32_t* positions, const float* inv_freq,
-                             int rot_dims, int traditional, void* stream) {
+                             int rot_dims, int traditional, void* queries, int num_q_heads, void* stream) {
   if (num_tokens > 0 && (!rope_ok(positions, inv_freq, rot_dims, head_dim) || rot_dims % (traditional ? 4 : 8) != 0))
     return fail(EMX_ERR_INVALID,
                 "rope: positions and inv_freq needed, rot_dims in (0, head_dim] and a multiple of 8 (4 if traditional)");
+  if (queries != nullptr && num_q_heads <= 0) return fail(EMX_ERR_INVALID, "queries need num_q_heads > 0");
   return fp8_write_impl(keys, values, dtype, slot_mapping, num_tokens, num_kv_heads, head_dim, page_size, num_blocks,
                         key_cache, value_cache, k_scales, v_scales, workspace, workspace_bytes,
-                        emx::RopeArgs{inv_freq, positions, rot_dims, traditional ? 1 : 0}, stream);
+                        emx::RopeArgs{inv_freq, positions, rot_dims, traditional ? 1 : 0}, queries, num_q_heads,
+                        stream);
 }
 
 int emx_paged_attention_fp8(const void* queries, int num_tokens, int num_q_heads, int head_dim, int dtype,

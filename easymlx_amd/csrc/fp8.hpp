@@ -31,6 +31,9 @@ struct Fp8WriteArgs {
   float* vs;
   float* part;           // [2][kFp8Parts] per-workgroup maxima
   RopeArgs rope;         // K turned before the scale and the codes (inv_freq null: none)
+  h16* q;                // [T, Hq, D] fp16 queries turned in place by the one-launch write (null: none)
+  int Hq;
+  int nwg;               // workgroups of the write proper; later ones turn the queries
 };
 
 __device__ __forceinline__ float round_to(float x, h16*) { return (float)(h16)x; }
@@ -113,6 +116,22 @@ __global__ __launch_bounds__(SELF ? 1024 : 256) void fp8_write(Fp8WriteArgs a, i
   constexpr int NTH = SELF ? 1024 : 256;  // threads per workgroup
   __shared__ float sc[2];
   if constexpr (SELF) {
+    if ((int)blockIdx.x >= a.nwg) {  // the query rotation rides in the same launch
+      const RopeArgs& r = a.rope;
+      const int half = r.rot / 2;
+      const long n = (long)a.T * a.Hq * half;
+      for (long i = (long)(blockIdx.x - a.nwg) * NTH + threadIdx.x; i < n; i += (long)(gridDim.x - a.nwg) * NTH) {
+        const int p = (int)(i % half);
+        const long rh = i / half;
+        h16* v = a.q + rh * a.D;
+        const int i0 = r.traditional ? 2 * p : p, i1 = r.traditional ? 2 * p + 1 : p + half;
+        float y0, y1;
+        rope_rotate((float)v[i0], (float)v[i1], (float)r.positions[rh / a.Hq] * r.inv_freq[p], y0, y1);
+        v[i0] = (h16)y0;
+        v[i1] = (h16)y1;
+      }
+      return;
+    }
     // a small write in one launch: every workgroup takes the maxima over all the
     // written values itself (exact and order-free, so each gets the same
     // scales); four words per thread in flight together
@@ -180,7 +199,8 @@ __global__ __launch_bounds__(SELF ? 1024 : 256) void fp8_write(Fp8WriteArgs a, i
   const T* v = reinterpret_cast<const T*>(a.v);
   const int row4 = a.Hkv * a.D / 4;
   const size_t n4 = (size_t)a.T * row4;
-  for (size_t e = (size_t)blockIdx.x * NTH + threadIdx.x; e < n4; e += (size_t)gridDim.x * NTH) {
+  const int nwg = SELF ? a.nwg : (int)gridDim.x;
+  for (size_t e = (size_t)blockIdx.x * NTH + threadIdx.x; e < n4; e += (size_t)nwg * NTH) {
     const int t = (int)(e / row4), r = (int)(e % row4);
     const int slot = a.slot[t];
     if (slot < 0) continue;

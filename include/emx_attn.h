@@ -183,7 +183,8 @@ int emx_fp8_cache_write(const void* keys, const void* values, int dtype, const i
  * emx_fp8_cache_write with rotary position embedding fused in: the call's K
  * scale and codes are taken over the keys turned as in
  * emx_affine_cache_write_rope and rounded to dtype.  rot_dims a multiple of 8
- * (of 4 when traditional).
+ * (of 4 when traditional).  queries (fp16 [num_tokens, num_q_heads, head_dim],
+ * or null) are turned in place, in the same launch for decode-size writes.
  * Replaces the RoPE of PageCacheView.concatenate_to_cache
  *   lib/python/easymlx/caching/paged/cache.py:1161-1166 followed by its FP8 write :1171-1184.
  */
@@ -191,7 +192,7 @@ int emx_fp8_cache_write_rope(const void* keys, const void* values, int dtype, co
                              int num_tokens, int num_kv_heads, int head_dim, int page_size, int num_blocks,
                              uint8_t* key_cache, uint8_t* value_cache, float* k_scales, float* v_scales,
                              void* workspace, size_t workspace_bytes, const int32_t* positions, const float* inv_freq,
-                             int rot_dims, int traditional, void* stream);
+                             int rot_dims, int traditional, void* queries, int num_q_heads, void* stream);
 
 /*
  * Paged attention over an FP8 (E4M3) cache key/value [num_blocks, page_size,

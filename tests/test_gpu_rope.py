@@ -129,15 +129,15 @@ def test_concatenate_fused_vs_callable(cuda):
         assert views[0].kv_lens.cpu().tolist() == views[1].kv_lens.cpu().tolist()
 
 
-@pytest.mark.parametrize("traditional", [False, True])
-def test_fp8_fused_write_equals_rotate_then_write(cuda, traditional):
+@pytest.mark.parametrize("traditional,T", [(False, 200), (True, 200), (False, 24)])
+def test_fp8_fused_write_equals_rotate_then_write(cuda, traditional, T):
     """FP8 cache: the call's scale and the codes over the turned keys, in the write kernels == emx_rope_rows on K,
     then the plain FP8 write: every byte of the pages and every page scale."""
     from easymlx_amd import Fp8PageCacheView
 
-    print(f"[fp8 fused rope write traditional={traditional}]", flush=True)
-    rng = np.random.default_rng(11 + traditional)
-    T, hkv, d, bs, nb = 200, 8, 128, 32, 64
+    print(f"[fp8 fused rope write traditional={traditional} T={T}]", flush=True)
+    rng = np.random.default_rng(11 + traditional + T)
+    hkv, d, bs, nb = 8, 128, 32, 64  # T = 24: the one-launch write (queries turned by its extra workgroups)
     rope = RotaryEmbedding.llama3(128, base=500000.0, traditional=traditional)
     k = torch.from_numpy((rng.standard_normal((T, hkv, d)) * 2).astype(np.float16)).to(cuda)
     v = torch.from_numpy((rng.standard_normal((T, hkv, d)) * 2).astype(np.float16)).to(cuda)
@@ -156,15 +156,19 @@ def test_fp8_fused_write_equals_rotate_then_write(cuda, traditional):
     a, b = view(), view()
     lib = _native.load()
     ws = torch.empty(int(lib.emx_fp8_write_workspace_bytes()), dtype=torch.uint8, device=cuda)
+    q = torch.from_numpy(rng.standard_normal((T, 16, d)).astype(np.float16)).to(cuda)
+    qa = q.clone()
     _native.check(lib.emx_fp8_cache_write_rope(
         k.data_ptr(), v.data_ptr(), _native.DTYPE_F16, slots.data_ptr(), T, hkv, d, bs, nb, a.key_cache.data_ptr(),
         a.value_cache.data_ptr(), a.k_scales.data_ptr(), a.v_scales.data_ptr(), ws.data_ptr(), ws.numel(),
-        pos.data_ptr(), rope.inv_freq(cuda).data_ptr(), rope.dims, int(traditional),
+        pos.data_ptr(), rope.inv_freq(cuda).data_ptr(), rope.dims, int(traditional), qa.data_ptr(), 16,
         torch.cuda.current_stream(cuda).cuda_stream))
-    kr = k.clone()
+    kr, qb = k.clone(), q.clone()
     _rope_rows(kr, pos, rope)
+    _rope_rows(qb, pos, rope)
     b.write_slots(kr, v, slots)
     torch.cuda.synchronize()
+    assert torch.equal(qa, qb), "queries"
     for name in ("key_cache", "value_cache", "k_scales", "v_scales"):
         assert torch.equal(getattr(a, name), getattr(b, name)), name
 

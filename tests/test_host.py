@@ -264,8 +264,9 @@ def test_abi_rope_and_prefill_split_arguments(lib):
     assert lib.emx_affine_cache_write_rope(*args, p_one, p_inv, 0, 0, None, 0, None) == err
     assert lib.emx_affine_cache_write_rope(*args, p_one, p_inv, 128, 0, p_one, 0, None) == err  # no q heads
     fargs = [p_one, p_one, _native.DTYPE_F16, p_one, 4, 8, 128, 128, 16, p_one, p_one, p_one, p_one, p_one, 2048]
-    assert lib.emx_fp8_cache_write_rope(*fargs, p_one, p_inv, 12, 0, None) == err
-    assert lib.emx_fp8_cache_write_rope(*fargs, p_one, p_inv, 10, 1, None) == err
+    assert lib.emx_fp8_cache_write_rope(*fargs, p_one, p_inv, 12, 0, None, 0, None) == err
+    assert lib.emx_fp8_cache_write_rope(*fargs, p_one, p_inv, 10, 1, None, 0, None) == err
+    assert lib.emx_fp8_cache_write_rope(*fargs, p_one, p_inv, 128, 0, p_one, 0, None) == err  # no q heads
     # prefill key-split workspace: host arithmetic, 0 where the split cannot apply, growing with the tokens
     c3 = lib.emx_paged_prefill_workspace_bytes(2076, 32, 32, 8, 128)
     assert c3 > 0 and c3 % 4 == 0
