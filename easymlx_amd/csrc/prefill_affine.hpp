@@ -64,7 +64,7 @@ struct PrefillArgs {
 };
 
 constexpr int kPrefillParts = 3;          // most parts a tile is split into
-constexpr int kPrefillSplitKeys = 768;    // keys per part the split aims at
+constexpr int kPrefillSplitKeys = 512;    // keys per part the split aims at (c3: 768 -> 121.5, 512 -> 111.7, 384 -> 117.6 us)
 constexpr int kPrefillPartVec = 17;       // f32x4 per lane of a stored state: acc[2][8], (m0, m1, l0, l1)
 constexpr int kPrefillPartBytes = 4 * kPrefillPartVec * 64 * 16;  // one part of one workgroup
 constexpr int kPrefillCounters = 65536;   // arrival counters (max_items * Hkv * 4 must fit)
