@@ -656,6 +656,7 @@ static int fp8_write_impl(const void* keys, const void* values, int dtype, const
   a.Hq = num_q_heads;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const size_t n = (size_t)num_tokens * num_kv_heads * head_dim;
+  if (n / 4 >= ((size_t)1 << 31)) return fail(EMX_ERR_UNSUPPORTED, "%zu values per tensor exceed the 2^33 limit", n);
   const int nparts = (int)std::min<size_t>(emx::kFp8Parts, (n / 4 + 255) / 256);
   const int nwrite = (int)std::min<size_t>(1024, (n / 4 + 255) / 256);
   const bool turn_q = rope.inv_freq != nullptr && queries != nullptr;

@@ -45,15 +45,15 @@ __device__ __forceinline__ float round_to(float x, float*) { return x; }
 // reference writes the rotated keys of the model's dtype).  Needs rot % 8 == 0
 // (non-traditional): a word and its partner word lie in one half each.
 template <typename T>
-__device__ __forceinline__ void k_word(const Fp8WriteArgs& a, const T* k, const size_t e, float (&x)[4]) {
+__device__ __forceinline__ void k_word(const Fp8WriteArgs& a, const T* k, const uint32_t e, float (&x)[4]) {
 #pragma unroll
-  for (int j = 0; j < 4; ++j) x[j] = to_f32(k[4 * e + j]);
+  for (int j = 0; j < 4; ++j) x[j] = to_f32(k[4 * (size_t)e + j]);
   const RopeArgs& r = a.rope;
   if (r.inv_freq == nullptr) return;
-  const int wpr = a.D / 4;  // words per head row
+  const uint32_t wpr = a.D / 4;  // words per head row
   const int d0 = 4 * (int)(e % wpr);
   if (d0 >= r.rot) return;
-  const float pos = (float)r.positions[e / ((size_t)a.Hkv * wpr)];
+  const float pos = (float)r.positions[e / ((uint32_t)a.Hkv * wpr)];
   float y[4];
   if (r.traditional) {
 #pragma unroll
@@ -61,10 +61,10 @@ __device__ __forceinline__ void k_word(const Fp8WriteArgs& a, const T* k, const 
   } else {
     const int half = r.rot / 2;
     const bool lo = d0 < half;
-    const size_t pe = lo ? e + half / 4 : e - half / 4;  // the partner word
+    const uint32_t pe = lo ? e + half / 4 : e - half / 4;  // the partner word
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const float p = to_f32(k[4 * pe + j]);
+      const float p = to_f32(k[4 * (size_t)pe + j]);
       float y0, y1;
       const int i = (lo ? d0 : d0 - half) + j;
       if (lo)
@@ -83,16 +83,16 @@ __global__ __launch_bounds__(256) void fp8_amax(Fp8WriteArgs a) {
   typedef typename Tag::T T;
   const T* k = reinterpret_cast<const T*>(a.k);
   const T* v = reinterpret_cast<const T*>(a.v);
-  const size_t row4 = (size_t)a.Hkv * a.D / 4, n4 = (size_t)a.T * row4;
+  const uint32_t row4 = (uint32_t)a.Hkv * a.D / 4, n4 = (uint32_t)a.T * row4;  // n4 < 2^31 (host check)
   float mk = 0.f, mv = 0.f;
-  for (size_t e = (size_t)blockIdx.x * 256 + threadIdx.x; e < n4; e += (size_t)gridDim.x * 256) {
+  for (uint32_t e = blockIdx.x * 256u + threadIdx.x; e < n4; e += gridDim.x * 256u) {
     if (a.slot[e / row4] < 0) continue;
     float x[4];
     k_word(a, k, e, x);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       mk = fmaxf(mk, fabsf(x[j]));
-      mv = fmaxf(mv, fabsf(to_f32(v[4 * e + j])));
+      mv = fmaxf(mv, fabsf(to_f32(v[4 * (size_t)e + j])));
     }
   }
   mk = wave_max(mk);
@@ -137,19 +137,19 @@ __global__ __launch_bounds__(SELF ? 1024 : 256) void fp8_write(Fp8WriteArgs a, i
     // scales); four words per thread in flight together
     const T* k = reinterpret_cast<const T*>(a.k);
     const T* v = reinterpret_cast<const T*>(a.v);
-    const size_t row4 = (size_t)a.Hkv * a.D / 4, n4 = (size_t)a.T * row4;
+    const uint32_t row4 = (uint32_t)a.Hkv * a.D / 4, n4 = (uint32_t)a.T * row4;
     float mk = 0.f, mv = 0.f;
-    for (size_t e0 = threadIdx.x; e0 < n4; e0 += 4 * NTH) {
+    for (uint32_t e0 = threadIdx.x; e0 < n4; e0 += 4 * NTH) {
       float x[4][4], y[4][4];
       bool live[4];
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        const size_t e = e0 + (size_t)u * NTH;
+        const uint32_t e = e0 + (uint32_t)u * NTH;
         live[u] = e < n4 && a.slot[e / row4] >= 0;
-        const size_t ee = e < n4 ? e : e0;
+        const uint32_t ee = e < n4 ? e : e0;
         k_word(a, k, ee, x[u]);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) y[u][j] = to_f32(v[4 * ee + j]);
+        for (int j = 0; j < 4; ++j) y[u][j] = to_f32(v[4 * (size_t)ee + j]);
       }
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
@@ -197,10 +197,10 @@ __global__ __launch_bounds__(SELF ? 1024 : 256) void fp8_write(Fp8WriteArgs a, i
   const float kq = fmaxf(ksc, 1e-12f), vq = fmaxf(vsc, 1e-12f);
   const T* k = reinterpret_cast<const T*>(a.k);
   const T* v = reinterpret_cast<const T*>(a.v);
-  const int row4 = a.Hkv * a.D / 4;
-  const size_t n4 = (size_t)a.T * row4;
-  const int nwg = SELF ? a.nwg : (int)gridDim.x;
-  for (size_t e = (size_t)blockIdx.x * NTH + threadIdx.x; e < n4; e += (size_t)nwg * NTH) {
+  const uint32_t row4 = (uint32_t)a.Hkv * a.D / 4;
+  const uint32_t n4 = (uint32_t)a.T * row4;
+  const uint32_t nwg = SELF ? a.nwg : gridDim.x;
+  for (uint32_t e = blockIdx.x * (uint32_t)NTH + threadIdx.x; e < n4; e += nwg * NTH) {
     const int t = (int)(e / row4), r = (int)(e % row4);
     const int slot = a.slot[t];
     if (slot < 0) continue;
@@ -212,7 +212,7 @@ __global__ __launch_bounds__(SELF ? 1024 : 256) void fp8_write(Fp8WriteArgs a, i
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       ck |= f32_to_e4m3(x[j] / kq) << (8 * j);
-      cv |= f32_to_e4m3(to_f32(v[4 * e + j]) / vq) << (8 * j);
+      cv |= f32_to_e4m3(to_f32(v[4 * (size_t)e + j]) / vq) << (8 * j);
     }
     const size_t dst = ((size_t)blk * a.bs + off) * (size_t)row4 + r;  // [nb, bs, Hkv*D/4] words
     reinterpret_cast<uint32_t*>(a.kc)[dst] = ck;
