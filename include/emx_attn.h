@@ -168,7 +168,8 @@ size_t emx_fp8_write_workspace_bytes(void);
  * Hkv, head_dim] in dtype (EMX_DTYPE_*); slot_mapping int32 [num_tokens]
  * (block * page_size + offset, -1 to skip).  One scale per call,
  * max|x| / 240 over the written tokens; codes enc(x / max(scale, 1e-12));
- * each written page's scale becomes max(page scale, call scale).
+ * each written page's scale becomes max(page scale, call scale).  At most
+ * 2^33 - 4 values per tensor (EMX_ERR_UNSUPPORTED beyond).
  * Replaces the FP8 branch of PageCacheView.concatenate_to_cache
  *   lib/python/easymlx/caching/paged/cache.py:1171-1184 (compute_kv_scales
  *   :430-463, _fp8_quantize :466-478, encoder

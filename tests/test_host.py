@@ -267,6 +267,10 @@ def test_abi_rope_and_prefill_split_arguments(lib):
     assert lib.emx_fp8_cache_write_rope(*fargs, p_one, p_inv, 12, 0, None, 0, None) == err
     assert lib.emx_fp8_cache_write_rope(*fargs, p_one, p_inv, 10, 1, None, 0, None) == err
     assert lib.emx_fp8_cache_write_rope(*fargs, p_one, p_inv, 128, 0, p_one, 0, None) == err  # no q heads
+    # FP8 writes index words with 32 bits: more than 2^33 values per tensor are refused before any launch
+    big = list(fargs)
+    big[4] = 1 << 24  # 2^24 tokens x 8 heads x 128 dims = 2^34 values
+    assert lib.emx_fp8_cache_write(*big, None) == _native.EMX_ERR_UNSUPPORTED
     # prefill key-split workspace: host arithmetic, 0 where the split cannot apply, growing with the tokens
     c3 = lib.emx_paged_prefill_workspace_bytes(2076, 32, 32, 8, 128)
     assert c3 > 0 and c3 % 4 == 0
