@@ -281,22 +281,6 @@ __device__ __forceinline__ void q4_compute(Q4Loads<GS, HQ>& L, const bool full, 
   }
 }
 
-#ifdef EMX_TIMELINE
-// Diagnostic build only: per-wave timestamps (100 MHz s_memrealtime) of the
-// decode phases, slot layout [wave][kTraceSlots].
-constexpr int kTraceSlots = 48;
-__device__ unsigned long long emx_trace[4096 * kTraceSlots];
-#define EMX_TS(slot)                                                                                \
-  do {                                                                                              \
-    const unsigned long long t_ = __builtin_amdgcn_s_memrealtime();                                 \
-    if (lane == 0 && W < 4096 && (slot) < kTraceSlots) emx_trace[W * kTraceSlots + (slot)] = t_;    \
-  } while (0)
-#else
-#define EMX_TS(slot) \
-  do {               \
-  } while (0)
-#endif
-
 // Work decomposition of decode_q4_d128.  The unit of work is a workgroup of
 // four waves; a workgroup item is TW = 64 * 4 / HQ consecutive tokens of one
 // (sequence, kv_head) unit, wave k taking head quad k % HQ of the 64-token
@@ -325,9 +309,6 @@ __global__ __launch_bounds__(256, 2) void decode_q4_d128(DecodeArgs a) {
   using Geo = Q4Geom<HG>;
   constexpr int HQ = Geo::HQ, NSL = Geo::NSL, TW = Geo::TW;
   constexpr int D = 128, G = Q4Cfg<GS, 1>::G;
-#ifdef EMX_TIMELINE
-  const unsigned long long t_start = __builtin_amdgcn_s_memrealtime();
-#endif
 
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -385,13 +366,6 @@ __global__ __launch_bounds__(256, 2) void decode_q4_d128(DecodeArgs a) {
   if (wg >= NWG) return;
   const long long g0 = ((long long)wg * I) / NWG;
   const long long g1 = ((long long)(wg + 1) * I) / NWG;
-#ifdef EMX_TIMELINE
-  const int W = wg * 4 + wv;
-  if (lane == 0 && W < 4096) emx_trace[W * kTraceSlots + 0] = t_start;
-  EMX_TS(1);
-  int n_step = 0;
-  int npend_dbg = 0;  // unit ends seen (the first one is stamped in detail)
-#endif
 
   const int bs_log2 = __builtin_ctz(a.bs);
 
@@ -427,9 +401,6 @@ __global__ __launch_bounds__(256, 2) void decode_q4_d128(DecodeArgs a) {
     return b;
   };
   int blkv = blk_chunk(g0);
-#ifdef EMX_TIMELINE
-  EMX_TS(25);
-#endif
 
   // ---- query operand of a unit (this wave's head quad).  Lane L (head 4*quad + L%4,
   // 16-lane group n = L/16) holds, in VGPR pair r, the operand of k-step 4r + n: K word
@@ -513,13 +484,7 @@ __global__ __launch_bounds__(256, 2) void decode_q4_d128(DecodeArgs a) {
   size_t soff0;
   const TileRsrc rs0 = tile_of(blk, kvh, tb, soff0);
   q4_issue_loads(bufA, rs0, sptr, soff0, (tb & 127) / 64, lane, a.bs);
-#ifdef EMX_TIMELINE
-  EMX_TS(26);
-#endif
   build_q();
-#ifdef EMX_TIMELINE
-  EMX_TS(27);
-#endif
 
   Q4State st[1];
   auto reset = [&]() {
@@ -576,19 +541,11 @@ __global__ __launch_bounds__(256, 2) void decode_q4_d128(DecodeArgs a) {
 
     // ---- compute this wave's slice of the item (skipped when it holds no live
     // token, or its page is invalid, like the reference's Metal kernel)
-#ifdef EMX_TIMELINE
-    if (n_step == 0) EMX_TS(2);
-    __builtin_amdgcn_s_waitcnt(0x4F70);  // vmcnt(16): this item's loads done
-    EMX_TS(3 + 3 * min(n_step, 14));
-#endif
     if ((unsigned)blk < (unsigned)a.nb && tb + 64 > start_k) {
       q4_stage_scales<GS, 1>(cur, sst[wv], lane);
       const bool full = tb >= start_k && tb + 64 <= kv_len;
       q4_compute<GS, 1>(cur, full, lane, tb, start_k, kv_len, qB, qs, sc_l2, st);
     }
-#ifdef EMX_TIMELINE
-    EMX_TS(4 + 3 * min(n_step, 14));
-#endif
 
     // ---- unit finished (or range ends): the waves' (o, m, l) meet in LDS; the last
     // wave to arrive combines them into the output or the workgroup's partial while
@@ -623,9 +580,6 @@ __global__ __launch_bounds__(256, 2) void decode_q4_d128(DecodeArgs a) {
           sml[par][wv][lane][1] = l;
         }
       }
-#ifdef EMX_TIMELINE
-      if (npend_dbg == 0) EMX_TS(20);
-#endif
       int arrived = 0;
       if (has_next) {
         if (lane == 0) arrived = __hip_atomic_fetch_add(&scnt[par], 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -659,9 +613,6 @@ __global__ __launch_bounds__(256, 2) void decode_q4_d128(DecodeArgs a) {
           }
         }
       }
-#ifdef EMX_TIMELINE
-      if (npend_dbg == 0) EMX_TS(21);
-#endif
       if (arrived == 3) {  // last of the four waves: combine
         if (lane == 0) __hip_atomic_store(&scnt[par], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         PieceInfo pi;
@@ -709,10 +660,6 @@ __global__ __launch_bounds__(256, 2) void decode_q4_d128(DecodeArgs a) {
         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
         if (lane == 0) __hip_atomic_store(&sgen[par], nue, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
       }
-#ifdef EMX_TIMELINE
-      if (npend_dbg == 0) EMX_TS(22);
-      if (npend_dbg == 0) EMX_TS(23);
-#endif
       ++nue;
       if (!whole) {
         pend_u[npend] = u;
@@ -722,20 +669,11 @@ __global__ __launch_bounds__(256, 2) void decode_q4_d128(DecodeArgs a) {
         pend_first[npend] = unit_first;
         ++npend;
       }
-#ifdef EMX_TIMELINE
-      EMX_TS(5 + 3 * min(n_step, 14));
-#endif
       reset();
       if (has_next) {
         unit_first = g + 1;
         build_q();
-#ifdef EMX_TIMELINE
-        if (npend_dbg == 0) EMX_TS(24);
-#endif
       }
-#ifdef EMX_TIMELINE
-      ++npend_dbg;
-#endif
     }
 
     // ---- advance
@@ -750,9 +688,6 @@ __global__ __launch_bounds__(256, 2) void decode_q4_d128(DecodeArgs a) {
     it_lo = lo1;
     tb = tb1;
     blk = blk1;
-#ifdef EMX_TIMELINE
-    ++n_step;
-#endif
   };
   for (long long g = g0; g < g1; g += 2) {
     step(bufA, bufB, g);
@@ -763,13 +698,7 @@ __global__ __launch_bounds__(256, 2) void decode_q4_d128(DecodeArgs a) {
   // ---- arrivals of the shared units; the last workgroup to arrive merges
   if (npend > 0) {
     __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores are complete ...
-#ifdef EMX_TIMELINE
-    EMX_TS(40);
-#endif
     __syncthreads();                // ... and so are the workgroup's
-#ifdef EMX_TIMELINE
-    EMX_TS(41);
-#endif
     if (threadIdx.x < npend) {  // one thread per shared unit: both arrivals in flight together
       const int p = threadIdx.x;
       const int np = piece_count(pend_first[p], pend_n[p], I, NWG);
@@ -779,10 +708,6 @@ __global__ __launch_bounds__(256, 2) void decode_q4_d128(DecodeArgs a) {
       slast[p] = last;
     }
     __syncthreads();
-#ifdef EMX_TIMELINE
-    EMX_TS(42);
-    if (lane == 0 && W < 4096) emx_trace[W * kTraceSlots + 43] = (unsigned long long)(npend * 10 + slast[0] + 2 * (npend > 1 ? slast[1] : 0));
-#endif
     // Merge (page_attention.py:2006-2059): with two units to merge, waves 0-1 take
     // the first and waves 2-3 the second, so both units' loads are in flight
     // together; a thread owns float4 f of the unit's HG*D values and loads only
@@ -828,10 +753,6 @@ __global__ __launch_bounds__(256, 2) void decode_q4_d128(DecodeArgs a) {
       }
     }
   }
-#ifdef EMX_TIMELINE
-  EMX_TS(47);
-  if (lane == 0 && W < 4096) emx_trace[W * kTraceSlots + 46] = (unsigned long long)n_step;
-#endif
 }
 
 }  // namespace emx

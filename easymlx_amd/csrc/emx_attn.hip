@@ -6,7 +6,6 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
-#include <cstdlib>
 #include <string>
 
 #include "../../include/emx_attn.h"
@@ -40,19 +39,6 @@ int check_launch(const char* what) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// Waves per SIMD the persistent 16x16 / FP8 decode grid is sized for (launch
-// bounds allow 2; one measured faster: these kernels are latency-bound, and more
-// waves add split-K pieces rather than bandwidth); EMX_DECODE_WAVES_PER_SIMD
-// overrides it for tuning (1..2).
-int decode_waves_per_simd() {
-  static const int v = [] {
-    const char* e = std::getenv("EMX_DECODE_WAVES_PER_SIMD");
-    const int x = e ? std::atoi(e) : 1;
-    return x >= 1 && x <= 2 ? x : 1;
-  }();
-  return v;
-}
-
 // Compute units of the current device (256 on MI355X).
 int device_cus() {
   int dev = 0, cus = 0;
@@ -62,25 +48,12 @@ int device_cus() {
   return cus;
 }
 
-int decode_num_waves() {
-  // EMX_DECODE_WAVES overrides the wave count (tuning; multiple of 4, at most kMaxWaves)
-  static const int ov = [] {
-    const char* e = std::getenv("EMX_DECODE_WAVES");
-    const int x = e ? std::atoi(e) : 0;
-    return x >= 4 && x <= emx::kMaxWaves && x % 4 == 0 ? x : 0;
-  }();
-  return ov ? ov : device_cus() * 4 * decode_waves_per_simd();
-}
+// The 16x16 / FP8 decode grid: one four-wave workgroup per CU (measured faster than
+// two: these kernels are latency-bound, and more waves add split-K pieces rather
+// than bandwidth).
+int decode_num_waves() { return device_cus() * 4; }
 // The 4-bit kernel runs two four-wave workgroups per CU.
-int decode_q4_num_waves() {
-  // EMX_DECODE_Q4_WAVES overrides the wave count (tuning; multiple of 4, at most kMaxWaves)
-  static const int ov = [] {
-    const char* e = std::getenv("EMX_DECODE_Q4_WAVES");
-    const int x = e ? std::atoi(e) : 0;
-    return x >= 4 && x <= emx::kMaxWaves && x % 4 == 0 ? x : 0;
-  }();
-  return ov ? ov : device_cus() * 8;
-}
+int decode_q4_num_waves() { return device_cus() * 8; }
 // Partial slots are sized for the larger of the two persistent grids.
 int decode_max_waves() { return std::max(decode_num_waves(), decode_q4_num_waves()); }
 
@@ -136,25 +109,19 @@ DecodeFn pick_decode_hg(int hg) {
 }
 
 // 4-bit pages, group 64 / 128, GQA ratio 1, 2, 4 or 16: the 4x4x4 MFMA decode kernel.
-// EMX_DECODE_16X16=1 selects the 16x16x32 kernel instead (comparisons).
+// GQA 8 with groups of 64 fills all 16 columns of the 16x16x32 kernel, which serves it.
 template <int GS>
 DecodeFn pick_decode_q4_hg(int hg) {
   switch (hg) {
     case 1: return emx::decode_q4_d128<GS, 1>;
     case 2: return emx::decode_q4_d128<GS, 2>;
     case 4: return emx::decode_q4_d128<GS, 4>;
-    // GQA 8 with groups of 64 fills all 16 columns of the 16x16x32 kernel, which is faster there
     case 16: return emx::decode_q4_d128<GS, 16>;
   }
   return nullptr;
 }
 
 DecodeFn pick_decode_q4(int gs, int hg) {
-  static const bool off = [] {
-    const char* e = std::getenv("EMX_DECODE_16X16");
-    return e && std::atoi(e) == 1;
-  }();
-  if (off) return nullptr;
   if (gs == 64) return pick_decode_q4_hg<64>(hg);
   if (gs == 128) return pick_decode_q4_hg<128>(hg);
   return nullptr;
@@ -518,6 +485,7 @@ int emx_paged_attention_affine(const void* queries, int num_tokens, int num_q_he
     a.window = window;
     a.num_waves = nw;
     // tokens per work item: per wave (16x16 kernel) or per workgroup (4-bit kernel)
+    // tokens per work item: per workgroup (4-bit kernel) or per wave (16x16 kernel)
     a.nt = q4 ? 64 * (4 / ((hg + 3) / 4)) : bits == 4 ? 64 : 32;
     hipLaunchKernelGGL(fn, dim3((unsigned)(nw / 4)), dim3(256), 0, st, a);
     return check_launch("decode_affine_d128");
@@ -834,13 +802,3 @@ int emx_paged_attention_fp8(const void* queries, int num_tokens, int num_q_heads
 }
 
 }  // extern "C"
-
-#ifdef EMX_TIMELINE
-extern "C" int emx_trace_read(void* host, size_t bytes) {
-  return hipMemcpyFromSymbol(host, HIP_SYMBOL(emx::emx_trace), bytes) == hipSuccess ? 0 : 1;
-}
-extern "C" int emx_trace_clear() {
-  static unsigned long long zeros[4096 * emx::kTraceSlots];
-  return hipMemcpyToSymbol(HIP_SYMBOL(emx::emx_trace), zeros, sizeof(zeros)) == hipSuccess ? 0 : 1;
-}
-#endif

@@ -6,7 +6,9 @@
 //   * codes enc(x / max(scale, 1e-12)) with the reference's E4M3 encoder
 //     (_fp8_quantize :466-478; encoder _metal_header.py:339-419);
 //   * each written page's scale raised to max(page_scale, scale); the page's
-//     earlier codes are not requantized (the reference's rule).
+//     earlier codes are not requantized (the reference's rule);
+//   * a slot of -1, or one whose page lies outside the pool, is skipped: it is
+//     neither written nor counted in the call's maxima.
 // Two launches: per-workgroup maxima into a small workspace, then every
 // workgroup reduces them and quantizes its share (4 values per thread).  Writes
 // of up to kFp8SelfMax values per tensor (decode appends) take one launch in
@@ -86,7 +88,8 @@ __global__ __launch_bounds__(256) void fp8_amax(Fp8WriteArgs a) {
   const uint32_t row4 = (uint32_t)a.Hkv * a.D / 4, n4 = (uint32_t)a.T * row4;  // n4 < 2^31 (host check)
   float mk = 0.f, mv = 0.f;
   for (uint32_t e = blockIdx.x * 256u + threadIdx.x; e < n4; e += gridDim.x * 256u) {
-    if (a.slot[e / row4] < 0) continue;
+    const int sl = a.slot[e / row4];
+    if (sl < 0 || sl / a.bs >= a.nb) continue;  // skipped slots (-1 or page outside the pool) do not count
     float x[4];
     k_word(a, k, e, x);
 #pragma unroll
@@ -145,7 +148,8 @@ __global__ __launch_bounds__(SELF ? 1024 : 256) void fp8_write(Fp8WriteArgs a, i
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         const uint32_t e = e0 + (uint32_t)u * NTH;
-        live[u] = e < n4 && a.slot[e / row4] >= 0;
+        const int sl = e < n4 ? a.slot[e / row4] : -1;
+        live[u] = sl >= 0 && sl / a.bs < a.nb;  // as the write loop: a page outside the pool is skipped
         const uint32_t ee = e < n4 ? e : e0;
         k_word(a, k, ee, x[u]);
 #pragma unroll

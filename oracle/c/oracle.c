@@ -16,6 +16,16 @@
  *       codes [nb, bs, Hkv, D*bits/32], scales/biases [nb, bs, Hkv, D/g],
  *       dequantised per element as fp16(scale*q + bias), fp32 softmax.
  *       Parallelised over (seq, kv_head) with OpenMP.
+ *   oracle_attention_affine -- ragged / causal / sliding-window paged attention
+ *       (unified_attention.py:187-281 with the kernels' edge semantics
+ *       :290-465: causal limit max_k = kv_len - q_len + i, window start
+ *       max_k - window + 1, pages with a block id outside [0, nb) skipped,
+ *       empty rows zero) over the same logical affine layout, in double
+ *       precision, dequantising either exactly (scale*q + bias in fp32, the
+ *       fp32 parity target) or rounded to fp16.  Each (sequence, kv_head)
+ *       dequantises its keys once; rows run in parallel.  Used by tests/ as
+ *       the checker at the benchmark's full sizes, where the numpy oracle
+ *       takes minutes.
  */
 #include <math.h>
 #include <stdint.h>
@@ -170,5 +180,92 @@ void oracle_decode_affine(const uint16_t* q, const uint32_t* k_codes, const uint
           out[((size_t)s * hq + kh * rep + h) * d + i] = l[h] > 0.0f ? acc[h * d + i] / l[h] : 0.0f;
       free(kf); free(vf); free(qf); free(acc); free(m); free(l);
     }
+  }
+}
+
+/* Dequantised sequence of one kv head: out[pos * d + i], valid[pos]. */
+static void deq_sequence(const uint32_t* codes, const uint16_t* sc, const uint16_t* bi, const int32_t* table,
+                         int len, int kh, int hkv, int d, int bs, int num_blocks, int bits, int group_size,
+                         int round_fp16, double* out, unsigned char* valid) {
+  const int words = d * bits / 32, groups = d / group_size, per_word = 32 / bits;
+  for (int pos = 0; pos < len; ++pos) {
+    const int blk = table[pos / bs];
+    valid[pos] = blk >= 0 && blk < num_blocks;
+    if (!valid[pos]) {
+      for (int i = 0; i < d; ++i) out[(size_t)pos * d + i] = 0.0;
+      continue;
+    }
+    const size_t tok = ((size_t)blk * bs + pos % bs) * hkv + kh;
+    for (int i = 0; i < d; ++i) {
+      const uint32_t q = (codes[tok * words + i / per_word] >> ((i % per_word) * bits)) & ((1u << bits) - 1u);
+      float v = h2f(sc[tok * groups + i / group_size]) * (float)q + h2f(bi[tok * groups + i / group_size]);
+      if (round_fp16) v = h2f(f2h(v));
+      out[(size_t)pos * d + i] = (double)v;
+    }
+  }
+}
+
+/* q fp16 [T, Hq, D] (rows of sequence s at query_start_loc[s] ..); out double [T, Hq, D]. */
+void oracle_attention_affine(const uint16_t* q, const uint32_t* k_codes, const uint16_t* k_scales,
+                             const uint16_t* k_biases, const uint32_t* v_codes, const uint16_t* v_scales,
+                             const uint16_t* v_biases, const int32_t* block_tables, const int32_t* kv_lens,
+                             const int32_t* query_start_loc, int num_seqs, int hq, int hkv, int d, int bs,
+                             int num_blocks, int max_blocks, int bits, int group_size, double softmax_scale,
+                             int sliding_window, int round_fp16, double* out) {
+  const int rep = hq / hkv;
+  const int total = query_start_loc[num_seqs];
+  memset(out, 0, sizeof(double) * (size_t)total * hq * d);
+  for (int s = 0; s < num_seqs; ++s) {
+    const int q0 = query_start_loc[s], q_len = query_start_loc[s + 1] - q0;
+    int len = kv_lens[s];
+    if (len > max_blocks * bs) len = max_blocks * bs;
+    if (q_len <= 0 || len <= 0) continue;
+    double* kf = (double*)malloc(sizeof(double) * (size_t)len * d);
+    double* vf = (double*)malloc(sizeof(double) * (size_t)len * d);
+    unsigned char* valid = (unsigned char*)malloc((size_t)len);
+    for (int kh = 0; kh < hkv; ++kh) {
+      const int32_t* table = block_tables + (size_t)s * max_blocks;
+      deq_sequence(k_codes, k_scales, k_biases, table, len, kh, hkv, d, bs, num_blocks, bits, group_size,
+                   round_fp16, kf, valid);
+      deq_sequence(v_codes, v_scales, v_biases, table, len, kh, hkv, d, bs, num_blocks, bits, group_size,
+                   round_fp16, vf, valid);
+#pragma omp parallel for collapse(2) schedule(dynamic)
+      for (int i = 0; i < q_len; ++i) {
+        for (int h = 0; h < rep; ++h) {
+          const int head = kh * rep + h;
+          const int max_k = (len - q_len) + i < len - 1 ? (len - q_len) + i : len - 1;
+          if (max_k < 0) continue;
+          int start_k = 0;
+          if (sliding_window > 0 && max_k - sliding_window + 1 > 0) start_k = max_k - sliding_window + 1;
+          double qd[256];
+          const uint16_t* qp = q + ((size_t)(q0 + i) * hq + head) * d;
+          /* q scaled in fp32 before the dot product, as the reference does */
+          for (int c = 0; c < d; ++c) qd[c] = (double)(h2f(qp[c]) * (float)softmax_scale);
+          double* sc = (double*)malloc(sizeof(double) * (size_t)(max_k + 1));
+          double mx = -INFINITY;
+          for (int k = start_k; k <= max_k; ++k) {
+            if (!valid[k]) continue;
+            double acc = 0.0;
+            const double* kr = kf + (size_t)k * d;
+            for (int c = 0; c < d; ++c) acc += qd[c] * kr[c];
+            sc[k] = acc;
+            if (acc > mx) mx = acc;
+          }
+          double* o = out + ((size_t)(q0 + i) * hq + head) * d;
+          if (mx == -INFINITY) { free(sc); continue; }
+          double l = 0.0;
+          for (int k = start_k; k <= max_k; ++k) {
+            if (!valid[k]) continue;
+            const double p = exp(sc[k] - mx);
+            l += p;
+            const double* vr = vf + (size_t)k * d;
+            for (int c = 0; c < d; ++c) o[c] += p * vr[c];
+          }
+          for (int c = 0; c < d; ++c) o[c] /= l;
+          free(sc);
+        }
+      }
+    }
+    free(kf); free(vf); free(valid);
   }
 }

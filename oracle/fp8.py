@@ -153,17 +153,18 @@ def fp8_write(keys, values, slot_mapping, key_cache, value_cache, k_scales, v_sc
     """FP8 cache write (cache.py:1171-1184), in place.
 
     keys/values [T, Hkv, D] (any float dtype); slot_mapping [T] int (block * bs
-    + offset, -1 skips the token); key_cache/value_cache uint8 [nb, bs, Hkv, D];
+    + offset, -1 or a page outside the pool skips the token); key_cache/value_cache uint8 [nb, bs, Hkv, D];
     k_scales/v_scales float32 [nb].  The call's scale covers the written tokens.
     """
     slot_mapping = np.asarray(slot_mapping, dtype=np.int64)
-    live = slot_mapping >= 0
+    bs = key_cache.shape[1]
+    # -1 skips a token; so does a page outside the pool (the kernels' bounds rule, cache.py:859-861)
+    live = (slot_mapping >= 0) & (slot_mapping // bs < key_cache.shape[0])
     k = np.asarray(keys, dtype=np.float32)[live]
     v = np.asarray(values, dtype=np.float32)[live]
     slots = slot_mapping[live]
     if slots.size == 0:
         return
-    bs = key_cache.shape[1]
     ks, vs = fp8_scale(k), fp8_scale(v)
     blk, off = slots // bs, slots % bs
     key_cache[blk, off] = fp8_quantize(k, ks)

@@ -102,14 +102,15 @@ def paged_attention(
         mask = (kpos[None, :] <= max_k[:, None]) & (kpos[None, :] >= start_k[:, None])
         if invalid_block == "skip":
             mask &= valid[None, :]
-        scores = np.einsum("qhd,khd->qhk", q, k_seq)
+        # batched matmuls over heads (BLAS) instead of einsum: same sums, faster at full sizes
+        scores = np.matmul(q.transpose(1, 0, 2), k_seq.transpose(1, 2, 0)).transpose(1, 0, 2)  # [q, h, k]
         scores = np.where(mask[:, None, :], scores, -np.inf)
         row_max = scores.max(axis=-1, keepdims=True)
         has_any = np.isfinite(row_max)
         w = np.exp(scores - np.where(has_any, row_max, 0))
         w = np.where(mask[:, None, :], w, 0)
         l = w.sum(axis=-1, keepdims=True)
-        o = np.einsum("qhk,khd->qhd", w, v_seq)
+        o = np.matmul(w.transpose(1, 0, 2), v_seq.transpose(1, 0, 2)).transpose(1, 0, 2)  # [q, h, d]
         o = np.where(l > 0, o / np.where(l > 0, l, 1), 0)
         o = np.where((max_k >= 0)[:, None, None], o, 0)
         out[q_start:q_end] = o

@@ -104,3 +104,80 @@ def assert_attention_close(actual: np.ndarray, expected: np.ndarray, what: str =
         f"{what}: {int(bad.sum())} of {bad.size} outside atol={ATOL} rtol={RTOL}; "
         f"max abs err {err.max():.3e} at {np.unravel_index(err.argmax(), err.shape)}"
     )
+
+
+# ---------------------------------------------------------------- C oracle (full sizes)
+_C_ORACLE = None
+
+
+def c_oracle_lib():
+    """The C restatement ``oracle/c/liboracle.so`` (built by ``make -C oracle/c``)."""
+    global _C_ORACLE
+    if _C_ORACLE is None:
+        import ctypes
+        import os
+        import subprocess
+
+        root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+        path = os.path.join(root, "oracle", "c", "liboracle.so")
+        if not os.path.exists(path):
+            subprocess.run(["make", "-s", "-C", os.path.dirname(path)], check=True)
+        lib = ctypes.CDLL(path)
+        P, I = ctypes.c_void_p, ctypes.c_int
+        lib.oracle_affine_quantize.argtypes = [P, ctypes.c_long, I, I, I, P, P, P]
+        lib.oracle_affine_quantize.restype = None
+        lib.oracle_attention_affine.argtypes = [P] * 10 + [I] * 9 + [ctypes.c_double, I, I, P]
+        lib.oracle_attention_affine.restype = None
+        _C_ORACLE = lib
+    return _C_ORACLE
+
+
+def _ptr(a):
+    import ctypes
+
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def c_quantize(x: np.ndarray, group_size: int, bits: int):
+    """``oracle_affine_quantize`` over the last axis of fp16 ``x`` (bit-identical to oracle.affine)."""
+    x = np.ascontiguousarray(x, dtype=np.float16)
+    d = x.shape[-1]
+    rows = x.size // d
+    codes = np.zeros(x.shape[:-1] + (d * bits // 32,), np.uint32)
+    sc = np.zeros(x.shape[:-1] + (d // group_size,), np.float16)
+    bi = np.zeros_like(sc)
+    c_oracle_lib().oracle_affine_quantize(_ptr(x.view(np.uint16)), rows, d, group_size, bits, _ptr(codes),
+                                          _ptr(sc.view(np.uint16)), _ptr(bi.view(np.uint16)))
+    return codes, sc, bi
+
+
+def c_oracle_expected(wl: Workload, *, sliding_window: int = 0, block_tables=None, kv_lens=None,
+                      fp16_dequant: bool = False) -> np.ndarray:
+    """``oracle_expected`` computed by the C restatement (double precision), for full-size workloads.
+
+    Same semantics as :func:`oracle_expected` (pinned against it in
+    ``tests/test_oracle_attention.py``); quantizes with the C quantizer, which
+    is bit-identical to ``oracle.affine.affine_quantize``.
+    """
+    assert wl.bits is not None
+    b, o = wl.slot // wl.block_size, wl.slot % wl.block_size
+    pages = []
+    for x in (wl.k, wl.v):
+        c, s, bi = c_quantize(x, wl.group_size, wl.bits)
+        C = np.zeros((wl.num_blocks, wl.block_size) + c.shape[1:], np.uint32)
+        S = np.zeros((wl.num_blocks, wl.block_size) + s.shape[1:], np.float16)
+        B = np.zeros_like(S)
+        C[b, o], S[b, o], B[b, o] = c, s, bi
+        pages.append((C, S, B))
+    bt = np.ascontiguousarray(wl.block_tables if block_tables is None else block_tables, dtype=np.int32)
+    kl = np.ascontiguousarray(wl.kv_lens if kv_lens is None else kv_lens, dtype=np.int32)
+    qsl = np.ascontiguousarray(wl.query_start_loc, dtype=np.int32)
+    q = np.ascontiguousarray(wl.q, dtype=np.float16)
+    out = np.zeros(q.shape, np.float64)
+    (kc, ks, kb), (vc, vs, vb) = pages
+    c_oracle_lib().oracle_attention_affine(
+        _ptr(q.view(np.uint16)), _ptr(kc), _ptr(ks.view(np.uint16)), _ptr(kb.view(np.uint16)), _ptr(vc),
+        _ptr(vs.view(np.uint16)), _ptr(vb.view(np.uint16)), _ptr(bt), _ptr(kl), _ptr(qsl), int(kl.shape[0]),
+        wl.num_q_heads, wl.num_kv_heads, wl.head_dim, wl.block_size, wl.num_blocks, int(bt.shape[1]), wl.bits,
+        wl.group_size, 1.0 / np.sqrt(wl.head_dim), int(sliding_window), int(fp16_dequant), _ptr(out))
+    return out

@@ -6,7 +6,7 @@ import torch
 
 from easymlx_amd import paged_attention
 from easymlx_amd.workloads import config, decode_workload
-from tests.helpers import assert_attention_close, gpu_cache, oracle_expected
+from tests.helpers import assert_attention_close, c_oracle_expected, gpu_cache, oracle_expected
 
 pytestmark = pytest.mark.gpu
 
@@ -57,6 +57,28 @@ def test_decode_c2_full(cuda):
     wl = config("c2")
     view = gpu_cache(wl, cuda)
     assert_attention_close(_run(wl, view, cuda), oracle_expected(wl), "c2")
+
+
+@pytest.mark.xfail(reason="MLX-style fp16 dequantization is not the parity target: rounding each dequantized "
+                          "K/V element to fp16 moves c2 outputs by up to 4.5e-3 (2-3 of 131072 elements beyond "
+                          "2e-3 + 1e-2|exp|); the kernels dequantize in fp32", strict=False)
+def test_decode_c2_vs_fp16_dequant_target(cuda):
+    """c2 against the oracle with each dequantized element rounded to fp16 (recorded, not required)."""
+    print("[decode c2 vs fp16-dequant oracle]", flush=True)
+    wl = config("c2")
+    view = gpu_cache(wl, cuda)
+    assert_attention_close(_run(wl, view, cuda), c_oracle_expected(wl, fp16_dequant=True), "c2 fp16-dequant")
+
+
+@pytest.mark.timeout(400)
+def test_decode_c4_full(cuda):
+    """The c4 configuration exactly as bench.py times it: 8 x 32k tokens, Hq 64 / Hkv 8, 4096-page pool."""
+    print("[decode c4 full]", flush=True)
+    wl = config("c4")
+    view = gpu_cache(wl, cuda)
+    got = _run(wl, view, cuda)
+    del view
+    assert_attention_close(got, c_oracle_expected(wl), "c4")
 
 
 def test_decode_c1_full(cuda):

@@ -80,15 +80,22 @@ def test_fp8_write_bit_exact(cuda, dtype):
     np.testing.assert_array_equal(view.v_scales.cpu().numpy(), vs)
 
 
-def test_fp8_write_skips_and_large_batch(cuda):
-    """A 4096-token write (several workgroups in the max pass) with skipped slots."""
-    print("[fp8 write large]", flush=True)
+@pytest.mark.parametrize("t", [4096, 32])
+def test_fp8_write_skips_and_large_batch(cuda, t):
+    """A 4096-token write (several workgroups in the max pass) and a 32-token one-launch write, with skipped
+    slots: -1 and pages outside the pool (large values there must not enter the call's scale)."""
+    print(f"[fp8 write skips t={t}]", flush=True)
     rng = np.random.default_rng(3)
-    nb, bs, hkv, d, t = 64, 128, 4, 128, 4096
+    nb, bs, hkv, d = 64, 128, 4, 128
     k = (rng.standard_normal((t, hkv, d)) * rng.uniform(0.1, 8.0, (1, hkv, d))).astype(np.float16)
     v = rng.standard_normal((t, hkv, d)).astype(np.float16)
     slot = rng.permutation(nb * bs)[:t].astype(np.int32)
     slot[rng.random(t) < 0.1] = -1
+    out_of_pool = rng.random(t) < 0.05
+    out_of_pool[0] = True
+    slot[out_of_pool] = nb * bs + rng.integers(0, 5 * bs, int(out_of_pool.sum()))
+    k[out_of_pool] = 3000.0
+    v[out_of_pool] = -3000.0
     shape = (nb, bs, hkv, d)
     view = Fp8PageCacheView(key_cache=torch.zeros(shape, dtype=torch.uint8, device=cuda),
                             value_cache=torch.zeros(shape, dtype=torch.uint8, device=cuda),

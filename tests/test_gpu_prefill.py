@@ -13,8 +13,8 @@ import pytest
 import torch
 
 from easymlx_amd import paged_attention
-from easymlx_amd.workloads import unified_workload
-from helpers import assert_attention_close, gpu_cache, oracle_expected
+from easymlx_amd.workloads import config, unified_workload
+from helpers import assert_attention_close, c_oracle_expected, gpu_cache, oracle_expected
 
 pytestmark = pytest.mark.gpu
 
@@ -37,6 +37,16 @@ def test_c3_slice_full_chunks(cuda):
                           decode_ctx=(256, 4096), bits=4)
     view = gpu_cache(wl, cuda)
     assert_attention_close(_run(wl, view, cuda), oracle_expected(wl), "c3 slice")
+
+
+@pytest.mark.timeout(300)
+def test_c3_full(cuda):
+    """The c3 configuration exactly as bench.py times it (4 x 512-token chunks + 28 decode rows), with the
+    prefill key split on (bench-sized workspace), against the C oracle."""
+    print("[prefill c3 full]", flush=True)
+    wl = config("c3")
+    view = gpu_cache(wl, cuda)
+    assert_attention_close(_run(wl, view, cuda), c_oracle_expected(wl), "c3 full")
 
 
 @pytest.mark.parametrize("window", [0, 1, 77, 600])

@@ -246,3 +246,24 @@ def test_c_decode_matches_numpy(c_oracle, bits):
     exp = paged_attention(q, kd, vd, tables, lens, np.arange(S + 1, dtype=np.int32), compute_dtype=np.float64,
                           out_dtype=np.float64)
     np.testing.assert_allclose(out, exp, rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("bits,gs,fp16", [(4, 64, False), (8, 32, True), (4, 32, True), (8, 64, False)])
+@pytest.mark.parametrize("window", [0, 5, 40])
+def test_c_unified_matches_numpy(bits, gs, fp16, window):
+    """The C ragged/causal restatement (full-size checker) against the numpy oracle."""
+    from easymlx_amd.workloads import unified_workload
+    from helpers import c_oracle_expected, oracle_expected
+
+    wl = unified_workload("cpin", seed=bits + gs + window, num_prefill=2, chunk=37, prior_range=(0, 90),
+                          num_decode=3, decode_ctx=(1, 120), num_q_heads=8, num_kv_heads=2, head_dim=64,
+                          block_size=16, bits=bits, group_size=gs)
+    tables = wl.block_tables.copy()
+    lens = wl.kv_lens.copy()
+    tables[1, 0] = -1              # skipped page
+    tables[2, -1] = wl.num_blocks  # out-of-range page
+    lens[-1] = 0                   # empty decode row
+    exp = oracle_expected(wl, sliding_window=window, block_tables=tables, kv_lens=lens, fp16_dequant=fp16)
+    got = c_oracle_expected(wl, sliding_window=window, block_tables=tables, kv_lens=lens, fp16_dequant=fp16)
+    np.testing.assert_allclose(got, exp, rtol=1e-9, atol=1e-12)
+    assert np.all(got[wl.query_start_loc[-2]:] == 0)

@@ -72,6 +72,16 @@ def test_write_scale_and_page_scale_rules():
     # a skipped slot (-1) writes nothing and does not enter the scale
     fp8.fp8_write(np.full((1, hkv, d), 100.0, np.float32), k2, [-1], kc, vc, ks, vs)
     assert ks[0] == np.float32(2.0 / 240.0)
+    # so does a slot whose page lies outside the pool
+    before = kc.copy()
+    fp8.fp8_write(np.full((2, hkv, d), 100.0, np.float32), np.full((2, hkv, d), 100.0, np.float32),
+                  [nb * kc.shape[1] + 3, 3], kc, vc, ks, vs)
+    assert np.array_equal(kc[1:], before[1:])
+    assert ks[0] == np.float32(100.0 / 240.0) and ks[0] == vs[0]  # only the in-pool token (slot 3) counts
+    fp8.fp8_write(np.full((1, hkv, d), 1e4, np.float32), k2, [nb * kc.shape[1]], kc, vc, ks, vs)
+    assert ks[0] == np.float32(100.0 / 240.0) and np.all(ks[1:] == 0)
+    ks[0] = vs[0] = np.float32(2.0 / 240.0)
+    kc[0, 3] = vc[0, 3] = 0
     deq = fp8.fp8_dequant_cache(kc, ks)
     assert np.allclose(deq[0, :2], 2.0)
 
