@@ -6,6 +6,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <mutex>
 #include <string>
 
 #include "../../include/emx_attn.h"
@@ -16,6 +17,16 @@
 #include "quantize.hpp"
 #include "fp8.hpp"
 #include "decode_fp8.hpp"
+
+constexpr int kNoallocScratchFloats = 2 * emx::kFp8Parts;  // 2 KiB
+
+// Scratch of emx_fp8_cache_write_noalloc: the two-launch FP8 write's
+// per-workgroup maxima (written by fp8_amax before fp8_write reads them, so it
+// needs no clearing).  Each GPU holds its own copy until the process ends.  In
+// host code `scratch` is only a symbol: kernels get the device address that
+// hipGetSymbolAddress returns for the current device (noalloc_scratch()).
+static __device__ __align__(256) float scratch[kNoallocScratchFloats];
+
 
 namespace {
 
@@ -209,6 +220,31 @@ int launch_generic(const emx::GenericArgs& ga, const KV& kv, hipStream_t st) {
   dim3 grid(ga.T, ga.Hkv, (hg + 15) / 16);
   hipLaunchKernelGGL((emx::paged_generic<QT, KV>), grid, dim3(64), 0, st, ga, kv);
   return check_launch("paged_generic");
+}
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device, looked up once per device
+// (with that device current).  Null, with the last error set, on failure.
+void* noalloc_scratch() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    fail(EMX_ERR_HIP, "emx_fp8_cache_write_noalloc: no current device (or device id >= %d)", kMaxDevices);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      fail(EMX_ERR_HIP, "emx_fp8_cache_write_noalloc: hipGetSymbolAddress(scratch) failed: %s", hipGetErrorString(e));
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  return g_scratch_ptr[dev];
 }
 
 }  // namespace
@@ -668,6 +704,21 @@ int emx_fp8_cache_write(const void* keys, const void* values, int dtype, const i
                         size_t workspace_bytes, void* stream) {
   return fp8_write_impl(keys, values, dtype, slot_mapping, num_tokens, num_kv_heads, head_dim, page_size, num_blocks,
                         key_cache, value_cache, k_scales, v_scales, workspace, workspace_bytes,
+                        emx::RopeArgs{nullptr, nullptr, 0, 0}, nullptr, 0, stream);
+}
+
+int emx_fp8_cache_write_noalloc(const void* keys, const void* values, int dtype, const int32_t* slot_mapping,
+                                int num_tokens, int num_kv_heads, int head_dim, int page_size, int num_blocks,
+                                uint8_t* key_cache, uint8_t* value_cache, float* k_scales, float* v_scales,
+                                void* stream) {
+  static_assert(sizeof(float) * kNoallocScratchFloats >= sizeof(float) * 2 * emx::kFp8Parts,
+                "scratch holds the FP8 write's per-workgroup maxima");
+  // the scratch is a fixed 2 KiB whatever the call's size; the size limit is the
+  // FP8 write's own (fewer than 2^33 values per tensor, checked by fp8_write_impl)
+  void* ws = num_tokens > 0 ? noalloc_scratch() : nullptr;
+  if (num_tokens > 0 && ws == nullptr) return EMX_ERR_HIP;
+  return fp8_write_impl(keys, values, dtype, slot_mapping, num_tokens, num_kv_heads, head_dim, page_size, num_blocks,
+                        key_cache, value_cache, k_scales, v_scales, ws, sizeof(float) * kNoallocScratchFloats,
                         emx::RopeArgs{nullptr, nullptr, 0, 0}, nullptr, 0, stream);
 }
 

@@ -181,6 +181,22 @@ int emx_fp8_cache_write(const void* keys, const void* values, int dtype, const i
                         size_t workspace_bytes, void* stream);
 
 /*
+ * emx_fp8_cache_write that allocates nothing and takes no workspace: the
+ * two-launch path keeps its per-workgroup maxima in a fixed 2 KiB device array
+ * of the library (one per GPU, held until the process ends).  Same arguments,
+ * results and limits as emx_fp8_cache_write otherwise; calls no hipMalloc,
+ * hipFree or allocating library routine.  Calls that overlap in time on one GPU
+ * share that array and race: order them on one stream.
+ * No counterpart in the reference.  For callers that cannot allocate device
+ * memory or hold a workspace: code under HIP graph capture, tight serving
+ * loops, harnesses that forbid allocation.
+ */
+int emx_fp8_cache_write_noalloc(const void* keys, const void* values, int dtype, const int32_t* slot_mapping,
+                                int num_tokens, int num_kv_heads, int head_dim, int page_size, int num_blocks,
+                                uint8_t* key_cache, uint8_t* value_cache, float* k_scales, float* v_scales,
+                                void* stream);
+
+/*
  * emx_fp8_cache_write with rotary position embedding fused in: the call's K
  * scale and codes are taken over the keys turned as in
  * emx_affine_cache_write_rope and rounded to dtype.  rot_dims a multiple of 8
