@@ -96,10 +96,49 @@ def cpu_baseline(wl, n_seqs: int | None):
         "value": round(nbytes / per / 1e9, 4),
         "unit": "GB/s",
         "cores": cores,
+        "host_cores": {"affinity": len(os.sched_getaffinity(0)), "cpu_count": os.cpu_count()},
         "kind": "port",
-        "sample": f"C oracle (oracle/c/oracle.c, OpenMP over (seq, kv_head)) on {n} of {wl.num_seqs} sequences of the "
-                  f"same workload ({ntok} tokens), {reps} reps, {per * 1e3:.1f} ms each = {n / per:.1f} decode rows/s",
+        "sample": f"C oracle (oracle/c/oracle.c, OpenMP over (seq, kv_head), {cores} threads) on {n} of "
+                  f"{wl.num_seqs} sequences of the same workload ({ntok} tokens), {reps} reps, {per * 1e3:.1f} ms "
+                  f"each = {n / per:.1f} decode rows/s",
+        "numpy_restatement": numpy_baseline(wl, res),
     }
+
+
+def numpy_baseline(wl, pages, n_seqs=4, budget_s=8.0):
+    """The NumPy restatement of the reference's CPU path (``_paged_attention_reference``,
+    unified_attention.py:187-281, as ``oracle.paged_attention``) plus the affine dequantize, timed on a bounded
+    sample of the c2 workload (its first ``n_seqs`` sequences)."""
+    from oracle.affine import affine_dequantize
+    from oracle.paged_attention import paged_attention as np_attention
+
+    bs, g, bits = wl.block_size, wl.group_size, wl.bits
+    lens = wl.kv_lens[:n_seqs]
+    ntok = int(lens.sum())
+    q = wl.q[:n_seqs]
+    qsl = np.arange(n_seqs + 1, dtype=np.int32)
+    # only the sample's pages (renumbered), so each call dequantizes what it reads
+    used = [int(b) for s in range(n_seqs) for b in wl.block_tables[s, :-(-int(lens[s]) // bs)]]
+    remap = {b: i for i, b in enumerate(used)}
+    tables = np.array([[remap.get(int(b), -1) for b in row] for row in wl.block_tables[:n_seqs]], np.int32)
+    sub = {n: tuple(a[used] for a in pages[n]) for n in ("k", "v")}
+    reps, t_total = 0, 0.0
+    while t_total < budget_s and reps < 50:
+        t0 = time.perf_counter()
+        kc = affine_dequantize(sub["k"][0], sub["k"][1].view(np.float16), sub["k"][2].view(np.float16), g, bits,
+                               round_to_fp16=False)
+        vc = affine_dequantize(sub["v"][0], sub["v"][1].view(np.float16), sub["v"][2].view(np.float16), g, bits,
+                               round_to_fp16=False)
+        np_attention(q, kc, vc, tables, lens, qsl, compute_dtype=np.float32)
+        t_total += time.perf_counter() - t0
+        reps += 1
+    per = t_total / reps
+    nbytes = ntok * wl.num_kv_heads * 2 * (wl.head_dim * bits // 8 + (wl.head_dim // g) * 4)
+    blas = {k: os.environ.get(k) for k in ("OMP_NUM_THREADS", "OPENBLAS_NUM_THREADS", "MKL_NUM_THREADS")}
+    return {"value": round(nbytes / per / 1e9, 4), "unit": "GB/s", "kind": "port",
+            "sample": f"oracle.paged_attention (numpy, fp32) + oracle.affine.affine_dequantize of the sample's pages "
+                      f"per call, first {n_seqs} sequences of c2 ({ntok} tokens), {reps} reps, {per * 1e3:.1f} ms each",
+            "threads_env": blas}
 
 
 def measured_traffic():
@@ -257,7 +296,8 @@ def aux_c4(dev):
 def aux_fp8(dev):
     """FP8 (E4M3, per-page scale) cache: c2-shaped decode (batch 32, ctx U[512,4096]) and a 32-token write.
 
-    One pool (fits the 256 MB cache: an upper bound on the rate), HIP events per call.
+    The decode rotates over copies of the page pool (>= 1 GiB in all) so the 256 MB Infinity Cache cannot serve
+    the pages; HIP events per call.
     """
     import torch
 
@@ -278,13 +318,20 @@ def aux_fp8(dev):
     q = torch.from_numpy(wl.q).to(dev)
     qsl = torch.from_numpy(wl.query_start_loc).to(dev)
     out = torch.empty_like(q)
+    pool_bytes = 2 * view.key_cache.numel()
+    pools = [(view.key_cache, view.value_cache, view.k_scales, view.v_scales)]
+    while len(pools) * pool_bytes < 2**30:
+        pools.append(tuple(t.clone() for t in pools[0]))
 
     def call(i=0):
-        paged_attention(q, view.key_cache, view.value_cache, view.block_tables, view.kv_lens, qsl,
-                        k_scale=view.k_scales, v_scale=view.v_scales, single_token_decode=True, out=out)
+        kc, vc, ks, vs = pools[i % len(pools)]
+        paged_attention(q, kc, vc, view.block_tables, view.kv_lens, qsl, k_scale=ks, v_scale=vs,
+                        single_token_decode=True, out=out)
 
     warm(call, 0.3)
-    us = float(np.median(event_us(call, 50)))
+    us = float(np.median(event_us(call, 100)))
+    n_fp8_pools = len(pools)
+    del pools
     nbytes = int(wl.kv_lens.astype(np.int64).sum()) * wl.num_kv_heads * 2 * wl.head_dim
     kk = torch.randn(wl.num_seqs, wl.num_kv_heads, wl.head_dim, device=dev).half()
     slot = torch.from_numpy((wl.block_tables[:, 0] * wl.block_size).astype(np.int32)).to(dev)
@@ -315,6 +362,7 @@ def aux_fp8(dev):
     warm(ucall, 0.3)
     uus = float(np.median(event_us(ucall, 50)))
     return {"workload": "fp8 e4m3 cache, c2 shape: batch 32, Hq 32 / Hkv 8, D 128, page 128, ctx U[512,4096] (seed 2)",
+            "rotated_pools": n_fp8_pools, "pool_bytes": int(pool_bytes),
             "unified_c3_shape_us_p50": round(uus, 2),
             "decode_us_p50": round(us, 2), "kv_bytes": nbytes, "kv_GBs": round(nbytes / (us * 1e3), 1),
             "frac": round(nbytes / (us * 1e3) / HBM_PEAK_GBS, 4), "write_32_tokens_us_p50": round(wus, 2)}
@@ -386,6 +434,74 @@ def aux_quantize_on_write(dev):
     return res
 
 
+def aux_op_layer_step(dev, steps=100):
+    """The public op as a runner calls it, per layer-step of c2: ``concatenate_to_cache`` (quantize-on-write of
+    one token per sequence, Llama-3 RoPE fused) then ``UnifiedAttention.forward_native``.  Wall clock per step:
+    eager Python calls, and the same step captured once in a HIP graph through ``CompiledPagedCacheProxy``
+    (the counterpart of the reference's compiled decode) and replayed."""
+    import torch
+
+    from easymlx_amd import CompiledPagedCacheProxy, PageMetadata, RotaryEmbedding, UnifiedAttention
+    from easymlx_amd.caching import affine_pool
+    from easymlx_amd.workloads import config
+
+    wl = config("c2")
+    S, hq, hkv, d, bs = wl.num_seqs, wl.num_q_heads, wl.num_kv_heads, wl.head_dim, wl.block_size
+    extra = 2  # fresh pages per sequence for the appended tokens
+    tables = np.full((S, wl.block_tables.shape[1] + extra), -1, np.int32)
+    for s in range(S):
+        used = -(-int(wl.kv_lens[s]) // bs)
+        tables[s, :used] = wl.block_tables[s, :used]
+        tables[s, used:used + extra] = wl.num_blocks + extra * s + np.arange(extra)
+    rope = RotaryEmbedding.llama3(d, base=500000.0)
+    op = UnifiedAttention()
+    g = torch.Generator(device=dev).manual_seed(0)
+    q = torch.randn((S, hq, d), device=dev, generator=g).half()
+    k = torch.randn((S, hkv, d), device=dev, generator=g).half()
+    v = torch.randn((S, hkv, d), device=dev, generator=g).half()
+    res = {}
+    for mode in ("eager", "graph"):
+        view = affine_pool(num_blocks=wl.num_blocks + extra * S, num_kv_heads=hkv, head_dim=d, block_size=bs, bits=4,
+                           group_size=64, block_tables=torch.from_numpy(tables).to(dev),
+                           kv_lens=torch.from_numpy(wl.kv_lens).to(dev))
+        view.write_slots(torch.from_numpy(wl.k).to(dev), torch.from_numpy(wl.v).to(dev),
+                         torch.from_numpy(wl.slot.astype(np.int32)).to(dev))
+        md0 = PageMetadata(query_start_loc=torch.arange(S + 1, dtype=torch.int32, device=dev),
+                           slot_ids=tuple(range(S)))
+        qlens = (1,) * S
+        cache = CompiledPagedCacheProxy(view) if mode == "graph" else view
+        out_buf = torch.empty_like(q)
+
+        def step():
+            q2, kc, vc, md = cache.concatenate_to_cache(q, k, v, cache_metadata=md0, rope=rope, query_lens=qlens)
+            out_buf.copy_(op.forward_native(query=q2, key=kc, value=vc, cache_metadata=md,
+                                            cache_view=view).attention_outputs)
+
+        side = torch.cuda.Stream(dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):
+            step()
+            if mode == "graph":
+                graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graph, stream=side):
+                    step()
+                run = graph.replay
+            else:
+                run = step
+            for _ in range(5):
+                run()
+            side.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                run()
+            side.synchronize()
+            res[f"{mode}_us_per_layer_step"] = round((time.perf_counter() - t0) / steps * 1e6, 2)
+        del view
+    res["workload"] = ("c2 layer-step through the public op: concatenate_to_cache (1 token x 32 seqs, Llama-3 "
+                       "RoPE fused) + UnifiedAttention.forward_native, wall clock")
+    return res
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -442,6 +558,7 @@ def main():
         aux["c4_long_context"] = aux_c4(dev)
         torch.cuda.empty_cache()
         aux["quantize_on_write"] = aux_quantize_on_write(dev)
+        aux["op_layer_step"] = aux_op_layer_step(dev)
         aux["fp8_cache"] = aux_fp8(dev)
 
     value = bytes_per_step / (ms_per_step * 1e-3) / 1e9

@@ -7,6 +7,7 @@ attention-operation plugin interface.
 """
 
 from .caching.paged import AffinePageCacheView, Fp8PageCacheView, PageCacheView, PageMetadata, build_query_start_loc
+from .caching.compiled import CompiledPagedCacheProxy
 from .caching.rope import RotaryEmbedding
 from .operations import AttentionOutput, BaseOperation, OperationRegistry, UnifiedAttention, paged_attention
 from .quantize import affine_quantize
@@ -15,6 +16,7 @@ __all__ = (
     "AffinePageCacheView",
     "AttentionOutput",
     "BaseOperation",
+    "CompiledPagedCacheProxy",
     "Fp8PageCacheView",
     "OperationRegistry",
     "PageCacheView",

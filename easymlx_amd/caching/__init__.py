@@ -1,6 +1,7 @@
 """Paged KV caches (dense, FP8 E4M3 and affine-quantized)."""
 
 from .rope import RotaryEmbedding
+from .compiled import CompiledPagedCacheProxy
 from .paged import AffinePageCacheView, Fp8PageCacheView, PageCacheView, PageMetadata, affine_pool, build_query_start_loc
 
-__all__ = ("AffinePageCacheView", "Fp8PageCacheView", "PageCacheView", "PageMetadata", "affine_pool", "build_query_start_loc", "RotaryEmbedding")
+__all__ = ("AffinePageCacheView", "CompiledPagedCacheProxy", "Fp8PageCacheView", "PageCacheView", "PageMetadata", "affine_pool", "build_query_start_loc", "RotaryEmbedding")

@@ -11,8 +11,9 @@ Mirrors the write-side contract of the reference's ``PageCacheView``
 
 ``concatenate_to_cache`` keeps the reference's signature and return value
 ``(queries, key_cache, value_cache, resolved_metadata)``.  Block tables and
-``kv_lens`` live on the device; slot arithmetic for a step is done with a few
-device ops, never with a host round trip of device data.
+``kv_lens`` live on the device; the slot arithmetic of a write is one kernel
+(``emx_cache_slots``) that also advances ``kv_lens``, so a write never reads
+device data back to the host.
 """
 
 from __future__ import annotations
@@ -147,35 +148,35 @@ class PageCacheView:
     def num_blocks(self) -> int:
         return int(self.key_cache.shape[0])
 
-    # -- slot arithmetic shared by both views (cache.py:1127-1170, 1230-1261)
-    def _slot_mapping(self, slot_ids, query_lens) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-        mapping, slots, base, _ = self._slot_mapping_positions(slot_ids, query_lens)
-        return mapping, slots, base
+    # -- slot arithmetic shared by all views (cache.py:1126-1170, 1211-1261), on the device
+    def _slots(self, slot_ids, qlens):
+        """Slot mapping and position of every written token, by ``emx_cache_slots``; advances ``kv_lens``.
 
-    def _slot_mapping_positions(self, slot_ids, query_lens):
-        """Slot of every token, the sequences' slots and prior lengths, and every token's position."""
+        Returns ``(slot_mapping, slots, positions, query_start_loc)`` as int32
+        device tensors.  The only host work is one copy of the call's slot ids
+        and query offsets (host data in the reference's API) to the device.
+        """
         dev = self.block_tables.device
-        qlens = [max(0, int(q)) for q in query_lens]
-        slots = torch.tensor(list(slot_ids), dtype=torch.long, device=dev)
-        base = self.kv_lens.index_select(0, slots).to(torch.long)
-        total = sum(qlens)
-        if total == 0:
-            empty = torch.empty((0,), dtype=torch.int32, device=dev)
-            return empty, slots, base, empty
-        qlen_t = torch.tensor(qlens, dtype=torch.long, device=dev)
-        tok_slot = torch.repeat_interleave(slots, qlen_t, output_size=total)
-        starts = [0]
-        for q in qlens[:-1]:
-            starts.append(starts[-1] + q)
-        local = torch.arange(total, device=dev) - torch.repeat_interleave(
-            torch.tensor(starts, dtype=torch.long, device=dev), qlen_t, output_size=total
-        )
-        pos = torch.repeat_interleave(base, qlen_t, output_size=total) + local
-        col = torch.clamp(pos // self.block_size, max=self.blocks_per_seq - 1)
-        blk = self.block_tables[tok_slot, col].to(torch.long)
-        ok = (blk >= 0) & (pos // self.block_size < self.blocks_per_seq)
-        mapping = torch.where(ok, blk * self.block_size + pos % self.block_size, torch.full_like(blk, -1))
-        return mapping.to(torch.int32), slots, base, pos.to(torch.int32)
+        if dev.type != "cuda" or self.kv_lens.device != dev:
+            raise RuntimeError(f"cache writes run on the GPU only; block_tables / kv_lens are on {dev}")
+        if self.block_tables.dtype != torch.int32 or self.kv_lens.dtype != torch.int32:
+            raise ValueError("block_tables and kv_lens must be int32")
+        n = len(slot_ids)
+        qsl = [0]
+        for q in qlens:
+            qsl.append(qsl[-1] + max(0, int(q)))
+        total = qsl[-1]
+        meta = torch.tensor(list(slot_ids) + qsl, dtype=torch.int32, device=dev)
+        slots, qsl_d = meta[:n], meta[n:]
+        mapping = torch.empty((total,), dtype=torch.int32, device=dev)
+        positions = torch.empty((total,), dtype=torch.int32, device=dev)
+        if n:
+            bt = self.block_tables.contiguous()
+            _native.check(_native.load().emx_cache_slots(
+                slots.data_ptr(), qsl_d.data_ptr(), n, total, bt.data_ptr(), int(bt.shape[0]), int(bt.shape[1]),
+                self.block_size, self.kv_lens.data_ptr(), mapping.data_ptr(), positions.data_ptr(),
+                _stream_ptr(dev)))
+        return mapping, slots, positions, qsl_d
 
     def _resolve(self, cache_metadata, slot_ids, query_lens, n_tokens):
         if slot_ids is None:
@@ -190,37 +191,65 @@ class PageCacheView:
         single = bool(qlens) and n_tokens == len(qlens) and all(q == 1 for q in qlens)
         return slot_ids, qlens, single
 
-    def _apply_rope(self, rope, queries, keys, slots, base, qlens, single):
+    def _apply_rope(self, rope, queries, keys, positions, qsl, qlens, single):
+        """A RoPE callable applied as the reference applies it (``cache.py:1161-1166``, ``:1223-1229``).
+
+        A :class:`RotaryEmbedding` over fp16 rows turns on the device by
+        ``emx_rope_rows`` at every token's position (the rotation of the fused
+        writes); any other callable gets per-sequence offsets."""
+        from .rope import RotaryEmbedding
+
         if rope is None:
             return queries, keys
+        if (isinstance(rope, RotaryEmbedding) and queries.dtype == torch.float16 and keys.dtype == torch.float16
+                and rope.dims <= self.head_dim and queries.shape[-1] == self.head_dim):
+            n = int(positions.shape[0])
+            lib = _native.load()
+            inv = rope.inv_freq(queries.device)
+            stream = _stream_ptr(queries.device)
+            q_out, k_out = queries[:n].contiguous().clone(), keys[:n].contiguous().clone()
+            for x in (q_out, k_out):
+                if n:
+                    _native.check(lib.emx_rope_rows(x.data_ptr(), n, int(x.shape[1]), self.head_dim,
+                                                    positions.data_ptr(), inv.data_ptr(), rope.dims,
+                                                    int(rope.traditional), stream))
+            return q_out, k_out
         if single:
             qb = queries.unsqueeze(1).transpose(1, 2)
             kb = keys.unsqueeze(1).transpose(1, 2)
             return (
-                rope(qb, offset=base).transpose(1, 2)[:, 0],
-                rope(kb, offset=base).transpose(1, 2)[:, 0],
+                rope(qb, offset=positions).transpose(1, 2)[:, 0],
+                rope(kb, offset=positions).transpose(1, 2)[:, 0],
             )
         q_out, k_out, start = [], [], 0
-        base_host = base.tolist()
-        for i, n in enumerate(qlens):
+        # per-chunk integer offsets for an arbitrary callable (the fused RotaryEmbedding path needs none)
+        first = [int(qsl[i]) for i in range(len(qlens)) if qlens[i] > 0]
+        base_host = positions[first].tolist() if first else []
+        for n in qlens:
             if n <= 0:
                 continue
             qc = queries[start : start + n][None].transpose(1, 2)
             kc = keys[start : start + n][None].transpose(1, 2)
-            q_out.append(rope(qc, offset=int(base_host[i])).transpose(1, 2)[0])
-            k_out.append(rope(kc, offset=int(base_host[i])).transpose(1, 2)[0])
+            off = int(base_host[len(q_out)])
+            q_out.append(rope(qc, offset=off).transpose(1, 2)[0])
+            k_out.append(rope(kc, offset=off).transpose(1, 2)[0])
             start += n
         if not q_out:
             return queries[:0], keys[:0]
         return torch.cat(q_out), torch.cat(k_out)
 
     def _write(self, keys, values, slot_mapping):
-        ok = slot_mapping >= 0
-        idx = slot_mapping[ok].to(torch.long)
-        kc = self.key_cache.view(-1, self.num_kv_heads, self.head_dim)
-        vc = self.value_cache.view(-1, self.num_kv_heads, self.head_dim)
-        kc[idx] = keys[ok].to(kc.dtype)
-        vc[idx] = values[ok].to(vc.dtype)
+        # cast like the cache (cache.py:1186-1190), then the scatter kernel (-1 skips)
+        codes = {torch.float16: _native.DTYPE_F16, torch.bfloat16: _native.DTYPE_BF16, torch.float32: _native.DTYPE_F32}
+        if self.key_cache.dtype not in codes:
+            raise NotImplementedError(f"unquantized caches hold fp16/bf16/fp32, not {self.key_cache.dtype}")
+        keys = keys.to(self.key_cache.dtype).contiguous()
+        values = values.to(self.value_cache.dtype).contiguous()
+        slot_mapping = slot_mapping.to(torch.int32).contiguous()
+        _native.check(_native.load().emx_dense_cache_write(
+            keys.data_ptr(), values.data_ptr(), codes[self.key_cache.dtype], slot_mapping.data_ptr(),
+            int(keys.shape[0]), self.num_kv_heads, self.head_dim, self.block_size, self.num_blocks,
+            self.key_cache.data_ptr(), self.value_cache.data_ptr(), _stream_ptr(keys.device)))
 
     def concatenate_to_cache(
         self,
@@ -235,20 +264,22 @@ class PageCacheView:
     ):
         """Append K/V for the scheduled slots (``cache.py:1088-1306``)."""
         slot_ids, qlens, single = self._resolve(cache_metadata, slot_ids, query_lens, int(queries.shape[0]))
-        slot_mapping, slots, base = self._slot_mapping(slot_ids, qlens)
-        queries, keys = self._apply_rope(rope, queries, keys, slots, base, qlens, single)
+        slot_mapping, slots, positions, qsl = self._slots(slot_ids, qlens)
+        queries, keys = self._apply_rope(rope, queries, keys, positions, qsl, qlens, single)
         if slot_mapping.numel():
             self._write(keys.contiguous(), values.contiguous(), slot_mapping)
-        if len(slot_ids):
-            add = torch.tensor(qlens, dtype=torch.int32, device=self.kv_lens.device)
-            self.kv_lens.index_copy_(0, slots, (base + add).to(torch.int32))
+        return queries, self.key_cache, self.value_cache, self._resolved(cache_metadata, slots, single)
+
+    def _resolved(self, cache_metadata, slots, single):
+        """Metadata with this cache's tables and lengths for the written slots (``cache.py:1297-1305``)."""
+        n = int(slots.shape[0])
         md = cache_metadata.with_cache_state(
-            block_tables=self.block_tables.index_select(0, slots) if len(slot_ids) else self.block_tables[:0],
-            kv_lens=self.kv_lens.index_select(0, slots) if len(slot_ids) else self.kv_lens[:0],
+            block_tables=self.block_tables.index_select(0, slots) if n else self.block_tables[:0],
+            kv_lens=self.kv_lens.index_select(0, slots) if n else self.kv_lens[:0],
             block_size=self.block_size,
         )
         md.is_single_token_decode = single
-        return queries, self.key_cache, self.value_cache, md
+        return md
 
     def _concatenate_rope_fused(self, queries, keys, values, cache_metadata, rope, slot_ids, query_lens, write,
                                 rot_multiple, writes_queries=False):
@@ -261,7 +292,7 @@ class PageCacheView:
             return PageCacheView.concatenate_to_cache(self, queries, keys, values, cache_metadata=cache_metadata,
                                                       rope=rope, slot_ids=slot_ids, query_lens=query_lens)
         slot_ids, qlens, single = self._resolve(cache_metadata, slot_ids, query_lens, int(queries.shape[0]))
-        slot_mapping, slots, base, positions = self._slot_mapping_positions(slot_ids, qlens)
+        slot_mapping, slots, positions, _ = self._slots(slot_ids, qlens)
         lib = _native.load()
         n = int(slot_mapping.numel())
         q_out = queries.contiguous().clone()
@@ -273,16 +304,7 @@ class PageCacheView:
                                                 positions.data_ptr(), inv.data_ptr(), rope.dims,
                                                 int(rope.traditional), stream))
             _native.check(write(keys, values, slot_mapping, positions, inv, rope, stream, q_out))
-        if len(slot_ids):
-            add = torch.tensor(qlens, dtype=torch.int32, device=self.kv_lens.device)
-            self.kv_lens.index_copy_(0, slots, (base + add).to(torch.int32))
-        md = cache_metadata.with_cache_state(
-            block_tables=self.block_tables.index_select(0, slots) if len(slot_ids) else self.block_tables[:0],
-            kv_lens=self.kv_lens.index_select(0, slots) if len(slot_ids) else self.kv_lens[:0],
-            block_size=self.block_size,
-        )
-        md.is_single_token_decode = single
-        return q_out, self.key_cache, self.value_cache, md
+        return q_out, self.key_cache, self.value_cache, self._resolved(cache_metadata, slots, single)
 
     def append(self, seq_idx: int, key: torch.Tensor, value: torch.Tensor) -> None:
         """Append ``[num_tokens, Hkv, D]`` tokens to one sequence (``cache.py:834-872``)."""
@@ -298,11 +320,10 @@ class PageCacheView:
         n = int(key.shape[0])
         if start + n > self.max_seq_len:
             raise ValueError("Cannot append tokens: sequence length would exceed cache capacity")
-        slot_mapping, _, _ = self._slot_mapping([seq_idx], [n])
+        slot_mapping, _, _, _ = self._slots([seq_idx], [n])  # advances kv_lens[seq_idx] by n
         if n:
             self._write(key.to(self.block_tables.device).contiguous(), value.to(self.block_tables.device).contiguous(),
                         slot_mapping)
-        self.kv_lens[seq_idx] = start + n
 
     def reset(self, seq_idx: int) -> None:
         """Zero one sequence's pages and its length (``cache.py:874-906``, with page ids used correctly)."""

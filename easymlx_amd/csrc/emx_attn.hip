@@ -17,6 +17,7 @@
 #include "quantize.hpp"
 #include "fp8.hpp"
 #include "decode_fp8.hpp"
+#include "slots.hpp"
 
 constexpr int kNoallocScratchFloats = 2 * emx::kFp8Parts;  // 2 KiB
 
@@ -375,6 +376,44 @@ int emx_affine_cache_write_rope(const void* keys, const void* values, const int3
                            page_size, num_blocks, k_codes, k_scales, k_biases, v_codes, v_scales, v_biases,
                            emx::RopeArgs{inv_freq, positions, rot_dims, traditional ? 1 : 0}, queries, num_q_heads,
                            stream);
+}
+
+int emx_cache_slots(const int32_t* slot_ids, const int32_t* query_start_loc, int num_slots, int num_tokens,
+                    const int32_t* block_tables, int num_seqs, int max_blocks_per_seq, int page_size,
+                    int32_t* kv_lens, int32_t* slot_mapping, int32_t* positions, void* stream) {
+  if (num_slots < 0 || num_tokens < 0) return fail(EMX_ERR_INVALID, "num_slots and num_tokens must be >= 0");
+  if (num_slots > emx::kMaxSlots)
+    return fail(EMX_ERR_UNSUPPORTED, "%d sequences in one write exceed %d", num_slots, emx::kMaxSlots);
+  if (num_seqs <= 0 || max_blocks_per_seq <= 0 || page_size <= 0)
+    return fail(EMX_ERR_INVALID, "num_seqs, max_blocks_per_seq and page_size must be positive");
+  if (num_slots == 0) return num_tokens == 0 ? EMX_OK : fail(EMX_ERR_INVALID, "tokens without sequences");
+  if (!slot_ids || !query_start_loc || !block_tables || !kv_lens || (num_tokens > 0 && (!slot_mapping || !positions)))
+    return fail(EMX_ERR_INVALID, "null pointer");
+  emx::SlotArgs a{slot_ids, query_start_loc, num_slots, num_tokens, block_tables, num_seqs, max_blocks_per_seq,
+                  page_size, kv_lens, slot_mapping, positions};
+  hipLaunchKernelGGL(emx::cache_slots, dim3(1), dim3(1024), 0, reinterpret_cast<hipStream_t>(stream), a);
+  return check_launch("cache_slots");
+}
+
+int emx_dense_cache_write(const void* keys, const void* values, int dtype, const int32_t* slot_mapping,
+                          int num_tokens, int num_kv_heads, int head_dim, int page_size, int num_blocks,
+                          void* key_cache, void* value_cache, void* stream) {
+  if (num_tokens < 0) return fail(EMX_ERR_INVALID, "num_tokens must be >= 0");
+  if (num_kv_heads <= 0 || head_dim <= 0 || page_size <= 0 || num_blocks <= 0)
+    return fail(EMX_ERR_INVALID, "num_kv_heads, head_dim, page_size, num_blocks must be positive");
+  const int elem = dtype == EMX_DTYPE_F32 ? 4 : dtype == EMX_DTYPE_F16 || dtype == EMX_DTYPE_BF16 ? 2 : 0;
+  if (elem == 0) return fail(EMX_ERR_INVALID, "unknown dtype %d", dtype);
+  const long row_bytes = (long)num_kv_heads * head_dim * elem;
+  if (row_bytes % 4) return fail(EMX_ERR_UNSUPPORTED, "a token's row of %ld bytes is not whole words", row_bytes);
+  if (num_tokens == 0) return EMX_OK;
+  if (!keys || !values || !slot_mapping || !key_cache || !value_cache) return fail(EMX_ERR_INVALID, "null pointer");
+  const long n = (long)num_tokens * (row_bytes / 4);
+  const unsigned grid = (unsigned)std::min<long>((n + 255) / 256, 4096);
+  hipLaunchKernelGGL(emx::dense_cache_write, dim3(grid), dim3(256), 0, reinterpret_cast<hipStream_t>(stream),
+                     reinterpret_cast<const uint32_t*>(keys), reinterpret_cast<const uint32_t*>(values), slot_mapping,
+                     num_tokens, (int)(row_bytes / 4), page_size, num_blocks, reinterpret_cast<uint32_t*>(key_cache),
+                     reinterpret_cast<uint32_t*>(value_cache));
+  return check_launch("dense_cache_write");
 }
 
 int emx_rope_rows(void* x, int rows, int heads, int head_dim, const int32_t* positions, const float* inv_freq,

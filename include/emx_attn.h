@@ -88,6 +88,37 @@ int emx_affine_cache_write_rope(const void* keys, const void* values, const int3
                                 int rot_dims, int traditional, void* queries, int num_q_heads, void* stream);
 
 /*
+ * Write positions of a cache write, on the device: token t of sequence i
+ * (query_start_loc[i] <= t < query_start_loc[i+1], i < num_slots, int32 arrays
+ * on the device) of slot s = slot_ids[i] goes to position
+ * p = kv_lens[s] + t - query_start_loc[i], slot_mapping[t] =
+ * block_tables[s, p / page_size] * page_size + p % page_size (-1 when s is
+ * outside [0, num_seqs), the page column beyond max_blocks_per_seq or the
+ * block id negative), positions[t] = p; then kv_lens[s] += query length of i
+ * (in place).  num_tokens = query_start_loc[num_slots]; at most 4096 sequences.
+ * One launch, no host round trip: usable under HIP graph capture.
+ * Replaces the slot arithmetic of PageCacheView.concatenate_to_cache
+ *   lib/python/easymlx/caching/paged/cache.py:1126-1170, 1211-1261, 1297
+ *   and of the compiled decode proxy
+ *   lib/python/easymlx/inference/esurge/runners/model_runner.py:164-184.
+ */
+int emx_cache_slots(const int32_t* slot_ids, const int32_t* query_start_loc, int num_slots, int num_tokens,
+                    const int32_t* block_tables, int num_seqs, int max_blocks_per_seq, int page_size,
+                    int32_t* kv_lens, int32_t* slot_mapping, int32_t* positions, void* stream);
+
+/*
+ * Unquantized cache write: token t's rows keys/values [num_tokens, Hkv,
+ * head_dim] (dtype EMX_DTYPE_*) to slot slot_mapping[t] of key_cache /
+ * value_cache [num_blocks, page_size, Hkv, head_dim] of the same dtype (-1 or a
+ * page outside the pool skips the token).
+ * Replaces reshape_and_cache lib/python/easymlx/caching/paged/cache.py:36-93
+ *   (the cast-and-scatter of concatenate_to_cache :1186-1190, :1273-1277).
+ */
+int emx_dense_cache_write(const void* keys, const void* values, int dtype, const int32_t* slot_mapping,
+                          int num_tokens, int num_kv_heads, int head_dim, int page_size, int num_blocks,
+                          void* key_cache, void* value_cache, void* stream);
+
+/*
  * Rotary position embedding in place on fp16 rows x [rows, heads, head_dim]
  * (row r at positions[r]), the same rotation as emx_affine_cache_write_rope.
  * Replaces the RoPE applied to queries in concatenate_to_cache

@@ -46,36 +46,24 @@ def test_write_goldens(name, initial, qlens):
     sm, lens = write_positions(z["block_tables"], z["kv_lens"], z["query_start_loc"], [0, 1, 2], bs)
     assert sm.tolist() == exp and lens.tolist() == z["expected_kv_lens"].tolist()
 
-    # the host cache view (dense, CPU tensors) performs the same write
-    view = PageCacheView(key_cache=torch.from_numpy(z["key_cache"].copy()),
-                         value_cache=torch.from_numpy(z["value_cache"].copy()),
-                         block_tables=torch.from_numpy(z["block_tables"].copy()),
-                         kv_lens=torch.from_numpy(z["kv_lens"].copy()), block_size=bs,
-                         num_kv_heads=z["key_cache"].shape[2], head_dim=z["key_cache"].shape[3])
-    md = PageMetadata(query_start_loc=torch.from_numpy(z["query_start_loc"]))
-    q, kc, vc, md2 = view.concatenate_to_cache(torch.from_numpy(z["queries"]), torch.from_numpy(z["keys"]),
-                                               torch.from_numpy(z["values"]), cache_metadata=md, slot_ids=[0, 1, 2])
-    assert view.kv_lens.tolist() == z["expected_kv_lens"].tolist()
-    assert md2.kv_lens.tolist() == z["expected_kv_lens"].tolist()
-    assert md2.is_single_token_decode == (name == "write_rng7")
-    flat_k = kc.reshape(-1, *kc.shape[2:]).numpy()
-    flat_v = vc.reshape(-1, *vc.shape[2:]).numpy()
-    np.testing.assert_array_equal(flat_k[exp], z["keys"])
-    np.testing.assert_array_equal(flat_v[exp], z["values"])
-    untouched = np.ones(flat_k.shape[0], bool)
-    untouched[exp] = False
-    np.testing.assert_array_equal(flat_k[untouched], z["key_cache"].reshape(flat_k.shape)[untouched])
+    # the cache views perform the same write on the GPU: tests/test_gpu_write.py
 
 
 def test_slot_mapping_out_of_table_and_negative_blocks():
-    tables = torch.tensor([[3, -1], [0, 1]], dtype=torch.int32)
-    view = PageCacheView(key_cache=torch.zeros(4, 4, 1, 2), value_cache=torch.zeros(4, 4, 1, 2), block_tables=tables,
-                         kv_lens=torch.tensor([3, 7], dtype=torch.int32), block_size=4, num_kv_heads=1, head_dim=2)
-    sm, _, _ = view._slot_mapping([0, 1], [2, 2])
-    # seq 0: pos 3 -> block 3 off 3; pos 4 -> block -1 -> skipped.  seq 1: pos 7 -> block 1 off 3; pos 8 -> past table
-    assert sm.tolist() == [15, -1, 7, -1]
-    exp, _ = write_positions(tables.numpy(), [3, 7], [0, 2, 4], [0, 1], 4)
-    assert exp.tolist()[:3] == [15, -1, 7]
+    # seq 0: pos 3 -> block 3 off 3; pos 4 -> block -1 -> skipped.  seq 1: pos 7 -> block 1 off 3
+    tables = np.array([[3, -1], [0, 1]], dtype=np.int32)
+    exp, lens = write_positions(tables, [3, 7], [0, 2, 4], [0, 1], 4)
+    assert exp.tolist()[:3] == [15, -1, 7] and lens.tolist() == [5, 9]
+
+
+def test_cache_writes_refuse_host_tensors():
+    """No host fallback: a view over CPU tensors refuses to write."""
+    view = PageCacheView(key_cache=torch.zeros(4, 4, 1, 2), value_cache=torch.zeros(4, 4, 1, 2),
+                         block_tables=torch.zeros(1, 4, dtype=torch.int32), kv_lens=torch.zeros(1, dtype=torch.int32),
+                         block_size=4, num_kv_heads=1, head_dim=2)
+    with pytest.raises(RuntimeError, match="GPU"):
+        view.concatenate_to_cache(torch.zeros(1, 2, 2), torch.zeros(1, 1, 2), torch.zeros(1, 1, 2),
+                                  cache_metadata=PageMetadata(query_start_loc=[0, 1]), slot_ids=[0])
 
 
 def test_build_query_start_loc():
