@@ -8,6 +8,7 @@ attention-operation plugin interface.
 
 from .caching.paged import AffinePageCacheView, Fp8PageCacheView, PageCacheView, PageMetadata, build_query_start_loc
 from .caching.compiled import CompiledPagedCacheProxy
+from .caching.pagecache import PageCache, PageCacheConfig, validate_cache_dtype
 from .caching.rope import RotaryEmbedding
 from .operations import AttentionOutput, BaseOperation, OperationRegistry, UnifiedAttention, paged_attention
 from .quantize import affine_quantize
@@ -19,6 +20,8 @@ __all__ = (
     "CompiledPagedCacheProxy",
     "Fp8PageCacheView",
     "OperationRegistry",
+    "PageCache",
+    "PageCacheConfig",
     "PageCacheView",
     "PageMetadata",
     "RotaryEmbedding",
@@ -26,4 +29,5 @@ __all__ = (
     "affine_quantize",
     "build_query_start_loc",
     "paged_attention",
+    "validate_cache_dtype",
 )

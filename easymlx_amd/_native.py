@@ -41,6 +41,8 @@ SIGNATURES: dict[str, tuple] = {
     "emx_rope_rows": (_I, [_P, _I, _I, _I, _P, _P, _I, _I, _P]),
     "emx_cache_slots": (_I, [_P, _P, _I, _I, _P, _I, _I, _I, _P, _P, _P, _P]),
     "emx_dense_cache_write": (_I, [_P, _P, _I, _P, _I, _I, _I, _I, _I, _P, _P, _P]),
+    "emx_copy_blocks": (_I, [_I, _P, _P, _I, _P, _I, _P]),
+    "emx_zero_blocks": (_I, [_I, _P, _P, _I, _P, _I, _P]),
     "emx_paged_workspace_bytes": (_SZ, [_I, _I, _I, _I, _I, _I]),
     "emx_paged_prefill_workspace_bytes": (_SZ, [_I, _I, _I, _I, _I]),
     "emx_paged_attention_affine": (

@@ -70,6 +70,29 @@ def build_query_start_loc(query_lens: tp.Iterable[int], device=None) -> torch.Te
     return torch.tensor(offsets, dtype=torch.int32, device=device)
 
 
+def _torch_float_dtype(dtype) -> torch.dtype:
+    """``dtype`` as a torch float dtype; names as the reference maps them (``cache.py:758-773``), else fp16."""
+    if isinstance(dtype, torch.dtype):
+        return dtype
+    names = {"float16": torch.float16, "bfloat16": torch.bfloat16, "float32": torch.float32}
+    return names.get(str(dtype).replace("torch.", ""), torch.float16)
+
+
+def block_mapping_on_device(block_mapping, device) -> torch.Tensor:
+    """``[num_pairs, 2]`` (src, dst) rows as an int32 device tensor; host data is checked not to chain copies
+    (a destination that is also a source would read a block the same call overwrites)."""
+    on_device = isinstance(block_mapping, torch.Tensor) and block_mapping.is_cuda
+    m = block_mapping if isinstance(block_mapping, torch.Tensor) else torch.as_tensor(block_mapping)
+    if m.ndim != 2 or m.shape[1] != 2:
+        raise ValueError("block_mapping must be rank-2 with shape [num_pairs, 2]")
+    if not on_device and m.shape[0]:
+        pairs = [(int(a), int(b)) for a, b in m.tolist() if int(a) != int(b)]
+        srcs = {a for a, _ in pairs}
+        if any(b in srcs for _, b in pairs):
+            raise ValueError("block_mapping chains copies: a destination block is also a source")
+    return m.to(device=device, dtype=torch.int32).contiguous()
+
+
 def _stream_ptr(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
@@ -108,9 +131,33 @@ class PageCacheView:
         num_kv_heads: int,
         head_dim: int,
         block_size: int = 16,
-        dtype: torch.dtype = torch.float16,
+        dtype: torch.dtype | str = torch.float16,
+        cache_dtype: str | None = None,
+        cache_bits: int | None = None,
+        group_size: int = 64,
         device: tp.Any = "cuda",
     ) -> "PageCacheView":
+        """Allocate a zero-initialised cache (``cache.py:700-825``).
+
+        ``cache_dtype`` selects the storage as the reference's does: ``None`` /
+        ``"auto"`` / a float name stores ``dtype``; ``"fp8"`` an
+        :class:`Fp8PageCacheView`; ``"affine4"`` / ``"affine8"`` an
+        :class:`AffinePageCacheView` (this build's affine modes, ``group_size``
+        per quantization group).  TurboQuant modes are outside this build.
+        """
+        from .pagecache import resolve_cache_dtype
+
+        kind, bits = resolve_cache_dtype(cache_dtype, cache_bits)
+        if cls is PageCacheView and kind == "fp8":
+            return Fp8PageCacheView.init(num_seqs=num_seqs, max_seq_len=max_seq_len, num_kv_heads=num_kv_heads,
+                                         head_dim=head_dim, block_size=block_size, device=device)
+        if cls is PageCacheView and kind == "affine":
+            return AffinePageCacheView.init(num_seqs=num_seqs, max_seq_len=max_seq_len, num_kv_heads=num_kv_heads,
+                                            head_dim=head_dim, block_size=block_size, bits=bits,
+                                            group_size=group_size, device=device)
+        if kind == "float" and cache_dtype not in (None, "auto"):
+            dtype = cache_dtype
+        dtype = _torch_float_dtype(dtype)
         if num_seqs <= 0:
             raise ValueError("num_seqs must be positive")
         if max_seq_len <= 0:
@@ -325,18 +372,64 @@ class PageCacheView:
             self._write(key.to(self.block_tables.device).contiguous(), value.to(self.block_tables.device).contiguous(),
                         slot_mapping)
 
+    # -- page lifecycle (cache.py:874-972; runner model_runner.py:1058-1094), on the device
+    def page_arrays(self) -> list[torch.Tensor]:
+        """Every array of the cache indexed by block first (codes, then scales / biases where present)."""
+        return [self.key_cache, self.value_cache]
+
+    def _page_call(self, fn, ids: torch.Tensor, count: int) -> None:
+        import ctypes
+
+        arrays = self.page_arrays()
+        for t in arrays:
+            if not t.is_cuda or not t.is_contiguous() or int(t.shape[0]) != self.num_blocks:
+                raise RuntimeError("page arrays must be contiguous device tensors with num_blocks rows")
+        ptrs = (ctypes.c_void_p * len(arrays))(*[t.data_ptr() for t in arrays])
+        sizes = (ctypes.c_int64 * len(arrays))(*[t[0].numel() * t.element_size() for t in arrays])
+        _native.check(fn(len(arrays), ptrs, sizes, self.num_blocks, ids.data_ptr(), count,
+                         _stream_ptr(arrays[0].device)))
+
+    def zero_pages(self, page_ids) -> None:
+        """Zero the given pages of every array (the runner's ``_zero_pages``, ``model_runner.py:1058-1094``).
+
+        ``page_ids``: host ints or a device int32 tensor; ids outside ``[0, num_blocks)`` are skipped."""
+        ids = torch.as_tensor(page_ids, dtype=torch.int32).reshape(-1).to(self.key_cache.device).contiguous()
+        if ids.numel():
+            self._page_call(_native.load().emx_zero_blocks, ids, int(ids.numel()))
+
+    def copy_blocks(self, block_mapping) -> None:
+        """Copy-on-write block copies (``cache.py:944-972``): rows ``(src, dst)`` of ``[num_pairs, 2]``.
+
+        Host mappings are checked not to chain (a destination that is also a
+        source); a device tensor is used as given."""
+        m = block_mapping_on_device(block_mapping, self.key_cache.device)
+        if m.shape[0]:
+            self._page_call(_native.load().emx_copy_blocks, m, int(m.shape[0]))
+
     def reset(self, seq_idx: int) -> None:
-        """Zero one sequence's pages and its length (``cache.py:874-906``, with page ids used correctly)."""
+        """Zero one sequence's pages and its length (``cache.py:874-906``, pages addressed by id)."""
         if seq_idx < 0 or seq_idx >= self.num_seqs:
             raise IndexError(f"Invalid seq_idx {seq_idx}")
-        ids = self.block_tables[seq_idx]
-        ids = ids[(ids >= 0) & (ids < self.num_blocks)].to(torch.long)
-        self._zero_blocks(ids)
+        self.zero_pages(self.block_tables[seq_idx])  # invalid ids (-1) are skipped by the kernel
         self.kv_lens[seq_idx] = 0
 
-    def _zero_blocks(self, ids: torch.Tensor) -> None:
-        self.key_cache[ids] = 0
-        self.value_cache[ids] = 0
+    def reset_batch(self, seq_indices) -> None:
+        """``cache.py:908-915``."""
+        for seq_idx in seq_indices:
+            self.reset(int(seq_idx))
+
+    def clear(self, seq_idx: int | None = None) -> None:
+        """Zero the whole cache and every length, or one sequence (``cache.py:917-933``)."""
+        if seq_idx is not None:
+            self.reset(int(seq_idx))
+            return
+        for t in self.page_arrays():
+            t.zero_()
+        self.kv_lens.zero_()
+
+    def clear_many(self, seq_indices) -> None:
+        """``cache.py:935-942``."""
+        self.reset_batch(seq_indices)
 
 
 class Fp8PageCacheView(PageCacheView):
@@ -442,10 +535,9 @@ class Fp8PageCacheView(PageCacheView):
         if keys.shape[0]:
             self._write(keys, values, slot_mapping)
 
-    def _zero_blocks(self, ids: torch.Tensor) -> None:
-        super()._zero_blocks(ids)
-        self.k_scales[ids] = 0
-        self.v_scales[ids] = 0
+    def page_arrays(self) -> list[torch.Tensor]:
+        # the per-page scales travel with their pages (zeroed pages restart from scale 0)
+        return [self.key_cache, self.value_cache, self.k_scales, self.v_scales]
 
 
 class AffinePageCacheView(PageCacheView):
@@ -597,9 +689,8 @@ class AffinePageCacheView(PageCacheView):
         return self._concatenate_rope_fused(queries, keys, values, cache_metadata, rope, slot_ids, query_lens, write,
                                             rot_multiple=2, writes_queries=True)
 
-    def _zero_blocks(self, ids: torch.Tensor) -> None:
-        for t in (self.key_cache, self.value_cache, self.k_scales, self.k_biases, self.v_scales, self.v_biases):
-            t[ids] = 0
+    def page_arrays(self) -> list[torch.Tensor]:
+        return [self.key_cache, self.value_cache, self.k_scales, self.k_biases, self.v_scales, self.v_biases]
 
 
 def affine_pool(

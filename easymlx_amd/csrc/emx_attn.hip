@@ -18,6 +18,7 @@
 #include "fp8.hpp"
 #include "decode_fp8.hpp"
 #include "slots.hpp"
+#include "pages.hpp"
 
 constexpr int kNoallocScratchFloats = 2 * emx::kFp8Parts;  // 2 KiB
 
@@ -414,6 +415,48 @@ int emx_dense_cache_write(const void* keys, const void* values, int dtype, const
                      num_tokens, (int)(row_bytes / 4), page_size, num_blocks, reinterpret_cast<uint32_t*>(key_cache),
                      reinterpret_cast<uint32_t*>(value_cache));
   return check_launch("dense_cache_write");
+}
+
+static int page_arrays(int num_arrays, void* const* arrays, const int64_t* block_bytes, int num_blocks,
+                       emx::PageArrays& pa) {
+  if (num_arrays <= 0 || num_arrays > emx::kMaxPageArrays)
+    return fail(EMX_ERR_INVALID, "num_arrays must be in [1, %d]", emx::kMaxPageArrays);
+  if (num_blocks <= 0) return fail(EMX_ERR_INVALID, "num_blocks must be positive");
+  if (!arrays || !block_bytes) return fail(EMX_ERR_INVALID, "null pointer");
+  pa.n = num_arrays;
+  pa.nb = num_blocks;
+  for (int k = 0; k < num_arrays; ++k) {
+    if (!arrays[k] || block_bytes[k] <= 0 || block_bytes[k] % 4 || (reinterpret_cast<uintptr_t>(arrays[k]) & 3))
+      return fail(EMX_ERR_INVALID, "array %d: null, unaligned or a block of %lld bytes (need a positive multiple of 4)",
+                  k, (long long)block_bytes[k]);
+    pa.base[k] = arrays[k];
+    pa.block_bytes[k] = block_bytes[k];
+  }
+  return EMX_OK;
+}
+
+int emx_copy_blocks(int num_arrays, void* const* arrays, const int64_t* block_bytes, int num_blocks,
+                    const int32_t* block_mapping, int num_pairs, void* stream) {
+  if (num_pairs < 0) return fail(EMX_ERR_INVALID, "num_pairs must be >= 0");
+  emx::PageArrays pa{};
+  if (int rc = page_arrays(num_arrays, arrays, block_bytes, num_blocks, pa)) return rc;
+  if (num_pairs == 0) return EMX_OK;
+  if (!block_mapping) return fail(EMX_ERR_INVALID, "null block_mapping");
+  hipLaunchKernelGGL(emx::copy_blocks, dim3((unsigned)num_pairs, (unsigned)num_arrays), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), pa, block_mapping);
+  return check_launch("copy_blocks");
+}
+
+int emx_zero_blocks(int num_arrays, void* const* arrays, const int64_t* block_bytes, int num_blocks,
+                    const int32_t* page_ids, int num_pages, void* stream) {
+  if (num_pages < 0) return fail(EMX_ERR_INVALID, "num_pages must be >= 0");
+  emx::PageArrays pa{};
+  if (int rc = page_arrays(num_arrays, arrays, block_bytes, num_blocks, pa)) return rc;
+  if (num_pages == 0) return EMX_OK;
+  if (!page_ids) return fail(EMX_ERR_INVALID, "null page_ids");
+  hipLaunchKernelGGL(emx::zero_blocks, dim3((unsigned)num_pages, (unsigned)num_arrays), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), pa, page_ids);
+  return check_launch("zero_blocks");
 }
 
 int emx_rope_rows(void* x, int rows, int heads, int head_dim, const int32_t* positions, const float* inv_freq,

@@ -119,6 +119,30 @@ int emx_dense_cache_write(const void* keys, const void* values, int dtype, const
                           void* key_cache, void* value_cache, void* stream);
 
 /*
+ * Copy-on-write block copies over every array of a cache: arrays[k] holds
+ * num_blocks blocks of block_bytes[k] bytes each (a positive multiple of 4;
+ * host arrays of num_arrays <= 8 entries, e.g. codes, scales and biases of K
+ * and V).  For each row (src, dst) of block_mapping int32 [num_pairs, 2] on the
+ * device, block dst of every array becomes a copy of block src; ids outside
+ * [0, num_blocks) are skipped.  No destination may also be a source of another
+ * pair in the same call (copy-on-write mappings never chain).
+ * Replaces PageCacheView.copy_blocks / PageCache.copy_blocks
+ *   lib/python/easymlx/caching/paged/cache.py:944-972, 1438-1445 (Metal kernel :95-136).
+ */
+int emx_copy_blocks(int num_arrays, void* const* arrays, const int64_t* block_bytes, int num_blocks,
+                    const int32_t* block_mapping, int num_pairs, void* stream);
+
+/*
+ * Zero the blocks page_ids int32 [num_pages] (device) of every array of a cache
+ * (same array description as emx_copy_blocks; ids outside [0, num_blocks) skipped).
+ * Replaces the runner's _zero_pages
+ *   lib/python/easymlx/inference/esurge/runners/model_runner.py:1058-1094 and the page
+ *   zeroing of PageCacheView.reset lib/python/easymlx/caching/paged/cache.py:874-906.
+ */
+int emx_zero_blocks(int num_arrays, void* const* arrays, const int64_t* block_bytes, int num_blocks,
+                    const int32_t* page_ids, int num_pages, void* stream);
+
+/*
  * Rotary position embedding in place on fp16 rows x [rows, heads, head_dim]
  * (row r at positions[r]), the same rotation as emx_affine_cache_write_rope.
  * Replaces the RoPE applied to queries in concatenate_to_cache

@@ -10,7 +10,10 @@ Restates ``PageCacheView.concatenate_to_cache``
   (``:1155``, ``:1254``), block ``block_tables[slot, pos // bs]``, in-block
   offset ``pos % bs`` (``:1168-1169``, ``:1256-1257``);
 * the flat ``slot_mapping = block * bs + offset`` (``:1259``);
-* afterwards ``kv_lens[slot] += q_len`` (``:1199``, ``:1297``).
+* afterwards ``kv_lens[slot] += q_len`` (``:1199``, ``:1297``);
+* page lifecycle: copy-on-write block copies (``:944-972``) and the runner's
+  page zeroing (``model_runner.py:1058-1094``), both over every array of a
+  cache.
 """
 
 from __future__ import annotations
@@ -51,3 +54,24 @@ def write_positions(block_tables, kv_lens, query_start_loc, slot_ids, block_size
                 slot_mapping[start + j] = block * block_size + pos % block_size
         kv[slot] = base + max(0, end - start)
     return slot_mapping, kv
+
+
+def copy_blocks(arrays, block_mapping):
+    """Copy-on-write block copies (``cache.py:944-972``, Metal kernel ``:95-136``), in place on numpy arrays
+    indexed by block first: for each row ``(src, dst)``, block ``dst`` of every array becomes block ``src`` as it
+    was before the call (the kernel reads its input arrays).  Ids outside ``[0, num_blocks)`` are skipped."""
+    before = [np.array(a, copy=True) for a in arrays]
+    for src, dst in np.asarray(block_mapping).reshape(-1, 2).tolist():
+        for a, b in zip(arrays, before):
+            nb = a.shape[0]
+            if 0 <= src < nb and 0 <= dst < nb:
+                a[dst] = b[src]
+
+
+def zero_pages(arrays, page_ids):
+    """The runner's ``_zero_pages`` (``model_runner.py:1058-1094``): the listed pages of every array become zero;
+    negative ids (and ids past the pool) are skipped."""
+    for a in arrays:
+        for p in np.asarray(page_ids).reshape(-1).tolist():
+            if 0 <= p < a.shape[0]:
+                a[p] = 0

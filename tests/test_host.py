@@ -273,3 +273,53 @@ def test_bench_refuses_more_than_one_gpu():
     r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True, text=True,
                        timeout=60)
     assert r.returncode == 2 and "one GPU" in r.stdout
+
+
+# ---------------------------------------------------------------- page lifecycle (host side)
+def test_oracle_copy_and_zero_known_answers():
+    from oracle.cache_write import copy_blocks, zero_pages
+
+    a = np.arange(5 * 3, dtype=np.int32).reshape(5, 3)
+    b = np.arange(5 * 2, dtype=np.float32).reshape(5, 2) + 100
+    copy_blocks([a, b], [[0, 4], [2, 1], [7, 3], [3, 3]])  # (7, 3) skipped: past the pool; (3, 3) a no-op
+    assert a.tolist() == [[0, 1, 2], [6, 7, 8], [6, 7, 8], [9, 10, 11], [0, 1, 2]]
+    assert b[4].tolist() == [100, 101] and b[1].tolist() == [104, 105]
+    # reads come from the arrays as they were: swapping two blocks in one call
+    c = np.array([[1], [2]])
+    copy_blocks([c], [[0, 1], [1, 0]])
+    assert c.ravel().tolist() == [2, 1]
+    zero_pages([a, b], [1, -1, 9, 4])
+    assert a[1].tolist() == [0, 0, 0] and a[4].tolist() == [0, 0, 0] and a[2].tolist() == [6, 7, 8]
+    assert b[1].tolist() == [0, 0] and b[0].tolist() == [100, 101]
+
+
+def test_cache_dtype_validation_and_config():
+    from easymlx_amd.caching.pagecache import CacheConfigError, PageCacheConfig, resolve_cache_dtype, validate_cache_dtype
+
+    for ok in (None, "auto", "float16", "bfloat16", "float32", "fp8", "affine4", "affine8"):
+        validate_cache_dtype(ok)
+    for bad in ("int4", "fp16", "affine2", "q4"):
+        with pytest.raises(CacheConfigError, match="Unsupported cache_dtype"):
+            validate_cache_dtype(bad)
+    with pytest.raises(CacheConfigError, match="TurboQuant"):
+        validate_cache_dtype("turboquant3")
+    with pytest.raises(CacheConfigError, match="contradicts"):
+        validate_cache_dtype("affine4", cache_bits=8)
+    assert resolve_cache_dtype("affine8") == ("affine", 8)
+    assert resolve_cache_dtype("fp8") == ("fp8", None)
+    assert resolve_cache_dtype(None) == ("float", None)
+    cfg = PageCacheConfig.create(num_hidden_layers=2, num_kv_heads=8, head_dim=128, page_size=128, max_num_reqs=3,
+                                 max_model_length=1000, cache_dtype="affine4")
+    assert cfg.num_pages == 8 * 3  # ceil(1000 / 128) pages per request (cache.py:1358-1362)
+    with pytest.raises(CacheConfigError):
+        PageCacheConfig(num_hidden_layers=1, num_kv_heads=1, head_dim=64, cache_dtype="int8")
+
+
+def test_block_mapping_checks():
+    from easymlx_amd.caching.paged import block_mapping_on_device
+
+    with pytest.raises(ValueError, match="rank-2"):
+        block_mapping_on_device([1, 2, 3], "cpu")
+    with pytest.raises(ValueError, match="chains"):
+        block_mapping_on_device([[0, 1], [1, 2]], "cpu")
+    assert block_mapping_on_device([[0, 1], [2, 3], [4, 4]], "cpu").dtype == torch.int32
