@@ -406,6 +406,40 @@ class PageCacheView:
         if m.shape[0]:
             self._page_call(_native.load().emx_copy_blocks, m, int(m.shape[0]))
 
+    def gather_kv_cache(self, block_table, cu_seq_lens, *, out_dtype: torch.dtype | None = None):
+        """Dense ``(k, v)`` ``[total_tokens, Hkv, D]`` of a ragged batch from the pages (``cache.py:974-1027``).
+
+        Token ``t`` of sequence ``b`` (``cu_seq_lens[b] <= t < cu_seq_lens[b+1]``)
+        is entry ``j % block_size`` of page ``block_table[b, j // block_size]``,
+        ``j = t - cu_seq_lens[b]``.  ``out_dtype`` defaults to the cache dtype
+        for unquantized caches and to fp16 for FP8 / affine pages, which are
+        returned dequantized (the reference gathers its unquantized packed copy)."""
+        dev = self.key_cache.device
+        bt = torch.as_tensor(block_table).to(device=dev, dtype=torch.int32).contiguous()
+        cu = torch.as_tensor(cu_seq_lens).to(device=dev, dtype=torch.int32).contiguous()
+        if bt.ndim != 2 or cu.ndim != 1 or cu.shape[0] != bt.shape[0] + 1:
+            raise ValueError("block_table must be [num_seqs, max_blocks] and cu_seq_lens [num_seqs + 1]")
+        total = int(cu[-1].item())  # the output size, as the reference reads it (cache.py:1000-1002)
+        if out_dtype is None:
+            out_dtype = self.key_cache.dtype if self.key_cache.dtype.is_floating_point else torch.float16
+        codes = {torch.float16: _native.DTYPE_F16, torch.bfloat16: _native.DTYPE_BF16, torch.float32: _native.DTYPE_F32}
+        if out_dtype not in codes:
+            raise NotImplementedError(f"gather_kv_cache returns fp16/bf16/fp32, not {out_dtype}")
+        k_out = torch.empty((total, self.num_kv_heads, self.head_dim), dtype=out_dtype, device=dev)
+        v_out = torch.empty_like(k_out)
+        if total:
+            self._gather(bt, cu, total, codes[out_dtype], k_out, v_out)
+        return k_out, v_out
+
+    def _gather(self, bt, cu, total, out_code, k_out, v_out):
+        codes = {torch.float16: _native.DTYPE_F16, torch.bfloat16: _native.DTYPE_BF16, torch.float32: _native.DTYPE_F32}
+        if self.key_cache.dtype not in codes:
+            raise NotImplementedError(f"no gather for a {self.key_cache.dtype} cache")
+        _native.check(_native.load().emx_gather_kv_dense(
+            self.key_cache.data_ptr(), self.value_cache.data_ptr(), codes[self.key_cache.dtype], self.num_blocks,
+            self.block_size, self.num_kv_heads, self.head_dim, bt.data_ptr(), int(bt.shape[0]), int(bt.shape[1]),
+            cu.data_ptr(), total, out_code, k_out.data_ptr(), v_out.data_ptr(), _stream_ptr(k_out.device)))
+
     def reset(self, seq_idx: int) -> None:
         """Zero one sequence's pages and its length (``cache.py:874-906``, pages addressed by id)."""
         if seq_idx < 0 or seq_idx >= self.num_seqs:
@@ -538,6 +572,13 @@ class Fp8PageCacheView(PageCacheView):
     def page_arrays(self) -> list[torch.Tensor]:
         # the per-page scales travel with their pages (zeroed pages restart from scale 0)
         return [self.key_cache, self.value_cache, self.k_scales, self.v_scales]
+
+    def _gather(self, bt, cu, total, out_code, k_out, v_out):
+        _native.check(_native.load().emx_gather_kv_fp8(
+            self.key_cache.data_ptr(), self.value_cache.data_ptr(), self.k_scales.data_ptr(), self.v_scales.data_ptr(),
+            self.num_blocks, self.block_size, self.num_kv_heads, self.head_dim, bt.data_ptr(), int(bt.shape[0]),
+            int(bt.shape[1]), cu.data_ptr(), total, out_code, k_out.data_ptr(), v_out.data_ptr(),
+            _stream_ptr(k_out.device)))
 
 
 class AffinePageCacheView(PageCacheView):
@@ -691,6 +732,13 @@ class AffinePageCacheView(PageCacheView):
 
     def page_arrays(self) -> list[torch.Tensor]:
         return [self.key_cache, self.value_cache, self.k_scales, self.k_biases, self.v_scales, self.v_biases]
+
+    def _gather(self, bt, cu, total, out_code, k_out, v_out):
+        _native.check(_native.load().emx_gather_kv_affine(
+            self.key_cache.data_ptr(), self.k_scales.data_ptr(), self.k_biases.data_ptr(), self.value_cache.data_ptr(),
+            self.v_scales.data_ptr(), self.v_biases.data_ptr(), self.num_blocks, self.block_size, self.num_kv_heads,
+            self.head_dim, self.bits, self.group_size, bt.data_ptr(), int(bt.shape[0]), int(bt.shape[1]),
+            cu.data_ptr(), total, out_code, k_out.data_ptr(), v_out.data_ptr(), _stream_ptr(k_out.device)))
 
 
 def affine_pool(

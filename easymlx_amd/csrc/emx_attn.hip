@@ -249,6 +249,34 @@ void* noalloc_scratch() {
   return g_scratch_ptr[dev];
 }
 
+template <typename KV>
+int launch_gather(const KV& kv, const int32_t* block_table, int num_seqs, int max_blocks,
+                         const int32_t* cu_seq_lens, int total_tokens, int num_blocks, int out_dtype, void* k_out,
+                         void* v_out, void* stream) {
+  if (num_seqs <= 0 || max_blocks <= 0 || total_tokens < 0 || num_blocks <= 0)
+    return fail(EMX_ERR_INVALID, "num_seqs, max_blocks and num_blocks must be positive, total_tokens >= 0");
+  if (total_tokens == 0) return EMX_OK;
+  if (!block_table || !cu_seq_lens || !k_out || !v_out) return fail(EMX_ERR_INVALID, "null pointer");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const dim3 grid((unsigned)total_tokens);
+  switch (out_dtype) {
+    case EMX_DTYPE_F16:
+      hipLaunchKernelGGL((emx::gather_kv<emx::F16, KV>), grid, dim3(256), 0, st, kv, block_table, cu_seq_lens,
+                         num_seqs, max_blocks, total_tokens, num_blocks, k_out, v_out);
+      break;
+    case EMX_DTYPE_BF16:
+      hipLaunchKernelGGL((emx::gather_kv<emx::BF16, KV>), grid, dim3(256), 0, st, kv, block_table, cu_seq_lens,
+                         num_seqs, max_blocks, total_tokens, num_blocks, k_out, v_out);
+      break;
+    case EMX_DTYPE_F32:
+      hipLaunchKernelGGL((emx::gather_kv<emx::F32, KV>), grid, dim3(256), 0, st, kv, block_table, cu_seq_lens,
+                         num_seqs, max_blocks, total_tokens, num_blocks, k_out, v_out);
+      break;
+    default: return fail(EMX_ERR_INVALID, "unknown out_dtype %d", out_dtype);
+  }
+  return check_launch("gather_kv");
+}
+
 }  // namespace
 
 extern "C" {
@@ -457,6 +485,72 @@ int emx_zero_blocks(int num_arrays, void* const* arrays, const int64_t* block_by
   hipLaunchKernelGGL(emx::zero_blocks, dim3((unsigned)num_pages, (unsigned)num_arrays), dim3(256), 0,
                      reinterpret_cast<hipStream_t>(stream), pa, page_ids);
   return check_launch("zero_blocks");
+}
+
+int emx_gather_kv_affine(const uint32_t* k_codes, const void* k_scales, const void* k_biases, const uint32_t* v_codes,
+                         const void* v_scales, const void* v_biases, int num_blocks, int page_size, int num_kv_heads,
+                         int head_dim, int bits, int group_size, const int32_t* block_table, int num_seqs,
+                         int max_blocks_per_seq, const int32_t* cu_seq_lens, int total_tokens, int out_dtype,
+                         void* k_out, void* v_out, void* stream) {
+  if (bits != 4 && bits != 8) return fail(EMX_ERR_UNSUPPORTED, "bits must be 4 or 8, got %d", bits);
+  if (num_kv_heads <= 0 || head_dim <= 0 || page_size <= 0 || group_size <= 0 || head_dim % group_size ||
+      (head_dim * bits) % 32 || (page_size * bits) % 32 || (page_size > 256 / bits && page_size % (256 / bits)))
+    return fail(EMX_ERR_INVALID, "affine page geometry (head_dim %d, group_size %d, page_size %d, bits %d)", head_dim,
+                group_size, page_size, bits);
+  if (total_tokens > 0 && (!k_codes || !k_scales || !k_biases || !v_codes || !v_scales || !v_biases))
+    return fail(EMX_ERR_INVALID, "null cache pointer");
+  const emx::h16 *ks = reinterpret_cast<const emx::h16*>(k_scales), *kb = reinterpret_cast<const emx::h16*>(k_biases);
+  const emx::h16 *vs = reinterpret_cast<const emx::h16*>(v_scales), *vb = reinterpret_cast<const emx::h16*>(v_biases);
+  if (bits == 4)
+    return launch_gather(emx::AffineKV<4>{k_codes, ks, kb, v_codes, vs, vb, num_kv_heads, head_dim, page_size,
+                                          group_size},
+                         block_table, num_seqs, max_blocks_per_seq, cu_seq_lens, total_tokens, num_blocks, out_dtype,
+                         k_out, v_out, stream);
+  return launch_gather(emx::AffineKV<8>{k_codes, ks, kb, v_codes, vs, vb, num_kv_heads, head_dim, page_size,
+                                        group_size},
+                       block_table, num_seqs, max_blocks_per_seq, cu_seq_lens, total_tokens, num_blocks, out_dtype,
+                       k_out, v_out, stream);
+}
+
+int emx_gather_kv_fp8(const uint8_t* key_cache, const uint8_t* value_cache, const float* k_scale,
+                      const float* v_scale, int num_blocks, int page_size, int num_kv_heads, int head_dim,
+                      const int32_t* block_table, int num_seqs, int max_blocks_per_seq, const int32_t* cu_seq_lens,
+                      int total_tokens, int out_dtype, void* k_out, void* v_out, void* stream) {
+  if (num_kv_heads <= 0 || head_dim <= 0 || page_size <= 0) return fail(EMX_ERR_INVALID, "bad cache geometry");
+  if (total_tokens > 0 && (!key_cache || !value_cache || !k_scale || !v_scale))
+    return fail(EMX_ERR_INVALID, "null cache pointer");
+  return launch_gather(emx::Fp8KV{key_cache, value_cache, k_scale, v_scale, num_kv_heads, head_dim, page_size},
+                       block_table, num_seqs, max_blocks_per_seq, cu_seq_lens, total_tokens, num_blocks, out_dtype,
+                       k_out, v_out, stream);
+}
+
+int emx_gather_kv_dense(const void* key_cache, const void* value_cache, int dtype, int num_blocks, int page_size,
+                        int num_kv_heads, int head_dim, const int32_t* block_table, int num_seqs,
+                        int max_blocks_per_seq, const int32_t* cu_seq_lens, int total_tokens, int out_dtype,
+                        void* k_out, void* v_out, void* stream) {
+  if (num_kv_heads <= 0 || head_dim <= 0 || page_size <= 0) return fail(EMX_ERR_INVALID, "bad cache geometry");
+  if (total_tokens > 0 && (!key_cache || !value_cache)) return fail(EMX_ERR_INVALID, "null cache pointer");
+  switch (dtype) {
+    case EMX_DTYPE_F16:
+      return launch_gather(emx::DenseKV<emx::F16>{reinterpret_cast<const emx::h16*>(key_cache),
+                                                  reinterpret_cast<const emx::h16*>(value_cache), num_kv_heads,
+                                                  head_dim, page_size},
+                           block_table, num_seqs, max_blocks_per_seq, cu_seq_lens, total_tokens, num_blocks,
+                           out_dtype, k_out, v_out, stream);
+    case EMX_DTYPE_BF16:
+      return launch_gather(emx::DenseKV<emx::BF16>{reinterpret_cast<const uint16_t*>(key_cache),
+                                                   reinterpret_cast<const uint16_t*>(value_cache), num_kv_heads,
+                                                   head_dim, page_size},
+                           block_table, num_seqs, max_blocks_per_seq, cu_seq_lens, total_tokens, num_blocks,
+                           out_dtype, k_out, v_out, stream);
+    case EMX_DTYPE_F32:
+      return launch_gather(emx::DenseKV<emx::F32>{reinterpret_cast<const float*>(key_cache),
+                                                  reinterpret_cast<const float*>(value_cache), num_kv_heads,
+                                                  head_dim, page_size},
+                           block_table, num_seqs, max_blocks_per_seq, cu_seq_lens, total_tokens, num_blocks,
+                           out_dtype, k_out, v_out, stream);
+  }
+  return fail(EMX_ERR_INVALID, "unknown dtype %d", dtype);
 }
 
 int emx_rope_rows(void* x, int rows, int heads, int head_dim, const int32_t* positions, const float* inv_freq,

@@ -218,3 +218,39 @@ __global__ __launch_bounds__(64) void paged_generic(GenericArgs a, KV kv) {
 }
 
 }  // namespace emx
+
+namespace emx {
+
+// Dense K/V of a ragged batch from pages (PageCacheView.gather_kv_cache,
+// lib/python/easymlx/caching/paged/cache.py:974-1027; Metal kernel :138-193):
+// token t of sequence b (cu[b] <= t < cu[b+1]) at offset j = t - cu[b] is
+// entry j % bs of page block_table[b, j / bs]; out [T, Hkv, D] in the output
+// dtype, through the cache's loader (affine / FP8 dequantized in fp32, dense
+// cast).  A page id outside [0, nb) or a column beyond the table yields zeros.
+// One workgroup per token.
+template <typename OutTag, typename KV>
+__global__ __launch_bounds__(256) void gather_kv(KV kv, const int32_t* block_table, const int32_t* cu, int S,
+                                                 int max_blocks, int T, int nb, void* k_out, void* v_out) {
+  typedef typename OutTag::T OT;
+  const int t = blockIdx.x;
+  if (t >= T) return;
+  int lo = 0, hi = S;  // the b with cu[b] <= t < cu[b + 1]
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (cu[mid] <= t) lo = mid; else hi = mid;
+  }
+  const int j = t - cu[lo];
+  const int col = j / kv.bs;
+  const int blk = col < max_blocks ? block_table[(size_t)lo * max_blocks + col] : -1;
+  const bool ok = blk >= 0 && blk < nb;
+  const int n = kv.Hkv * kv.D;
+  OT* ko = reinterpret_cast<OT*>(k_out) + (size_t)t * n;
+  OT* vo = reinterpret_cast<OT*>(v_out) + (size_t)t * n;
+  for (int e = threadIdx.x; e < n; e += 256) {
+    const int h = e / kv.D, d = e % kv.D;
+    from_f32(ok ? kv.key(blk, j % kv.bs, h, d) : 0.f, ko + e);
+    from_f32(ok ? kv.val(blk, j % kv.bs, h, d) : 0.f, vo + e);
+  }
+}
+
+}  // namespace emx

@@ -143,6 +143,31 @@ int emx_zero_blocks(int num_arrays, void* const* arrays, const int64_t* block_by
                     const int32_t* page_ids, int num_pages, void* stream);
 
 /*
+ * Dense K/V of a ragged batch gathered from pages: token t of sequence b
+ * (cu_seq_lens[b] <= t < cu_seq_lens[b+1], int32 [num_seqs+1] on the device) at
+ * offset j = t - cu_seq_lens[b] is entry j % page_size of page
+ * block_table[b, j / page_size]; k_out/v_out [total_tokens, Hkv, head_dim] in
+ * out_dtype (EMX_DTYPE_*).  Affine pages are dequantized (scale * code + bias
+ * in fp32), FP8 pages decoded times their page scale, dense pages cast.  A page
+ * id outside [0, num_blocks) or a column beyond the table yields zeros.
+ * Replaces PageCacheView.gather_kv_cache
+ *   lib/python/easymlx/caching/paged/cache.py:974-1027 (Metal kernel :138-193).
+ */
+int emx_gather_kv_affine(const uint32_t* k_codes, const void* k_scales, const void* k_biases, const uint32_t* v_codes,
+                         const void* v_scales, const void* v_biases, int num_blocks, int page_size, int num_kv_heads,
+                         int head_dim, int bits, int group_size, const int32_t* block_table, int num_seqs,
+                         int max_blocks_per_seq, const int32_t* cu_seq_lens, int total_tokens, int out_dtype,
+                         void* k_out, void* v_out, void* stream);
+int emx_gather_kv_fp8(const uint8_t* key_cache, const uint8_t* value_cache, const float* k_scale,
+                      const float* v_scale, int num_blocks, int page_size, int num_kv_heads, int head_dim,
+                      const int32_t* block_table, int num_seqs, int max_blocks_per_seq, const int32_t* cu_seq_lens,
+                      int total_tokens, int out_dtype, void* k_out, void* v_out, void* stream);
+int emx_gather_kv_dense(const void* key_cache, const void* value_cache, int dtype, int num_blocks, int page_size,
+                        int num_kv_heads, int head_dim, const int32_t* block_table, int num_seqs,
+                        int max_blocks_per_seq, const int32_t* cu_seq_lens, int total_tokens, int out_dtype,
+                        void* k_out, void* v_out, void* stream);
+
+/*
  * Rotary position embedding in place on fp16 rows x [rows, heads, head_dim]
  * (row r at positions[r]), the same rotation as emx_affine_cache_write_rope.
  * Replaces the RoPE applied to queries in concatenate_to_cache

@@ -123,3 +123,43 @@ def test_attention_over_copied_pages(cuda, kind):
     torch.cuda.synchronize()
     assert torch.isfinite(out).all() and out.abs().sum() > 0
     assert torch.equal(out[0], out[1])
+
+
+@pytest.mark.parametrize("kind", ["dense", "fp8", "affine4", "affine8"])
+def test_gather_kv_cache_matches_oracle(cuda, kind):
+    """gather_kv_cache (cache.py:974-1027) against the oracle's dequantized logical pages."""
+    from oracle.affine import affine_dequantize
+    from oracle.fp8 import fp8_dequant_cache
+    from tests.helpers import gpu_pages_to_logical
+
+    print(f"[gather {kind}]", flush=True)
+    rng = np.random.default_rng(11)
+    view = _filled(kind, cuda, rng)
+    S, bs = view.num_seqs, view.block_size
+    lens = [200, 0, 256, 37]
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    bt = view.block_tables.cpu().numpy().copy()
+    bt[3, 0] = -1  # an unassigned page gathers zeros
+    k, v = view.gather_kv_cache(torch.from_numpy(bt), torch.from_numpy(cu), out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    if kind == "dense":
+        lk, lv = view.key_cache.float().cpu().numpy(), view.value_cache.float().cpu().numpy()
+    elif kind == "fp8":
+        lk = fp8_dequant_cache(view.key_cache.cpu().numpy(), view.k_scales.cpu().numpy())
+        lv = fp8_dequant_cache(view.value_cache.cpu().numpy(), view.v_scales.cpu().numpy())
+    else:
+        pages = gpu_pages_to_logical(view)
+        lk = affine_dequantize(*pages["k"], view.group_size, view.bits, round_to_fp16=False)
+        lv = affine_dequantize(*pages["v"], view.group_size, view.bits, round_to_fp16=False)
+    exp_k = np.zeros((cu[-1],) + lk.shape[2:], np.float32)
+    exp_v = np.zeros_like(exp_k)
+    for b in range(S):
+        for j in range(lens[b]):
+            blk = bt[b, j // bs]
+            if blk >= 0:
+                exp_k[cu[b] + j] = lk[blk, j % bs]
+                exp_v[cu[b] + j] = lv[blk, j % bs]
+    np.testing.assert_array_equal(k.cpu().numpy(), exp_k)
+    np.testing.assert_array_equal(v.cpu().numpy(), exp_v)
+    assert view.gather_kv_cache(torch.from_numpy(bt), torch.from_numpy(cu))[0].dtype == (
+        torch.float16 if kind != "dense" else view.key_cache.dtype)
