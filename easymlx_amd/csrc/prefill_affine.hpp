@@ -64,6 +64,7 @@ struct PrefillArgs {
 };
 
 constexpr int kPrefillParts = 3;          // most parts a tile is split into
+constexpr float kLazyMax = 8.f;           // growth of a column's maximum (log2 units) that triggers a rescale
 constexpr int kPrefillSplitKeys = 512;    // keys per part the split aims at (c3: 768 -> 121.5, 512 -> 111.7, 384 -> 117.6 us)
 constexpr int kPrefillPartVec = 17;       // f32x4 per lane of a stored state: acc[2][8], (m0, m1, l0, l1)
 constexpr int kPrefillPartBytes = 4 * kPrefillPartVec * 64 * 16;  // one part of one workgroup
@@ -461,41 +462,47 @@ __global__ __launch_bounds__(256, 2) void prefill_affine_d128(PrefillArgs a) {
 #pragma unroll
           for (int r = 0; r < 4; ++r) tmax = fmaxf(tmax, sc[ct][t][r]);
         tmax = rows4_max(tmax);
+        // The reference maximum m_run moves only when a score passes it by more than
+        // kLazyMax (log2 units), so the accumulator is rescaled rarely; p <= 2^kLazyMax
+        // otherwise, well inside fp16.  The result does not depend on the reference.
         const float m_new = fmaxf(m_run[ct], tmax * sc_l2);
-        if (m_new == -INFINITY) {  // nothing visible yet for this column
+        const bool grow = m_new > m_run[ct] + kLazyMax;  // also the first finite maximum
+        if (__any(grow)) {
+          const float m_ref = grow ? m_new : m_run[ct];
+          const float alpha = grow ? __builtin_amdgcn_exp2f(m_run[ct] - m_ref) : 1.f;
+          l_part[ct] *= alpha;
 #pragma unroll
-          for (int t = 0; t < 2; ++t)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) sc[ct][t][r] = 0.f;
-        } else {
-          if (__any(m_new != m_run[ct])) {
-            const float alpha = __builtin_amdgcn_exp2f(m_run[ct] - m_new);
-            l_part[ct] *= alpha;
-#pragma unroll
-            for (int dt = 0; dt < 8; ++dt) acc[ct][dt] *= alpha;
-            m_run[ct] = m_new;
-          }
-#pragma unroll
-          for (int t = 0; t < 2; ++t)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const float p = __builtin_amdgcn_exp2f(fmaf(sc[ct][t][r], sc_l2, -m_run[ct]));
-              sc[ct][t][r] = p;
-              l_part[ct] += p;
-            }
+          for (int dt = 0; dt < 8; ++dt) acc[ct][dt] *= alpha;
+          m_run[ct] = m_ref;
         }
+        // nothing visible yet (m_run = -inf): every score is -inf and p = 0
+        const float m_sub = fmaxf(m_run[ct], -3.0e38f);
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float p = __builtin_amdgcn_exp2f(fmaf(sc[ct][t][r], sc_l2, -m_sub));
+            sc[ct][t][r] = p;
+            l_part[ct] += p;
+          }
       }
 
       // ---- O^T += V^T P^T over the half's 32 keys: lane (col, jj) holds keys
       // 32h + 4jj + r (sub-tile 2h) and 32h + 16 + 4jj + r (sub-tile 2h + 1)
       h16x8 pB[2];
 #pragma unroll
-      for (int ct = 0; ct < 2; ++ct)
+      for (int ct = 0; ct < 2; ++ct) {
+        typedef float f32x2v __attribute__((ext_vector_type(2)));
+        typedef h16 h16x2v __attribute__((ext_vector_type(2)));
+        uint32_t pw[4];  // pairs converted together (v_cvt_pk_f16_f32)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          pB[ct][r] = (h16)sc[ct][0][r];
-          pB[ct][4 + r] = (h16)sc[ct][1][r];
-        }
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int r = 0; r < 4; r += 2)
+            pw[2 * t + r / 2] = __builtin_bit_cast(
+                uint32_t, __builtin_convertvector(f32x2v{sc[ct][t][r], sc[ct][t][r + 1]}, h16x2v));
+        pB[ct] = __builtin_bit_cast(h16x8, u32x4{pw[0], pw[1], pw[2], pw[3]});
+      }
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) {
         const h16x8 Av = *reinterpret_cast<const h16x8*>(ve + (16 * dt + col) * P::VSTR + 32 * h + 8 * jj);
