@@ -184,4 +184,18 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+constexpr int kRsrcFlags = 0x00020000;  // raw 32-bit buffer, gfx9 family
+constexpr int kLoadAux = 0;             // default cache policy
+
+// Raw buffer descriptor of `bytes` bytes at p, built from wave-uniform values
+// moved to SGPRs (a descriptor the compiler keeps in VGPRs makes it wrap every
+// load through it in a per-lane loop).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t uniform_rsrc(const void* p, const int bytes) {
+  const uint64_t x = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)x);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(x >> 32));
+  return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(((uint64_t)hi << 32) | lo), (short)0,
+                                           __builtin_amdgcn_readfirstlane(bytes), kRsrcFlags);
+}
+
 }  // namespace emx

@@ -315,29 +315,36 @@ __global__ __launch_bounds__(256) void affine_cache_write_small(WriteArgs a) {
   const float n_bins = (float)((1 << BITS) - 1);
   __shared__ float sp[2][kSmallWrite][2];  // [K|V][token] -> (scale, bias) of this block's group
   __shared__ __attribute__((aligned(16))) h16 sgrp[2][kSmallWrite][kSmallMaxGroup];  // group values
-  __shared__ int sslot[kSmallWrite];
+  __shared__ __attribute__((aligned(16))) int sslot[kSmallWrite];
   __shared__ int salone[kSmallWrite];
-  for (int t = tid; t < T; t += 256) {
-    int sl = a.slot_mapping[t];
-    if (sl >= 0 && sl / a.bs >= a.nb) sl = -1;
-    sslot[t] = sl;
-  }
-  __syncthreads();
-  for (int t = tid; t < T; t += 256) {  // alone: no other token of the call in the same 32/BITS-token word
-    const int sl = sslot[t];
-    bool alone = true;
-    for (int u = 0; u < T && sl >= 0; ++u)
-      if (u != t && sslot[u] >= 0 && sslot[u] / PW == sl / PW) alone = false;
-    salone[t] = alone;
-  }
-  // the quantization group holding this dim block, for every token: one cooperative load
+  // One round trip for what the workgroup reads: the tokens' slots and the
+  // quantization group holding this dim block (neither depends on the other).
+  // Every load is issued unconditionally (buffer loads: an offset past the end
+  // returns zeros), so none waits behind a branch for the one before it.
   const int g = d0 / a.gs;
+  constexpr int kOob = 0x7FFFFFF0;  // past the end of every descriptor below
+  const int sl_raw = (int)__builtin_amdgcn_raw_buffer_load_b32(uniform_rsrc(a.slot_mapping, T * 4),
+                                                               tid < T ? tid * 4 : kOob, 0, kLoadAux);
+  const int sl_in = tid < T ? sl_raw : -1;
+  constexpr int kPieces = 2 * kSmallWrite * (kSmallMaxGroup / 8) / 256;  // 16-byte pieces per thread
+  const int per_tok = a.gs / 8;
+  const int row_bytes = T * a.Hkv * a.D * 2;
+  const __amdgpu_buffer_rsrc_t rkey = uniform_rsrc(a.keys, row_bytes), rval = uniform_rsrc(a.values, row_bytes);
+  // byte offset of piece c of token t's group (this head)
+  auto goff = [&](int t, int c) { return ((t * a.Hkv + h) * a.D + g * a.gs + 8 * c) * 2; };
+  u32x4 piece[kPieces];
   if constexpr (ROPE) {
     __shared__ __attribute__((aligned(16))) h16 krow[kSmallWrite][kWriteMaxDim];
     for (int i = tid; i < T * (a.D / 8); i += 256) {
       const int t = i / (a.D / 8), c = i % (a.D / 8);
       *reinterpret_cast<u32x4*>(&krow[t][8 * c]) =
           *reinterpret_cast<const u32x4*>(a.keys + ((size_t)t * a.Hkv + h) * a.D + 8 * c);
+    }
+#pragma unroll
+    for (int k = 0; k < kPieces / 2; ++k) {  // V only: K comes from the turned rows
+      const int i = tid + 256 * k;
+      piece[k] = __builtin_amdgcn_raw_buffer_load_b128(rval, i < T * per_tok ? goff(i / per_tok, i % per_tok) : kOob,
+                                                       0, kLoadAux);
     }
     __syncthreads();
     const RopeArgs& r = a.rope;
@@ -348,18 +355,65 @@ __global__ __launch_bounds__(256) void affine_cache_write_small(WriteArgs a) {
       rope_pair(krow[t][i0], krow[t][i1], (float)r.positions[t] * r.inv_freq[p]);
     }
     __syncthreads();
-    for (int i = tid; i < T * (a.gs / 8); i += 256) {
-      const int t = i / (a.gs / 8), c = i % (a.gs / 8);
+    for (int i = tid; i < T * per_tok; i += 256) {
+      const int t = i / per_tok, c = i % per_tok;
       *reinterpret_cast<u32x4*>(&sgrp[0][t][8 * c]) = *reinterpret_cast<const u32x4*>(&krow[t][g * a.gs + 8 * c]);
     }
+#pragma unroll
+    for (int k = 0; k < kPieces / 2; ++k) {
+      const int i = tid + 256 * k;
+      if (i < T * per_tok) *reinterpret_cast<u32x4*>(&sgrp[1][i / per_tok][8 * (i % per_tok)]) = piece[k];
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < kPieces; ++k) {  // pieces of K first, then of V (a piece index is uniform in kv per k
+      const int i = tid + 256 * k;      // only when T * per_tok is a multiple of 256, so both are issued)
+      const int r = i % (T * per_tok);
+      const int off = i < 2 * T * per_tok ? goff(r / per_tok, r % per_tok) : kOob;
+      const u32x4 pk = __builtin_amdgcn_raw_buffer_load_b128(rkey, i < T * per_tok ? off : kOob, 0, kLoadAux);
+      const u32x4 pv = __builtin_amdgcn_raw_buffer_load_b128(rval, i >= T * per_tok ? off : kOob, 0, kLoadAux);
+      piece[k] = pk | pv;  // one of the two is zeros
+    }
+#pragma unroll
+    for (int k = 0; k < kPieces; ++k) {
+      const int i = tid + 256 * k;
+      if (i < 2 * T * per_tok) {
+        const int kv = i / (T * per_tok), r = i % (T * per_tok);
+        *reinterpret_cast<u32x4*>(&sgrp[kv][r / per_tok][8 * (r % per_tok)]) = piece[k];
+      }
+    }
   }
-  for (int i = tid; i < (ROPE ? 1 : 2) * T * (a.gs / 8); i += 256) {
-    const int kv = ROPE ? 1 : i / (T * (a.gs / 8)), r = i % (T * (a.gs / 8));
-    const int t = r / (a.gs / 8), c = r % (a.gs / 8);
-    const h16* src = (kv ? a.values : a.keys) + ((size_t)t * a.Hkv + h) * a.D + (size_t)g * a.gs + 8 * c;
-    *reinterpret_cast<u32x4*>(&sgrp[kv][t][8 * c]) = *reinterpret_cast<const u32x4*>(src);
-  }
+  if (tid < T) sslot[tid] = sl_in >= 0 && sl_in / a.bs >= a.nb ? -1 : sl_in;  // page out of range: not written
   __syncthreads();
+  // The value words this thread updates, read now so that the read-modify-write
+  // at the end does not wait for them (4-bit: a word holds 8 tokens of one dim).
+  constexpr int kVTasks = kSmallWrite * DB / 256;
+  uint32_t vword[kVTasks];
+  if constexpr (BITS == 4) {
+#pragma unroll
+    for (int k = 0; k < kVTasks; ++k) {  // (an unused task reads word 0 of the pool)
+      const int task = tid + 256 * k;
+      const int t = min(task / DB, kSmallWrite - 1), d = d0 + task % DB;
+      const int sl = task < T * DB ? sslot[t] : -1;
+      const size_t ph = (size_t)(max(sl, 0) / a.bs) * a.Hkv + h;
+      vword[k] = a.vc[sl >= 0 ? v_word_index<BITS>(ph, sl % a.bs, d, a.D, a.bs) : 0];
+    }
+  }
+  // alone: no other token of the call in the same 32/BITS-token value word
+  if (tid < T) {
+    const int sl = sslot[tid];
+    bool alone = true;
+    if (sl >= 0) {
+      for (int u0 = 0; u0 < T; u0 += 4) {
+        const int4 w = *reinterpret_cast<const int4*>(&sslot[u0]);
+        const int wu[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          if (u0 + k < T && u0 + k != tid && wu[k] >= 0 && wu[k] / PW == sl / PW) alone = false;
+      }
+    }
+    salone[tid] = alone;
+  }
   // scale / bias (the first dim block of each group stores them)
   for (int task = tid; task < 2 * T; task += 256) {
     const int kv = task / T, t = task % T;
@@ -391,7 +445,10 @@ __global__ __launch_bounds__(256) void affine_cache_write_small(WriteArgs a) {
     a.kc[(ph * a.bs + sl % a.bs) * (a.D / PW) + w] = word;
   }
   // V codes: one value per (token, dim)
-  for (int task = tid; task < T * DB; task += 256) {
+#pragma unroll
+  for (int k = 0; k < kVTasks; ++k) {
+    const int task = tid + 256 * k;
+    if (task >= T * DB) continue;
     const int t = task / DB, d = d0 + task % DB;
     const int sl = sslot[t];
     if (sl < 0) continue;
@@ -404,7 +461,7 @@ __global__ __launch_bounds__(256) void affine_cache_write_small(WriteArgs a) {
     if (BITS == 8) {
       reinterpret_cast<uint8_t*>(wp)[sl % 4] = (uint8_t)code;
     } else if (salone[t]) {
-      *wp = (*wp & ~(M << sh)) | (code << sh);  // the word's only writer in this call
+      *wp = (vword[k] & ~(M << sh)) | (code << sh);  // the word's only writer in this call
     } else {
       atomicAnd(wp, ~(M << sh));
       atomicOr(wp, code << sh);
