@@ -213,7 +213,18 @@ class PageCacheView:
         for q in qlens:
             qsl.append(qsl[-1] + max(0, int(q)))
         total = qsl[-1]
-        meta = torch.tensor(list(slot_ids) + qsl, dtype=torch.int32, device=dev)
+        # the device copy of (slot ids, offsets) is kept per distinct call shape: every
+        # layer of a step (and most steps) writes the same slots, and a host-to-device
+        # copy from pageable memory waits for the stream
+        key = (tuple(slot_ids), tuple(qsl))
+        meta = self._meta_cache.get(key) if hasattr(self, "_meta_cache") else None
+        if meta is None:
+            if not hasattr(self, "_meta_cache"):
+                self._meta_cache = {}
+            if len(self._meta_cache) >= 64:
+                self._meta_cache.pop(next(iter(self._meta_cache)))
+            meta = torch.tensor(list(slot_ids) + qsl, dtype=torch.int32, device=dev)
+            self._meta_cache[key] = meta
         slots, qsl_d = meta[:n], meta[n:]
         mapping = torch.empty((total,), dtype=torch.int32, device=dev)
         positions = torch.empty((total,), dtype=torch.int32, device=dev)
@@ -315,16 +326,21 @@ class PageCacheView:
         queries, keys = self._apply_rope(rope, queries, keys, positions, qsl, qlens, single)
         if slot_mapping.numel():
             self._write(keys.contiguous(), values.contiguous(), slot_mapping)
-        return queries, self.key_cache, self.value_cache, self._resolved(cache_metadata, slots, single)
+        return queries, self.key_cache, self.value_cache, self._resolved(cache_metadata, slots, single, slot_ids)
 
-    def _resolved(self, cache_metadata, slots, single):
-        """Metadata with this cache's tables and lengths for the written slots (``cache.py:1297-1305``)."""
+    def _resolved(self, cache_metadata, slots, single, slot_ids=None):
+        """Metadata with this cache's tables and lengths for the written slots (``cache.py:1297-1305``).
+
+        A call that writes every sequence in order gets the cache's own ``block_tables`` and
+        ``kv_lens`` (no copies): a later write to this cache advances the lengths the returned
+        metadata holds, so use it for this layer-step's attention, as the runner does."""
         n = int(slots.shape[0])
-        md = cache_metadata.with_cache_state(
-            block_tables=self.block_tables.index_select(0, slots) if n else self.block_tables[:0],
-            kv_lens=self.kv_lens.index_select(0, slots) if n else self.kv_lens[:0],
-            block_size=self.block_size,
-        )
+        if slot_ids is not None and n == self.num_seqs and tuple(slot_ids) == tuple(range(n)):
+            tables, lens = self.block_tables, self.kv_lens
+        else:
+            tables = self.block_tables.index_select(0, slots) if n else self.block_tables[:0]
+            lens = self.kv_lens.index_select(0, slots) if n else self.kv_lens[:0]
+        md = cache_metadata.with_cache_state(block_tables=tables, kv_lens=lens, block_size=self.block_size)
         md.is_single_token_decode = single
         return md
 
@@ -351,7 +367,7 @@ class PageCacheView:
                                                 positions.data_ptr(), inv.data_ptr(), rope.dims,
                                                 int(rope.traditional), stream))
             _native.check(write(keys, values, slot_mapping, positions, inv, rope, stream, q_out))
-        return q_out, self.key_cache, self.value_cache, self._resolved(cache_metadata, slots, single)
+        return q_out, self.key_cache, self.value_cache, self._resolved(cache_metadata, slots, single, slot_ids)
 
     def append(self, seq_idx: int, key: torch.Tensor, value: torch.Tensor) -> None:
         """Append ``[num_tokens, Hkv, D]`` tokens to one sequence (``cache.py:834-872``)."""
