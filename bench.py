@@ -44,6 +44,8 @@ def parse():
     p.add_argument("--pool-gib", type=float, default=1.5, help="total size of the rotated page pools")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-aux", action="store_true", help="skip the c3 / c4 / quantize-on-write measurements")
+    p.add_argument("--aux-only", choices=("c3", "c4", "write", "op", "fp8"),
+                   help="run one auxiliary measurement alone and print its JSON (for profiler runs)")
     p.add_argument("--cpu-seqs", type=int, default=0, help="sequences in the CPU baseline sample (0 = auto)")
     p.add_argument("--copy-probe-mib", type=int, default=0,
                    help="after the timed region, run 5 plain device copies of this size (counter calibration)")
@@ -515,6 +517,11 @@ def main():
     from easymlx_amd.workloads import config
 
     dev = torch.device("cuda", 0)
+    if args.aux_only:
+        fn = {"c3": aux_c3, "c4": aux_c4, "write": aux_quantize_on_write, "op": aux_op_layer_step,
+              "fp8": aux_fp8}[args.aux_only]
+        print(json.dumps({args.aux_only: fn(dev)}))
+        return
     wl = config("c2")
     bytes_per_step = wl.kv_bytes()
     st = Setup(wl, args.pool_gib, dev)
