@@ -200,7 +200,9 @@ __global__ __launch_bounds__(256, 2) void prefill_affine_d128(PrefillArgs a) {
   // ---- query operands: MFMA w spans dims [32w, 32w + 32); lane group jj holds dims
   // 32w + 8jj + i in the element order of the expanded keys (unpack4 / unpack8 order)
   h16x8 qB[2][4];
-  float qs[2][G];  // per-group sum of the query, in the 2^-24 units of the MFMA output
+  // B operand of the bias MFMA: lane group 0 holds the query's per-group sums, each
+  // as fp16 hi + lo (x = hi + lo to ~22 bits), k-elements 2g, 2g + 1; the other lanes 0
+  h16x8 qbias[2];
 #pragma unroll
   for (int ct = 0; ct < 2; ++ct) {
     const h16* qp = a.q + ((size_t)(q0 + (cvalid[ct] ? ctok[ct] : 0)) * a.Hq + (size_t)kvh * HG + chead[ct]) * D;
@@ -215,12 +217,18 @@ __global__ __launch_bounds__(256, 2) void prefill_affine_d128(PrefillArgs a) {
         gs[(32 * w) / GS] += (float)v;
       }
     }
+    qbias[ct] = h16x8{(h16)0.f, (h16)0.f, (h16)0.f, (h16)0.f, (h16)0.f, (h16)0.f, (h16)0.f, (h16)0.f};
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       float x = gs[g];
       x += __shfl_xor(x, 16, 64);
       x += __shfl_xor(x, 32, 64);
-      qs[ct][g] = x * (1.0f / kTwo24);
+      const h16 hi = (h16)x;
+      const h16 lo = (h16)(x - (float)hi);
+      if (jj == 0) {
+        qbias[ct][2 * g] = hi;
+        qbias[ct][2 * g + 1] = lo;
+      }
     }
   }
 
@@ -229,7 +237,8 @@ __global__ __launch_bounds__(256, 2) void prefill_affine_d128(PrefillArgs a) {
   __shared__ __attribute__((aligned(16))) h16 raw_s[4 * G * NT];   // [arr][g][NT]
   __shared__ __attribute__((aligned(16))) h16 ke[NT * P::KSTR];    // [key][dims, unpack order]
   __shared__ __attribute__((aligned(16))) h16 ve[D * P::VSTR];     // [dim][keys, pv_slot order]
-  __shared__ __attribute__((aligned(16))) float ksf[2][G][NT];    // k_scale, k_bias in fp32
+  __shared__ __attribute__((aligned(16))) float ksf[G][NT];       // k_scale * 2^24 in fp32
+  __shared__ __attribute__((aligned(16))) h16x8 kbe[NT];          // A operand of the bias MFMA: kb_g at 2g, 2g + 1
 
   // Cooperative load of one step into registers: thread owns one 16-byte piece of K and of V,
   // and (threads < SEGS * SEGB / 16) one piece of the scales.
@@ -298,11 +307,8 @@ __global__ __launch_bounds__(256, 2) void prefill_affine_d128(PrefillArgs a) {
                     e4m3x2_to_h16x2(__builtin_amdgcn_perm(0u, w[2 * e + 1], 0x0C010C00u)),
                     e4m3x2_to_h16x2(__builtin_amdgcn_perm(0u, w[2 * e + 1], 0x0C030C02u)));
       }
-      // scores keep the affine formula: key scale = page scale * 2^8 * 2^-24, biases 0
-      if (tid < NT) {
-        ksf[0][0][tid] = psk * (256.0f / kTwo24);
-        ksf[1][0][tid] = 0.f;
-      }
+      // scores keep the affine formula: key scale = page scale * 2^8 (codes are value * 2^-8), biases 0
+      if (tid < NT) ksf[0][tid] = psk * 256.0f;
       vsc = psv;
       reinterpret_cast<u32x4*>(raw_v)[tid] = rv;  // [64 keys][128 bytes]
       reinterpret_cast<u32x4*>(raw_v)[256 + tid] = rv2;
@@ -380,8 +386,15 @@ __global__ __launch_bounds__(256, 2) void prefill_affine_d128(PrefillArgs a) {
       }
       *reinterpret_cast<u32x2*>(vd + pv_slot(kk)) = u32x2{o[0], o[1]};
     }
-    // K scales / biases of the step in fp32
-    for (int i = tid; i < 2 * G * NT; i += 256) ksf[i / (G * NT)][(i / NT) % G][i % NT] = (float)raw_s[i];
+    // K scales of the step in fp32, times 2^24 (the codes enter the MFMA as code * 2^-24), and
+    // the K biases as the bias MFMA's A rows
+    for (int i = tid; i < G * NT; i += 256) ksf[i / NT][i % NT] = (float)raw_s[i] * kTwo24;
+    if (tid < NT) {
+      h16x8 b = {(h16)0.f, (h16)0.f, (h16)0.f, (h16)0.f, (h16)0.f, (h16)0.f, (h16)0.f, (h16)0.f};
+#pragma unroll
+      for (int g = 0; g < G; ++g) b[2 * g] = b[2 * g + 1] = raw_s[(G + g) * NT + tid];
+      kbe[tid] = b;
+    }
   };
 
   float m_run[2] = {-INFINITY, -INFINITY}, l_part[2] = {0.f, 0.f};
@@ -390,7 +403,7 @@ __global__ __launch_bounds__(256, 2) void prefill_affine_d128(PrefillArgs a) {
   for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc[ct][i] = f32x4{0.f, 0.f, 0.f, 0.f};
-  const float sc_l2 = a.scale_log2 * kTwo24;
+  const float sc_l2 = a.scale_log2;  // the scores come out in natural units
 
   if (step_lo <= step_hi) load_step(step_lo);
   for (int st = step_lo; st <= step_hi; ++st) {
@@ -424,13 +437,19 @@ __global__ __launch_bounds__(256, 2) void prefill_affine_d128(PrefillArgs a) {
             const h16x8 A = *reinterpret_cast<const h16x8*>(kr + 32 * w);
             cg[(32 * w) / GS] = mfma16x16x32(A, qB[ct][w], cg[(32 * w) / GS]);
           }
-          float v[4] = {0.f, 0.f, 0.f, 0.f};
+          // bias term sum_g kb[t,g] * sum_{d in g} q_d on the matrix core (FP8: no biases)
+          f32x4 cb = {0.f, 0.f, 0.f, 0.f};
+          if constexpr (!FP8) {
+            const h16x8 zero8 = {(h16)0.f, (h16)0.f, (h16)0.f, (h16)0.f, (h16)0.f, (h16)0.f, (h16)0.f, (h16)0.f};
+            const h16x8 Ab = jj == 0 ? kbe[16 * at + col] : zero8;
+            cb = mfma16x16x32(Ab, qbias[ct], cb);
+          }
+          float v[4] = {cb[0], cb[1], cb[2], cb[3]};
 #pragma unroll
           for (int g = 0; g < G; ++g) {
-            const f32x4 ks4 = *reinterpret_cast<const f32x4*>(&ksf[0][g][16 * at + 4 * jj]);
-            const f32x4 kb4 = *reinterpret_cast<const f32x4*>(&ksf[1][g][16 * at + 4 * jj]);
+            const f32x4 ks4 = *reinterpret_cast<const f32x4*>(&ksf[g][16 * at + 4 * jj]);
 #pragma unroll
-            for (int r = 0; r < 4; ++r) v[r] = fmaf(cg[g][r], ks4[r], fmaf(kb4[r], qs[ct][g], v[r]));
+            for (int r = 0; r < 4; ++r) v[r] = fmaf(cg[g][r], ks4[r], v[r]);
           }
 #pragma unroll
           for (int r = 0; r < 4; ++r) sc[ct][t][r] = v[r];
