@@ -749,6 +749,49 @@ class AffinePageCacheView(PageCacheView):
     def page_arrays(self) -> list[torch.Tensor]:
         return [self.key_cache, self.value_cache, self.k_scales, self.k_biases, self.v_scales, self.v_biases]
 
+    @classmethod
+    def from_logical(cls, *, k_codes, k_scales, k_biases, v_codes, v_scales, v_biases, block_tables, kv_lens, bits,
+                     group_size) -> "AffinePageCacheView":
+        """A view over pages converted on the device from the logical layout (``emx_affine_pages_from_logical``):
+        codes ``[nb, bs, Hkv, D*bits/32]`` (int32/uint32 words), scales/biases ``[nb, bs, Hkv, D/group_size]``
+        fp16 -- ``mlx.core.quantize`` of the reference's dense cache ``[nb, bs, Hkv, D]`` (``cache.py:790-791``)."""
+        dev = k_codes.device
+        if dev.type != "cuda":
+            raise RuntimeError("layout conversion runs on the GPU only")
+        nb, bs, hkv, w = (int(x) for x in k_codes.shape)
+        d = w * 32 // int(bits)
+        G = d // int(group_size)
+        for name, t, shape in (("v_codes", v_codes, (nb, bs, hkv, w)), ("k_scales", k_scales, (nb, bs, hkv, G)),
+                               ("k_biases", k_biases, (nb, bs, hkv, G)), ("v_scales", v_scales, (nb, bs, hkv, G)),
+                               ("v_biases", v_biases, (nb, bs, hkv, G))):
+            if tuple(t.shape) != shape:
+                raise ValueError(f"{name} must be {list(shape)} in the logical layout, got {list(t.shape)}")
+        view = affine_pool(num_blocks=nb, num_kv_heads=hkv, head_dim=d, block_size=bs, bits=int(bits),
+                           group_size=int(group_size), block_tables=block_tables.to(dev), kv_lens=kv_lens.to(dev))
+        src = [x.contiguous() for x in (k_codes, v_codes)]
+        par = [x.to(torch.float16).contiguous() for x in (k_scales, k_biases, v_scales, v_biases)]
+        _native.check(_native.load().emx_affine_pages_from_logical(
+            src[0].data_ptr(), src[1].data_ptr(), *(x.data_ptr() for x in par), nb, bs, hkv, d, int(bits),
+            int(group_size), view.key_cache.data_ptr(), view.value_cache.data_ptr(), view.k_scales.data_ptr(),
+            view.k_biases.data_ptr(), view.v_scales.data_ptr(), view.v_biases.data_ptr(), _stream_ptr(dev)))
+        return view
+
+    def to_logical(self) -> dict[str, torch.Tensor]:
+        """The pages in the logical layout (device tensors; ``emx_affine_logical_from_pages``)."""
+        nb, hkv, bs, d = self.num_blocks, self.num_kv_heads, self.block_size, self.head_dim
+        w, G = d * self.bits // 32, d // self.group_size
+        dev = self.key_cache.device
+        out = {"k_codes": torch.empty((nb, bs, hkv, w), dtype=torch.int32, device=dev),
+               "v_codes": torch.empty((nb, bs, hkv, w), dtype=torch.int32, device=dev)}
+        for n in ("k_scales", "k_biases", "v_scales", "v_biases"):
+            out[n] = torch.empty((nb, bs, hkv, G), dtype=torch.float16, device=dev)
+        _native.check(_native.load().emx_affine_logical_from_pages(
+            self.key_cache.data_ptr(), self.value_cache.data_ptr(), self.k_scales.data_ptr(),
+            self.k_biases.data_ptr(), self.v_scales.data_ptr(), self.v_biases.data_ptr(), nb, bs, hkv, d, self.bits,
+            self.group_size, out["k_codes"].data_ptr(), out["v_codes"].data_ptr(), out["k_scales"].data_ptr(),
+            out["k_biases"].data_ptr(), out["v_scales"].data_ptr(), out["v_biases"].data_ptr(), _stream_ptr(dev)))
+        return out
+
     def _gather(self, bt, cu, total, out_code, k_out, v_out):
         _native.check(_native.load().emx_gather_kv_affine(
             self.key_cache.data_ptr(), self.k_scales.data_ptr(), self.k_biases.data_ptr(), self.value_cache.data_ptr(),

@@ -487,6 +487,70 @@ int emx_zero_blocks(int num_arrays, void* const* arrays, const int64_t* block_by
   return check_launch("zero_blocks");
 }
 
+namespace {
+
+int convert_layout(bool to_pages, const uint32_t* kc, const uint32_t* vc, const void* const (&sc)[4], int num_blocks,
+                   int page_size, int num_kv_heads, int head_dim, int bits, int group_size, uint32_t* kd,
+                   uint32_t* vd, void* const (&sd)[4], void* stream) {
+  if (bits != 4 && bits != 8) return fail(EMX_ERR_UNSUPPORTED, "bits must be 4 or 8, got %d", bits);
+  if (num_blocks < 0 || num_kv_heads <= 0 || head_dim <= 0 || page_size <= 0 || group_size <= 0 ||
+      head_dim % group_size || (head_dim * bits) % 32 || (page_size * bits) % 32 ||
+      (page_size > 256 / bits && page_size % (256 / bits)))
+    return fail(EMX_ERR_INVALID, "affine page geometry (head_dim %d, group_size %d, page_size %d, bits %d)", head_dim,
+                group_size, page_size, bits);
+  if (num_blocks == 0) return EMX_OK;
+  if (!kc || !vc || !kd || !vd) return fail(EMX_ERR_INVALID, "null codes pointer");
+  emx::LayoutArgs a;
+  a.sk = kc;
+  a.sv = vc;
+  a.dk = kd;
+  a.dv = vd;
+  for (int i = 0; i < 4; ++i) {
+    if (!sc[i] || !sd[i]) return fail(EMX_ERR_INVALID, "null scale / bias pointer");
+    a.ss[i] = static_cast<const emx::h16*>(sc[i]);
+    a.ds[i] = static_cast<emx::h16*>(sd[i]);
+  }
+  a.nb = num_blocks;
+  a.bs = page_size;
+  a.Hkv = num_kv_heads;
+  a.D = head_dim;
+  a.gs = group_size;
+  const long words = (long)num_blocks * num_kv_heads * page_size * head_dim * bits / 32;
+  const unsigned grid = (unsigned)std::min<long>((words + 255) / 256, 8192);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (to_pages)
+    hipLaunchKernelGGL(bits == 4 ? emx::pages_from_logical<4> : emx::pages_from_logical<8>, dim3(grid), dim3(256), 0,
+                       st, a);
+  else
+    hipLaunchKernelGGL(bits == 4 ? emx::logical_from_pages<4> : emx::logical_from_pages<8>, dim3(grid), dim3(256), 0,
+                       st, a);
+  return check_launch(to_pages ? "pages_from_logical" : "logical_from_pages");
+}
+
+}  // namespace
+
+int emx_affine_pages_from_logical(const uint32_t* k_codes_in, const uint32_t* v_codes_in, const void* k_scales_in,
+                                  const void* k_biases_in, const void* v_scales_in, const void* v_biases_in,
+                                  int num_blocks, int page_size, int num_kv_heads, int head_dim, int bits,
+                                  int group_size, uint32_t* k_codes, uint32_t* v_codes, void* k_scales,
+                                  void* k_biases, void* v_scales, void* v_biases, void* stream) {
+  const void* const src[4] = {k_scales_in, k_biases_in, v_scales_in, v_biases_in};
+  void* const dst[4] = {k_scales, k_biases, v_scales, v_biases};
+  return convert_layout(true, k_codes_in, v_codes_in, src, num_blocks, page_size, num_kv_heads, head_dim, bits,
+                        group_size, k_codes, v_codes, dst, stream);
+}
+
+int emx_affine_logical_from_pages(const uint32_t* k_codes, const uint32_t* v_codes, const void* k_scales,
+                                  const void* k_biases, const void* v_scales, const void* v_biases, int num_blocks,
+                                  int page_size, int num_kv_heads, int head_dim, int bits, int group_size,
+                                  uint32_t* k_codes_out, uint32_t* v_codes_out, void* k_scales_out,
+                                  void* k_biases_out, void* v_scales_out, void* v_biases_out, void* stream) {
+  const void* const src[4] = {k_scales, k_biases, v_scales, v_biases};
+  void* const dst[4] = {k_scales_out, k_biases_out, v_scales_out, v_biases_out};
+  return convert_layout(false, k_codes, v_codes, src, num_blocks, page_size, num_kv_heads, head_dim, bits,
+                        group_size, k_codes_out, v_codes_out, dst, stream);
+}
+
 int emx_gather_kv_affine(const uint32_t* k_codes, const void* k_scales, const void* k_biases, const uint32_t* v_codes,
                          const void* v_scales, const void* v_biases, int num_blocks, int page_size, int num_kv_heads,
                          int head_dim, int bits, int group_size, const int32_t* block_table, int num_seqs,

@@ -143,6 +143,28 @@ int emx_zero_blocks(int num_arrays, void* const* arrays, const int64_t* block_by
                     const int32_t* page_ids, int num_pages, void* stream);
 
 /*
+ * Affine cache layout conversion on the device, both directions (out-of-place;
+ * every destination element written once).  Logical layout: what
+ * mlx.core.quantize gives for the reference's dense cache [nb, bs, Hkv, D]
+ * (lib/python/easymlx/caching/paged/cache.py:790-791; quantize at
+ * lib/python/easymlx/infra/mixins/bridge.py:304,361): codes uint32
+ * [nb, bs, Hkv, D*bits/32], scales / biases fp16 [nb, bs, Hkv, D/group_size].
+ * Page layout: the one emx_paged_attention_affine and the writes use (above).
+ * Lets a caller holding reference-layout affine caches hand them to this
+ * library (and read pages back) without a host round trip.
+ */
+int emx_affine_pages_from_logical(const uint32_t* k_codes_in, const uint32_t* v_codes_in, const void* k_scales_in,
+                                  const void* k_biases_in, const void* v_scales_in, const void* v_biases_in,
+                                  int num_blocks, int page_size, int num_kv_heads, int head_dim, int bits,
+                                  int group_size, uint32_t* k_codes, uint32_t* v_codes, void* k_scales,
+                                  void* k_biases, void* v_scales, void* v_biases, void* stream);
+int emx_affine_logical_from_pages(const uint32_t* k_codes, const uint32_t* v_codes, const void* k_scales,
+                                  const void* k_biases, const void* v_scales, const void* v_biases, int num_blocks,
+                                  int page_size, int num_kv_heads, int head_dim, int bits, int group_size,
+                                  uint32_t* k_codes_out, uint32_t* v_codes_out, void* k_scales_out,
+                                  void* k_biases_out, void* v_scales_out, void* v_biases_out, void* stream);
+
+/*
  * Dense K/V of a ragged batch gathered from pages: token t of sequence b
  * (cu_seq_lens[b] <= t < cu_seq_lens[b+1], int32 [num_seqs+1] on the device) at
  * offset j = t - cu_seq_lens[b] is entry j % page_size of page
