@@ -320,13 +320,6 @@ __global__ __launch_bounds__(256, 2) void decode_q4_d128(DecodeArgs a) {
   __shared__ int qrw[kMaxSeqs];
   __shared__ float so[2][4][4][D];  // two slot sets; per wave: o * 2^24 + bias term of its 4 heads
   __shared__ float sml[2][4][4][2];  // per wave: (m, l) of its 4 heads
-  __shared__ int scnt[2];            // waves arrived at the set's current unit end
-  __shared__ int sgen[2];            // last unit end whose combine on the set completed
-  if (threadIdx.x == 0) {
-    scnt[0] = scnt[1] = 0;
-    sgen[0] = -2;
-    sgen[1] = -1;
-  }
   __shared__ int slast[2];
   // Block tables of up to kTableCache entries are read into LDS together with
   // kv_lens (one memory round trip for both), larger ones from global memory.
@@ -547,20 +540,17 @@ __global__ __launch_bounds__(256, 2) void decode_q4_d128(DecodeArgs a) {
       q4_compute<GS, 1>(cur, full, lane, tb, start_k, kv_len, qB, qs, sc_l2, st);
     }
 
-    // ---- unit finished (or range ends): the waves' (o, m, l) meet in LDS; the last
-    // wave to arrive combines them into the output or the workgroup's partial while
-    // the others go on.  Unit ends alternate between two slot sets; a wave reusing a
-    // set first waits for the combine of two unit ends back (done by a sibling wave
-    // that waits on nothing, so the wait ends).
+    // ---- unit finished (or range ends): the waves' (o, m, l) meet in LDS and, after one
+    // workgroup barrier, all four combine them into the output or the workgroup's
+    // partial.  Unit ends alternate between two slot sets: a set is written again two
+    // unit ends later, after every wave has passed the barrier of the unit end between,
+    // so its reads are done.  (Measured against a last-arriver protocol with an arrival
+    // counter: c2 28.4 -> 27.4 us, batch 128 81.2 -> 78.1 us.)
     if (unit_end) {
       const bool whole = unit_first >= g0 && unit_first + n_s <= g1;
       const int u = s * Hkv + kvh;
       const int par = nue & 1;
       const int row = uru(qrw[s]);
-      if (nue >= 2) {
-        while (__hip_atomic_load(&sgen[par], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < nue - 2)
-          __builtin_amdgcn_s_sleep(1);
-      }
       {
         const float l = head_sum(st[0].l);
         float pbs[2];
@@ -580,12 +570,8 @@ __global__ __launch_bounds__(256, 2) void decode_q4_d128(DecodeArgs a) {
           sml[par][wv][lane][1] = l;
         }
       }
-      int arrived = 0;
-      if (has_next) {
-        if (lane == 0) arrived = __hip_atomic_fetch_add(&scnt[par], 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
-        arrived = __builtin_amdgcn_readfirstlane(arrived);
-      } else {
-        // the range's last unit: every wave is done, so all four combine it together
+      {
+        // every wave has its (o, m, l) of the unit in LDS: all four combine it together
         __syncthreads();
         PieceInfo pi;
         if (!whole) pi = piece_info<HG>(a, wg, u, unit_first, n_s, I, NWG);
@@ -612,53 +598,6 @@ __global__ __launch_bounds__(256, 2) void decode_q4_d128(DecodeArgs a) {
                                                     pi.me * HG * 8, kCoherent);
           }
         }
-      }
-      if (arrived == 3) {  // last of the four waves: combine
-        if (lane == 0) __hip_atomic_store(&scnt[par], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-        PieceInfo pi;
-        if (!whole) pi = piece_info<HG>(a, wg, u, unit_first, n_s, I, NWG);
-        // per-head weights of the slices: lane h (< HG) computes them, every lane reads them back
-        float fw[NSL], Lh = 0.f, Mh = -INFINITY;
-        {
-          const int h = lane < HG ? lane : 0, q = h / 4, i = h % 4;
-#pragma unroll
-          for (int sl = 0; sl < NSL; ++sl) Mh = fmaxf(Mh, sml[par][q + HQ * sl][i][0]);
-#pragma unroll
-          for (int sl = 0; sl < NSL; ++sl) {
-            const float m = sml[par][q + HQ * sl][i][0];
-            fw[sl] = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - Mh);
-            Lh = fmaf(fw[sl], sml[par][q + HQ * sl][i][1], Lh);
-          }
-        }
-#pragma unroll
-        for (int h = 0; h < HG; ++h) {
-          const int q = h / 4, i = h % 4;
-          const float L = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, Lh), h));
-          const float M = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, Mh), h));
-          const float inv = L > 0.f ? 1.f / L : 0.f;
-#pragma unroll
-          for (int c = 0; c < 2; ++c) {
-            const int d = 64 * c + lane;
-            float O = 0.f;
-#pragma unroll
-            for (int sl = 0; sl < NSL; ++sl) {
-              const float f = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, fw[sl]), h));
-              O = fmaf(f, so[par][q + HQ * sl][i][d], O);
-            }
-            if (whole) {
-              a.out[((size_t)row * a.Hq + (size_t)kvh * HG + h) * D + d] = (h16)(O * inv);
-            } else {
-              __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, O), pi.ro, (h * D + d) * 4,
-                                                    pi.me * HG * D * 4, kCoherent);
-            }
-          }
-          if (!whole && lane == 0)
-            __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, f32x2{M, L}), pi.rm, h * 8,
-                                                  pi.me * HG * 8, kCoherent);
-        }
-        // the slot set may be rewritten once every lane's reads above are done
-        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
-        if (lane == 0) __hip_atomic_store(&sgen[par], nue, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
       }
       ++nue;
       if (!whole) {
