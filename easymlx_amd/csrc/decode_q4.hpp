@@ -255,7 +255,7 @@ __device__ __forceinline__ void q4_compute(Q4Loads<GS, HQ>& L, const bool full, 
     float p[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      p[i] = __builtin_amdgcn_exp2f(fmaf(sc[i], sc_l2, -st[hq].m));
+      p[i] = __builtin_amdgcn_exp2f(fmaf(sc[i], sc_l2, -fmaxf(st[hq].m, -3.0e38f)));  // 0 for a dead score
       st[hq].l += p[i];
     }
     // ---- O += P' V, P' = p * v_scale (elements 2, 3 of each quad / 16: their codes enter * 16)
@@ -498,7 +498,13 @@ __global__ __launch_bounds__(256, 2) void decode_q4_d128(DecodeArgs a) {
   long long pend_first[2];
 
   auto step = [&](Q4Loads<GS, 1>& cur, Q4Loads<GS, 1>& nxt, const long long g) {
-    // ---- next item
+    // ---- next item (the state is wave-uniform: scalar registers and branches)
+    s = uru(s);
+    kvh = uru(kvh);
+    j = uru(j);
+    n_s = uru(n_s);
+    kv_len = uru(kv_len);
+    it_lo = uru(it_lo);
     int s1 = s, kvh1 = kvh, j1 = j + 1, n1 = n_s, kl1 = kv_len, lo1 = it_lo;
     if (j1 == n_s) {
       j1 = 0;
@@ -532,12 +538,16 @@ __global__ __launch_bounds__(256, 2) void decode_q4_d128(DecodeArgs a) {
     const TileRsrc rs1 = tile_of(blk1, kvh1, tb1, soff1);
     q4_issue_loads(nxt, rs1, sptr, soff1, (tb1 & 127) / 64, lane, a.bs);
 
-    // ---- compute this wave's slice of the item (skipped when it holds no live
-    // token, or its page is invalid, like the reference's Metal kernel)
-    if ((unsigned)blk < (unsigned)a.nb && tb + 64 > start_k) {
+    // ---- compute this wave's slice of the item.  A slice without a live token or
+    // with an invalid page (skipped by the reference's Metal kernel) is computed
+    // with every token dead, so it adds nothing: a branch around it left the
+    // compiler unable to order this item's loads against the next item's, and
+    // it waited for all of them before issuing the next page loads.
+    {
+      const bool ok = (unsigned)blk < (unsigned)a.nb;
       q4_stage_scales<GS, 1>(cur, sst[wv], lane);
-      const bool full = tb >= start_k && tb + 64 <= kv_len;
-      q4_compute<GS, 1>(cur, full, lane, tb, start_k, kv_len, qB, qs, sc_l2, st);
+      const bool full = ok && tb >= start_k && tb + 64 <= kv_len;
+      q4_compute<GS, 1>(cur, full, lane, tb, start_k, ok ? kv_len : 0, qB, qs, sc_l2, st);
     }
 
     // ---- unit finished (or range ends): the waves' (o, m, l) meet in LDS and, after one
@@ -575,7 +585,12 @@ __global__ __launch_bounds__(256, 2) void decode_q4_d128(DecodeArgs a) {
         __syncthreads();
         PieceInfo pi;
         if (!whole) pi = piece_info<HG>(a, wg, u, unit_first, n_s, I, NWG);
-        for (int e = threadIdx.x; e < HG * D; e += 256) {
+        // a fixed number of store instructions, so the compiler can still count the
+        // loads in flight past them (a loop of unknown trip count made it wait for all)
+#pragma unroll
+        for (int k = 0; k < (HG * D + 255) / 256; ++k) {
+          const int e = threadIdx.x + 256 * k;
+          if (HG * D % 256 != 0 && e >= HG * D) break;
           const int h = e / D, d = e % D, q = h / 4, i = h % 4;
           float M = -INFINITY;
 #pragma unroll
