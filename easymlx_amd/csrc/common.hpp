@@ -14,6 +14,21 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kTwo24 = 16777216.0f;  // codes enter the MFMA as fp16 subnormals n * 2^-24
 
+// One LDS arena that the 4-bit decode and the prefill kernel bodies carve their
+// arrays from.  A kernel allocates every __shared__ variable it references, so
+// the two bodies of one launch (unified_q4) overlap in it instead of adding up;
+// either kernel alone takes the arena's size.
+constexpr int kArenaBytes = 62 * 1024;
+__shared__ __attribute__((aligned(16))) unsigned char lds_arena[kArenaBytes];
+
+// The object of type T at byte offset off of the arena.
+template <class T>
+__device__ __forceinline__ T& lds_at(const int off) {
+  return *reinterpret_cast<T*>(lds_arena + off);
+}
+// Offset after an object of `bytes` at `off`, 16-byte aligned.
+constexpr int lds_next(const int off, const int bytes) { return (off + bytes + 15) & ~15; }
+
 __device__ __forceinline__ h16x8 as_h8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
   u32x4 v = {a, b, c, d};
   return __builtin_bit_cast(h16x8, v);

@@ -304,8 +304,10 @@ struct Q4Geom {
 
 constexpr int kTableCache = 4096;  // block-table entries a workgroup keeps in LDS
 
+// The kernel body as workgroup `bid` of `nblocks` (a grid of its own, or the
+// decode part of a mixed batch's single launch, unified_q4).
 template <int GS, int HG>
-__global__ __launch_bounds__(256, 2) void decode_q4_d128(DecodeArgs a) {
+__device__ __forceinline__ void decode_q4_body(const DecodeArgs& a, const int bid, const int nblocks) {
   using Geo = Q4Geom<HG>;
   constexpr int HQ = Geo::HQ, NSL = Geo::NSL, TW = Geo::TW;
   constexpr int D = 128, G = Q4Cfg<GS, 1>::G;
@@ -315,15 +317,21 @@ __global__ __launch_bounds__(256, 2) void decode_q4_d128(DecodeArgs a) {
   const int quad = wv % HQ, slice = wv / HQ;
   const int hl = 4 * quad + (lane & 3);  // head of this lane's query operand and scores
 
-  __shared__ int cum[kMaxSeqs + 1];
-  __shared__ int kvl[kMaxSeqs];
-  __shared__ int qrw[kMaxSeqs];
-  __shared__ float so[2][4][4][D];  // two slot sets; per wave: o * 2^24 + bias term of its 4 heads
-  __shared__ float sml[2][4][4][2];  // per wave: (m, l) of its 4 heads
-  __shared__ int slast[2];
+  // LDS, carved from the shared arena
+  constexpr int oCum = 0, oKvl = lds_next(oCum, 4 * (kMaxSeqs + 1)), oQrw = lds_next(oKvl, 4 * kMaxSeqs);
+  constexpr int oSo = lds_next(oQrw, 4 * kMaxSeqs), oSml = lds_next(oSo, 4 * 2 * 4 * 4 * D);
+  constexpr int oSlast = lds_next(oSml, 4 * 2 * 4 * 4 * 2), oSbt = lds_next(oSlast, 4 * 2);
+  constexpr int oSst = lds_next(oSbt, 4 * kTableCache), oEnd = lds_next(oSst, 8 * 4 * 16 * 4 * G);
+  static_assert(oEnd <= kArenaBytes, "LDS arena too small");
+  int(&cum)[kMaxSeqs + 1] = lds_at<int[kMaxSeqs + 1]>(oCum);
+  int(&kvl)[kMaxSeqs] = lds_at<int[kMaxSeqs]>(oKvl);
+  int(&qrw)[kMaxSeqs] = lds_at<int[kMaxSeqs]>(oQrw);
+  float(&so)[2][4][4][D] = lds_at<float[2][4][4][D]>(oSo);  // two slot sets; per wave: o * 2^24 + bias term of its 4 heads
+  float(&sml)[2][4][4][2] = lds_at<float[2][4][4][2]>(oSml);  // per wave: (m, l) of its 4 heads
+  int(&slast)[2] = lds_at<int[2]>(oSlast);
   // Block tables of up to kTableCache entries are read into LDS together with
   // kv_lens (one memory round trip for both), larger ones from global memory.
-  __shared__ int sbt[kTableCache];
+  int(&sbt)[kTableCache] = lds_at<int[kTableCache]>(oSbt);
   const int nbt = a.S * a.max_blocks;
   const bool bt_lds = nbt <= kTableCache;
   int btv[kTableCache / 256];
@@ -342,7 +350,7 @@ __global__ __launch_bounds__(256, 2) void decode_q4_d128(DecodeArgs a) {
   }
   {  // decoded sequences without a live token produce zeros (the reference's l == 0 case)
     const int per_seq = a.Hq * D / 8;
-    for (int i = blockIdx.x * 256 + threadIdx.x; i < a.S * per_seq; i += gridDim.x * 256) {
+    for (int i = bid * 256 + threadIdx.x; i < a.S * per_seq; i += nblocks * 256) {
       const int si = i / per_seq;
       if (kvl[si] >= 0 && cum[si + 1] == cum[si])
         reinterpret_cast<u32x4*>(a.out)[(size_t)qrw[si] * per_seq + i % per_seq] = u32x4{0u, 0u, 0u, 0u};
@@ -354,8 +362,8 @@ __global__ __launch_bounds__(256, 2) void decode_q4_d128(DecodeArgs a) {
   // per-item scheduling arithmetic stays scalar
   auto uru = [](int v) { return __builtin_amdgcn_readfirstlane(v); };
   const long long I = (long long)Hkv * uru(cum[S]);
-  const int NWG = (int)min((long long)gridDim.x, I);  // every range non-empty
-  const int wg = blockIdx.x;
+  const int NWG = (int)min((long long)nblocks, I);  // every range non-empty
+  const int wg = bid;
   if (wg >= NWG) return;
   const long long g0 = ((long long)wg * I) / NWG;
   const long long g1 = ((long long)(wg + 1) * I) / NWG;
@@ -468,7 +476,7 @@ __global__ __launch_bounds__(256, 2) void decode_q4_d128(DecodeArgs a) {
     return r;
   };
   const Q4ScalePtrs<GS> sptr = q4_scale_ptrs<GS>(a, lane);
-  __shared__ u32x2 sst[4][16 * 4 * G];  // per wave: scale staging [16 quads][4 * G segments]
+  u32x2(&sst)[4][16 * 4 * G] = lds_at<u32x2[4][16 * 4 * G]>(oSst);  // per wave: scale staging [16 quads][4 * G segments]
 
   // ---- first item's loads (its query is already in flight)
   int tb = (it_lo + j) * TW + 64 * slice;
@@ -715,6 +723,11 @@ __global__ __launch_bounds__(256, 2) void decode_q4_d128(DecodeArgs a) {
       }
     }
   }
+}
+
+template <int GS, int HG>
+__global__ __launch_bounds__(256, 2) void decode_q4_d128(DecodeArgs a) {
+  decode_q4_body<GS, HG>(a, blockIdx.x, gridDim.x);
 }
 
 }  // namespace emx

@@ -3,6 +3,7 @@
 // it does not assume.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -14,6 +15,7 @@
 #include "paged_generic.hpp"
 #include "prefill_affine.hpp"
 #include "decode_q4.hpp"
+#include "unified.hpp"
 #include "quantize.hpp"
 #include "fp8.hpp"
 #include "decode_fp8.hpp"
@@ -137,6 +139,26 @@ DecodeFn pick_decode_q4_hg(int hg) {
 DecodeFn pick_decode_q4(int gs, int hg) {
   if (gs == 64) return pick_decode_q4_hg<64>(hg);
   if (gs == 128) return pick_decode_q4_hg<128>(hg);
+  return nullptr;
+}
+
+// A mixed batch over 4-bit pages in one launch (prefill and 4-bit decode bodies).
+typedef void (*UnifiedFn)(emx::PrefillArgs, emx::DecodeArgs, int);
+
+template <int GS>
+UnifiedFn pick_unified_q4_hg(int hg) {
+  switch (hg) {
+    case 1: return emx::unified_q4<GS, 1>;
+    case 2: return emx::unified_q4<GS, 2>;
+    case 4: return emx::unified_q4<GS, 4>;
+    case 16: return emx::unified_q4<GS, 16>;
+  }
+  return nullptr;
+}
+
+UnifiedFn pick_unified_q4(int gs, int hg) {
+  if (gs == 64) return pick_unified_q4_hg<64>(hg);
+  if (gs == 128) return pick_unified_q4_hg<128>(hg);
   return nullptr;
 }
 
@@ -695,8 +717,9 @@ int emx_paged_attention_affine(const void* queries, int num_tokens, int num_q_he
       return fail(EMX_ERR_INVALID, "queries and cache tensors must be 16-byte aligned");
     if (workspace == nullptr || workspace_bytes < need)
       return fail(EMX_ERR_INVALID, "workspace too small: need %zu bytes, got %zu", need, workspace_bytes);
+    emx::PrefillArgs p;
+    long pgrid = 0;  // prefill workgroups (mixed batch)
     if (!single_token_decode) {
-      emx::PrefillArgs p;
       p.q = reinterpret_cast<const emx::h16*>(queries);
       p.kc = k_codes;
       p.ks = reinterpret_cast<const emx::h16*>(k_scales);
@@ -723,9 +746,13 @@ int emx_paged_attention_affine(const void* queries, int num_tokens, int num_q_he
         return fail(EMX_ERR_UNSUPPORTED, "no prefill kernel for bits=%d group_size=%d gqa=%d", bits, group_size, hg);
       // tiles of 128/hg query tokens: at most num_tokens/tile + num_seqs of them per kv head
       const int tokb = 128 / hg;
-      const long grid = (long)((num_tokens + tokb - 1) / tokb + num_seqs) * num_kv_heads * p.nparts;
-      hipLaunchKernelGGL(pf, dim3((unsigned)grid), dim3(256), 0, st, p);
-      if (int r = check_launch("prefill_affine_d128")) return r;
+      pgrid = (long)((num_tokens + tokb - 1) / tokb + num_seqs) * num_kv_heads * p.nparts;
+      // with the 4-bit decode kernel both go out as one launch (below)
+      if (!(bits == 4 && (page_size & (page_size - 1)) == 0 && pick_unified_q4(group_size, hg))) {
+        hipLaunchKernelGGL(pf, dim3((unsigned)pgrid), dim3(256), 0, st, p);
+        if (int r = check_launch("prefill_affine_d128")) return r;
+        pgrid = 0;
+      }
     }
     // the 4-bit kernel addresses pages with shifts: power-of-two page sizes
     DecodeFn fn = bits == 4 && (page_size & (page_size - 1)) == 0 ? pick_decode_q4(group_size, hg) : nullptr;
@@ -763,6 +790,18 @@ int emx_paged_attention_affine(const void* queries, int num_tokens, int num_q_he
     // tokens per work item: per wave (16x16 kernel) or per workgroup (4-bit kernel)
     // tokens per work item: per workgroup (4-bit kernel) or per wave (16x16 kernel)
     a.nt = q4 ? 64 * (4 / ((hg + 3) / 4)) : bits == 4 ? 64 : 32;
+    if (pgrid > 0) {
+      // Decode workgroups sized to the decode rows' share of the step: prefill time
+      // ~ prefill tokens * Hq (matrix work), decode time ~ decode rows * Hkv (page
+      // bytes); 28 is their ratio per unit at the rates measured on MI355X.  Enough
+      // workgroups that the decode, beside the prefill, ends with it (c3: 112;
+      // 64 .. 128 all gave 96 us against 105 us for two launches, 32 gave 123 us).
+      const double share = 28.0 * num_seqs / std::max(1, num_tokens - num_seqs) * num_kv_heads / num_q_heads;
+      const int ndec = std::clamp((int)std::ceil(1024.0 * share), device_cus() / 4, nw / 4);
+      UnifiedFn uf = pick_unified_q4(group_size, hg);
+      hipLaunchKernelGGL(uf, dim3((unsigned)(pgrid + ndec)), dim3(256), 0, st, p, a, ndec);
+      return check_launch("unified_q4");
+    }
     hipLaunchKernelGGL(fn, dim3((unsigned)(nw / 4)), dim3(256), 0, st, a);
     return check_launch("decode_affine_d128");
   }

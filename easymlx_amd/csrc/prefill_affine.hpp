@@ -106,8 +106,10 @@ __device__ __forceinline__ constexpr int pv_slot(int k) { return 8 * ((k & 15) >
 // of a multiple of 64 tokens): K expands to dec(code) * 2^-8 exactly with the
 // page scale * 2^8 * 2^-24 as the key scale (so the scores keep the affine
 // formula with zero biases), V dequantizes to dec(code) * scale.
+// The kernel body as workgroup `bid` (a grid of its own, or the prefill part of
+// a mixed batch's single launch, unified_q4).
 template <int BITS, int GS, int HG, bool FP8 = false>
-__global__ __launch_bounds__(256, 2) void prefill_affine_d128(PrefillArgs a) {
+__device__ __forceinline__ void prefill_body(const PrefillArgs& a, const int bid) {
   static_assert(!FP8 || (BITS == 4 && GS == 128), "the FP8 cache runs on the 64-key geometry, one group");
   constexpr int RAWV = FP8 ? 2 * PrefillCfg<BITS, GS, HG>::RAWV : PrefillCfg<BITS, GS, HG>::RAWV;
   using P = PrefillCfg<BITS, GS, HG>;
@@ -122,8 +124,14 @@ __global__ __launch_bounds__(256, 2) void prefill_affine_d128(PrefillArgs a) {
   // ---- work item: blockIdx -> (sequence, tile, kv_head); later tiles (more keys) first
   // ---- per-sequence tile counts, scanned by the whole workgroup (one pass of
   // global loads in parallel, not a serial walk by one thread)
-  __shared__ int tcum[kMaxSeqs + 1];
-  __shared__ int wred[4];
+  // LDS, carved from the shared arena
+  constexpr int oTcum = 0, oWred = lds_next(oTcum, 4 * (kMaxSeqs + 1)), oRawv = lds_next(oWred, 16);
+  constexpr int oRaws = lds_next(oRawv, RAWV), oKe = lds_next(oRaws, 2 * 4 * G * NT);
+  constexpr int oVe = lds_next(oKe, 2 * NT * P::KSTR), oKsf = lds_next(oVe, 2 * D * P::VSTR);
+  constexpr int oKbe = lds_next(oKsf, 4 * G * NT), oEnd = lds_next(oKbe, 16 * NT);
+  static_assert(oEnd <= kArenaBytes, "LDS arena too small");
+  int(&tcum)[kMaxSeqs + 1] = lds_at<int[kMaxSeqs + 1]>(oTcum);
+  int(&wred)[4] = lds_at<int[4]>(oWred);
   {
     const int ch = (a.S + 255) / 256, s0 = tid * ch;
     int tsum = 0;
@@ -156,9 +164,9 @@ __global__ __launch_bounds__(256, 2) void prefill_affine_d128(PrefillArgs a) {
   }
   __syncthreads();
   const int ntiles = tcum[a.S];
-  const int kvh = blockIdx.x % a.Hkv;
-  const int part = (blockIdx.x / a.Hkv) % a.nparts;
-  const int item = blockIdx.x / a.Hkv / a.nparts;
+  const int kvh = bid % a.Hkv;
+  const int part = (bid / a.Hkv) % a.nparts;
+  const int item = bid / a.Hkv / a.nparts;
   if (item >= ntiles) return;
   int s = 0;
   while (tcum[s + 1] <= item) ++s;
@@ -233,12 +241,12 @@ __global__ __launch_bounds__(256, 2) void prefill_affine_d128(PrefillArgs a) {
   }
 
   // ---- LDS: the step's raw V tile and scales, then the expanded K, dequantized V and fp32 K scales
-  __shared__ __attribute__((aligned(16))) uint8_t raw_v[RAWV];
-  __shared__ __attribute__((aligned(16))) h16 raw_s[4 * G * NT];   // [arr][g][NT]
-  __shared__ __attribute__((aligned(16))) h16 ke[NT * P::KSTR];    // [key][dims, unpack order]
-  __shared__ __attribute__((aligned(16))) h16 ve[D * P::VSTR];     // [dim][keys, pv_slot order]
-  __shared__ __attribute__((aligned(16))) float ksf[G][NT];       // k_scale * 2^24 in fp32
-  __shared__ __attribute__((aligned(16))) h16x8 kbe[NT];          // A operand of the bias MFMA: kb_g at 2g, 2g + 1
+  uint8_t(&raw_v)[RAWV] = lds_at<uint8_t[RAWV]>(oRawv);
+  h16(&raw_s)[4 * G * NT] = lds_at<h16[4 * G * NT]>(oRaws);  // [arr][g][NT]
+  h16(&ke)[NT * P::KSTR] = lds_at<h16[NT * P::KSTR]>(oKe);    // [key][dims, unpack order]
+  h16(&ve)[D * P::VSTR] = lds_at<h16[D * P::VSTR]>(oVe);      // [dim][keys, pv_slot order]
+  float(&ksf)[G][NT] = lds_at<float[G][NT]>(oKsf);            // k_scale * 2^24 in fp32
+  h16x8(&kbe)[NT] = lds_at<h16x8[NT]>(oKbe);                  // A operand of the bias MFMA: kb_g at 2g, 2g + 1
 
   // Cooperative load of one step into registers: thread owns one 16-byte piece of K and of V,
   // and (threads < SEGS * SEGB / 16) one piece of the scales.
@@ -591,6 +599,11 @@ __global__ __launch_bounds__(256, 2) void prefill_affine_d128(PrefillArgs a) {
                                                 (h16)(acc[ct][dt][2] * inv), (h16)(acc[ct][dt][3] * inv)};
     }
   }
+}
+
+template <int BITS, int GS, int HG, bool FP8 = false>
+__global__ __launch_bounds__(256, 2) void prefill_affine_d128(PrefillArgs a) {
+  prefill_body<BITS, GS, HG, FP8>(a, blockIdx.x);
 }
 
 }  // namespace emx

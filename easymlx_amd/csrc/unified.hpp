@@ -1,0 +1,25 @@
+// One launch for a mixed batch over 4-bit pages (the unified ragged step of
+// lib/python/easymlx/operations/kernels/unified_attention.py:290-609, which the
+// reference runs as one Metal dispatch over all rows): the first ndec workgroups
+// run the 4-bit decode body on the single-token rows, the others the prefill
+// body on the rows of sequences with more than one query token.  Workgroups
+// start in index order, so the decode workgroups (few: the host sizes them to
+// the decode rows' share of the work) take one slot on some compute units from
+// the start and stream their pages beside the prefill's matrix work on the
+// same units.  The two bodies share the LDS arena and nothing else.
+#pragma once
+
+#include "decode_q4.hpp"
+#include "prefill_affine.hpp"
+
+namespace emx {
+
+template <int GS, int HG>
+__global__ __launch_bounds__(256, 2) void unified_q4(PrefillArgs p, DecodeArgs d, int ndec) {
+  if ((int)blockIdx.x < ndec)
+    decode_q4_body<GS, HG>(d, blockIdx.x, ndec);
+  else
+    prefill_body<4, GS, HG>(p, (int)blockIdx.x - ndec);
+}
+
+}  // namespace emx
