@@ -159,8 +159,11 @@ __device__ __forceinline__ void fp8_compute(const Fp8Loads& L, const bool full, 
   }
 }
 
+// The kernel body as workgroup `bid` of `nblocks` (a grid of its own, or the
+// decode part of a mixed batch's single launch, unified_fp8); a.num_waves is the
+// number of waves the ranges are split over.
 template <int HG>
-__global__ __launch_bounds__(256, 2) void decode_fp8_d128(DecodeArgs a) {
+__device__ __forceinline__ void decode_fp8_body(const DecodeArgs& a, const int bid, const int nblocks) {
   constexpr int D = 128, NT = kFp8DecodeNT;
   static_assert(HG >= 1 && HG <= 16, "GQA group must fit 16 MFMA columns");
 
@@ -170,14 +173,18 @@ __global__ __launch_bounds__(256, 2) void decode_fp8_d128(DecodeArgs a) {
   const int jj = lane >> 4;
   const bool col_ok = col < HG;
 
-  __shared__ int cum[kMaxSeqs + 1];
-  __shared__ int kvl[kMaxSeqs];
-  __shared__ int qrw[kMaxSeqs];
-  __shared__ __attribute__((aligned(16))) float xst[4][HG * D];  // per wave: a partial, head-major
+  // LDS, carved from the shared arena
+  constexpr int oCum = 0, oKvl = lds_next(oCum, 4 * (kMaxSeqs + 1)), oQrw = lds_next(oKvl, 4 * kMaxSeqs);
+  constexpr int oXst = lds_next(oQrw, 4 * kMaxSeqs), oEnd = lds_next(oXst, 4 * 4 * HG * D);
+  static_assert(oEnd <= kArenaBytes, "LDS arena too small");
+  int(&cum)[kMaxSeqs + 1] = lds_at<int[kMaxSeqs + 1]>(oCum);
+  int(&kvl)[kMaxSeqs] = lds_at<int[kMaxSeqs]>(oKvl);
+  int(&qrw)[kMaxSeqs] = lds_at<int[kMaxSeqs]>(oQrw);
+  float(&xst)[4][HG * D] = lds_at<float[4][HG * D]>(oXst);  // per wave: a partial, head-major
   seq_table(a, cum, kvl, qrw);
   {  // decoded sequences without a live token produce zeros (the reference's l == 0 case)
     const int per_seq = a.Hq * D / 8;
-    for (int i = blockIdx.x * 256 + threadIdx.x; i < a.S * per_seq; i += gridDim.x * 256) {
+    for (int i = bid * 256 + threadIdx.x; i < a.S * per_seq; i += nblocks * 256) {
       const int si = i / per_seq;
       if (kvl[si] >= 0 && cum[si + 1] == cum[si])
         reinterpret_cast<u32x4*>(a.out)[(size_t)qrw[si] * per_seq + i % per_seq] = u32x4{0u, 0u, 0u, 0u};
@@ -188,7 +195,7 @@ __global__ __launch_bounds__(256, 2) void decode_fp8_d128(DecodeArgs a) {
   auto uru = [](int v) { return __builtin_amdgcn_readfirstlane(v); };
   const long long I = (long long)Hkv * uru(cum[S]);
   const int NW = (int)min((long long)a.num_waves, I);
-  const int W = blockIdx.x * 4 + wv;
+  const int W = bid * 4 + wv;
   if (W >= NW) return;
   const long long g0 = ((long long)W * I) / NW;
   const long long g1 = ((long long)(W + 1) * I) / NW;
@@ -368,6 +375,11 @@ __global__ __launch_bounds__(256, 2) void decode_fp8_d128(DecodeArgs a) {
     if (g + 1 >= g1) break;
     step(bufB, bufA, g + 1);
   }
+}
+
+template <int HG>
+__global__ __launch_bounds__(256, 2) void decode_fp8_d128(DecodeArgs a) {
+  decode_fp8_body<HG>(a, blockIdx.x, gridDim.x);
 }
 
 }  // namespace emx

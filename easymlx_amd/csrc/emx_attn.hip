@@ -156,6 +156,17 @@ UnifiedFn pick_unified_q4_hg(int hg) {
   return nullptr;
 }
 
+UnifiedFn pick_unified_fp8(int hg) {
+  switch (hg) {
+    case 1: return emx::unified_fp8<1>;
+    case 2: return emx::unified_fp8<2>;
+    case 4: return emx::unified_fp8<4>;
+    case 8: return emx::unified_fp8<8>;
+    case 16: return emx::unified_fp8<16>;
+  }
+  return nullptr;
+}
+
 UnifiedFn pick_unified_q4(int gs, int hg) {
   if (gs == 64) return pick_unified_q4_hg<64>(hg);
   if (gs == 128) return pick_unified_q4_hg<128>(hg);
@@ -1057,7 +1068,7 @@ int emx_paged_attention_fp8(const void* queries, int num_tokens, int num_q_heads
   const DecodeFn dfn = mfma_ok && need > 0 ? pick_decode_fp8(hg) : nullptr;
   // the FP8 prefill kernel walks 64-key steps inside one page
   const PrefillFn pf = mfma_ok && page_size % 64 == 0 ? pick_prefill_fp8(hg) : nullptr;
-  auto launch_prefill = [&](int min_q) {
+  auto prefill_args = [&](int min_q) {
     emx::PrefillArgs p{};
     p.q = reinterpret_cast<const emx::h16*>(queries);
     p.block_tables = block_tables;
@@ -1078,9 +1089,15 @@ int emx_paged_attention_fp8(const void* queries, int num_tokens, int num_q_heads
     p.kps = k_scale;
     p.vps = v_scale;
     prefill_split(p, num_tokens, num_q_heads, num_kv_heads, workspace, workspace_bytes, need);
+    return p;
+  };
+  auto prefill_grid = [&](const emx::PrefillArgs& p) {
     const int tokb = 128 / hg;
-    const long grid = (long)((num_tokens + tokb - 1) / tokb + num_seqs) * num_kv_heads * p.nparts;
-    hipLaunchKernelGGL(pf, dim3((unsigned)grid), dim3(256), 0, st, p);
+    return (long)((num_tokens + tokb - 1) / tokb + num_seqs) * num_kv_heads * p.nparts;
+  };
+  auto launch_prefill = [&](int min_q) {
+    const emx::PrefillArgs p = prefill_args(min_q);
+    hipLaunchKernelGGL(pf, dim3((unsigned)prefill_grid(p)), dim3(256), 0, st, p);
     return check_launch("prefill_affine_d128 (fp8)");
   };
   // head_dim 128, fp16 queries: decode rows (one query token) on the split-K FP8
@@ -1088,8 +1105,6 @@ int emx_paged_attention_fp8(const void* queries, int num_tokens, int num_q_heads
   if (dfn && (single_token_decode || (pf && query_start_loc))) {
     if (workspace == nullptr || workspace_bytes < need)
       return fail(EMX_ERR_INVALID, "workspace too small: need %zu bytes, got %zu", need, workspace_bytes);
-    if (!single_token_decode)
-      if (int r = launch_prefill(2)) return r;
     const int nw = decode_num_waves();
     emx::DecodeArgs a{};
     a.q = reinterpret_cast<const emx::h16*>(queries);
@@ -1116,6 +1131,18 @@ int emx_paged_attention_fp8(const void* queries, int num_tokens, int num_q_heads
     a.window = ga.window;
     a.num_waves = nw;
     a.nt = emx::kFp8DecodeNT;
+    if (!single_token_decode) {
+      // a mixed batch in one launch: the decode workgroups first, sized to the decode
+      // rows' share of the step as for affine pages (ratio 50: 256 page bytes per
+      // token and kv head against 144)
+      const emx::PrefillArgs p = prefill_args(2);
+      const double share = 50.0 * num_seqs / std::max(1, num_tokens - num_seqs) * num_kv_heads / num_q_heads;
+      const int ndec = std::clamp((int)std::ceil(1024.0 * share), device_cus() / 4, nw / 4);
+      a.num_waves = 4 * ndec;
+      hipLaunchKernelGGL(pick_unified_fp8(hg), dim3((unsigned)(prefill_grid(p) + ndec)), dim3(256), 0, st, p, a,
+                         ndec);
+      return check_launch("unified_fp8");
+    }
     hipLaunchKernelGGL(dfn, dim3((unsigned)(nw / 4)), dim3(256), 0, st, a);
     return check_launch("decode_fp8_d128");
   }

@@ -1,4 +1,4 @@
-// One launch for a mixed batch over 4-bit pages (the unified ragged step of
+// One launch for a mixed batch over 4-bit pages or an FP8 cache (the unified ragged step of
 // lib/python/easymlx/operations/kernels/unified_attention.py:290-609, which the
 // reference runs as one Metal dispatch over all rows): the first ndec workgroups
 // run the 4-bit decode body on the single-token rows, the others the prefill
@@ -9,6 +9,7 @@
 // same units.  The two bodies share the LDS arena and nothing else.
 #pragma once
 
+#include "decode_fp8.hpp"
 #include "decode_q4.hpp"
 #include "prefill_affine.hpp"
 
@@ -20,6 +21,16 @@ __global__ __launch_bounds__(256, 2) void unified_q4(PrefillArgs p, DecodeArgs d
     decode_q4_body<GS, HG>(d, blockIdx.x, ndec);
   else
     prefill_body<4, GS, HG>(p, (int)blockIdx.x - ndec);
+}
+
+// The same over an FP8 (E4M3) cache: the FP8 decode body, then the prefill body
+// on its FP8 geometry.  d.num_waves = 4 * ndec.
+template <int HG>
+__global__ __launch_bounds__(256, 2) void unified_fp8(PrefillArgs p, DecodeArgs d, int ndec) {
+  if ((int)blockIdx.x < ndec)
+    decode_fp8_body<HG>(d, blockIdx.x, ndec);
+  else
+    prefill_body<4, 128, HG, true>(p, (int)blockIdx.x - ndec);
 }
 
 }  // namespace emx
