@@ -543,8 +543,11 @@ __device__ __forceinline__ void merge_piece(const DecodeArgs& a, const int W, co
   merge_pieces<HG>(a, pi, u, row, kvh, lane);
 }
 
+// The kernel body as workgroup `bid` of `nblocks` (a grid of its own, or the
+// decode part of a mixed batch's single launch, unified_affine); a.num_waves is
+// the number of waves the ranges are split over.
 template <int BITS, int GS, int HG>
-__global__ __launch_bounds__(256, 2) void decode_affine_d128(DecodeArgs a) {
+__device__ __forceinline__ void decode_affine_body(const DecodeArgs& a, const int bid, const int nblocks) {
   using C = DecodeCfg<BITS, GS, HG>;
   constexpr int D = C::D, G = C::G, GSTRIDE = C::GSTRIDE, NT = C::NT;
 
@@ -556,15 +559,20 @@ __global__ __launch_bounds__(256, 2) void decode_affine_d128(DecodeArgs a) {
   const int gg = col / GSTRIDE;
   const bool col_ok = hh < HG;
 
-  __shared__ int cum[kMaxSeqs + 1];
-  __shared__ int kvl[kMaxSeqs];
-  __shared__ int qrw[kMaxSeqs];
-  __shared__ __attribute__((aligned(16))) h16 stage_all[4][C::SHALVES];
-  __shared__ __attribute__((aligned(16))) float xst[4][HG * 128];  // per wave: a partial, head-major
+  // LDS, carved from the shared arena
+  constexpr int oCum = 0, oKvl = lds_next(oCum, 4 * (kMaxSeqs + 1)), oQrw = lds_next(oKvl, 4 * kMaxSeqs);
+  constexpr int oStage = lds_next(oQrw, 4 * kMaxSeqs), oXst = lds_next(oStage, 2 * 4 * C::SHALVES);
+  constexpr int oEnd = lds_next(oXst, 4 * 4 * HG * 128);
+  static_assert(oEnd <= kArenaBytes, "LDS arena too small");
+  int(&cum)[kMaxSeqs + 1] = lds_at<int[kMaxSeqs + 1]>(oCum);
+  int(&kvl)[kMaxSeqs] = lds_at<int[kMaxSeqs]>(oKvl);
+  int(&qrw)[kMaxSeqs] = lds_at<int[kMaxSeqs]>(oQrw);
+  h16(&stage_all)[4][C::SHALVES] = lds_at<h16[4][C::SHALVES]>(oStage);
+  float(&xst)[4][HG * 128] = lds_at<float[4][HG * 128]>(oXst);  // per wave: a partial, head-major
   seq_table(a, cum, kvl, qrw);
   {  // decoded sequences without a live token produce zeros (the reference's l == 0 case)
     const int per_seq = a.Hq * D / 8;
-    for (int i = blockIdx.x * 256 + threadIdx.x; i < a.S * per_seq; i += gridDim.x * 256) {
+    for (int i = bid * 256 + threadIdx.x; i < a.S * per_seq; i += nblocks * 256) {
       const int si = i / per_seq;
       if (kvl[si] >= 0 && cum[si + 1] == cum[si])
         reinterpret_cast<u32x4*>(a.out)[(size_t)qrw[si] * per_seq + i % per_seq] = u32x4{0u, 0u, 0u, 0u};
@@ -577,7 +585,7 @@ __global__ __launch_bounds__(256, 2) void decode_affine_d128(DecodeArgs a) {
   auto uru = [](int v) { return __builtin_amdgcn_readfirstlane(v); };
   const long long I = (long long)Hkv * uru(cum[S]);
   const int NW = (int)min((long long)a.num_waves, I);  // every wave range non-empty
-  const int W = blockIdx.x * 4 + wv;
+  const int W = bid * 4 + wv;
   if (W >= NW) return;
   const long long g0 = ((long long)W * I) / NW;
   const long long g1 = ((long long)(W + 1) * I) / NW;
@@ -776,6 +784,11 @@ __global__ __launch_bounds__(256, 2) void decode_affine_d128(DecodeArgs a) {
     if (g + 1 >= g1) break;
     step(bufB, bufA, g + 1);
   }
+}
+
+template <int BITS, int GS, int HG>
+__global__ __launch_bounds__(256, 2) void decode_affine_d128(DecodeArgs a) {
+  decode_affine_body<BITS, GS, HG>(a, blockIdx.x, gridDim.x);
 }
 
 }  // namespace emx

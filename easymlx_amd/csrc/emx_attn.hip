@@ -156,6 +156,29 @@ UnifiedFn pick_unified_q4_hg(int hg) {
   return nullptr;
 }
 
+template <int BITS, int GS>
+UnifiedFn pick_unified_affine_hg(int hg) {
+  constexpr int G = 128 / GS;
+  switch (hg) {
+    case 1: return emx::unified_affine<BITS, GS, 1>;
+    case 2: return emx::unified_affine<BITS, GS, 2>;
+    case 4: return emx::unified_affine<BITS, GS, 4>;
+    case 8: if constexpr (8 * G <= 16) return emx::unified_affine<BITS, GS, 8>; else return nullptr;
+    case 16: if constexpr (16 * G <= 16) return emx::unified_affine<BITS, GS, 16>; else return nullptr;
+  }
+  return nullptr;
+}
+
+template <int BITS>
+UnifiedFn pick_unified_affine(int gs, int hg) {
+  switch (gs) {
+    case 32: return pick_unified_affine_hg<BITS, 32>(hg);
+    case 64: return pick_unified_affine_hg<BITS, 64>(hg);
+    case 128: return pick_unified_affine_hg<BITS, 128>(hg);
+  }
+  return nullptr;
+}
+
 UnifiedFn pick_unified_fp8(int hg) {
   switch (hg) {
     case 1: return emx::unified_fp8<1>;
@@ -729,7 +752,8 @@ int emx_paged_attention_affine(const void* queries, int num_tokens, int num_q_he
     if (workspace == nullptr || workspace_bytes < need)
       return fail(EMX_ERR_INVALID, "workspace too small: need %zu bytes, got %zu", need, workspace_bytes);
     emx::PrefillArgs p;
-    long pgrid = 0;  // prefill workgroups (mixed batch)
+    long pgrid = 0;          // prefill workgroups (mixed batch)
+    UnifiedFn uf = nullptr;  // the mixed batch's single launch
     if (!single_token_decode) {
       p.q = reinterpret_cast<const emx::h16*>(queries);
       p.kc = k_codes;
@@ -758,8 +782,12 @@ int emx_paged_attention_affine(const void* queries, int num_tokens, int num_q_he
       // tiles of 128/hg query tokens: at most num_tokens/tile + num_seqs of them per kv head
       const int tokb = 128 / hg;
       pgrid = (long)((num_tokens + tokb - 1) / tokb + num_seqs) * num_kv_heads * p.nparts;
-      // with the 4-bit decode kernel both go out as one launch (below)
-      if (!(bits == 4 && (page_size & (page_size - 1)) == 0 && pick_unified_q4(group_size, hg))) {
+      // prefill and decode rows go out as one launch (below) when a unified kernel
+      // pairs this prefill with the decode kernel picked for the rows
+      const bool q4u = bits == 4 && (page_size & (page_size - 1)) == 0 && pick_decode_q4(group_size, hg);
+      uf = q4u ? pick_unified_q4(group_size, hg)
+               : bits == 4 ? pick_unified_affine<4>(group_size, hg) : pick_unified_affine<8>(group_size, hg);
+      if (!uf) {
         hipLaunchKernelGGL(pf, dim3((unsigned)pgrid), dim3(256), 0, st, p);
         if (int r = check_launch("prefill_affine_d128")) return r;
         pgrid = 0;
@@ -803,15 +831,18 @@ int emx_paged_attention_affine(const void* queries, int num_tokens, int num_q_he
     a.nt = q4 ? 64 * (4 / ((hg + 3) / 4)) : bits == 4 ? 64 : 32;
     if (pgrid > 0) {
       // Decode workgroups sized to the decode rows' share of the step: prefill time
-      // ~ prefill tokens * Hq (matrix work), decode time ~ decode rows * Hkv (page
-      // bytes); 28 is their ratio per unit at the rates measured on MI355X.  Enough
-      // workgroups that the decode, beside the prefill, ends with it (c3: 112;
-      // 64 .. 128 all gave 96 us against 105 us for two launches, 32 gave 123 us).
-      const double share = 28.0 * num_seqs / std::max(1, num_tokens - num_seqs) * num_kv_heads / num_q_heads;
+      // ~ prefill tokens * Hq (matrix work), decode time ~ decode rows * Hkv * page
+      // bytes per token; 28 is their ratio at 144 bytes (4-bit, group 64) at the
+      // rates measured on MI355X.  Enough workgroups that the decode, beside the
+      // prefill, ends with it (c3: 112; 64 .. 128 all gave 96 us against 105 us for
+      // two launches, 32 gave 123 us).
+      const double tok_bytes = 2.0 * head_dim * bits / 8 + 8.0 * head_dim / group_size;
+      const double share = 28.0 * tok_bytes / 144.0 * num_seqs / std::max(1, num_tokens - num_seqs) * num_kv_heads /
+                           num_q_heads;
       const int ndec = std::clamp((int)std::ceil(1024.0 * share), device_cus() / 4, nw / 4);
-      UnifiedFn uf = pick_unified_q4(group_size, hg);
+      a.num_waves = 4 * ndec;  // the 16x16 body splits its ranges over these waves
       hipLaunchKernelGGL(uf, dim3((unsigned)(pgrid + ndec)), dim3(256), 0, st, p, a, ndec);
-      return check_launch("unified_q4");
+      return check_launch(q4 ? "unified_q4" : "unified_affine");
     }
     hipLaunchKernelGGL(fn, dim3((unsigned)(nw / 4)), dim3(256), 0, st, a);
     return check_launch("decode_affine_d128");

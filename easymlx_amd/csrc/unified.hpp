@@ -33,4 +33,14 @@ __global__ __launch_bounds__(256, 2) void unified_fp8(PrefillArgs p, DecodeArgs 
     prefill_body<4, 128, HG, true>(p, (int)blockIdx.x - ndec);
 }
 
+// The same with the 16x16x32 decode body (8-bit pages, group 32, GQA 8).
+// d.num_waves = 4 * ndec.
+template <int BITS, int GS, int HG>
+__global__ __launch_bounds__(256, 2) void unified_affine(PrefillArgs p, DecodeArgs d, int ndec) {
+  if ((int)blockIdx.x < ndec)
+    decode_affine_body<BITS, GS, HG>(d, blockIdx.x, ndec);
+  else
+    prefill_body<BITS, GS, HG>(p, (int)blockIdx.x - ndec);
+}
+
 }  // namespace emx

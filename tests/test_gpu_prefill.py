@@ -71,6 +71,17 @@ def test_prefill_shapes(cuda, hq, hkv, gs, bits):
     assert_attention_close(_run(wl, view, cuda), oracle_expected(wl), f"shape {hq}/{hkv}/{gs}/{bits}")
 
 
+@pytest.mark.parametrize("bits,hq", [(4, 32), (8, 32), (4, 64)], ids=["4bit", "8bit", "4bit-gqa8"])
+def test_mixed_decode_heavy(cuda, bits, hq):
+    """Mostly decode rows beside one short prefill chunk: the single launch gives the decode rows their
+    largest workgroup count (ranges split over every decode workgroup)."""
+    print(f"[mixed decode-heavy bits={bits} hq={hq}]", flush=True)
+    wl = unified_workload("dheavy", seed=70 + bits + hq, num_prefill=1, chunk=40, prior_range=(0, 300),
+                          num_decode=60, decode_ctx=(1, 2000), num_q_heads=hq, bits=bits)
+    view = gpu_cache(wl, cuda)
+    assert_attention_close(_run(wl, view, cuda), oracle_expected(wl), f"decode-heavy {bits}/{hq}")
+
+
 def test_kv_shorter_than_query_rows(cuda):
     """kv_len < q_len: early query rows see no key (zeros, like the reference's max_k < 0 rows)."""
     print("[prefill short kv]", flush=True)
