@@ -419,6 +419,7 @@ def aux_quantize_on_write(dev):
     k = torch.randn(n, hkv, d, device=dev).half()
     v = torch.randn(n, hkv, d, device=dev).half()
     q = torch.randn(n, 32, d, device=dev).half()
+    q_out = torch.empty_like(q)  # the turned queries (the inputs stay as they are)
     s = torch.tensor(appends, dtype=torch.int32, device=dev)
     pos = torch.from_numpy(wl.kv_lens.astype(np.int32)).to(dev)
 
@@ -426,7 +427,7 @@ def aux_quantize_on_write(dev):
         rc = lib.emx_affine_cache_write_rope(
             k.data_ptr(), v.data_ptr(), s.data_ptr(), n, hkv, d, 64, 4, bs, nb, view.k_codes.data_ptr(),
             view.k_scales.data_ptr(), view.k_biases.data_ptr(), view.v_codes.data_ptr(), view.v_scales.data_ptr(),
-            view.v_biases.data_ptr(), pos.data_ptr(), inv.data_ptr(), d, 0, q.data_ptr(), 32, stream)
+            view.v_biases.data_ptr(), pos.data_ptr(), inv.data_ptr(), d, 0, q.data_ptr(), q_out.data_ptr(), 32, stream)
         if rc:
             _native.check(rc)
 
@@ -472,12 +473,12 @@ def aux_op_layer_step(dev, steps=100):
                            slot_ids=tuple(range(S)))
         qlens = (1,) * S
         cache = CompiledPagedCacheProxy(view) if mode == "graph" else view
-        out_buf = torch.empty_like(q)
+        outs = []
 
         def step():
             q2, kc, vc, md = cache.concatenate_to_cache(q, k, v, cache_metadata=md0, rope=rope, query_lens=qlens)
-            out_buf.copy_(op.forward_native(query=q2, key=kc, value=vc, cache_metadata=md,
-                                            cache_view=view).attention_outputs)
+            outs[:] = [op.forward_native(query=q2, key=kc, value=vc, cache_metadata=md,
+                                         cache_view=view).attention_outputs]
 
         side = torch.cuda.Stream(dev)
         side.wait_stream(torch.cuda.current_stream(dev))

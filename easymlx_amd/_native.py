@@ -35,9 +35,9 @@ SIGNATURES: dict[str, tuple] = {
     "emx_last_error": (ctypes.c_char_p, []),
     "emx_affine_quantize": (_I, [_P, _L, _I, _I, _I, _P, _P, _P, _P]),
     "emx_affine_cache_write": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P]),
-    "emx_affine_cache_write_rope": (_I, [_P, _P, _P] + [_I] * 7 + [_P] * 6 + [_P, _P, _I, _I, _P, _I, _P]),
+    "emx_affine_cache_write_rope": (_I, [_P, _P, _P] + [_I] * 7 + [_P] * 6 + [_P, _P, _I, _I, _P, _P, _I, _P]),
     "emx_fp8_cache_write_rope": (
-        _I, [_P, _P, _I, _P, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _SZ, _P, _P, _I, _I, _P, _I, _P]),
+        _I, [_P, _P, _I, _P, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _SZ, _P, _P, _I, _I, _P, _P, _I, _P]),
     "emx_rope_rows": (_I, [_P, _I, _I, _I, _P, _P, _I, _I, _P]),
     "emx_cache_slots": (_I, [_P, _P, _I, _I, _P, _I, _I, _I, _P, _P, _P, _P]),
     "emx_dense_cache_write": (_I, [_P, _P, _I, _P, _I, _I, _I, _I, _I, _P, _P, _P]),

@@ -138,14 +138,15 @@ class CompiledPagedCacheProxy:
                 c._write(k, v, mapping)
                 return queries
             if fused:
-                q_out = queries.contiguous().clone()
+                q_in = queries.contiguous()
+                q_out = torch.empty_like(q_in)  # every row written by the launch, turned
                 inv = rope.inv_freq(k.device)
                 _native.check(lib.emx_affine_cache_write_rope(
                     k.data_ptr(), v.data_ptr(), mapping.data_ptr(), n, c.num_kv_heads, c.head_dim, c.group_size,
                     c.bits, c.block_size, c.num_blocks, c.key_cache.data_ptr(), c.k_scales.data_ptr(),
                     c.k_biases.data_ptr(), c.value_cache.data_ptr(), c.v_scales.data_ptr(), c.v_biases.data_ptr(),
-                    positions.data_ptr(), inv.data_ptr(), rope.dims, int(rope.traditional), q_out.data_ptr(),
-                    int(q_out.shape[1]), stream))
+                    positions.data_ptr(), inv.data_ptr(), rope.dims, int(rope.traditional), q_in.data_ptr(),
+                    q_out.data_ptr(), int(q_out.shape[1]), stream))
                 return q_out
         elif isinstance(c, Fp8PageCacheView):
             codes = {torch.float16: _native.DTYPE_F16, torch.bfloat16: _native.DTYPE_BF16,
@@ -156,15 +157,16 @@ class CompiledPagedCacheProxy:
             if rope is None or turn:
                 k, v = keys.contiguous(), values.contiguous()
                 if turn:
-                    q_out = queries.contiguous().clone()
+                    q_in = queries.contiguous()
+                    q_out = torch.empty_like(q_in)  # every row written by the launch, turned
                     inv = rope.inv_freq(k.device)
                     ws = self._fp8_workspace(lib, k.device)
                     _native.check(lib.emx_fp8_cache_write_rope(
                         k.data_ptr(), v.data_ptr(), codes[k.dtype], mapping.data_ptr(), n, c.num_kv_heads,
                         c.head_dim, c.block_size, c.num_blocks, c.key_cache.data_ptr(), c.value_cache.data_ptr(),
                         c.k_scales.data_ptr(), c.v_scales.data_ptr(), ws.data_ptr(), ws.numel(),
-                        positions.data_ptr(), inv.data_ptr(), rope.dims, int(rope.traditional), q_out.data_ptr(),
-                        int(q_out.shape[1]), stream))
+                        positions.data_ptr(), inv.data_ptr(), rope.dims, int(rope.traditional), q_in.data_ptr(),
+                        q_out.data_ptr(), int(q_out.shape[1]), stream))
                     return q_out
                 # no workspace: the library's own scratch (a decode step's append takes one launch anyway)
                 _native.check(lib.emx_fp8_cache_write_noalloc(

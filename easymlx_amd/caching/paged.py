@@ -358,15 +358,22 @@ class PageCacheView:
         slot_mapping, slots, positions, _ = self._slots(slot_ids, qlens)
         lib = _native.load()
         n = int(slot_mapping.numel())
-        q_out = queries.contiguous().clone()
-        if n:
-            inv = rope.inv_freq(q_out.device)
-            stream = _stream_ptr(q_out.device)
-            if not writes_queries:
-                _native.check(lib.emx_rope_rows(q_out.data_ptr(), n, int(q_out.shape[1]), self.head_dim,
-                                                positions.data_ptr(), inv.data_ptr(), rope.dims,
-                                                int(rope.traditional), stream))
-            _native.check(write(keys, values, slot_mapping, positions, inv, rope, stream, q_out))
+        q_in = queries.contiguous()
+        if n and writes_queries and n == int(q_in.shape[0]):
+            # the write kernel turns every query row into a fresh tensor (no copy first)
+            q_out = torch.empty_like(q_in)
+            _native.check(write(keys, values, slot_mapping, positions, rope.inv_freq(q_in.device), rope,
+                                _stream_ptr(q_in.device), q_in, q_out))
+        else:
+            q_out = q_in.clone()
+            if n:
+                inv = rope.inv_freq(q_out.device)
+                stream = _stream_ptr(q_out.device)
+                if not writes_queries:
+                    _native.check(lib.emx_rope_rows(q_out.data_ptr(), n, int(q_out.shape[1]), self.head_dim,
+                                                    positions.data_ptr(), inv.data_ptr(), rope.dims,
+                                                    int(rope.traditional), stream))
+                _native.check(write(keys, values, slot_mapping, positions, inv, rope, stream, None, q_out))
         return q_out, self.key_cache, self.value_cache, self._resolved(cache_metadata, slots, single, slot_ids)
 
     def append(self, seq_idx: int, key: torch.Tensor, value: torch.Tensor) -> None:
@@ -558,7 +565,7 @@ class Fp8PageCacheView(PageCacheView):
 
         codes = {torch.float16: DTYPE_F16, torch.bfloat16: DTYPE_BF16, torch.float32: DTYPE_F32}
 
-        def write(keys, values, slot_mapping, positions, inv, rope, stream, q_out):
+        def write(keys, values, slot_mapping, positions, inv, rope, stream, q_in, q_out):
             if keys.dtype not in codes or values.dtype != keys.dtype:
                 raise NotImplementedError(f"FP8 cache writes take fp16/bf16/fp32 keys and values, got {keys.dtype}")
             lib = _native.load()
@@ -572,7 +579,7 @@ class Fp8PageCacheView(PageCacheView):
                 self.num_kv_heads, self.head_dim, self.block_size, self.num_blocks, self.key_cache.data_ptr(),
                 self.value_cache.data_ptr(), self.k_scales.data_ptr(), self.v_scales.data_ptr(), self._ws.data_ptr(),
                 self._ws.numel(), positions.data_ptr(), inv.data_ptr(), rope.dims, int(rope.traditional),
-                q_out.data_ptr(), int(q_out.shape[1]), stream)
+                None if q_in is None else q_in.data_ptr(), q_out.data_ptr(), int(q_out.shape[1]), stream)
 
         return self._concatenate_rope_fused(queries, keys, values, cache_metadata, rope, slot_ids, query_lens, write,
                                             rot_multiple=4 if getattr(rope, "traditional", False) else 8,
@@ -732,7 +739,7 @@ class AffinePageCacheView(PageCacheView):
         """``PageCacheView.concatenate_to_cache`` with a :class:`RotaryEmbedding` fused in: K turns inside the
         quantize-on-write kernel and Q in the same launch (``cache.py:1161-1166`` then ``:1186-1190``)."""
 
-        def write(keys, values, slot_mapping, positions, inv, rope, stream, q_out):
+        def write(keys, values, slot_mapping, positions, inv, rope, stream, q_in, q_out):
             keys = keys.to(torch.float16).contiguous()
             values = values.to(torch.float16).contiguous()
             return _native.load().emx_affine_cache_write_rope(
@@ -740,8 +747,8 @@ class AffinePageCacheView(PageCacheView):
                 self.head_dim, self.group_size, self.bits, self.block_size, self.num_blocks,
                 self.key_cache.data_ptr(), self.k_scales.data_ptr(), self.k_biases.data_ptr(),
                 self.value_cache.data_ptr(), self.v_scales.data_ptr(), self.v_biases.data_ptr(),
-                positions.data_ptr(), inv.data_ptr(), rope.dims, int(rope.traditional), q_out.data_ptr(),
-                int(q_out.shape[1]), stream)
+                positions.data_ptr(), inv.data_ptr(), rope.dims, int(rope.traditional),
+                None if q_in is None else q_in.data_ptr(), q_out.data_ptr(), int(q_out.shape[1]), stream)
 
         return self._concatenate_rope_fused(queries, keys, values, cache_metadata, rope, slot_ids, query_lens, write,
                                             rot_multiple=2, writes_queries=True)

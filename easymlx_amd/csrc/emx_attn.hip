@@ -369,8 +369,8 @@ int emx_affine_quantize(const void* x, long rows, int head_dim, int group_size, 
 static int affine_write_impl(const void* keys, const void* values, const int32_t* slot_mapping, int num_tokens,
                       int num_kv_heads, int head_dim, int group_size, int bits, int page_size, int num_blocks,
                       uint32_t* k_codes, void* k_scales, void* k_biases, uint32_t* v_codes, void* v_scales,
-                      void* v_biases, const emx::RopeArgs& rope, void* queries, int num_q_heads,
-                      void* stream) {
+                      void* v_biases, const emx::RopeArgs& rope, const void* queries_in, void* queries,
+                      int num_q_heads, void* stream) {
   if (num_tokens < 0) return fail(EMX_ERR_INVALID, "num_tokens must be >= 0");
   if (bits != 4 && bits != 8) return fail(EMX_ERR_UNSUPPORTED, "bits must be 4 or 8, got %d", bits);
   if (num_kv_heads <= 0 || head_dim <= 0 || page_size <= 0 || num_blocks <= 0)
@@ -405,6 +405,7 @@ static int affine_write_impl(const void* keys, const void* values, const int32_t
                 emx::kWriteMaxDim, emx::kWriteMaxGroups);
   a.rope = rope;
   a.q = reinterpret_cast<emx::h16*>(queries);
+  a.q_in = queries_in ? reinterpret_cast<const emx::h16*>(queries_in) : a.q;
   a.Hq = num_q_heads;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (num_tokens <= emx::kSmallWrite && head_dim % 16 == 0 && group_size % 16 == 0 &&
@@ -426,10 +427,10 @@ static int affine_write_impl(const void* keys, const void* values, const int32_t
     hipLaunchKernelGGL(emx::affine_cache_write<8>, grid, dim3(256), 0, st, a);
   if (int rc = check_launch("affine_cache_write")) return rc;
   if (rope.inv_freq != nullptr && queries != nullptr) {  // larger writes: the queries in their own launch
-    const long n = (long)num_tokens * num_q_heads * (rope.rot / 2);
+    const long n = (long)num_tokens * num_q_heads * (head_dim / 2);
     const unsigned qgrid = (unsigned)std::min<long>((n + 255) / 256, 4096);
-    hipLaunchKernelGGL(emx::rope_rows, dim3(qgrid), dim3(256), 0, st, reinterpret_cast<emx::h16*>(queries),
-                       num_tokens, num_q_heads, head_dim, rope);
+    hipLaunchKernelGGL(emx::rope_rows, dim3(qgrid), dim3(256), 0, st, a.q, a.q_in, num_tokens, num_q_heads, head_dim,
+                       rope);
     return check_launch("rope_rows");
   }
   return EMX_OK;
@@ -441,7 +442,7 @@ int emx_affine_cache_write(const void* keys, const void* values, const int32_t* 
                            void* v_biases, void* stream) {
   return affine_write_impl(keys, values, slot_mapping, num_tokens, num_kv_heads, head_dim, group_size, bits,
                            page_size, num_blocks, k_codes, k_scales, k_biases, v_codes, v_scales, v_biases,
-                           emx::RopeArgs{nullptr, nullptr, 0, 0}, nullptr, 0, stream);
+                           emx::RopeArgs{nullptr, nullptr, 0, 0}, nullptr, nullptr, 0, stream);
 }
 
 static bool rope_ok(const int32_t* positions, const float* inv_freq, int rot_dims, int head_dim) {
@@ -452,15 +453,17 @@ int emx_affine_cache_write_rope(const void* keys, const void* values, const int3
                                 int num_kv_heads, int head_dim, int group_size, int bits, int page_size,
                                 int num_blocks, uint32_t* k_codes, void* k_scales, void* k_biases, uint32_t* v_codes,
                                 void* v_scales, void* v_biases, const int32_t* positions, const float* inv_freq,
-                                int rot_dims, int traditional, void* queries, int num_q_heads, void* stream) {
+                                int rot_dims, int traditional, const void* queries_in, void* queries,
+                                int num_q_heads, void* stream) {
   if (num_tokens > 0 && !rope_ok(positions, inv_freq, rot_dims, head_dim))
     return fail(EMX_ERR_INVALID, "rope: positions and inv_freq needed, rot_dims even and in (0, head_dim]");
   if (queries != nullptr && (num_q_heads <= 0 || !aligned16(queries)))
     return fail(EMX_ERR_INVALID, "queries need num_q_heads > 0 and 16-byte alignment");
+  if (queries_in != nullptr && queries == nullptr) return fail(EMX_ERR_INVALID, "queries_in needs queries");
   return affine_write_impl(keys, values, slot_mapping, num_tokens, num_kv_heads, head_dim, group_size, bits,
                            page_size, num_blocks, k_codes, k_scales, k_biases, v_codes, v_scales, v_biases,
-                           emx::RopeArgs{inv_freq, positions, rot_dims, traditional ? 1 : 0}, queries, num_q_heads,
-                           stream);
+                           emx::RopeArgs{inv_freq, positions, rot_dims, traditional ? 1 : 0}, queries_in, queries,
+                           num_q_heads, stream);
 }
 
 int emx_cache_slots(const int32_t* slot_ids, const int32_t* query_start_loc, int num_slots, int num_tokens,
@@ -682,7 +685,7 @@ int emx_rope_rows(void* x, int rows, int heads, int head_dim, const int32_t* pos
   const long n = (long)rows * heads * (rot_dims / 2);
   const unsigned grid = (unsigned)std::min<long>((n + 255) / 256, 4096);
   hipLaunchKernelGGL(emx::rope_rows, dim3(grid), dim3(256), 0, reinterpret_cast<hipStream_t>(stream),
-                     reinterpret_cast<emx::h16*>(x), rows, heads, head_dim,
+                     reinterpret_cast<emx::h16*>(x), reinterpret_cast<const emx::h16*>(x), rows, heads, head_dim,
                      emx::RopeArgs{inv_freq, positions, rot_dims, traditional ? 1 : 0});
   return check_launch("rope_rows");
 }
@@ -947,8 +950,8 @@ size_t emx_fp8_write_workspace_bytes(void) { return sizeof(float) * 2 * emx::kFp
 static int fp8_write_impl(const void* keys, const void* values, int dtype, const int32_t* slot_mapping, int num_tokens,
                           int num_kv_heads, int head_dim, int page_size, int num_blocks, uint8_t* key_cache,
                           uint8_t* value_cache, float* k_scales, float* v_scales, void* workspace,
-                          size_t workspace_bytes, const emx::RopeArgs& rope, void* queries, int num_q_heads,
-                          void* stream) {
+                          size_t workspace_bytes, const emx::RopeArgs& rope, const void* queries_in,
+                          void* queries, int num_q_heads, void* stream) {
   if (num_tokens < 0) return fail(EMX_ERR_INVALID, "num_tokens must be >= 0");
   if (num_kv_heads <= 0 || head_dim <= 0 || page_size <= 0 || num_blocks <= 0)
     return fail(EMX_ERR_INVALID, "num_kv_heads, head_dim, page_size, num_blocks must be positive");
@@ -978,6 +981,7 @@ static int fp8_write_impl(const void* keys, const void* values, int dtype, const
   a.part = reinterpret_cast<float*>(workspace);
   a.rope = rope;
   a.q = reinterpret_cast<emx::h16*>(queries);
+  a.q_in = queries_in ? reinterpret_cast<const emx::h16*>(queries_in) : a.q;
   a.Hq = num_q_heads;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const size_t n = (size_t)num_tokens * num_kv_heads * head_dim;
@@ -1011,9 +1015,9 @@ static int fp8_write_impl(const void* keys, const void* values, int dtype, const
   }
   if (int rc = check_launch("fp8_cache_write")) return rc;
   if (turn_q) {  // larger writes: the queries in their own launch
-    const long nq = (long)num_tokens * num_q_heads * (rope.rot / 2);
+    const long nq = (long)num_tokens * num_q_heads * (head_dim / 2);
     hipLaunchKernelGGL(emx::rope_rows, dim3((unsigned)std::min<long>((nq + 255) / 256, 4096)), dim3(256), 0, st,
-                       reinterpret_cast<emx::h16*>(queries), num_tokens, num_q_heads, head_dim, rope);
+                       a.q, a.q_in, num_tokens, num_q_heads, head_dim, rope);
     return check_launch("rope_rows");
   }
   return EMX_OK;
@@ -1025,7 +1029,7 @@ int emx_fp8_cache_write(const void* keys, const void* values, int dtype, const i
                         size_t workspace_bytes, void* stream) {
   return fp8_write_impl(keys, values, dtype, slot_mapping, num_tokens, num_kv_heads, head_dim, page_size, num_blocks,
                         key_cache, value_cache, k_scales, v_scales, workspace, workspace_bytes,
-                        emx::RopeArgs{nullptr, nullptr, 0, 0}, nullptr, 0, stream);
+                        emx::RopeArgs{nullptr, nullptr, 0, 0}, nullptr, nullptr, 0, stream);
 }
 
 int emx_fp8_cache_write_noalloc(const void* keys, const void* values, int dtype, const int32_t* slot_mapping,
@@ -1040,22 +1044,24 @@ int emx_fp8_cache_write_noalloc(const void* keys, const void* values, int dtype,
   if (num_tokens > 0 && ws == nullptr) return EMX_ERR_HIP;
   return fp8_write_impl(keys, values, dtype, slot_mapping, num_tokens, num_kv_heads, head_dim, page_size, num_blocks,
                         key_cache, value_cache, k_scales, v_scales, ws, sizeof(float) * kNoallocScratchFloats,
-                        emx::RopeArgs{nullptr, nullptr, 0, 0}, nullptr, 0, stream);
+                        emx::RopeArgs{nullptr, nullptr, 0, 0}, nullptr, nullptr, 0, stream);
 }
 
 int emx_fp8_cache_write_rope(const void* keys, const void* values, int dtype, const int32_t* slot_mapping,
                              int num_tokens, int num_kv_heads, int head_dim, int page_size, int num_blocks,
                              uint8_t* key_cache, uint8_t* value_cache, float* k_scales, float* v_scales,
                              void* workspace, size_t workspace_bytes, const int32_t* positions, const float* inv_freq,
-                             int rot_dims, int traditional, void* queries, int num_q_heads, void* stream) {
+                             int rot_dims, int traditional, const void* queries_in, void* queries,
+                             int num_q_heads, void* stream) {
   if (num_tokens > 0 && (!rope_ok(positions, inv_freq, rot_dims, head_dim) || rot_dims % (traditional ? 4 : 8) != 0))
     return fail(EMX_ERR_INVALID,
                 "rope: positions and inv_freq needed, rot_dims in (0, head_dim] and a multiple of 8 (4 if traditional)");
   if (queries != nullptr && num_q_heads <= 0) return fail(EMX_ERR_INVALID, "queries need num_q_heads > 0");
+  if (queries_in != nullptr && queries == nullptr) return fail(EMX_ERR_INVALID, "queries_in needs queries");
   return fp8_write_impl(keys, values, dtype, slot_mapping, num_tokens, num_kv_heads, head_dim, page_size, num_blocks,
                         key_cache, value_cache, k_scales, v_scales, workspace, workspace_bytes,
-                        emx::RopeArgs{inv_freq, positions, rot_dims, traditional ? 1 : 0}, queries, num_q_heads,
-                        stream);
+                        emx::RopeArgs{inv_freq, positions, rot_dims, traditional ? 1 : 0}, queries_in, queries,
+                        num_q_heads, stream);
 }
 
 int emx_paged_attention_fp8(const void* queries, int num_tokens, int num_q_heads, int head_dim, int dtype,

@@ -16,6 +16,7 @@
 #pragma once
 
 #include "common.hpp"
+#include "quantize.hpp"  // turn_rows
 
 namespace emx {
 
@@ -33,7 +34,8 @@ struct Fp8WriteArgs {
   float* vs;
   float* part;           // [2][kFp8Parts] per-workgroup maxima
   RopeArgs rope;         // K turned before the scale and the codes (inv_freq null: none)
-  h16* q;                // [T, Hq, D] fp16 queries turned in place by the one-launch write (null: none)
+  h16* q;                // [T, Hq, D] fp16 turned queries, written by the one-launch write (null: none)
+  const h16* q_in;       // the queries to turn (== q: in place)
   int Hq;
   int nwg;               // workgroups of the write proper; later ones turn the queries
 };
@@ -120,19 +122,8 @@ __global__ __launch_bounds__(SELF ? 1024 : 256) void fp8_write(Fp8WriteArgs a, i
   __shared__ float sc[2];
   if constexpr (SELF) {
     if ((int)blockIdx.x >= a.nwg) {  // the query rotation rides in the same launch
-      const RopeArgs& r = a.rope;
-      const int half = r.rot / 2;
-      const long n = (long)a.T * a.Hq * half;
-      for (long i = (long)(blockIdx.x - a.nwg) * NTH + threadIdx.x; i < n; i += (long)(gridDim.x - a.nwg) * NTH) {
-        const int p = (int)(i % half);
-        const long rh = i / half;
-        h16* v = a.q + rh * a.D;
-        const int i0 = r.traditional ? 2 * p : p, i1 = r.traditional ? 2 * p + 1 : p + half;
-        float y0, y1;
-        rope_rotate((float)v[i0], (float)v[i1], (float)r.positions[rh / a.Hq] * r.inv_freq[p], y0, y1);
-        v[i0] = (h16)y0;
-        v[i1] = (h16)y1;
-      }
+      turn_rows(a.q, a.q_in, a.T, a.Hq, a.D, a.rope, (long)(blockIdx.x - a.nwg) * NTH + threadIdx.x,
+                (long)(gridDim.x - a.nwg) * NTH);
       return;
     }
     // a small write in one launch: every workgroup takes the maxima over all the

@@ -107,18 +107,35 @@ __device__ __forceinline__ void rope_pair(h16& a0, h16& a1, const float theta) {
   a1 = (h16)y1;
 }
 
-// Rows x [rows, heads, D] fp16 rotated in place; row r is at positions[r].
-__global__ __launch_bounds__(256) void rope_rows(h16* x, int rows, int heads, int D, RopeArgs r) {
+// Rows [rows, heads, D] fp16: x = src turned; row r is at positions[r].  src ==
+// x turns in place; otherwise the dims past r.rot are copied as they are.  Pair
+// slot i of a thread range [i_first, n) with stride `stride`.
+__device__ __forceinline__ void turn_rows(h16* x, const h16* src, const int rows, const int heads, const int D,
+                                          const RopeArgs& r, const long i_first, const long stride) {
   const int half = r.rot / 2;
-  const long n = (long)rows * heads * half;
-  for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n; i += (long)gridDim.x * 256) {
-    const int p = (int)(i % half);
-    const long rh = i / half;
-    const int row = (int)(rh / heads);
+  const int per_row = src == x ? half : D / 2;  // out of place: every dim pair of the row
+  const long n = (long)rows * heads * per_row;
+  for (long i = i_first; i < n; i += stride) {
+    const int p = (int)(i % per_row);
+    const long rh = i / per_row;
+    const h16* u = src + rh * D;
     h16* v = x + rh * D;
-    const int i0 = r.traditional ? 2 * p : p, i1 = r.traditional ? 2 * p + 1 : p + half;
-    rope_pair(v[i0], v[i1], (float)r.positions[row] * r.inv_freq[p]);
+    if (p < half) {
+      const int i0 = r.traditional ? 2 * p : p, i1 = r.traditional ? 2 * p + 1 : p + half;
+      h16 a0 = u[i0], a1 = u[i1];
+      rope_pair(a0, a1, (float)r.positions[rh / heads] * r.inv_freq[p]);
+      v[i0] = a0;
+      v[i1] = a1;
+    } else {
+      const int j = r.rot + 2 * (p - half);
+      v[j] = u[j];
+      v[j + 1] = u[j + 1];
+    }
   }
+}
+
+__global__ __launch_bounds__(256) void rope_rows(h16* x, const h16* src, int rows, int heads, int D, RopeArgs r) {
+  turn_rows(x, src, rows, heads, D, r, (long)blockIdx.x * 256 + threadIdx.x, (long)gridDim.x * 256);
 }
 
 struct WriteArgs {
@@ -131,7 +148,8 @@ struct WriteArgs {
   h16 *vs, *vb;                // [nb, Hkv, D/gs, bs]
   int T, Hkv, D, gs, bs, nb;
   RopeArgs rope;               // K rotation before quantizing (inv_freq null: none)
-  h16* q;                      // [T, Hq, D] queries turned in place by the same launch (null: none)
+  h16* q;                      // [T, Hq, D] turned queries, written by the same launch (null: none)
+  const h16* q_in;             // the queries to turn (== q: in place)
   int Hq;
 };
 
@@ -295,18 +313,9 @@ __global__ __launch_bounds__(256) void affine_cache_write_small(WriteArgs a) {
     // the extra rows of workgroups turn the queries (rows of gridDim.x * kQRopeBlocks workgroups)
     if (d0 >= a.D) {
       if (a.q == nullptr) return;
-      const RopeArgs& r = a.rope;
-      const int half = r.rot / 2;
       const int nwg = gridDim.x * kQRopeBlocks;
       const int wg = (blockIdx.y - a.D / DB) * gridDim.x + blockIdx.x;
-      const long n = (long)a.T * a.Hq * half;
-      for (long i = (long)wg * 256 + tid; i < n; i += (long)nwg * 256) {
-        const int p = (int)(i % half);
-        const long rh = i / half;
-        h16* v = a.q + rh * a.D;
-        const int i0 = r.traditional ? 2 * p : p, i1 = r.traditional ? 2 * p + 1 : p + half;
-        rope_pair(v[i0], v[i1], (float)r.positions[rh / a.Hq] * r.inv_freq[p]);
-      }
+      turn_rows(a.q, a.q_in, a.T, a.Hq, a.D, a.rope, (long)wg * 256 + tid, (long)nwg * 256);
       return;
     }
   }

@@ -74,8 +74,10 @@ int emx_affine_cache_write(const void* keys, const void* values, const int32_t* 
  * ((i, i + rot_dims/2), or (2i, 2i+1) when traditional != 0), are rounded to
  * fp16 and then quantized exactly as emx_affine_cache_write does.  V is not
  * rotated.  positions int32 [num_tokens], inv_freq float32 [rot_dims/2].
- * queries (fp16 [num_tokens, num_q_heads, head_dim], or null) are turned in
- * place by the same rotation, in the same launch for decode-size writes.
+ * queries (fp16 [num_tokens, num_q_heads, head_dim], or null) receive
+ * queries_in turned by the same rotation (the dims past rot_dims copied), in
+ * the same launch for decode-size writes; queries_in null turns queries in
+ * place.
  * Replaces the RoPE applied to keys in PageCacheView.concatenate_to_cache
  *   lib/python/easymlx/caching/paged/cache.py:1161-1166 (multi-token :1208-1253)
  *   followed by the write :1186-1190, with the RoPE of
@@ -85,7 +87,8 @@ int emx_affine_cache_write_rope(const void* keys, const void* values, const int3
                                 int num_kv_heads, int head_dim, int group_size, int bits, int page_size,
                                 int num_blocks, uint32_t* k_codes, void* k_scales, void* k_biases, uint32_t* v_codes,
                                 void* v_scales, void* v_biases, const int32_t* positions, const float* inv_freq,
-                                int rot_dims, int traditional, void* queries, int num_q_heads, void* stream);
+                                int rot_dims, int traditional, const void* queries_in, void* queries,
+                                int num_q_heads, void* stream);
 
 /*
  * Write positions of a cache write, on the device: token t of sequence i
@@ -303,7 +306,8 @@ int emx_fp8_cache_write_noalloc(const void* keys, const void* values, int dtype,
  * scale and codes are taken over the keys turned as in
  * emx_affine_cache_write_rope and rounded to dtype.  rot_dims a multiple of 8
  * (of 4 when traditional).  queries (fp16 [num_tokens, num_q_heads, head_dim],
- * or null) are turned in place, in the same launch for decode-size writes.
+ * or null) receive queries_in turned (null: queries turned in place), in the
+ * same launch for decode-size writes.
  * Replaces the RoPE of PageCacheView.concatenate_to_cache
  *   lib/python/easymlx/caching/paged/cache.py:1161-1166 followed by its FP8 write :1171-1184.
  */
@@ -311,7 +315,8 @@ int emx_fp8_cache_write_rope(const void* keys, const void* values, int dtype, co
                              int num_tokens, int num_kv_heads, int head_dim, int page_size, int num_blocks,
                              uint8_t* key_cache, uint8_t* value_cache, float* k_scales, float* v_scales,
                              void* workspace, size_t workspace_bytes, const int32_t* positions, const float* inv_freq,
-                             int rot_dims, int traditional, void* queries, int num_q_heads, void* stream);
+                             int rot_dims, int traditional, const void* queries_in, void* queries,
+                             int num_q_heads, void* stream);
 
 /*
  * Paged attention over an FP8 (E4M3) cache key/value [num_blocks, page_size,

@@ -62,13 +62,14 @@ def test_rope_rows_vs_float64(cuda, traditional, kind):
     assert np.array_equal(got[..., rope.dims:], x[..., rope.dims:])
 
 
-@pytest.mark.parametrize("bits,T", [(4, 300), (4, 32), (8, 77)])
-def test_fused_write_equals_rotate_then_write(cuda, bits, T):
-    """One launch (rotate K in LDS, quantize) == emx_rope_rows on K, then emx_affine_cache_write: every byte."""
-    print(f"[fused rope write bits={bits} T={T}]", flush=True)
+@pytest.mark.parametrize("bits,T,rot", [(4, 300, 128), (4, 32, 128), (8, 77, 128), (4, 32, 64), (4, 300, 64)])
+def test_fused_write_equals_rotate_then_write(cuda, bits, T, rot):
+    """One launch (rotate K in LDS, quantize) == emx_rope_rows on K, then emx_affine_cache_write: every byte.
+    The queries come out turned into a separate tensor (dims past rot copied), or turned in place."""
+    print(f"[fused rope write bits={bits} T={T} rot={rot}]", flush=True)
     rng = np.random.default_rng(9 + bits + T)
     hkv, d, bs, nb = 8, 128, 128, 16
-    rope = RotaryEmbedding.llama3(128, base=500000.0)
+    rope = RotaryEmbedding.llama3(rot, base=500000.0)
     k = torch.from_numpy((rng.standard_normal((T, hkv, d)) * 2).astype(np.float16)).to(cuda)
     v = torch.from_numpy((rng.standard_normal((T, hkv, d)) * 2).astype(np.float16)).to(cuda)
     slots = torch.from_numpy(rng.permutation(nb * bs)[:T].astype(np.int32)).to(cuda)
@@ -83,17 +84,26 @@ def test_fused_write_equals_rotate_then_write(cuda, bits, T):
     st = torch.cuda.current_stream(cuda).cuda_stream
     inv = rope.inv_freq(cuda)
     q = torch.from_numpy(rng.standard_normal((T, 32, d)).astype(np.float16)).to(cuda)
-    qa = q.clone()  # turned by the write's own launch
-    _native.check(lib.emx_affine_cache_write_rope(
-        k.data_ptr(), v.data_ptr(), slots.data_ptr(), T, hkv, d, 64, bits, bs, nb, a.key_cache.data_ptr(),
-        a.k_scales.data_ptr(), a.k_biases.data_ptr(), a.value_cache.data_ptr(), a.v_scales.data_ptr(),
-        a.v_biases.data_ptr(), pos.data_ptr(), inv.data_ptr(), rope.dims, 0, qa.data_ptr(), 32, st))
+    q0 = q.clone()
+    qo = torch.full_like(q, float("nan"))  # every element written by the launch
+    qa = q.clone()  # turned in place
+
+    def call(q_in, q_out):
+        _native.check(lib.emx_affine_cache_write_rope(
+            k.data_ptr(), v.data_ptr(), slots.data_ptr(), T, hkv, d, 64, bits, bs, nb, a.key_cache.data_ptr(),
+            a.k_scales.data_ptr(), a.k_biases.data_ptr(), a.value_cache.data_ptr(), a.v_scales.data_ptr(),
+            a.v_biases.data_ptr(), pos.data_ptr(), inv.data_ptr(), rope.dims, 0, q_in, q_out.data_ptr(), 32, st))
+
+    call(q.data_ptr(), qo)
+    call(None, qa)  # the same write again: the pages come out the same
     kr, qb = k.clone(), q.clone()
     _rope_rows(kr, pos, rope)
     _rope_rows(qb, pos, rope)
     b.write_slots(kr, v, slots)
     torch.cuda.synchronize()
-    assert torch.equal(qa, qb), "queries"
+    assert torch.equal(q, q0), "queries_in left as it was"
+    assert torch.equal(qo, qb), "queries turned out of place"
+    assert torch.equal(qa, qb), "queries turned in place"
     for name in ("key_cache", "k_scales", "k_biases", "value_cache", "v_scales", "v_biases"):
         assert torch.equal(getattr(a, name), getattr(b, name)), name
 
@@ -157,18 +167,20 @@ def test_fp8_fused_write_equals_rotate_then_write(cuda, traditional, T):
     lib = _native.load()
     ws = torch.empty(int(lib.emx_fp8_write_workspace_bytes()), dtype=torch.uint8, device=cuda)
     q = torch.from_numpy(rng.standard_normal((T, 16, d)).astype(np.float16)).to(cuda)
-    qa = q.clone()
+    q0 = q.clone()
+    qo = torch.full_like(q, float("nan"))  # every element written by the launch
     _native.check(lib.emx_fp8_cache_write_rope(
         k.data_ptr(), v.data_ptr(), _native.DTYPE_F16, slots.data_ptr(), T, hkv, d, bs, nb, a.key_cache.data_ptr(),
         a.value_cache.data_ptr(), a.k_scales.data_ptr(), a.v_scales.data_ptr(), ws.data_ptr(), ws.numel(),
-        pos.data_ptr(), rope.inv_freq(cuda).data_ptr(), rope.dims, int(traditional), qa.data_ptr(), 16,
+        pos.data_ptr(), rope.inv_freq(cuda).data_ptr(), rope.dims, int(traditional), q.data_ptr(), qo.data_ptr(), 16,
         torch.cuda.current_stream(cuda).cuda_stream))
     kr, qb = k.clone(), q.clone()
     _rope_rows(kr, pos, rope)
     _rope_rows(qb, pos, rope)
     b.write_slots(kr, v, slots)
     torch.cuda.synchronize()
-    assert torch.equal(qa, qb), "queries"
+    assert torch.equal(q, q0), "queries_in left as it was"
+    assert torch.equal(qo, qb), "queries"
     for name in ("key_cache", "value_cache", "k_scales", "v_scales"):
         assert torch.equal(getattr(a, name), getattr(b, name)), name
 

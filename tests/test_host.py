@@ -248,13 +248,15 @@ def test_abi_rope_and_prefill_split_arguments(lib):
     assert b"rope" in lib.emx_last_error()
     # fused writes: the same checks before any pointer is touched; FP8 needs rot_dims % 8 (4 if traditional)
     args = [p_one, p_one, p_one, 4, 8, 128, 64, 4, 128, 16] + [p_one] * 6
-    assert lib.emx_affine_cache_write_rope(*args, None, p_inv, 128, 0, None, 0, None) == err
-    assert lib.emx_affine_cache_write_rope(*args, p_one, p_inv, 0, 0, None, 0, None) == err
-    assert lib.emx_affine_cache_write_rope(*args, p_one, p_inv, 128, 0, p_one, 0, None) == err  # no q heads
+    assert lib.emx_affine_cache_write_rope(*args, None, p_inv, 128, 0, None, None, 0, None) == err
+    assert lib.emx_affine_cache_write_rope(*args, p_one, p_inv, 0, 0, None, None, 0, None) == err
+    assert lib.emx_affine_cache_write_rope(*args, p_one, p_inv, 128, 0, None, p_one, 0, None) == err  # no q heads
+    assert lib.emx_affine_cache_write_rope(*args, p_one, p_inv, 128, 0, p_one, None, 8, None) == err  # in, no out
     fargs = [p_one, p_one, _native.DTYPE_F16, p_one, 4, 8, 128, 128, 16, p_one, p_one, p_one, p_one, p_one, 2048]
-    assert lib.emx_fp8_cache_write_rope(*fargs, p_one, p_inv, 12, 0, None, 0, None) == err
-    assert lib.emx_fp8_cache_write_rope(*fargs, p_one, p_inv, 10, 1, None, 0, None) == err
-    assert lib.emx_fp8_cache_write_rope(*fargs, p_one, p_inv, 128, 0, p_one, 0, None) == err  # no q heads
+    assert lib.emx_fp8_cache_write_rope(*fargs, p_one, p_inv, 12, 0, None, None, 0, None) == err
+    assert lib.emx_fp8_cache_write_rope(*fargs, p_one, p_inv, 10, 1, None, None, 0, None) == err
+    assert lib.emx_fp8_cache_write_rope(*fargs, p_one, p_inv, 128, 0, None, p_one, 0, None) == err  # no q heads
+    assert lib.emx_fp8_cache_write_rope(*fargs, p_one, p_inv, 128, 0, p_one, None, 8, None) == err  # in, no out
     # FP8 writes index words with 32 bits: more than 2^33 values per tensor are refused before any launch
     big = list(fargs)
     big[4] = 1 << 24  # 2^24 tokens x 8 heads x 128 dims = 2^34 values
