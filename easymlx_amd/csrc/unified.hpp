@@ -1,14 +1,16 @@
-// One launch for a mixed batch over 4-bit pages or an FP8 cache (the unified ragged step of
+// One launch for a mixed batch (the unified ragged step of
 // lib/python/easymlx/operations/kernels/unified_attention.py:290-609, which the
 // reference runs as one Metal dispatch over all rows): the first ndec workgroups
-// run the 4-bit decode body on the single-token rows, the others the prefill
-// body on the rows of sequences with more than one query token.  Workgroups
+// run a decode body (4-bit 4x4x4, 16x16x32 or FP8) on the single-token rows, the
+// others the prefill body on the rows of sequences with more than one query
+// token.  Workgroups
 // start in index order, so the decode workgroups (few: the host sizes them to
 // the decode rows' share of the work) take one slot on some compute units from
 // the start and stream their pages beside the prefill's matrix work on the
 // same units.  The two bodies share the LDS arena and nothing else.
 #pragma once
 
+#include "decode_affine.hpp"
 #include "decode_fp8.hpp"
 #include "decode_q4.hpp"
 #include "prefill_affine.hpp"
