@@ -96,6 +96,33 @@ def test_decode_long_context_split(cuda):
     assert_attention_close(_run(wl, view, cuda), oracle_expected(wl), "c4-shape")
 
 
+@pytest.mark.parametrize("seqs,ctx", [(64, (64, 512)), (40, (257, 512)), (300, (1, 256))],
+                         ids=["short64", "two-item-units", "one-item-units"])
+def test_decode_short_units_whole_ranges(cuda, seqs, ctx):
+    """4-bit decode where every unit is at most two items: ranges end on unit starts (some empty), so no
+    unit is split between workgroups."""
+    print(f"[decode short units seqs={seqs} ctx={ctx}]", flush=True)
+    wl = decode_workload(seed=31 + seqs, num_seqs=seqs, ctx_range=ctx, bits=4)
+    view = gpu_cache(wl, cuda)
+    got = _run(wl, view, cuda)
+    assert_attention_close(got, oracle_expected(wl), f"short units {seqs}")
+    assert np.array_equal(_run(wl, view, cuda), got), "repeat differs"
+
+
+@pytest.mark.parametrize("seed,bits,hq,gs,seqs,ctx", [(331, 8, 32, 64, 300, (1, 256)), (332, 4, 64, 64, 300, (1, 256)),
+                                                       (333, 8, 32, 32, 200, (1, 600)), (334, 4, 32, 64, 300, (1, 256))],
+                         ids=["8bit", "4bit-gqa8", "8bit-g32", "4bit"])
+def test_decode_bias_cancellation(cuda, seed, bits, hq, gs, seqs, ctx):
+    """Short contexts over channels with large biases: outputs near zero come from sum P' * code cancelling
+    sum p * v_bias, so P' = p * v_scale must enter the matrix core with more than fp16's 11 bits (these cases
+    had 6 (4bit-gqa8) and 1 (4bit) elements outside the tolerance with a single fp16 P'; max err / tol is now
+    0.05 - 0.31)."""
+    print(f"[decode bias cancellation bits={bits} hq={hq} gs={gs}]", flush=True)
+    wl = decode_workload(seed=seed, num_seqs=seqs, ctx_range=ctx, bits=bits, num_q_heads=hq, group_size=gs)
+    view = gpu_cache(wl, cuda)
+    assert_attention_close(_run(wl, view, cuda), oracle_expected(wl), f"bias cancellation {bits}/{hq}/{gs}")
+
+
 def test_decode_sliding_window(cuda):
     print("[decode sliding window]", flush=True)
     wl = decode_workload(seed=8, num_seqs=6, ctx_range=(10, 2000), bits=4)
