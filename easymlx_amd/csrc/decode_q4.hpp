@@ -18,7 +18,7 @@
 //            s = sum_g scale[t,g] * C_g + bias[t,g] * sum_{d in g} q_d
 //   softmax: online, base 2, fp32; the per-head max and sum run over the 16
 //          lanes of a head (DPP row rotations, then two cross-row shuffles).
-//   PV   : A = P' = p * v_scale[t, g] in fp16, lane layout exactly as the QK
+//   PV   : A = P' = p * v_scale[t, g] as fp16 hi + lo (two MFMAs), lane layout exactly as the QK
 //          output; block tau of A is broadcast to all blocks (cbsz 4, abid
 //          tau), so no transpose is needed.  B = V codes, lane L holds dims L
 //          and 64 + L (one group half each).  Output: lane L holds dims L and
