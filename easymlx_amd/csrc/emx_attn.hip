@@ -20,6 +20,7 @@
 #include "fp8.hpp"
 #include "decode_fp8.hpp"
 #include "slots.hpp"
+#include "probe.hpp"
 #include "pages.hpp"
 
 constexpr int kNoallocScratchFloats = 2 * emx::kFp8Parts;  // 2 KiB
@@ -633,6 +634,50 @@ int emx_gather_kv_affine(const uint32_t* k_codes, const void* k_scales, const vo
                                         group_size},
                        block_table, num_seqs, max_blocks_per_seq, cu_seq_lens, total_tokens, num_blocks, out_dtype,
                        k_out, v_out, stream);
+}
+
+int emx_probe_page_read(const uint32_t* k_codes, const void* k_scales, const void* k_biases, const uint32_t* v_codes,
+                        const void* v_scales, const void* v_biases, int num_blocks, int page_size, int num_kv_heads,
+                        int head_dim, int bits, int group_size, const int32_t* block_tables, int num_seqs,
+                        int max_blocks_per_seq, const int32_t* kv_lens, uint32_t* sink, int sink_words,
+                        void* stream) {
+  if (bits != 4 && bits != 8) return fail(EMX_ERR_UNSUPPORTED, "bits must be 4 or 8, got %d", bits);
+  if (head_dim != 128 || page_size <= 0 || page_size % 64 || num_kv_heads <= 0 || num_blocks <= 0 ||
+      (group_size != 32 && group_size != 64 && group_size != 128))
+    return fail(EMX_ERR_UNSUPPORTED, "probe geometry: head_dim 128, page_size a multiple of 64, group 32/64/128");
+  if (num_seqs <= 0 || max_blocks_per_seq <= 0 || sink_words <= 0)
+    return fail(EMX_ERR_INVALID, "num_seqs, max_blocks_per_seq and sink_words must be > 0");
+  if (!k_codes || !k_scales || !k_biases || !v_codes || !v_scales || !v_biases || !block_tables || !kv_lens || !sink)
+    return fail(EMX_ERR_INVALID, "null pointer");
+  if (!aligned16(k_codes) || !aligned16(v_codes) || !aligned16(k_scales) || !aligned16(k_biases) ||
+      !aligned16(v_scales) || !aligned16(v_biases))
+    return fail(EMX_ERR_INVALID, "cache tensors must be 16-byte aligned");
+  emx::ProbeArgs a;
+  a.kc = k_codes;
+  a.ks = reinterpret_cast<const emx::h16*>(k_scales);
+  a.kb = reinterpret_cast<const emx::h16*>(k_biases);
+  a.vs = reinterpret_cast<const emx::h16*>(v_scales);
+  a.vb = reinterpret_cast<const emx::h16*>(v_biases);
+  a.vc = v_codes;
+  a.block_tables = block_tables;
+  a.kv_lens = kv_lens;
+  a.sink = sink;
+  a.S = num_seqs;
+  a.Hkv = num_kv_heads;
+  a.bs = page_size;
+  a.nb = num_blocks;
+  a.max_blocks = max_blocks_per_seq;
+  a.G = head_dim / group_size;
+  const long long nsl = (long long)num_seqs * max_blocks_per_seq * (page_size / 64) * num_kv_heads;
+  if (nsl >= (1LL << 31) - (1LL << 24)) return fail(EMX_ERR_UNSUPPORTED, "too many page slices (%lld)", nsl);
+  a.nsl = (int)nsl;
+  const int grid = std::min(sink_words, 8 * device_cus());
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (bits == 4)
+    hipLaunchKernelGGL(emx::probe_page_read<4>, dim3(grid), dim3(256), 0, st, a);
+  else
+    hipLaunchKernelGGL(emx::probe_page_read<8>, dim3(grid), dim3(256), 0, st, a);
+  return check_launch("probe_page_read");
 }
 
 int emx_gather_kv_fp8(const uint8_t* key_cache, const uint8_t* value_cache, const float* k_scale,

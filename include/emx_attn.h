@@ -168,6 +168,21 @@ int emx_affine_logical_from_pages(const uint32_t* k_codes, const uint32_t* v_cod
                                   void* k_biases_out, void* v_scales_out, void* v_biases_out, void* stream);
 
 /*
+ * Page-read probe (measurement only; no counterpart in the reference): reads
+ * exactly the page bytes a decode call over these 4-bit or 8-bit affine pages
+ * (head_dim 128, page_size a multiple of 64) reads -- K codes, V codes and the
+ * four scale / bias runs of every 64-token slice of a page-head that holds a
+ * token below kv_lens -- and nothing else, so bytes / time is the read
+ * bandwidth this call's scattered pattern gets from the memory system.  Each
+ * workgroup stores the XOR of the 32-bit words it read into sink[w]; it runs
+ * min(sink_words, 8 x compute units) workgroups of 256 threads.
+ */
+int emx_probe_page_read(const uint32_t* k_codes, const void* k_scales, const void* k_biases, const uint32_t* v_codes,
+                        const void* v_scales, const void* v_biases, int num_blocks, int page_size, int num_kv_heads,
+                        int head_dim, int bits, int group_size, const int32_t* block_tables, int num_seqs,
+                        int max_blocks_per_seq, const int32_t* kv_lens, uint32_t* sink, int sink_words, void* stream);
+
+/*
  * Dense K/V of a ragged batch gathered from pages: token t of sequence b
  * (cu_seq_lens[b] <= t < cu_seq_lens[b+1], int32 [num_seqs+1] on the device) at
  * offset j = t - cu_seq_lens[b] is entry j % page_size of page
