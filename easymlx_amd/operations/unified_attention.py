@@ -56,6 +56,10 @@ def _validate_inputs(queries, key_cache, value_cache, block_tables, kv_lens, que
         raise ValueError("queries must be rank-3: [total_tokens, num_q_heads, head_dim]")
     if not affine and (key_cache.ndim != 4 or value_cache.ndim != 4):
         raise ValueError("key_cache/value_cache must be rank-4: [num_blocks, block_size, num_kv_heads, head_dim]")
+    if affine and key_cache.ndim == 4 and value_cache.ndim == 4:
+        # mlx.core.quantize of the reference's dense [num_blocks, block_size, Hkv, D] caches: the logical layout
+        raise ValueError("affine caches in the logical layout [num_blocks, block_size, num_kv_heads, W] must be "
+                         "converted to pages once (AffinePageCacheView.from_logical / emx_affine_pages_from_logical)")
     if affine and (key_cache.ndim != 4 or value_cache.ndim != 5):
         raise ValueError("affine pages must be key codes [num_blocks, num_kv_heads, block_size, W] and value codes "
                          "[num_blocks, num_kv_heads, block_size/T, head_dim, T*bits/32]")

@@ -152,6 +152,11 @@ def test_validation_messages():
         paged_attention(q, k, v, bt, kl, qsl[:-1])
     with pytest.raises(ValueError, match="affine caches need"):
         paged_attention(q, k, v, bt, kl, qsl, k_scales=torch.zeros(1))
+    # affine codes in the logical (mlx.core.quantize) layout: told how to convert them
+    z = torch.zeros(1)
+    with pytest.raises(ValueError, match="from_logical"):
+        paged_attention(q, k.int(), v.int(), bt, kl, qsl, k_scales=z, k_biases=z, v_scales=z, v_biases=z, bits=4,
+                        group_size=8)
     # zero tokens -> zeros without touching a device (unified_attention.py:1425-1426)
     out = paged_attention(torch.ones(0, 4, 8), k, v, bt, kl, torch.zeros(3, dtype=torch.int32))
     assert out.shape == (0, 4, 8)
