@@ -86,8 +86,10 @@ def _validate_inputs(queries, key_cache, value_cache, block_tables, kv_lens, que
 
 
 def _is_single_token_decode(query_start_loc: torch.Tensor, total_tokens: int) -> bool:
-    """``unified_attention.py:175-184`` (reads ``query_start_loc`` on the host)."""
-    if total_tokens <= 0:
+    """``unified_attention.py:175-184``.  Reads ``query_start_loc`` on the host only when its length allows a
+    pure decode batch (one token per sequence needs ``num_seqs == total_tokens``): the shape decides the rest
+    without a device synchronisation."""
+    if total_tokens <= 0 or query_start_loc.ndim != 1 or query_start_loc.shape[0] != total_tokens + 1:
         return False
     qsl = query_start_loc.detach().to("cpu", torch.int64)
     if qsl.ndim != 1 or qsl.shape[0] != total_tokens + 1 or int(qsl[0]) != 0:
