@@ -355,7 +355,7 @@ def aux_fp8(dev):
     """
     import torch
 
-    from easymlx_amd import Fp8PageCacheView, paged_attention
+    from easymlx_amd import Fp8PageCacheView, _native, paged_attention
     from easymlx_amd.workloads import decode_workload
 
     wl = decode_workload(seed=2, bits=None)
@@ -385,6 +385,26 @@ def aux_fp8(dev):
     warm(call, 0.3)
     us = float(np.median(event_us(call, 100)))
     b2b = b2b_us(call, 100)
+    # measured read peak: the FP8 page-read probe over the same pools (the rows the decode reads, loads only)
+    lib = _native.load()
+    sink = torch.zeros(2048, dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    mb = int(wl.block_tables.shape[1])
+
+    def probe_call(i=0, words=1024):
+        kc, vc, ks, vs = pools[i % len(pools)]
+        _native.check(lib.emx_probe_page_read_fp8(
+            kc.data_ptr(), vc.data_ptr(), ks.data_ptr(), vs.data_ptr(), nb, wl.block_size, wl.num_kv_heads,
+            wl.head_dim, view.block_tables.data_ptr(), wl.num_seqs, mb, view.kv_lens.data_ptr(), sink.data_ptr(),
+            words, stream))
+
+    probe = {}
+    for words in (256, 512, 1024, 2048):
+        warm(lambda i=0: probe_call(i, words), 0.1)
+        probe[words] = b2b_us(lambda i=0: probe_call(i, words), 100)
+    pus = min(probe.values())
+    lens = np.maximum(wl.kv_lens.astype(np.int64), 0)
+    probe_bytes = int(((lens + 31) // 32).sum()) * wl.num_kv_heads * (2 * 32 * wl.head_dim + 8)
     n_fp8_pools = len(pools)
     del pools
     nbytes = int(wl.kv_lens.astype(np.int64).sum()) * wl.num_kv_heads * 2 * wl.head_dim
@@ -420,6 +440,8 @@ def aux_fp8(dev):
             "rotated_pools": n_fp8_pools, "pool_bytes": int(pool_bytes),
             "unified_c3_shape_us_p50": round(uus, 2),
             "decode_us_p50": round(us, 2), "decode_us_back_to_back": round(b2b, 2), "kv_bytes": nbytes,
+            "measured_read_peak": {"us": round(pus, 2), "GBs": round(probe_bytes / (pus * 1e3), 1),
+                                   "frac_of_it": round(pus / b2b, 4)},
             "kv_GBs": round(nbytes / (b2b * 1e3), 1), "frac": round(nbytes / (b2b * 1e3) / HBM_PEAK_GBS, 4),
             "write_32_tokens_us_p50": round(wus, 2),
             "timing": "*_us_p50: events around each call (launch gap included); kv_GBs and frac: back to back"}

@@ -46,6 +46,7 @@ SIGNATURES: dict[str, tuple] = {
     "emx_affine_pages_from_logical": (_I, [_P] * 6 + [_I] * 6 + [_P] * 7),
     "emx_affine_logical_from_pages": (_I, [_P] * 6 + [_I] * 6 + [_P] * 7),
     "emx_probe_page_read": (_I, [_P] * 6 + [_I] * 6 + [_P, _I, _I, _P, _P, _I, _P]),
+    "emx_probe_page_read_fp8": (_I, [_P] * 4 + [_I] * 4 + [_P, _I, _I, _P, _P, _I, _P]),
     "emx_gather_kv_fp8": (_I, [_P] * 4 + [_I] * 4 + [_P, _I, _I, _P, _I, _I, _P, _P, _P]),
     "emx_gather_kv_dense": (_I, [_P, _P] + [_I] * 5 + [_P, _I, _I, _P, _I, _I, _P, _P, _P]),
     "emx_zero_blocks": (_I, [_I, _P, _P, _I, _P, _I, _P]),

@@ -680,6 +680,37 @@ int emx_probe_page_read(const uint32_t* k_codes, const void* k_scales, const voi
   return check_launch("probe_page_read");
 }
 
+int emx_probe_page_read_fp8(const uint8_t* key_cache, const uint8_t* value_cache, const float* k_scale,
+                            const float* v_scale, int num_blocks, int page_size, int num_kv_heads, int head_dim,
+                            const int32_t* block_tables, int num_seqs, int max_blocks_per_seq, const int32_t* kv_lens,
+                            uint32_t* sink, int sink_words, void* stream) {
+  if (head_dim != 128 || page_size <= 0 || page_size % 32 || num_kv_heads <= 0 || num_blocks <= 0)
+    return fail(EMX_ERR_UNSUPPORTED, "probe geometry: head_dim 128, page_size a multiple of 32");
+  if (num_seqs <= 0 || max_blocks_per_seq <= 0 || sink_words <= 0)
+    return fail(EMX_ERR_INVALID, "num_seqs, max_blocks_per_seq and sink_words must be > 0");
+  if (!key_cache || !value_cache || !k_scale || !v_scale || !block_tables || !kv_lens || !sink)
+    return fail(EMX_ERR_INVALID, "null pointer");
+  const long long nsl = (long long)num_seqs * max_blocks_per_seq * (page_size / 32) * num_kv_heads;
+  if (nsl >= (1LL << 31) - (1LL << 24)) return fail(EMX_ERR_UNSUPPORTED, "too many page slices (%lld)", nsl);
+  emx::ProbeFp8Args a;
+  a.k8 = key_cache;
+  a.v8 = value_cache;
+  a.kps = k_scale;
+  a.vps = v_scale;
+  a.block_tables = block_tables;
+  a.kv_lens = kv_lens;
+  a.sink = sink;
+  a.S = num_seqs;
+  a.Hkv = num_kv_heads;
+  a.bs = page_size;
+  a.nb = num_blocks;
+  a.max_blocks = max_blocks_per_seq;
+  a.nsl = (int)nsl;
+  const int grid = std::min(sink_words, 8 * device_cus());
+  hipLaunchKernelGGL(emx::probe_page_read_fp8, dim3(grid), dim3(256), 0, reinterpret_cast<hipStream_t>(stream), a);
+  return check_launch("probe_page_read_fp8");
+}
+
 int emx_gather_kv_fp8(const uint8_t* key_cache, const uint8_t* value_cache, const float* k_scale,
                       const float* v_scale, int num_blocks, int page_size, int num_kv_heads, int head_dim,
                       const int32_t* block_table, int num_seqs, int max_blocks_per_seq, const int32_t* cu_seq_lens,

@@ -183,6 +183,19 @@ int emx_probe_page_read(const uint32_t* k_codes, const void* k_scales, const voi
                         int max_blocks_per_seq, const int32_t* kv_lens, uint32_t* sink, int sink_words, void* stream);
 
 /*
+ * The page-read probe over an FP8 (E4M3) cache in the reference layout
+ * [num_blocks, page_size, Hkv, 128] uint8 with fp32 page scales (measurement
+ * only; no counterpart in the reference): reads exactly what the FP8 decode
+ * reads -- the 32-token row blocks of every kv head holding a token below
+ * kv_lens, and their pages' two scales -- and nothing else.  page_size a
+ * multiple of 32; sink and workgroups as emx_probe_page_read.
+ */
+int emx_probe_page_read_fp8(const uint8_t* key_cache, const uint8_t* value_cache, const float* k_scale,
+                            const float* v_scale, int num_blocks, int page_size, int num_kv_heads, int head_dim,
+                            const int32_t* block_tables, int num_seqs, int max_blocks_per_seq, const int32_t* kv_lens,
+                            uint32_t* sink, int sink_words, void* stream);
+
+/*
  * Dense K/V of a ragged batch gathered from pages: token t of sequence b
  * (cu_seq_lens[b] <= t < cu_seq_lens[b+1], int32 [num_seqs+1] on the device) at
  * offset j = t - cu_seq_lens[b] is entry j % page_size of page

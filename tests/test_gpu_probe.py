@@ -66,3 +66,39 @@ def test_probe_rejects_unsupported_geometry(cuda):
     p = z.data_ptr()
     rc = lib.emx_probe_page_read(p, p, p, p, p, p, 1, 32, 1, 128, 4, 64, p, 1, 1, p, p, 1, None)
     assert rc == _native.EMX_ERR_UNSUPPORTED and b"page_size" in lib.emx_last_error()
+
+
+@pytest.mark.parametrize("bs", [128, 32])
+def test_probe_fp8_reads_exactly_the_live_rows(cuda, bs):
+    print(f"[probe fp8 bs={bs}]", flush=True)
+    rng = np.random.default_rng(100 + bs)
+    nb, hkv, d, S, mb = 30, 3, 128, 5, 6
+    kc = rng.integers(0, 256, (nb, bs, hkv, d), dtype=np.uint8)
+    vc = rng.integers(0, 256, (nb, bs, hkv, d), dtype=np.uint8)
+    ks = rng.random(nb, dtype=np.float32) + 0.5
+    vs = rng.random(nb, dtype=np.float32) + 0.5
+    tables = rng.integers(0, nb, (S, mb)).astype(np.int32)
+    tables[0, 1] = tables[1, 0]
+    tables[2, 2] = -1
+    lens = np.array([mb * bs, 3 * bs + 1, 5 * bs - 32, 0, 40], dtype=np.int32)
+    x = np.uint32(0)
+    for s in range(S):
+        for pg in range(mb):
+            for part in range(bs // 32):
+                b = int(tables[s, pg])
+                if pg * bs + 32 * part >= lens[s] or not 0 <= b < nb:
+                    continue
+                for kvh in range(hkv):
+                    for c in (kc, vc):
+                        x ^= np.bitwise_xor.reduce(c[b, 32 * part:32 * part + 32, kvh].copy().view(np.uint32).ravel())
+                    x ^= ks[b:b + 1].view(np.uint32)[0] ^ vs[b:b + 1].view(np.uint32)[0]
+    t = lambda a: torch.from_numpy(a).to(cuda)  # noqa: E731
+    tk, tv, tks, tvs, tt, tl = t(kc), t(vc), t(ks), t(vs), t(tables), t(lens)
+    sink = torch.zeros(1024, dtype=torch.int32, device=cuda)
+    lib = _native.load()
+    rc = lib.emx_probe_page_read_fp8(tk.data_ptr(), tv.data_ptr(), tks.data_ptr(), tvs.data_ptr(), nb, bs, hkv, d,
+                                     tt.data_ptr(), S, mb, tl.data_ptr(), sink.data_ptr(), sink.numel(),
+                                     torch.cuda.current_stream(cuda).cuda_stream)
+    _native.check(rc)
+    torch.cuda.synchronize()
+    assert np.bitwise_xor.reduce(sink.cpu().numpy().view(np.uint32)) == x
