@@ -77,6 +77,24 @@ class NativeLibraryMissing(RuntimeError):
     """Raised when ``libemx_attn.so`` has not been built."""
 
 
+def stream_ptr(device) -> int:
+    """The raw HIP stream torch currently launches on for ``device`` (what every entry point takes)."""
+    global _raw_stream, _torch
+    if _raw_stream is None:
+        import torch
+
+        _torch = torch
+        # torch's own accessor of the current raw stream (no Stream object per call); the public route otherwise
+        _raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None) or (
+            lambda i: torch.cuda.current_stream(i).cuda_stream)
+    idx = device.index
+    return _raw_stream(idx if idx is not None else _torch.cuda.current_device())
+
+
+_raw_stream = None
+_torch = None
+
+
 def load() -> ctypes.CDLL:
     """Load (once) and return the native library, with argtypes bound."""
     global _lib

@@ -109,7 +109,7 @@ class CompiledPagedCacheProxy:
         dev = c.block_tables.device
         buf = self._step_buffers(slots, dev)
         lib = _native.load()
-        stream = torch.cuda.current_stream(dev).cuda_stream
+        stream = _native.stream_ptr(dev)
         n = len(slots)
         _native.check(lib.emx_cache_slots(
             buf["slots"].data_ptr(), buf["qsl"].data_ptr(), n, n, c.block_tables.data_ptr(),

@@ -94,7 +94,7 @@ def block_mapping_on_device(block_mapping, device) -> torch.Tensor:
 
 
 def _stream_ptr(device: torch.device) -> int:
-    return torch.cuda.current_stream(device).cuda_stream
+    return _native.stream_ptr(device)
 
 
 def _contiguous_tables(num_seqs: int, blocks_per_seq: int, device) -> torch.Tensor:
@@ -209,23 +209,21 @@ class PageCacheView:
         if self.block_tables.dtype != torch.int32 or self.kv_lens.dtype != torch.int32:
             raise ValueError("block_tables and kv_lens must be int32")
         n = len(slot_ids)
-        qsl = [0]
-        for q in qlens:
-            qsl.append(qsl[-1] + max(0, int(q)))
-        total = qsl[-1]
         # the device copy of (slot ids, offsets) is kept per distinct call shape: every
         # layer of a step (and most steps) writes the same slots, and a host-to-device
         # copy from pageable memory waits for the stream
-        key = (tuple(slot_ids), tuple(qsl))
-        meta = self._meta_cache.get(key) if hasattr(self, "_meta_cache") else None
-        if meta is None:
-            if not hasattr(self, "_meta_cache"):
-                self._meta_cache = {}
-            if len(self._meta_cache) >= 64:
-                self._meta_cache.pop(next(iter(self._meta_cache)))
+        key = (tuple(slot_ids), tuple(qlens))
+        cache = self.__dict__.setdefault("_meta_cache", {})
+        hit = cache.get(key)
+        if hit is None:
+            qsl = [0]
+            for q in qlens:
+                qsl.append(qsl[-1] + max(0, int(q)))
+            if len(cache) >= 64:
+                cache.pop(next(iter(cache)))
             meta = torch.tensor(list(slot_ids) + qsl, dtype=torch.int32, device=dev)
-            self._meta_cache[key] = meta
-        slots, qsl_d = meta[:n], meta[n:]
+            hit = cache[key] = (meta[:n], meta[n:], qsl[-1])
+        slots, qsl_d, total = hit
         mapping = torch.empty((total,), dtype=torch.int32, device=dev)
         positions = torch.empty((total,), dtype=torch.int32, device=dev)
         if n:
@@ -239,15 +237,23 @@ class PageCacheView:
     def _resolve(self, cache_metadata, slot_ids, query_lens, n_tokens):
         if slot_ids is None:
             slot_ids = getattr(cache_metadata, "slot_ids", None) or ()
-        slot_ids = tuple(int(s) for s in slot_ids)
+        # a runner passes the same (immutable) tuples at every layer of a step: their
+        # conversion is kept for the last pair seen
+        memo = self.__dict__.get("_resolve_memo")
+        if memo is not None and memo[0] is slot_ids and memo[1] is query_lens and memo[2] == n_tokens:
+            return memo[3]
+        ids = tuple(int(s) for s in slot_ids)
         if query_lens is not None:
-            qlens = [int(q) for q in query_lens]
+            qlens = tuple(int(q) for q in query_lens)
         else:
             qsl = cache_metadata.query_start_loc
             qsl = qsl.tolist() if isinstance(qsl, torch.Tensor) else list(qsl)
-            qlens = [int(qsl[i + 1]) - int(qsl[i]) for i in range(len(slot_ids))]
+            qlens = tuple(int(qsl[i + 1]) - int(qsl[i]) for i in range(len(ids)))
         single = bool(qlens) and n_tokens == len(qlens) and all(q == 1 for q in qlens)
-        return slot_ids, qlens, single
+        res = (ids, qlens, single)
+        if type(slot_ids) is tuple and type(query_lens) is tuple:
+            self._resolve_memo = (slot_ids, query_lens, n_tokens, res)
+        return res
 
     def _apply_rope(self, rope, queries, keys, positions, qsl, qlens, single):
         """A RoPE callable applied as the reference applies it (``cache.py:1161-1166``, ``:1223-1229``).
@@ -335,7 +341,17 @@ class PageCacheView:
         ``kv_lens`` (no copies): a later write to this cache advances the lengths the returned
         metadata holds, so use it for this layer-step's attention, as the runner does."""
         n = int(slots.shape[0])
-        if slot_ids is not None and n == self.num_seqs and tuple(slot_ids) == tuple(range(n)):
+        in_order = self.__dict__.setdefault("_in_order", {})  # slot-id tuple -> writes every sequence in order
+        if slot_ids is not None:
+            key = tuple(slot_ids)
+            whole = in_order.get(key)
+            if whole is None:
+                whole = in_order[key] = n == self.num_seqs and key == tuple(range(n))
+                if len(in_order) > 64:
+                    in_order.pop(next(iter(in_order)))
+        else:
+            whole = False
+        if whole:
             tables, lens = self.block_tables, self.kv_lens
         else:
             tables = self.block_tables.index_select(0, slots) if n else self.block_tables[:0]
@@ -740,8 +756,10 @@ class AffinePageCacheView(PageCacheView):
         quantize-on-write kernel and Q in the same launch (``cache.py:1161-1166`` then ``:1186-1190``)."""
 
         def write(keys, values, slot_mapping, positions, inv, rope, stream, q_in, q_out):
-            keys = keys.to(torch.float16).contiguous()
-            values = values.to(torch.float16).contiguous()
+            if keys.dtype != torch.float16 or not keys.is_contiguous():
+                keys = keys.to(torch.float16).contiguous()
+            if values.dtype != torch.float16 or not values.is_contiguous():
+                values = values.to(torch.float16).contiguous()
             return _native.load().emx_affine_cache_write_rope(
                 keys.data_ptr(), values.data_ptr(), slot_mapping.data_ptr(), int(keys.shape[0]), self.num_kv_heads,
                 self.head_dim, self.group_size, self.bits, self.block_size, self.num_blocks,

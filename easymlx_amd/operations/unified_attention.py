@@ -124,6 +124,8 @@ def _workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor |
 def _i32(t, device) -> torch.Tensor:
     if not isinstance(t, torch.Tensor):
         t = torch.as_tensor(t)
+    if t.dtype == torch.int32 and t.device == device and t.is_contiguous():
+        return t  # the common case: the cache's own device tables (no conversion call)
     return t.to(device=device, dtype=torch.int32).contiguous()
 
 
@@ -186,7 +188,7 @@ def paged_attention(
         raise RuntimeError("paged_attention runs on the GPU only; queries are on " + str(dev))
     queries = queries.contiguous()
     lib = _native.load()
-    stream = torch.cuda.current_stream(dev).cuda_stream
+    stream = _native.stream_ptr(dev)
     S, max_blocks = int(block_tables.shape[0]), int(block_tables.shape[1])
 
     if affine:

@@ -102,3 +102,12 @@ def test_probe_fp8_reads_exactly_the_live_rows(cuda, bs):
     _native.check(rc)
     torch.cuda.synchronize()
     assert np.bitwise_xor.reduce(sink.cpu().numpy().view(np.uint32)) == x
+
+
+def test_stream_pointer_follows_the_current_stream(cuda):
+    """The raw stream every entry point launches on is torch's current stream, inside a stream context too."""
+    assert _native.stream_ptr(cuda) == torch.cuda.current_stream(cuda).cuda_stream
+    side = torch.cuda.Stream(cuda)
+    with torch.cuda.stream(side):
+        assert _native.stream_ptr(cuda) == side.cuda_stream
+    assert _native.stream_ptr(torch.device("cuda")) == torch.cuda.current_stream().cuda_stream
