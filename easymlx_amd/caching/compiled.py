@@ -111,19 +111,55 @@ class CompiledPagedCacheProxy:
         lib = _native.load()
         stream = _native.stream_ptr(dev)
         n = len(slots)
+        q_out = self._append(queries, keys, values, buf["slots"], rope, lib, stream)
+        if q_out is not None:  # positions, slots, write, Q's rotation and kv_lens in one launch
+            return q_out, c.key_cache, c.value_cache, self._metadata(cache_metadata, slots, buf)
         _native.check(lib.emx_cache_slots(
             buf["slots"].data_ptr(), buf["qsl"].data_ptr(), n, n, c.block_tables.data_ptr(),
             int(c.block_tables.shape[0]), int(c.block_tables.shape[1]), c.block_size, c.kv_lens.data_ptr(),
             buf["mapping"].data_ptr(), buf["positions"].data_ptr(), stream))
         mapping, positions = buf["mapping"], buf["positions"]
         q_out = self._write(queries, keys, values, mapping, positions, rope, lib, stream)
+        return q_out, c.key_cache, c.value_cache, self._metadata(cache_metadata, slots, buf)
+
+    def _metadata(self, cache_metadata, slots, buf):
+        c = self.cache
+        n = len(slots)
         if n == self.num_seqs and slots == tuple(range(n)):  # every sequence in order: the tables themselves
             tables, lens = c.block_tables, c.kv_lens
         else:
             tables, lens = c.block_tables.index_select(0, buf["slots"]), c.kv_lens.index_select(0, buf["slots"])
         md = cache_metadata.with_cache_state(block_tables=tables, kv_lens=lens, block_size=c.block_size)
         md.is_single_token_decode = True
-        return q_out, c.key_cache, c.value_cache, md
+        return md
+
+    def _append(self, queries, keys, values, slots_d, rope, lib, stream):
+        """The one-launch decode append of an affine cache with a fused RoPE (``emx_affine_cache_append_rope``);
+        None where it does not apply (the caller then takes the two launches)."""
+        from .rope import RotaryEmbedding
+
+        c = self.cache
+        if not (isinstance(c, AffinePageCacheView) and isinstance(rope, RotaryEmbedding) and rope.dims <= c.head_dim
+                and queries.dtype == torch.float16 and c.block_tables.is_contiguous()):
+            return None
+        if c.__dict__.get("_counter") is None and torch.cuda.is_current_stream_capturing():
+            raise RuntimeError("CompiledPagedCacheProxy: run one eager step before capture")
+        k = keys if keys.dtype == torch.float16 and keys.is_contiguous() else keys.to(torch.float16).contiguous()
+        v = values if values.dtype == torch.float16 and values.is_contiguous() else values.to(torch.float16).contiguous()
+        q_in = queries.contiguous()
+        q_out = torch.empty_like(q_in)
+        bt = c.block_tables
+        rc = lib.emx_affine_cache_append_rope(
+            k.data_ptr(), v.data_ptr(), slots_d.data_ptr(), int(k.shape[0]), bt.data_ptr(), int(bt.shape[0]),
+            int(bt.shape[1]), c.kv_lens.data_ptr(), c._append_counter().data_ptr(), c.num_kv_heads, c.head_dim,
+            c.group_size, c.bits, c.block_size, c.num_blocks, c.key_cache.data_ptr(), c.k_scales.data_ptr(),
+            c.k_biases.data_ptr(), c.value_cache.data_ptr(), c.v_scales.data_ptr(), c.v_biases.data_ptr(),
+            rope.inv_freq(k.device).data_ptr(), rope.dims, int(rope.traditional), q_in.data_ptr(), q_out.data_ptr(),
+            int(q_out.shape[1]), stream)
+        if rc == _native.EMX_ERR_UNSUPPORTED:
+            return None
+        _native.check(rc)
+        return q_out
 
     def _write(self, queries, keys, values, mapping, positions, rope, lib, stream):
         from .rope import RotaryEmbedding

@@ -196,6 +196,14 @@ class PageCacheView:
         return int(self.key_cache.shape[0])
 
     # -- slot arithmetic shared by all views (cache.py:1126-1170, 1211-1261), on the device
+    def _check_tables(self) -> torch.device:
+        dev = self.block_tables.device
+        if dev.type != "cuda" or self.kv_lens.device != dev:
+            raise RuntimeError(f"cache writes run on the GPU only; block_tables / kv_lens are on {dev}")
+        if self.block_tables.dtype != torch.int32 or self.kv_lens.dtype != torch.int32:
+            raise ValueError("block_tables and kv_lens must be int32")
+        return dev
+
     def _slots(self, slot_ids, qlens):
         """Slot mapping and position of every written token, by ``emx_cache_slots``; advances ``kv_lens``.
 
@@ -203,11 +211,7 @@ class PageCacheView:
         device tensors.  The only host work is one copy of the call's slot ids
         and query offsets (host data in the reference's API) to the device.
         """
-        dev = self.block_tables.device
-        if dev.type != "cuda" or self.kv_lens.device != dev:
-            raise RuntimeError(f"cache writes run on the GPU only; block_tables / kv_lens are on {dev}")
-        if self.block_tables.dtype != torch.int32 or self.kv_lens.dtype != torch.int32:
-            raise ValueError("block_tables and kv_lens must be int32")
+        dev = self._check_tables()
         n = len(slot_ids)
         # the device copy of (slot ids, offsets) is kept per distinct call shape: every
         # layer of a step (and most steps) writes the same slots, and a host-to-device
@@ -360,8 +364,25 @@ class PageCacheView:
         md.is_single_token_decode = single
         return md
 
+    def _slot_ids_device(self, slot_ids: tuple) -> torch.Tensor:
+        """The call's slot ids as a device int32 tensor, kept per distinct tuple (as ``_slots`` keeps them)."""
+        cache = self.__dict__.setdefault("_slot_id_cache", {})
+        t = cache.get(slot_ids)
+        if t is None:
+            if len(cache) >= 64:
+                cache.pop(next(iter(cache)))
+            t = cache[slot_ids] = torch.tensor(slot_ids, dtype=torch.int32, device=self.block_tables.device)
+        return t
+
+    def _append_counter(self) -> torch.Tensor:
+        """One device int the decode append counts its workgroups on (zero between calls)."""
+        c = self.__dict__.get("_counter")
+        if c is None:
+            c = self._counter = torch.zeros(1, dtype=torch.int32, device=self.block_tables.device)
+        return c
+
     def _concatenate_rope_fused(self, queries, keys, values, cache_metadata, rope, slot_ids, query_lens, write,
-                                rot_multiple, writes_queries=False):
+                                rot_multiple, writes_queries=False, append=None):
         """The write with a :class:`RotaryEmbedding` fused into ``write`` (a cache's C entry point) and Q turned
         by ``emx_rope_rows``; any other ``rope`` (or fp16-incompatible inputs) takes the reference's order."""
         from .rope import RotaryEmbedding
@@ -371,6 +392,20 @@ class PageCacheView:
             return PageCacheView.concatenate_to_cache(self, queries, keys, values, cache_metadata=cache_metadata,
                                                       rope=rope, slot_ids=slot_ids, query_lens=query_lens)
         slot_ids, qlens, single = self._resolve(cache_metadata, slot_ids, query_lens, int(queries.shape[0]))
+        if append is not None and single and int(keys.shape[0]) == len(slot_ids):
+            # one token per sequence: positions, slots, the K/V write, Q's rotation and the
+            # kv_lens update in one launch (emx_affine_cache_append_rope)
+            self._check_tables()
+            q_in = queries.contiguous()
+            q_out = torch.empty_like(q_in)
+            slots = self._slot_ids_device(slot_ids)
+            rc = append(keys, values, slots, rope.inv_freq(q_in.device), rope, _stream_ptr(q_in.device), q_in, q_out,
+                        self._append_counter())
+            if rc == _native.EMX_OK:
+                return q_out, self.key_cache, self.value_cache, self._resolved(cache_metadata, slots, single,
+                                                                               slot_ids)
+            if rc != _native.EMX_ERR_UNSUPPORTED:
+                _native.check(rc)
         slot_mapping, slots, positions, _ = self._slots(slot_ids, qlens)
         lib = _native.load()
         n = int(slot_mapping.numel())
@@ -768,8 +803,24 @@ class AffinePageCacheView(PageCacheView):
                 positions.data_ptr(), inv.data_ptr(), rope.dims, int(rope.traditional),
                 None if q_in is None else q_in.data_ptr(), q_out.data_ptr(), int(q_out.shape[1]), stream)
 
+        def append(keys, values, slots, inv, rope, stream, q_in, q_out, counter):
+            if keys.dtype != torch.float16 or not keys.is_contiguous():
+                keys = keys.to(torch.float16).contiguous()
+            if values.dtype != torch.float16 or not values.is_contiguous():
+                values = values.to(torch.float16).contiguous()
+            bt = self.block_tables
+            if not bt.is_contiguous():
+                return _native.EMX_ERR_UNSUPPORTED
+            return _native.load().emx_affine_cache_append_rope(
+                keys.data_ptr(), values.data_ptr(), slots.data_ptr(), int(keys.shape[0]), bt.data_ptr(),
+                int(bt.shape[0]), int(bt.shape[1]), self.kv_lens.data_ptr(), counter.data_ptr(), self.num_kv_heads,
+                self.head_dim, self.group_size, self.bits, self.block_size, self.num_blocks,
+                self.key_cache.data_ptr(), self.k_scales.data_ptr(), self.k_biases.data_ptr(),
+                self.value_cache.data_ptr(), self.v_scales.data_ptr(), self.v_biases.data_ptr(), inv.data_ptr(),
+                rope.dims, int(rope.traditional), q_in.data_ptr(), q_out.data_ptr(), int(q_out.shape[1]), stream)
+
         return self._concatenate_rope_fused(queries, keys, values, cache_metadata, rope, slot_ids, query_lens, write,
-                                            rot_multiple=2, writes_queries=True)
+                                            rot_multiple=2, writes_queries=True, append=append)
 
     def page_arrays(self) -> list[torch.Tensor]:
         return [self.key_cache, self.value_cache, self.k_scales, self.k_biases, self.v_scales, self.v_biases]

@@ -408,6 +408,11 @@ static int affine_write_impl(const void* keys, const void* values, const int32_t
   a.q = reinterpret_cast<emx::h16*>(queries);
   a.q_in = queries_in ? reinterpret_cast<const emx::h16*>(queries_in) : a.q;
   a.Hq = num_q_heads;
+  a.slot_ids = nullptr;  // slot_mapping given (the decode append sets these: emx_affine_cache_append_rope)
+  a.kv_lens = nullptr;
+  a.bt = nullptr;
+  a.S = a.max_blocks = 0;
+  a.counter = nullptr;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (num_tokens <= emx::kSmallWrite && head_dim % 16 == 0 && group_size % 16 == 0 &&
       group_size <= emx::kSmallMaxGroup) {
@@ -465,6 +470,67 @@ int emx_affine_cache_write_rope(const void* keys, const void* values, const int3
                            page_size, num_blocks, k_codes, k_scales, k_biases, v_codes, v_scales, v_biases,
                            emx::RopeArgs{inv_freq, positions, rot_dims, traditional ? 1 : 0}, queries_in, queries,
                            num_q_heads, stream);
+}
+
+int emx_affine_cache_append_rope(const void* keys, const void* values, const int32_t* slot_ids, int num_tokens,
+                                 const int32_t* block_tables, int num_seqs, int max_blocks_per_seq, int32_t* kv_lens,
+                                 int* counter, int num_kv_heads, int head_dim, int group_size, int bits,
+                                 int page_size, int num_blocks, uint32_t* k_codes, void* k_scales, void* k_biases,
+                                 uint32_t* v_codes, void* v_scales, void* v_biases, const float* inv_freq,
+                                 int rot_dims, int traditional, const void* queries_in, void* queries,
+                                 int num_q_heads, void* stream) {
+  if (num_tokens < 0 || num_seqs <= 0 || max_blocks_per_seq <= 0)
+    return fail(EMX_ERR_INVALID, "num_tokens >= 0, num_seqs and max_blocks_per_seq > 0 needed");
+  if (num_tokens > emx::kSmallWrite || head_dim % 16 != 0 || group_size % 16 != 0 ||
+      group_size > emx::kSmallMaxGroup || head_dim > emx::kWriteMaxDim)
+    return fail(EMX_ERR_UNSUPPORTED, "decode append: at most %d tokens, head_dim and group_size multiples of 16, "
+                "group_size <= %d", emx::kSmallWrite, emx::kSmallMaxGroup);
+  if (num_tokens == 0) return EMX_OK;
+  if (!slot_ids || !block_tables || !kv_lens || !counter) return fail(EMX_ERR_INVALID, "null pointer");
+  if (!inv_freq || rot_dims <= 0 || rot_dims % 2 != 0 || rot_dims > head_dim)
+    return fail(EMX_ERR_INVALID, "rope: inv_freq needed, rot_dims even and in (0, head_dim]");
+  if (queries != nullptr && (num_q_heads <= 0 || !aligned16(queries)))
+    return fail(EMX_ERR_INVALID, "queries need num_q_heads > 0 and 16-byte alignment");
+  if (queries_in != nullptr && queries == nullptr) return fail(EMX_ERR_INVALID, "queries_in needs queries");
+  if (bits != 4 && bits != 8) return fail(EMX_ERR_UNSUPPORTED, "bits must be 4 or 8, got %d", bits);
+  if (num_kv_heads <= 0 || page_size <= 0 || num_blocks <= 0 || group_size <= 0 || head_dim % group_size != 0)
+    return fail(EMX_ERR_INVALID, "num_kv_heads, page_size, num_blocks positive; head_dim a multiple of group_size");
+  if ((page_size * bits) % 32 != 0 || (page_size > 256 / bits && page_size % (256 / bits) != 0))
+    return fail(EMX_ERR_INVALID, "page_size %d must be a multiple of 32/bits, and of 256/bits when larger", page_size);
+  if (!keys || !values || !k_codes || !k_scales || !k_biases || !v_codes || !v_scales || !v_biases)
+    return fail(EMX_ERR_INVALID, "null pointer");
+  if (!aligned16(keys) || !aligned16(values)) return fail(EMX_ERR_INVALID, "keys/values must be 16-byte aligned");
+  emx::WriteArgs a;
+  a.keys = reinterpret_cast<const emx::h16*>(keys);
+  a.values = reinterpret_cast<const emx::h16*>(values);
+  a.slot_mapping = nullptr;
+  a.kc = k_codes;
+  a.ks = reinterpret_cast<emx::h16*>(k_scales);
+  a.kb = reinterpret_cast<emx::h16*>(k_biases);
+  a.vc = v_codes;
+  a.vs = reinterpret_cast<emx::h16*>(v_scales);
+  a.vb = reinterpret_cast<emx::h16*>(v_biases);
+  a.T = num_tokens;
+  a.Hkv = num_kv_heads;
+  a.D = head_dim;
+  a.gs = group_size;
+  a.bs = page_size;
+  a.nb = num_blocks;
+  a.rope = emx::RopeArgs{inv_freq, nullptr, rot_dims, traditional ? 1 : 0};
+  a.q = reinterpret_cast<emx::h16*>(queries);
+  a.q_in = queries_in ? reinterpret_cast<const emx::h16*>(queries_in) : a.q;
+  a.Hq = num_q_heads;
+  a.slot_ids = slot_ids;
+  a.kv_lens = kv_lens;
+  a.bt = block_tables;
+  a.S = num_seqs;
+  a.max_blocks = max_blocks_per_seq;
+  a.counter = counter;
+  const dim3 sgrid((unsigned)num_kv_heads, (unsigned)(head_dim / 16 + (queries ? emx::kQRopeBlocks : 0)));
+  typedef void (*SmallFn)(emx::WriteArgs);
+  SmallFn fn = bits == 4 ? emx::affine_cache_write_small<4, true> : emx::affine_cache_write_small<8, true>;
+  hipLaunchKernelGGL(fn, sgrid, dim3(256), 0, reinterpret_cast<hipStream_t>(stream), a);
+  return check_launch("affine_cache_write_small (append)");
 }
 
 int emx_cache_slots(const int32_t* slot_ids, const int32_t* query_start_loc, int num_slots, int num_tokens,

@@ -151,6 +151,14 @@ struct WriteArgs {
   h16* q;                      // [T, Hq, D] turned queries, written by the same launch (null: none)
   const h16* q_in;             // the queries to turn (== q: in place)
   int Hq;
+  // Decode append (slot_mapping null): token t is the next token of sequence
+  // slot_ids[t]; its position is kv_lens[slot] and its slot comes from the block
+  // table (the arithmetic of cache_slots), and kv_lens advances by one.
+  const int32_t* slot_ids;     // [T]
+  int32_t* kv_lens;            // [S]
+  const int32_t* bt;           // [S, max_blocks]
+  int S, max_blocks;
+  int* counter;                // workgroups that have read kv_lens: zero before and after every launch
 };
 
 constexpr int kQRopeBlocks = 4;  // extra workgroup rows of the small write that turn the queries
@@ -309,13 +317,67 @@ __global__ __launch_bounds__(256) void affine_cache_write_small(WriteArgs a) {
   const int tid = threadIdx.x;
   const int h = blockIdx.x;
   const int d0 = blockIdx.y * DB;
+  // Decode append (a.slot_ids set): every workgroup derives the tokens' positions
+  // and slots itself (cache_slots folded in; slots.hpp: position kv_lens[s], page
+  // block_tables[s, position / bs], -1 for a slot id outside [0, S), a column past
+  // the table or a negative page id), issuing those reads before its page data
+  // loads so both are in flight together.  Once its kv_lens values are in LDS it
+  // counts itself (the atomic's answer is only needed at its end); the workgroup
+  // counted last advances kv_lens at its end, so no workgroup reads an advanced
+  // length.
+  const bool app = a.slot_ids != nullptr;
+  __shared__ int spos[kSmallWrite];
+  __shared__ int sseq[kSmallWrite];
+  int sl_dev = -1, app_s = -1, app_pos = 0;
+  RopeArgs rope = a.rope;
+  if (app) {
+    if (tid < a.T) {
+      const int s = a.slot_ids[tid];
+      if (s >= 0 && s < a.S) {
+        app_s = s;
+        app_pos = a.kv_lens[s];
+        const int col = app_pos / a.bs;
+        if (app_pos >= 0 && col < a.max_blocks) {
+          const int b = a.bt[(size_t)s * a.max_blocks + col];
+          if (b >= 0) sl_dev = b * a.bs + app_pos % a.bs;
+        }
+      }
+    }
+    rope.positions = spos;
+  }
+  int arrived = 0;
+  auto publish = [&]() {  // before a barrier: this workgroup's positions and sequences to LDS
+    if (app && tid < a.T) {
+      spos[tid] = app_pos;
+      sseq[tid] = app_s;
+    }
+  };
+  auto count = [&]() {  // after that barrier: every kv_lens read of the workgroup has returned
+    if (app && tid == 0) arrived = __hip_atomic_fetch_add(a.counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  };
+  auto finish = [&]() {  // the end of the workgroup: the last one counted advances kv_lens
+    if (!app) return;
+    __shared__ int slast;
+    if (tid == 0) {
+      const int nwg = (int)(gridDim.x * gridDim.y);
+      slast = arrived == nwg - 1;
+      if (arrived == nwg - 1) __hip_atomic_store(a.counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (slast && tid < a.T && sseq[tid] >= 0) a.kv_lens[sseq[tid]] = spos[tid] + 1;
+  };
   if constexpr (ROPE) {
     // the extra rows of workgroups turn the queries (rows of gridDim.x * kQRopeBlocks workgroups)
     if (d0 >= a.D) {
-      if (a.q == nullptr) return;
-      const int nwg = gridDim.x * kQRopeBlocks;
-      const int wg = (blockIdx.y - a.D / DB) * gridDim.x + blockIdx.x;
-      turn_rows(a.q, a.q_in, a.T, a.Hq, a.D, a.rope, (long)wg * 256 + tid, (long)nwg * 256);
+      publish();
+      if (app) __syncthreads();
+      count();
+      if (a.q != nullptr) {
+        const int nwg = gridDim.x * kQRopeBlocks;
+        const int wg = (blockIdx.y - a.D / DB) * gridDim.x + blockIdx.x;
+        turn_rows(a.q, a.q_in, a.T, a.Hq, a.D, rope, (long)wg * 256 + tid, (long)nwg * 256);
+      }
+      finish();
       return;
     }
   }
@@ -332,9 +394,9 @@ __global__ __launch_bounds__(256) void affine_cache_write_small(WriteArgs a) {
   // returns zeros), so none waits behind a branch for the one before it.
   const int g = d0 / a.gs;
   constexpr int kOob = 0x7FFFFFF0;  // past the end of every descriptor below
-  const int sl_raw = (int)__builtin_amdgcn_raw_buffer_load_b32(uniform_rsrc(a.slot_mapping, T * 4),
-                                                               tid < T ? tid * 4 : kOob, 0, kLoadAux);
-  const int sl_in = tid < T ? sl_raw : -1;
+  const int sl_raw = (int)__builtin_amdgcn_raw_buffer_load_b32(
+      uniform_rsrc(a.slot_mapping, a.slot_mapping ? T * 4 : 0), tid < T ? tid * 4 : kOob, 0, kLoadAux);
+  const int sl_in = tid < T ? (a.slot_ids != nullptr ? sl_dev : sl_raw) : -1;
   constexpr int kPieces = 2 * kSmallWrite * (kSmallMaxGroup / 8) / 256;  // 16-byte pieces per thread
   const int per_tok = a.gs / 8;
   const int row_bytes = T * a.Hkv * a.D * 2;
@@ -355,8 +417,10 @@ __global__ __launch_bounds__(256) void affine_cache_write_small(WriteArgs a) {
       piece[k] = __builtin_amdgcn_raw_buffer_load_b128(rval, i < T * per_tok ? goff(i / per_tok, i % per_tok) : kOob,
                                                        0, kLoadAux);
     }
+    publish();
     __syncthreads();
-    const RopeArgs& r = a.rope;
+    count();
+    const RopeArgs& r = rope;  // positions: the device-derived ones in a decode append
     const int half = r.rot / 2;
     for (int task = tid; task < T * half; task += 256) {
       const int t = task / half, p = task % half;
@@ -393,7 +457,9 @@ __global__ __launch_bounds__(256) void affine_cache_write_small(WriteArgs a) {
     }
   }
   if (tid < T) sslot[tid] = sl_in >= 0 && sl_in / a.bs >= a.nb ? -1 : sl_in;  // page out of range: not written
+  if constexpr (!ROPE) publish();  // (with ROPE: published at the K rows' barrier above)
   __syncthreads();
+  if constexpr (!ROPE) count();
   // The value words this thread updates, read now so that the read-modify-write
   // at the end does not wait for them (4-bit: a word holds 8 tokens of one dim).
   constexpr int kVTasks = kSmallWrite * DB / 256;
@@ -476,6 +542,7 @@ __global__ __launch_bounds__(256) void affine_cache_write_small(WriteArgs a) {
       atomicOr(wp, code << sh);
     }
   }
+  finish();
 }
 
 #pragma clang fp contract(on)

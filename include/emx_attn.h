@@ -91,6 +91,31 @@ int emx_affine_cache_write_rope(const void* keys, const void* values, const int3
                                 int num_q_heads, void* stream);
 
 /*
+ * The decode-step append with RoPE in one launch: emx_cache_slots and
+ * emx_affine_cache_write_rope together for one token per sequence.  Token t
+ * (num_tokens <= 128) is the next token of sequence slot_ids[t]: its position
+ * is kv_lens[slot_ids[t]], its slot block_tables[s, position / page_size] *
+ * page_size + position % page_size (not written for a slot id outside
+ * [0, num_seqs), a column past the table or a negative page id), K is rotated
+ * at that position and quantized into the pages, queries_in rotated into
+ * queries, and kv_lens[s] advances by one.  `counter` is one int of device
+ * memory, zero before the first call; every call leaves it zero (calls that
+ * share it must not overlap).  head_dim and group_size multiples of 16,
+ * group_size <= 64; otherwise EMX_ERR_UNSUPPORTED (use the two calls).
+ * Replaces the decode branch of PageCacheView.concatenate_to_cache
+ *   lib/python/easymlx/caching/paged/cache.py:1126-1190 (RoPE :1161-1166)
+ * and the compiled decode proxy's write
+ *   lib/python/easymlx/inference/esurge/runners/model_runner.py:139-189.
+ */
+int emx_affine_cache_append_rope(const void* keys, const void* values, const int32_t* slot_ids, int num_tokens,
+                                 const int32_t* block_tables, int num_seqs, int max_blocks_per_seq, int32_t* kv_lens,
+                                 int* counter, int num_kv_heads, int head_dim, int group_size, int bits,
+                                 int page_size, int num_blocks, uint32_t* k_codes, void* k_scales, void* k_biases,
+                                 uint32_t* v_codes, void* v_scales, void* v_biases, const float* inv_freq,
+                                 int rot_dims, int traditional, const void* queries_in, void* queries,
+                                 int num_q_heads, void* stream);
+
+/*
  * Write positions of a cache write, on the device: token t of sequence i
  * (query_start_loc[i] <= t < query_start_loc[i+1], i < num_slots, int32 arrays
  * on the device) of slot s = slot_ids[i] goes to position
