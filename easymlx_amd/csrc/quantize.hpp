@@ -300,9 +300,11 @@ __global__ __launch_bounds__(256) void affine_cache_write(WriteArgs a) {
 
 // Small writes (decode appends, T <= kSmallWrite tokens): one workgroup per
 // (kv head, 16-dim block) sees every token, so each value word has a single
-// writing workgroup.  A token alone in its 8-token word (always the case for
-// one token per sequence) updates its nibble with a plain read-modify-write;
-// tokens sharing a word in this call fall back to atomics.  Scales, biases
+// writing workgroup.  A token's 4-bit value code goes into its 8-token word by
+// an atomic AND and OR that return nothing (tokens of the call sharing a word
+// touch disjoint bits); a plain read-modify-write of the word (where no other
+// token of the call shares it) measured 0.85 us slower per append, its read
+// being one more round trip.  Scales, biases
 // and K codes of the head are written by the workgroup of dim block 0 / by the
 // owner of each K word.
 constexpr int kSmallWrite = 128;
@@ -387,7 +389,6 @@ __global__ __launch_bounds__(256) void affine_cache_write_small(WriteArgs a) {
   __shared__ float sp[2][kSmallWrite][2];  // [K|V][token] -> (scale, bias) of this block's group
   __shared__ __attribute__((aligned(16))) h16 sgrp[2][kSmallWrite][kSmallMaxGroup];  // group values
   __shared__ __attribute__((aligned(16))) int sslot[kSmallWrite];
-  __shared__ int salone[kSmallWrite];
   // One round trip for what the workgroup reads: the tokens' slots and the
   // quantization group holding this dim block (neither depends on the other).
   // Every load is issued unconditionally (buffer loads: an offset past the end
@@ -460,35 +461,7 @@ __global__ __launch_bounds__(256) void affine_cache_write_small(WriteArgs a) {
   if constexpr (!ROPE) publish();  // (with ROPE: published at the K rows' barrier above)
   __syncthreads();
   if constexpr (!ROPE) count();
-  // The value words this thread updates, read now so that the read-modify-write
-  // at the end does not wait for them (4-bit: a word holds 8 tokens of one dim).
   constexpr int kVTasks = kSmallWrite * DB / 256;
-  uint32_t vword[kVTasks];
-  if constexpr (BITS == 4) {
-#pragma unroll
-    for (int k = 0; k < kVTasks; ++k) {  // (an unused task reads word 0 of the pool)
-      const int task = tid + 256 * k;
-      const int t = min(task / DB, kSmallWrite - 1), d = d0 + task % DB;
-      const int sl = task < T * DB ? sslot[t] : -1;
-      const size_t ph = (size_t)(max(sl, 0) / a.bs) * a.Hkv + h;
-      vword[k] = a.vc[sl >= 0 ? v_word_index<BITS>(ph, sl % a.bs, d, a.D, a.bs) : 0];
-    }
-  }
-  // alone: no other token of the call in the same 32/BITS-token value word
-  if (tid < T) {
-    const int sl = sslot[tid];
-    bool alone = true;
-    if (sl >= 0) {
-      for (int u0 = 0; u0 < T; u0 += 4) {
-        const int4 w = *reinterpret_cast<const int4*>(&sslot[u0]);
-        const int wu[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-        for (int k = 0; k < 4; ++k)
-          if (u0 + k < T && u0 + k != tid && wu[k] >= 0 && wu[k] / PW == sl / PW) alone = false;
-      }
-    }
-    salone[tid] = alone;
-  }
   // scale / bias (the first dim block of each group stores them)
   for (int task = tid; task < 2 * T; task += 256) {
     const int kv = task / T, t = task % T;
@@ -535,9 +508,7 @@ __global__ __launch_bounds__(256) void affine_cache_write_small(WriteArgs a) {
     constexpr uint32_t M = (1u << BITS) - 1u;
     if (BITS == 8) {
       reinterpret_cast<uint8_t*>(wp)[sl % 4] = (uint8_t)code;
-    } else if (salone[t]) {
-      *wp = (vword[k] & ~(M << sh)) | (code << sh);  // the word's only writer in this call
-    } else {
+    } else {  // the nibble by two atomics that return nothing: no read of the word to wait for
       atomicAnd(wp, ~(M << sh));
       atomicOr(wp, code << sh);
     }
