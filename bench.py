@@ -521,7 +521,7 @@ def aux_op_layer_step(dev, steps=100):
     (the counterpart of the reference's compiled decode) and replayed."""
     import torch
 
-    from easymlx_amd import CompiledPagedCacheProxy, PageMetadata, RotaryEmbedding, UnifiedAttention
+    from easymlx_amd import CompiledPagedCacheProxy, Fp8PageCacheView, PageMetadata, RotaryEmbedding, UnifiedAttention
     from easymlx_amd.caching import affine_pool
     from easymlx_amd.workloads import config
 
@@ -540,16 +540,26 @@ def aux_op_layer_step(dev, steps=100):
     k = torch.randn((S, hkv, d), device=dev, generator=g).half()
     v = torch.randn((S, hkv, d), device=dev, generator=g).half()
     res = {}
-    for mode in ("eager", "graph"):
-        view = affine_pool(num_blocks=wl.num_blocks + extra * S, num_kv_heads=hkv, head_dim=d, block_size=bs, bits=4,
-                           group_size=64, block_tables=torch.from_numpy(tables).to(dev),
-                           kv_lens=torch.from_numpy(wl.kv_lens).to(dev))
+    for mode in ("eager", "graph", "fp8_eager", "fp8_graph"):
+        nbp = wl.num_blocks + extra * S
+        if mode.startswith("fp8"):  # the reference's FP8 cache on the same pages
+            shape = (nbp, bs, hkv, d)
+            view = Fp8PageCacheView(key_cache=torch.zeros(shape, dtype=torch.uint8, device=dev),
+                                    value_cache=torch.zeros(shape, dtype=torch.uint8, device=dev),
+                                    k_scales=torch.zeros(nbp, device=dev), v_scales=torch.zeros(nbp, device=dev),
+                                    block_tables=torch.from_numpy(tables).to(dev),
+                                    kv_lens=torch.from_numpy(wl.kv_lens).to(dev), block_size=bs, num_kv_heads=hkv,
+                                    head_dim=d)
+        else:
+            view = affine_pool(num_blocks=nbp, num_kv_heads=hkv, head_dim=d, block_size=bs, bits=4, group_size=64,
+                               block_tables=torch.from_numpy(tables).to(dev),
+                               kv_lens=torch.from_numpy(wl.kv_lens).to(dev))
         view.write_slots(torch.from_numpy(wl.k).to(dev), torch.from_numpy(wl.v).to(dev),
                          torch.from_numpy(wl.slot.astype(np.int32)).to(dev))
         md0 = PageMetadata(query_start_loc=torch.arange(S + 1, dtype=torch.int32, device=dev),
                            slot_ids=tuple(range(S)))
         qlens = (1,) * S
-        cache = CompiledPagedCacheProxy(view) if mode == "graph" else view
+        cache = CompiledPagedCacheProxy(view) if mode.endswith("graph") else view
         outs = []
 
         def step():
@@ -561,7 +571,7 @@ def aux_op_layer_step(dev, steps=100):
         side.wait_stream(torch.cuda.current_stream(dev))
         with torch.cuda.stream(side):
             step()
-            if mode == "graph":
+            if mode.endswith("graph"):
                 graph = torch.cuda.CUDAGraph()
                 with torch.cuda.graph(graph, stream=side):
                     step()
@@ -580,7 +590,8 @@ def aux_op_layer_step(dev, steps=100):
             res[f"{mode}_us_per_layer_step"] = round((time.perf_counter() - t0) / steps * 1e6, 2)
         del view
     res["workload"] = ("c2 layer-step through the public op: concatenate_to_cache (1 token x 32 seqs, Llama-3 "
-                       "RoPE fused) + UnifiedAttention.forward_native, wall clock")
+                       "RoPE fused) + UnifiedAttention.forward_native, wall clock; fp8_*: the same over an FP8 "
+                       "(E4M3, per-page scale) cache")
     return res
 
 

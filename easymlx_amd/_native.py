@@ -41,6 +41,8 @@ SIGNATURES: dict[str, tuple] = {
     "emx_rope_rows": (_I, [_P, _I, _I, _I, _P, _P, _I, _I, _P]),
     "emx_affine_cache_append_rope": (_I, [_P, _P, _P, _I, _P, _I, _I, _P, _P] + [_I] * 6 + [_P] * 7 + [_I, _I, _P, _P,
                                                                                                     _I, _P]),
+    "emx_fp8_cache_append_rope": (
+        _I, [_P, _P, _I, _P, _I, _P, _I, _I, _P, _P] + [_I] * 4 + [_P] * 5 + [_I, _I, _P, _P, _I, _P]),
     "emx_cache_slots": (_I, [_P, _P, _I, _I, _P, _I, _I, _I, _P, _P, _P, _P]),
     "emx_dense_cache_write": (_I, [_P, _P, _I, _P, _I, _I, _I, _I, _I, _P, _P, _P]),
     "emx_copy_blocks": (_I, [_I, _P, _P, _I, _P, _I, _P]),

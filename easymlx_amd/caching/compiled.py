@@ -134,21 +134,38 @@ class CompiledPagedCacheProxy:
         return md
 
     def _append(self, queries, keys, values, slots_d, rope, lib, stream):
-        """The one-launch decode append of an affine cache with a fused RoPE (``emx_affine_cache_append_rope``);
-        None where it does not apply (the caller then takes the two launches)."""
+        """The one-launch decode append with a fused RoPE (``emx_affine_cache_append_rope`` /
+        ``emx_fp8_cache_append_rope``); None where it does not apply (the caller then takes the two launches)."""
         from .rope import RotaryEmbedding
 
         c = self.cache
-        if not (isinstance(c, AffinePageCacheView) and isinstance(rope, RotaryEmbedding) and rope.dims <= c.head_dim
-                and queries.dtype == torch.float16 and c.block_tables.is_contiguous()):
+        if not (isinstance(c, (AffinePageCacheView, Fp8PageCacheView)) and isinstance(rope, RotaryEmbedding)
+                and rope.dims <= c.head_dim and queries.dtype == torch.float16 and c.block_tables.is_contiguous()):
             return None
         if c.__dict__.get("_counter") is None and torch.cuda.is_current_stream_capturing():
             raise RuntimeError("CompiledPagedCacheProxy: run one eager step before capture")
-        k = keys if keys.dtype == torch.float16 and keys.is_contiguous() else keys.to(torch.float16).contiguous()
-        v = values if values.dtype == torch.float16 and values.is_contiguous() else values.to(torch.float16).contiguous()
         q_in = queries.contiguous()
         q_out = torch.empty_like(q_in)
         bt = c.block_tables
+        if isinstance(c, Fp8PageCacheView):
+            codes = {torch.float16: _native.DTYPE_F16, torch.bfloat16: _native.DTYPE_BF16,
+                     torch.float32: _native.DTYPE_F32}
+            if keys.dtype not in codes or values.dtype != keys.dtype or rope.dims % (4 if rope.traditional else 8):
+                return None
+            k, v = keys.contiguous(), values.contiguous()
+            rc = lib.emx_fp8_cache_append_rope(
+                k.data_ptr(), v.data_ptr(), codes[k.dtype], slots_d.data_ptr(), int(k.shape[0]), bt.data_ptr(),
+                int(bt.shape[0]), int(bt.shape[1]), c.kv_lens.data_ptr(), c._append_counter().data_ptr(),
+                c.num_kv_heads, c.head_dim, c.block_size, c.num_blocks, c.key_cache.data_ptr(),
+                c.value_cache.data_ptr(), c.k_scales.data_ptr(), c.v_scales.data_ptr(),
+                rope.inv_freq(k.device).data_ptr(), rope.dims, int(rope.traditional), q_in.data_ptr(),
+                q_out.data_ptr(), int(q_out.shape[1]), stream)
+            if rc == _native.EMX_ERR_UNSUPPORTED:
+                return None
+            _native.check(rc)
+            return q_out
+        k = keys if keys.dtype == torch.float16 and keys.is_contiguous() else keys.to(torch.float16).contiguous()
+        v = values if values.dtype == torch.float16 and values.is_contiguous() else values.to(torch.float16).contiguous()
         rc = lib.emx_affine_cache_append_rope(
             k.data_ptr(), v.data_ptr(), slots_d.data_ptr(), int(k.shape[0]), bt.data_ptr(), int(bt.shape[0]),
             int(bt.shape[1]), c.kv_lens.data_ptr(), c._append_counter().data_ptr(), c.num_kv_heads, c.head_dim,

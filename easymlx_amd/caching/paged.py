@@ -632,9 +632,22 @@ class Fp8PageCacheView(PageCacheView):
                 self._ws.numel(), positions.data_ptr(), inv.data_ptr(), rope.dims, int(rope.traditional),
                 None if q_in is None else q_in.data_ptr(), q_out.data_ptr(), int(q_out.shape[1]), stream)
 
+        def append(keys, values, slots, inv, rope, stream, q_in, q_out, counter):
+            if keys.dtype not in codes or values.dtype != keys.dtype or not self.block_tables.is_contiguous():
+                return _native.EMX_ERR_UNSUPPORTED
+            keys = keys.contiguous()
+            values = values.contiguous()
+            bt = self.block_tables
+            return _native.load().emx_fp8_cache_append_rope(
+                keys.data_ptr(), values.data_ptr(), codes[keys.dtype], slots.data_ptr(), int(keys.shape[0]),
+                bt.data_ptr(), int(bt.shape[0]), int(bt.shape[1]), self.kv_lens.data_ptr(), counter.data_ptr(),
+                self.num_kv_heads, self.head_dim, self.block_size, self.num_blocks, self.key_cache.data_ptr(),
+                self.value_cache.data_ptr(), self.k_scales.data_ptr(), self.v_scales.data_ptr(), inv.data_ptr(),
+                rope.dims, int(rope.traditional), q_in.data_ptr(), q_out.data_ptr(), int(q_out.shape[1]), stream)
+
         return self._concatenate_rope_fused(queries, keys, values, cache_metadata, rope, slot_ids, query_lens, write,
                                             rot_multiple=4 if getattr(rope, "traditional", False) else 8,
-                                            writes_queries=True)
+                                            writes_queries=True, append=append)
 
     def write_slots(self, keys: torch.Tensor, values: torch.Tensor, slot_mapping: torch.Tensor) -> None:
         """Write tokens to explicit slots (``block * block_size + offset``; -1 skips)."""

@@ -1125,6 +1125,11 @@ static int fp8_write_impl(const void* keys, const void* values, int dtype, const
   a.q = reinterpret_cast<emx::h16*>(queries);
   a.q_in = queries_in ? reinterpret_cast<const emx::h16*>(queries_in) : a.q;
   a.Hq = num_q_heads;
+  a.slot_ids = nullptr;  // slot_mapping given (emx_fp8_cache_append_rope sets these)
+  a.kv_lens = nullptr;
+  a.bt = nullptr;
+  a.S = a.max_blocks = 0;
+  a.counter = nullptr;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const size_t n = (size_t)num_tokens * num_kv_heads * head_dim;
   if (n / 4 >= ((size_t)1 << 31)) return fail(EMX_ERR_UNSUPPORTED, "%zu values per tensor exceed the 2^33 limit", n);
@@ -1204,6 +1209,68 @@ int emx_fp8_cache_write_rope(const void* keys, const void* values, int dtype, co
                         key_cache, value_cache, k_scales, v_scales, workspace, workspace_bytes,
                         emx::RopeArgs{inv_freq, positions, rot_dims, traditional ? 1 : 0}, queries_in, queries,
                         num_q_heads, stream);
+}
+
+int emx_fp8_cache_append_rope(const void* keys, const void* values, int dtype, const int32_t* slot_ids,
+                              int num_tokens, const int32_t* block_tables, int num_seqs, int max_blocks_per_seq,
+                              int32_t* kv_lens, int* counter, int num_kv_heads, int head_dim, int page_size,
+                              int num_blocks, uint8_t* key_cache, uint8_t* value_cache, float* k_scales,
+                              float* v_scales, const float* inv_freq, int rot_dims, int traditional,
+                              const void* queries_in, void* queries, int num_q_heads, void* stream) {
+  if (num_tokens < 0 || num_seqs <= 0 || max_blocks_per_seq <= 0)
+    return fail(EMX_ERR_INVALID, "num_tokens >= 0, num_seqs and max_blocks_per_seq > 0 needed");
+  if (num_kv_heads <= 0 || head_dim <= 0 || page_size <= 0 || num_blocks <= 0)
+    return fail(EMX_ERR_INVALID, "num_kv_heads, head_dim, page_size, num_blocks must be positive");
+  if (head_dim % 4 != 0) return fail(EMX_ERR_UNSUPPORTED, "head_dim %d must be a multiple of 4", head_dim);
+  if (dtype != EMX_DTYPE_F16 && dtype != EMX_DTYPE_BF16 && dtype != EMX_DTYPE_F32)
+    return fail(EMX_ERR_INVALID, "unknown dtype %d", dtype);
+  const size_t n = (size_t)num_tokens * num_kv_heads * head_dim;
+  if (num_tokens > emx::kFp8AppendMax || n > (size_t)emx::kFp8SelfMax)
+    return fail(EMX_ERR_UNSUPPORTED, "decode append: at most %d tokens and %d values per tensor", emx::kFp8AppendMax,
+                emx::kFp8SelfMax);
+  if (num_tokens == 0) return EMX_OK;
+  if (!inv_freq || rot_dims <= 0 || rot_dims > head_dim || rot_dims % (traditional ? 4 : 8) != 0)
+    return fail(EMX_ERR_INVALID, "rope: inv_freq needed, rot_dims in (0, head_dim] and a multiple of 8 (4 if traditional)");
+  if (queries != nullptr && num_q_heads <= 0) return fail(EMX_ERR_INVALID, "queries need num_q_heads > 0");
+  if (queries_in != nullptr && queries == nullptr) return fail(EMX_ERR_INVALID, "queries_in needs queries");
+  if (!keys || !values || !slot_ids || !block_tables || !kv_lens || !counter || !key_cache || !value_cache ||
+      !k_scales || !v_scales)
+    return fail(EMX_ERR_INVALID, "null pointer");
+  if ((reinterpret_cast<uintptr_t>(key_cache) | reinterpret_cast<uintptr_t>(value_cache)) & 3)
+    return fail(EMX_ERR_INVALID, "key/value cache must be 4-byte aligned");
+  emx::Fp8WriteArgs a;
+  a.k = keys;
+  a.v = values;
+  a.slot = nullptr;
+  a.T = num_tokens;
+  a.Hkv = num_kv_heads;
+  a.D = head_dim;
+  a.bs = page_size;
+  a.nb = num_blocks;
+  a.kc = key_cache;
+  a.vc = value_cache;
+  a.ks = k_scales;
+  a.vs = v_scales;
+  a.part = nullptr;
+  a.rope = emx::RopeArgs{inv_freq, nullptr, rot_dims, traditional ? 1 : 0};
+  a.q = reinterpret_cast<emx::h16*>(queries);
+  a.q_in = queries_in ? reinterpret_cast<const emx::h16*>(queries_in) : a.q;
+  a.Hq = num_q_heads;
+  a.slot_ids = slot_ids;
+  a.kv_lens = kv_lens;
+  a.bt = block_tables;
+  a.S = num_seqs;
+  a.max_blocks = max_blocks_per_seq;
+  a.counter = counter;
+  a.nwg = (int)((n / 4 + 1023) / 1024);
+  const dim3 g1((unsigned)(a.nwg + (queries ? 4 : 0)));  // + workgroups that turn the queries
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case EMX_DTYPE_F16: hipLaunchKernelGGL((emx::fp8_write<emx::F16, true>), g1, dim3(1024), 0, st, a, 0); break;
+    case EMX_DTYPE_BF16: hipLaunchKernelGGL((emx::fp8_write<emx::BF16, true>), g1, dim3(1024), 0, st, a, 0); break;
+    default: hipLaunchKernelGGL((emx::fp8_write<emx::F32, true>), g1, dim3(1024), 0, st, a, 0); break;
+  }
+  return check_launch("fp8_cache_write (append)");
 }
 
 int emx_paged_attention_fp8(const void* queries, int num_tokens, int num_q_heads, int head_dim, int dtype,

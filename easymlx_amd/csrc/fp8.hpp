@@ -38,7 +38,17 @@ struct Fp8WriteArgs {
   const h16* q_in;       // the queries to turn (== q: in place)
   int Hq;
   int nwg;               // workgroups of the write proper; later ones turn the queries
+  // Decode append (the one-launch write; slot null): token t is the next token of
+  // sequence slot_ids[t] (emx_affine_cache_append_rope's rule), kv_lens advances by one.
+  const int32_t* slot_ids;  // [T], T <= kFp8AppendMax
+  int32_t* kv_lens;         // [S]
+  const int32_t* bt;        // [S, max_blocks]
+  int S, max_blocks;
+  int* counter;             // workgroups that have read kv_lens: zero before and after every launch
 };
+
+constexpr int kFp8AppendMax = 1024;  // tokens of a one-launch decode append
+constexpr int kFp8RopeTab = 4096;    // (token, pair) angles of the one-launch write's LDS table
 
 __device__ __forceinline__ float round_to(float x, h16*) { return (float)(h16)x; }
 __device__ __forceinline__ float round_to(float x, uint16_t*) { return bf16_to_f32(f32_to_bf16(x)); }
@@ -48,8 +58,11 @@ __device__ __forceinline__ float round_to(float x, float*) { return x; }
 // the call's RoPE and rounded to the input dtype when a.rope is set (the
 // reference writes the rotated keys of the model's dtype).  Needs rot % 8 == 0
 // (non-traditional): a word and its partner word lie in one half each.
+// tab: null, or (sin, cos) of positions[t] * inv_freq[i] at t * (rot / 2) + i (the
+// one-launch write builds it once per workgroup instead of a sincosf per value).
 template <typename T>
-__device__ __forceinline__ void k_word(const Fp8WriteArgs& a, const T* k, const uint32_t e, float (&x)[4]) {
+__device__ __forceinline__ void k_word(const Fp8WriteArgs& a, const T* k, const uint32_t e, float (&x)[4],
+                                       const float2* tab = nullptr) {
 #pragma unroll
   for (int j = 0; j < 4; ++j) x[j] = to_f32(k[4 * (size_t)e + j]);
   const RopeArgs& r = a.rope;
@@ -57,11 +70,19 @@ __device__ __forceinline__ void k_word(const Fp8WriteArgs& a, const T* k, const 
   const uint32_t wpr = a.D / 4;  // words per head row
   const int d0 = 4 * (int)(e % wpr);
   if (d0 >= r.rot) return;
-  const float pos = (float)r.positions[e / ((uint32_t)a.Hkv * wpr)];
+  const uint32_t t = e / ((uint32_t)a.Hkv * wpr);
+  const float pos = tab ? 0.f : (float)r.positions[t];
+  const float2* tt = tab ? tab + (size_t)t * (r.rot / 2) : nullptr;
   float y[4];
   if (r.traditional) {
 #pragma unroll
-    for (int j = 0; j < 4; j += 2) rope_rotate(x[j], x[j + 1], pos * r.inv_freq[(d0 + j) >> 1], y[j], y[j + 1]);
+    for (int j = 0; j < 4; j += 2) {
+      const int i = (d0 + j) >> 1;
+      if (tab)
+        rope_rotate_sc(x[j], x[j + 1], tt[i], y[j], y[j + 1]);
+      else
+        rope_rotate(x[j], x[j + 1], pos * r.inv_freq[i], y[j], y[j + 1]);
+    }
   } else {
     const int half = r.rot / 2;
     const bool lo = d0 < half;
@@ -71,10 +92,17 @@ __device__ __forceinline__ void k_word(const Fp8WriteArgs& a, const T* k, const 
       const float p = to_f32(k[4 * (size_t)pe + j]);
       float y0, y1;
       const int i = (lo ? d0 : d0 - half) + j;
-      if (lo)
-        rope_rotate(x[j], p, pos * r.inv_freq[i], y0, y1);
-      else
-        rope_rotate(p, x[j], pos * r.inv_freq[i], y1, y0);
+      if (tab) {
+        if (lo)
+          rope_rotate_sc(x[j], p, tt[i], y0, y1);
+        else
+          rope_rotate_sc(p, x[j], tt[i], y1, y0);
+      } else {
+        if (lo)
+          rope_rotate(x[j], p, pos * r.inv_freq[i], y0, y1);
+        else
+          rope_rotate(p, x[j], pos * r.inv_freq[i], y1, y0);
+      }
       y[j] = y0;
     }
   }
@@ -120,10 +148,76 @@ __global__ __launch_bounds__(SELF ? 1024 : 256) void fp8_write(Fp8WriteArgs a, i
   typedef typename Tag::T T;
   constexpr int NTH = SELF ? 1024 : 256;  // threads per workgroup
   __shared__ float sc[2];
+  // Decode append (one-launch write with a.slot_ids): every workgroup derives the
+  // tokens' slots and positions into LDS (the arithmetic of cache_slots), counts
+  // itself once they are there, and the workgroup counted last advances kv_lens at
+  // its end, so no workgroup reads an advanced length.
+  const bool app = SELF && a.slot_ids != nullptr;
+  int arrived = 0;
+  if constexpr (SELF) {
+    __shared__ int fslot[kFp8AppendMax], fpos[kFp8AppendMax], fseq[kFp8AppendMax];
+    if (app) {
+      for (int t = threadIdx.x; t < a.T; t += NTH) {
+        int s = a.slot_ids[t], pos = 0, m = -1;
+        if (s >= 0 && s < a.S) {
+          pos = a.kv_lens[s];
+          const int col = pos / a.bs;
+          if (pos >= 0 && col < a.max_blocks) {
+            const int b = a.bt[(size_t)s * a.max_blocks + col];
+            if (b >= 0) m = b * a.bs + pos % a.bs;
+          }
+        } else {
+          s = -1;
+        }
+        fslot[t] = m;
+        fpos[t] = pos;
+        fseq[t] = s;
+      }
+      a.slot = fslot;
+      a.rope.positions = fpos;
+      __syncthreads();  // every kv_lens read of the workgroup has returned
+      if (threadIdx.x == 0)
+        arrived = __hip_atomic_fetch_add(a.counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  auto finish = [&]() {  // the end of the workgroup: the last one counted advances kv_lens
+    if constexpr (SELF) {
+      if (!app) return;
+      __shared__ int slast;
+      if (threadIdx.x == 0) {
+        slast = arrived == (int)gridDim.x - 1;
+        if (arrived == (int)gridDim.x - 1)
+          __hip_atomic_store(a.counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      __syncthreads();
+      if (slast)
+        for (int t = threadIdx.x; t < a.T; t += NTH)
+          if (a.rope.positions != nullptr && a.slot_ids[t] >= 0 && a.slot_ids[t] < a.S)
+            a.kv_lens[a.slot_ids[t]] = a.rope.positions[t] + 1;
+    }
+  };
+  // (sin, cos) of every (token, pair) angle, once per workgroup, for the K rotations
+  // of the maxima and of the codes (a sincosf per value made every workgroup of a
+  // 32-token append spend ~20 us turning all the keys for the maxima)
+  const float2* rtab = nullptr;
+  if constexpr (SELF) {
+    __shared__ float2 rsc[kFp8RopeTab];
+    const int half = a.rope.rot / 2;
+    if (a.rope.inv_freq != nullptr && (int)blockIdx.x < a.nwg && a.T * half <= kFp8RopeTab) {
+      for (int i = threadIdx.x; i < a.T * half; i += NTH) {
+        float sn, cs;
+        sincosf((float)a.rope.positions[i / half] * a.rope.inv_freq[i % half], &sn, &cs);
+        rsc[i] = float2{sn, cs};
+      }
+      __syncthreads();
+      rtab = rsc;
+    }
+  }
   if constexpr (SELF) {
     if ((int)blockIdx.x >= a.nwg) {  // the query rotation rides in the same launch
       turn_rows(a.q, a.q_in, a.T, a.Hq, a.D, a.rope, (long)(blockIdx.x - a.nwg) * NTH + threadIdx.x,
                 (long)(gridDim.x - a.nwg) * NTH);
+      finish();
       return;
     }
     // a small write in one launch: every workgroup takes the maxima over all the
@@ -142,7 +236,7 @@ __global__ __launch_bounds__(SELF ? 1024 : 256) void fp8_write(Fp8WriteArgs a, i
         const int sl = e < n4 ? a.slot[e / row4] : -1;
         live[u] = sl >= 0 && sl / a.bs < a.nb;  // as the write loop: a page outside the pool is skipped
         const uint32_t ee = e < n4 ? e : e0;
-        k_word(a, k, ee, x[u]);
+        k_word(a, k, ee, x[u], rtab);
 #pragma unroll
         for (int j = 0; j < 4; ++j) y[u][j] = to_f32(v[4 * (size_t)ee + j]);
       }
@@ -202,7 +296,7 @@ __global__ __launch_bounds__(SELF ? 1024 : 256) void fp8_write(Fp8WriteArgs a, i
     const int blk = slot / a.bs, off = slot % a.bs;
     if (blk >= a.nb) continue;
     float x[4];
-    k_word(a, k, e, x);
+    k_word(a, k, e, x, rtab);
     uint32_t ck = 0, cv = 0;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -217,6 +311,7 @@ __global__ __launch_bounds__(SELF ? 1024 : 256) void fp8_write(Fp8WriteArgs a, i
       atomicMax(reinterpret_cast<unsigned int*>(a.vs) + blk, __float_as_uint(vsc));
     }
   }
+  finish();
 }
 
 }  // namespace emx

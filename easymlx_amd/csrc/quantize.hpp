@@ -134,6 +134,13 @@ __device__ __forceinline__ void turn_rows(h16* x, const h16* src, const int rows
   }
 }
 
+// (x0, x1) turned by the angle whose sine and cosine are given: rope_rotate's
+// arithmetic on a precomputed sincosf, so both give the same bits.
+__device__ __forceinline__ void rope_rotate_sc(const float x0, const float x1, const float2 sc, float& y0, float& y1) {
+  y0 = __fsub_rn(__fmul_rn(x0, sc.y), __fmul_rn(x1, sc.x));
+  y1 = __fadd_rn(__fmul_rn(x0, sc.x), __fmul_rn(x1, sc.y));
+}
+
 __global__ __launch_bounds__(256) void rope_rows(h16* x, const h16* src, int rows, int heads, int D, RopeArgs r) {
   turn_rows(x, src, rows, heads, D, r, (long)blockIdx.x * 256 + threadIdx.x, (long)gridDim.x * 256);
 }

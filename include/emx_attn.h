@@ -116,6 +116,23 @@ int emx_affine_cache_append_rope(const void* keys, const void* values, const int
                                  int num_q_heads, void* stream);
 
 /*
+ * The FP8 decode-step append with RoPE in one launch: emx_cache_slots and
+ * emx_fp8_cache_write_rope together for one token per sequence, with the
+ * positions, slots and kv_lens rule of emx_affine_cache_append_rope
+ * (num_tokens <= 1024 and at most 65536 values per tensor; otherwise
+ * EMX_ERR_UNSUPPORTED).  `counter`: one device int, zero before the first call,
+ * left zero by every call (calls sharing it must not overlap).
+ * Replaces the FP8 decode write of PageCacheView.concatenate_to_cache
+ *   lib/python/easymlx/caching/paged/cache.py:1126-1184 (RoPE :1161-1166).
+ */
+int emx_fp8_cache_append_rope(const void* keys, const void* values, int dtype, const int32_t* slot_ids,
+                              int num_tokens, const int32_t* block_tables, int num_seqs, int max_blocks_per_seq,
+                              int32_t* kv_lens, int* counter, int num_kv_heads, int head_dim, int page_size,
+                              int num_blocks, uint8_t* key_cache, uint8_t* value_cache, float* k_scales,
+                              float* v_scales, const float* inv_freq, int rot_dims, int traditional,
+                              const void* queries_in, void* queries, int num_q_heads, void* stream);
+
+/*
  * Write positions of a cache write, on the device: token t of sequence i
  * (query_start_loc[i] <= t < query_start_loc[i+1], i < num_slots, int32 arrays
  * on the device) of slot s = slot_ids[i] goes to position

@@ -111,3 +111,67 @@ def test_append_rejects_unsupported_geometry(cuda):
     rc = lib.emx_affine_cache_append_rope(p, p, p, 1, p, 1, 1, p, p, 1, 128, 128, 4, 128, 1, p, p, p, p, p, p, p,
                                           128, 0, None, None, 0, None)
     assert rc == _native.EMX_ERR_UNSUPPORTED
+
+
+@pytest.mark.parametrize("bs,trad", [(128, False), (16, True)])
+def test_fp8_append_matches_the_two_launch_write(cuda, bs, trad):
+    """``emx_fp8_cache_append_rope`` against ``emx_cache_slots`` + ``emx_fp8_cache_write_rope``: codes, page
+    scales, kv_lens and the turned queries bit for bit."""
+    print(f"[fp8 append bs={bs} traditional={trad}]", flush=True)
+    from easymlx_amd import Fp8PageCacheView
+
+    rng = np.random.default_rng(500 + bs)
+    S, hkv, hq, d, mb = 12, 4, 16, 128, 5
+    nb = S * mb + 3
+    tables = rng.permutation(nb)[:S * mb].astype(np.int32).reshape(S, mb)
+    lens = rng.integers(0, mb * bs, S).astype(np.int32)
+    lens[1] = bs
+    lens[2] = mb * bs
+    tables[3, lens[3] // bs] = -1
+    rope = RotaryEmbedding(d, traditional=trad, base=10000.0)
+    lib = _native.load()
+    st = torch.cuda.current_stream(cuda).cuda_stream
+
+    def view():
+        kc = torch.from_numpy(rng.integers(0, 256, (nb, bs, hkv, d), dtype=np.uint8)).to(cuda)
+        return Fp8PageCacheView(key_cache=kc, value_cache=kc.clone(),
+                                k_scales=torch.from_numpy(rng.random(nb, dtype=np.float32)).to(cuda),
+                                v_scales=torch.from_numpy(rng.random(nb, dtype=np.float32)).to(cuda),
+                                block_tables=torch.from_numpy(tables).to(cuda),
+                                kv_lens=torch.from_numpy(lens).to(cuda), block_size=bs, num_kv_heads=hkv,
+                                head_dim=d)
+
+    base = view()
+    counter = torch.zeros(1, dtype=torch.int32, device=cuda)
+    ws = torch.empty(int(lib.emx_fp8_write_workspace_bytes()), dtype=torch.uint8, device=cuda)
+    inv = rope.inv_freq(cuda)
+    for slots in (tuple(range(S)), (7, 3, 11, 4, 0, 2), (6, -1, 9, S + 2, 10)):
+        a = [t.clone() for t in (base.key_cache, base.value_cache, base.k_scales, base.v_scales, base.kv_lens)]
+        b = [t.clone() for t in a]
+        bt = base.block_tables
+        for rep in range(2):
+            n = len(slots)
+            k = torch.from_numpy(rng.standard_normal((n, hkv, d)).astype(np.float16) * 3).to(cuda)
+            v = torch.from_numpy(rng.standard_normal((n, hkv, d)).astype(np.float16) * 3).to(cuda)
+            q = torch.from_numpy(rng.standard_normal((n, hq, d)).astype(np.float16)).to(cuda)
+            meta = torch.tensor(list(slots) + list(range(n + 1)), dtype=torch.int32, device=cuda)
+            mapping = torch.empty(n, dtype=torch.int32, device=cuda)
+            pos = torch.empty(n, dtype=torch.int32, device=cuda)
+            _native.check(lib.emx_cache_slots(meta[:n].data_ptr(), meta[n:].data_ptr(), n, n, bt.data_ptr(), S, mb,
+                                              bs, a[4].data_ptr(), mapping.data_ptr(), pos.data_ptr(), st))
+            qa = torch.empty_like(q)
+            _native.check(lib.emx_fp8_cache_write_rope(
+                k.data_ptr(), v.data_ptr(), _native.DTYPE_F16, mapping.data_ptr(), n, hkv, d, bs, nb,
+                a[0].data_ptr(), a[1].data_ptr(), a[2].data_ptr(), a[3].data_ptr(), ws.data_ptr(), ws.numel(),
+                pos.data_ptr(), inv.data_ptr(), rope.dims, int(trad), q.data_ptr(), qa.data_ptr(), hq, st))
+            qb = torch.empty_like(q)
+            _native.check(lib.emx_fp8_cache_append_rope(
+                k.data_ptr(), v.data_ptr(), _native.DTYPE_F16, meta[:n].data_ptr(), n, bt.data_ptr(), S, mb,
+                b[4].data_ptr(), counter.data_ptr(), hkv, d, bs, nb, b[0].data_ptr(), b[1].data_ptr(),
+                b[2].data_ptr(), b[3].data_ptr(), inv.data_ptr(), rope.dims, int(trad), q.data_ptr(), qb.data_ptr(),
+                hq, st))
+            torch.cuda.synchronize()
+            assert torch.equal(qa, qb), (slots, rep)
+            for x, y in zip(a, b):
+                assert torch.equal(x, y), (slots, rep)
+            assert int(counter.item()) == 0
