@@ -54,17 +54,23 @@ __device__ __forceinline__ float round_to(float x, h16*) { return (float)(h16)x;
 __device__ __forceinline__ float round_to(float x, uint16_t*) { return bf16_to_f32(f32_to_bf16(x)); }
 __device__ __forceinline__ float round_to(float x, float*) { return x; }
 
-// The 4 K values of word e (dims 4w .. 4w+3 of one token and head), turned by
-// the call's RoPE and rounded to the input dtype when a.rope is set (the
-// reference writes the rotated keys of the model's dtype).  Needs rot % 8 == 0
-// (non-traditional): a word and its partner word lie in one half each.
-// tab: null, or (sin, cos) of positions[t] * inv_freq[i] at t * (rot / 2) + i (the
-// one-launch write builds it once per workgroup instead of a sincosf per value).
+// The word whose values pair with word e's in the rotation (non-traditional: the
+// other half of the rotated dims); e itself when word e is not turned in pairs
+// across words.
+__device__ __forceinline__ uint32_t k_partner(const Fp8WriteArgs& a, const uint32_t e) {
+  const RopeArgs& r = a.rope;
+  if (r.inv_freq == nullptr || r.traditional) return e;
+  const uint32_t wpr = a.D / 4;
+  const int d0 = 4 * (int)(e % wpr);
+  if (d0 >= r.rot) return e;
+  const int half = r.rot / 2;
+  return d0 < half ? e + half / 4 : e - half / 4;
+}
+
+// Word e's 4 values x turned, given its partner word's values p (k_partner).
 template <typename T>
-__device__ __forceinline__ void k_word(const Fp8WriteArgs& a, const T* k, const uint32_t e, float (&x)[4],
-                                       const float2* tab = nullptr) {
-#pragma unroll
-  for (int j = 0; j < 4; ++j) x[j] = to_f32(k[4 * (size_t)e + j]);
+__device__ __forceinline__ void k_turn(const Fp8WriteArgs& a, const uint32_t e, float (&x)[4], const float (&p)[4],
+                                       const float2* tab) {
   const RopeArgs& r = a.rope;
   if (r.inv_freq == nullptr) return;
   const uint32_t wpr = a.D / 4;  // words per head row
@@ -86,28 +92,45 @@ __device__ __forceinline__ void k_word(const Fp8WriteArgs& a, const T* k, const 
   } else {
     const int half = r.rot / 2;
     const bool lo = d0 < half;
-    const uint32_t pe = lo ? e + half / 4 : e - half / 4;  // the partner word
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const float p = to_f32(k[4 * (size_t)pe + j]);
       float y0, y1;
       const int i = (lo ? d0 : d0 - half) + j;
       if (tab) {
         if (lo)
-          rope_rotate_sc(x[j], p, tt[i], y0, y1);
+          rope_rotate_sc(x[j], p[j], tt[i], y0, y1);
         else
-          rope_rotate_sc(p, x[j], tt[i], y1, y0);
+          rope_rotate_sc(p[j], x[j], tt[i], y1, y0);
       } else {
         if (lo)
-          rope_rotate(x[j], p, pos * r.inv_freq[i], y0, y1);
+          rope_rotate(x[j], p[j], pos * r.inv_freq[i], y0, y1);
         else
-          rope_rotate(p, x[j], pos * r.inv_freq[i], y1, y0);
+          rope_rotate(p[j], x[j], pos * r.inv_freq[i], y1, y0);
       }
       y[j] = y0;
     }
   }
 #pragma unroll
   for (int j = 0; j < 4; ++j) x[j] = round_to(y[j], (T*)nullptr);
+}
+
+// The 4 K values of word e (dims 4w .. 4w+3 of one token and head), turned by
+// the call's RoPE and rounded to the input dtype when a.rope is set (the
+// reference writes the rotated keys of the model's dtype).  Needs rot % 8 == 0
+// (non-traditional): a word and its partner word lie in one half each.
+// tab: null, or (sin, cos) of positions[t] * inv_freq[i] at t * (rot / 2) + i (the
+// one-launch write builds it once per workgroup instead of a sincosf per value).
+template <typename T>
+__device__ __forceinline__ void k_word(const Fp8WriteArgs& a, const T* k, const uint32_t e, float (&x)[4],
+                                       const float2* tab = nullptr) {
+  const uint32_t pe = k_partner(a, e);
+  float p[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    x[j] = to_f32(k[4 * (size_t)e + j]);
+    p[j] = to_f32(k[4 * (size_t)pe + j]);
+  }
+  k_turn<T>(a, e, x, p, tab);
 }
 
 template <typename Tag>
@@ -230,16 +253,24 @@ __global__ __launch_bounds__(SELF ? 1024 : 256) void fp8_write(Fp8WriteArgs a, i
     for (uint32_t e0 = threadIdx.x; e0 < n4; e0 += 4 * NTH) {
       float x[4][4], y[4][4];
       bool live[4];
+      float p[4][4];
+      uint32_t ee[4];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
+      for (int u = 0; u < 4; ++u) {  // every load of the four words first, then the turns
         const uint32_t e = e0 + (uint32_t)u * NTH;
         const int sl = e < n4 ? a.slot[e / row4] : -1;
         live[u] = sl >= 0 && sl / a.bs < a.nb;  // as the write loop: a page outside the pool is skipped
-        const uint32_t ee = e < n4 ? e : e0;
-        k_word(a, k, ee, x[u], rtab);
+        ee[u] = e < n4 ? e : e0;
+        const uint32_t pe = k_partner(a, ee[u]);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) y[u][j] = to_f32(v[4 * (size_t)ee + j]);
+        for (int j = 0; j < 4; ++j) {
+          x[u][j] = to_f32(k[4 * (size_t)ee[u] + j]);
+          p[u][j] = to_f32(k[4 * (size_t)pe + j]);
+          y[u][j] = to_f32(v[4 * (size_t)ee[u] + j]);
+        }
       }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) k_turn<T>(a, ee[u], x[u], p[u], rtab);
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         if (!live[u]) continue;
