@@ -310,6 +310,54 @@ struct Q4Geom {
   static_assert(HQ == 1 || HQ == 2 || HQ == 4, "GQA ratio 1, 2, 4, 8 or 16");
 };
 
+// Cost-balanced ranges.  A workgroup's time grows with its items (kCostItem
+// each), with the units it touches (kCostUnit each: the unit-end reductions,
+// combine and stores, and the split-K partial and merge of a shared unit) and,
+// for a workgroup that starts in the second slot of a compute unit, by a start
+// delay (kCostLag: its first loads queue behind the first workgroup's).  With
+//   C(x) = kCostItem * x + kCostUnit * #{unit starts <= x}   (units with items)
+// workgroup w starts at b_w = min{x : NWG * C(x) >= T_w}, where
+//   T_w = w * P                    for w <= N1 (first-slot workgroups),
+//   T_w = N1 * P + (w - N1) * Q    after,  P = C(I) + Le * (NWG - N1), Q = P - NWG * Le,
+// so every range gets an equal share of C, the second-slot ones Le less, and
+// T_NWG = NWG * C(I).  A target inside the step of C at a unit start lands on
+// that start, so ranges prefer to end at unit boundaries.  Only wave-uniform
+// integer multiplications and float estimates corrected by exact comparisons: no
+// 64-bit division.  c2: equal item ranges 27.2 us, these 26.1 us (kCostUnit 20..32
+// and kCostLag 31..48 all within 0.2 us of each other); the same ranges handed in
+// from the host measured 24.9-25.1 us, the difference being this search on every
+// workgroup's critical path (~2 us from kv_lens to the boundaries).
+constexpr int kCostItem = 16, kCostUnit = 24, kCostLag = 48;
+
+struct Q4Balance {
+  long long P, Q;
+  int NWG, N1;
+  __device__ __forceinline__ long long target(const int w) const {
+    return w <= N1 ? (long long)w * P : (long long)N1 * P + (long long)(w - N1) * Q;
+  }
+  // The workgroup whose range holds an item x with NWG * C(x) = X: max{w < NWG : T_w <= X}.
+  __device__ __forceinline__ int wg_of(const long long X) const {
+    const long long XN = (long long)N1 * P;
+    int w = X < XN ? (int)((float)X / (float)P) : N1 + (int)((float)(X - XN) / (float)Q);
+    w = min(max(w, 0), NWG - 1);
+    while (w + 1 < NWG && target(w + 1) <= X) ++w;
+    while (w > 0 && target(w) > X) --w;
+    return w;
+  }
+};
+
+// Q4Balance::wg_of with one lane per candidate around the float estimate (one
+// ballot); the scalar correction loop only if the estimate were off by > 31.
+__device__ __forceinline__ int wg_of_lanes(const Q4Balance& bl, const long long X, const int lane) {
+  const long long XN = (long long)bl.N1 * bl.P;
+  const int est = X < XN ? (int)((float)X * __builtin_amdgcn_rcpf((float)bl.P))
+                         : bl.N1 + (int)((float)(X - XN) * __builtin_amdgcn_rcpf((float)bl.Q));
+  const int w = est - 31 + lane;
+  const unsigned long long pb = __ballot(w <= 0 || (w < bl.NWG && bl.target(w) <= X));
+  if (pb != ~0ull && (pb & 1ull)) return min(max(est - 31 + 63 - __builtin_clzll(pb), 0), bl.NWG - 1);
+  return bl.wg_of(X);
+}
+
 constexpr int kTableCache = 4096;  // block-table entries a workgroup keeps in LDS
 constexpr int kSnapItems = 2;     // unit length (items) up to which ranges end on unit starts ...
 constexpr int kSnapRange = 4;     // ... when the ranges average at most this many items
@@ -331,7 +379,8 @@ __device__ __forceinline__ void decode_q4_body(const DecodeArgs& a, const int bi
   constexpr int oCum = 0, oKvl = lds_next(oCum, 4 * (kMaxSeqs + 1)), oQrw = lds_next(oKvl, 4 * kMaxSeqs);
   constexpr int oSo = lds_next(oQrw, 4 * kMaxSeqs), oSml = lds_next(oSo, 4 * 2 * 4 * 4 * D);
   constexpr int oSlast = lds_next(oSml, 4 * 2 * 4 * 4 * 2), oSbt = lds_next(oSlast, 4 * 2);
-  constexpr int oSst = lds_next(oSbt, 4 * kTableCache), oEnd = lds_next(oSst, 8 * 4 * 16 * 4 * G);
+  constexpr int oSst = lds_next(oSbt, 4 * kTableCache), oXb = lds_next(oSst, 8 * 4 * 16 * 4 * G);
+  constexpr int oEnd = lds_next(oXb, 24);
   static_assert(oEnd <= kArenaBytes, "LDS arena too small");
   int(&cum)[kMaxSeqs + 1] = lds_at<int[kMaxSeqs + 1]>(oCum);
   int(&kvl)[kMaxSeqs] = lds_at<int[kMaxSeqs]>(oKvl);
@@ -358,9 +407,10 @@ __device__ __forceinline__ void decode_q4_body(const DecodeArgs& a, const int bi
     for (int k = 0; k < kTableCache / 256; ++k) sbt[threadIdx.x + 256 * k] = btv[k];
     __syncthreads();
   }
-  {  // decoded sequences without a live token produce zeros (the reference's l == 0 case)
+  if (wv >= 2) {  // decoded sequences without a live token produce zeros (the reference's l == 0 case);
+                  // waves 2-3, while waves 0-1 find the workgroup's range (below)
     const int per_seq = a.Hq * D / 8;
-    for (int i = bid * 256 + threadIdx.x; i < a.S * per_seq; i += nblocks * 256) {
+    for (int i = bid * 128 + threadIdx.x - 128; i < a.S * per_seq; i += nblocks * 128) {
       const int si = i / per_seq;
       if (kvl[si] >= 0 && cum[si + 1] == cum[si])
         reinterpret_cast<u32x4*>(a.out)[(size_t)qrw[si] * per_seq + i % per_seq] = u32x4{0u, 0u, 0u, 0u};
@@ -380,8 +430,109 @@ __device__ __forceinline__ void decode_q4_body(const DecodeArgs& a, const int bi
   // move to the next unit start instead, so no unit is shared between workgroups
   // and no split-K partial, arrival or merge is left (batch 64, contexts 64..512:
   // 17.3 -> 15.1 us).  A range may then be empty.
-  long long g0 = ((long long)wg * I) / NWG;
-  long long g1 = ((long long)(wg + 1) * I) / NWG;
+  // ---- cost-balanced range [g0, g1) of this workgroup (see Q4Balance).  Wave 0 finds
+  // the start, wave 1 the end, each with the pieces of the unit the boundary cuts
+  // (if any); they meet in LDS.  One wave per boundary: the workgroup's waves share one
+  // scalar unit per compute unit, and eight waves each repeating the search cost ~5 us.
+  long long(&xb)[2] = lds_at<long long[2]>(oXb);
+  int(&xpk)[2] = lds_at<int[2]>(oXb + 16);
+  if (wv < 2) {
+    int ne_tot = 0;  // sequences with items
+    for (int c = 0; c < S; c += 64) {
+      const int si = c + lane;
+      ne_tot += __builtin_popcountll(__ballot(si < S && cum[si + 1] > cum[si]));
+    }
+    ne_tot = uru(ne_tot);
+    const long long Ctot = (long long)kCostItem * I + (long long)kCostUnit * Hkv * ne_tot;
+    const int N1 = a.first_slot > 0 ? min(a.first_slot, NWG) : NWG;
+    int Le = 0;
+    if (N1 < NWG) {  // Q >= NWG * kCostItem keeps ranges inside a unit non-empty
+      Le = min(kCostLag, max(0, (int)((float)Ctot / (float)NWG) - kCostItem));
+      while (Le > 0 && Ctot - (long long)Le * N1 < (long long)NWG * kCostItem) --Le;
+    }
+    const Q4Balance bl{Ctot + (long long)Le * (NWG - N1), Ctot - (long long)Le * N1, NWG, N1};
+    // b = min{x in [0, I] : NWG * C(x) >= T}: the last sequence with items whose start
+    // lies below T (ballot over 64 sequences at a time), its last unit below T, then
+    // the item inside that unit.  A boundary inside a unit also yields that unit's
+    // pieces, pk = wf | np << 16 (the workgroups holding its first and last item).
+    const int w = wg + wv;
+    long long b = w == 0 ? 0 : I;
+    int pk = 1 << 16;
+    if (w > 0 && w < NWG) {
+      const long long T = bl.target(w);
+      int sb = -1, sne = 0, ne_run = 0;
+      for (int c = 0; c < S; c += 64) {
+        const int si = c + lane;
+        const int n = si < S ? cum[si + 1] - cum[si] : 0;
+        const unsigned long long live = __ballot(n > 0);
+        const int ne = ne_run + __builtin_popcountll(live & ((1ull << lane) - 1ull));
+        const long long Cs =
+            (long long)kCostItem * Hkv * (si < S ? cum[si] : 0) + (long long)kCostUnit * ((long long)Hkv * ne + 1);
+        const bool below = n > 0 && (long long)NWG * Cs < T;
+        const unsigned long long pb = __ballot(below);
+        if (pb) {
+          const int Lb = 63 - __builtin_clzll(pb);
+          sb = c + Lb;
+          sne = __builtin_amdgcn_readlane(ne, Lb);
+        }
+        ne_run += __builtin_popcountll(live);
+        if (__ballot(n > 0 && !below)) break;
+      }
+      b = 0;
+      if (sb >= 0) {
+        sb = uru(sb);
+        sne = uru(sne);
+        const int n = uru(cum[sb + 1]) - uru(cum[sb]);
+        const long long st0 = (long long)Hkv * uru(cum[sb]);
+        const long long C0 = (long long)kCostItem * st0 + (long long)kCostUnit * ((long long)Hkv * sne + 1);
+        const long long slope = (long long)kCostItem * n + kCostUnit;  // C between consecutive unit starts
+        // lane-parallel from here (a wave's serial scalar chain runs at a few hundred
+        // instructions per microsecond, and this is on every workgroup's critical path):
+        // the unit h = last with NWG * C(start of h) < T, one lane per unit ...
+        int h = 0;
+        for (int c = 0; c < Hkv; c += 64) {
+          const int hh = c + lane;
+          const unsigned long long pb = __ballot(hh < Hkv && (long long)NWG * (C0 + (long long)hh * slope) < T);
+          if (pb) h = c + 63 - __builtin_clzll(pb);
+          if (!(pb >> 63)) break;
+        }
+        h = uru(h);
+        const long long Cu = C0 + (long long)h * slope;
+        // ... then jj = 1 + #{j in [1, n) : NWG * (Cu + kCostItem * j) < T}, one lane per j
+        // (jj = n: the next unit start, whose step of C reaches T)
+        int jj = 1;
+        for (int c = 1; c < n; c += 64) {
+          const int j = c + lane;
+          const unsigned long long pb = __ballot(j < n && (long long)NWG * (Cu + (long long)kCostItem * j) < T);
+          jj += __builtin_popcountll(pb);
+          if (!(pb >> 63)) break;
+        }
+        jj = uru(jj);
+        b = st0 + (long long)h * n + jj;
+        if (jj < n) {  // the range boundary cuts the unit: its pieces
+          const int wf = wg_of_lanes(bl, (long long)NWG * Cu, lane);
+          const int np = wg_of_lanes(bl, (long long)NWG * (Cu + (long long)kCostItem * (n - 1)), lane) - wf + 1;
+          pk = wf | (np << 16);
+        }
+      }
+    }
+    if (lane == 0) {
+      xb[wv] = b;
+      xpk[wv] = pk;
+    }
+  }
+  __syncthreads();
+  // LDS reads are per lane to the compiler: the boundaries go back to scalar registers
+  auto uru64 = [](long long v) {
+    return (long long)(((unsigned long long)(unsigned)__builtin_amdgcn_readfirstlane((int)(v >> 32)) << 32) |
+                       (unsigned)__builtin_amdgcn_readfirstlane((int)v));
+  };
+  long long g0 = uru64(xb[0]);
+  long long g1 = uru64(xb[1]);
+  // pieces (wf | np << 16, both below kMaxWaves) of the units the range shares: its first
+  // (begun before g0) and its last (going on past g1)
+  int pk_first = uru(xpk[0]), pk_last = uru(xpk[1]);
+  if (g0 >= g1) return;
   int max_items = kSnapItems + 1;
   if (I <= (long long)kSnapRange * NWG) {  // longest unit, by every wave for itself (no barrier)
     max_items = 0;
@@ -402,11 +553,6 @@ __device__ __forceinline__ void decode_q4_body(const DecodeArgs& a, const int bi
       const long long base = (long long)Hkv * cum[lo];
       const int n = cum[lo + 1] - cum[lo];
       return base + (long long)((((int)(x - base)) + n - 1) / n) * n;
-    };
-    // LDS reads are per lane to the compiler: the boundaries go back to scalar registers
-    auto uru64 = [](long long v) {
-      return (long long)(((unsigned long long)(unsigned)__builtin_amdgcn_readfirstlane((int)(v >> 32)) << 32) |
-                         (unsigned)__builtin_amdgcn_readfirstlane((int)v));
     };
     g0 = uru64(wg == 0 ? 0 : unit_start(g0));
     g1 = uru64(wg + 1 == NWG ? I : unit_start(g1));
@@ -547,8 +693,16 @@ __device__ __forceinline__ void decode_q4_body(const DecodeArgs& a, const int bi
   // shared units awaiting their arrival (at most the range's first and last unit)
   int npend = 0;
   int nue = 0;  // unit ends passed (uniform across the workgroup)
-  int pend_u[2], pend_row[2], pend_kvh[2], pend_n[2];
-  long long pend_first[2];
+  int pend_u[2], pend_row[2], pend_kvh[2], pend_wf[2], pend_np[2];
+  auto pieces = [&](const int u, const int wf, const int np) {
+    PieceInfo pi;
+    pi.np = __builtin_amdgcn_readfirstlane(np);
+    pi.slot0 = __builtin_amdgcn_readfirstlane(wf + u);  // the pieces of unit u sit in slots wf+u .. wl+u
+    pi.me = __builtin_amdgcn_readfirstlane(wg - wf);
+    pi.ro = uniform_rsrc(a.ws_o + (size_t)pi.slot0 * (HG * D), pi.np * HG * D * 4);
+    pi.rm = uniform_rsrc(a.ws_ml + (size_t)pi.slot0 * (HG * 2), pi.np * HG * 2 * 4);
+    return pi;
+  };
 
   auto step = [&](Q4Loads<GS, 1>& cur, Q4Loads<GS, 1>& nxt, const long long g) {
     // ---- next item (the state is wave-uniform: scalar registers and branches)
@@ -633,11 +787,17 @@ __device__ __forceinline__ void decode_q4_body(const DecodeArgs& a, const int bi
           sml[par][wv][lane][1] = l;
         }
       }
+      int wf = 0, np = 1;
       {
         // every wave has its (o, m, l) of the unit in LDS: all four combine it together
         __syncthreads();
         PieceInfo pi;
-        if (!whole) pi = piece_info<HG>(a, wg, u, unit_first, n_s, I, NWG);
+        if (!whole) {  // the range's first unit (begun before g0) or its last (going on past g1)
+          const int pk = unit_first < g0 ? pk_first : pk_last;
+          wf = pk & 0xFFFF;
+          np = pk >> 16;
+          pi = pieces(u, wf, np);
+        }
         // Two adjacent dims per thread, so a thread issues one 4-byte output store
         // (or one 8-byte partial store): the stores wait for room in the memory
         // queue the page loads keep full, and one element per store made this
@@ -680,8 +840,8 @@ __device__ __forceinline__ void decode_q4_body(const DecodeArgs& a, const int bi
         pend_u[npend] = u;
         pend_row[npend] = row;
         pend_kvh[npend] = kvh;
-        pend_n[npend] = n_s;
-        pend_first[npend] = unit_first;
+        pend_wf[npend] = wf;
+        pend_np[npend] = np;
         ++npend;
       }
       reset();
@@ -716,7 +876,7 @@ __device__ __forceinline__ void decode_q4_body(const DecodeArgs& a, const int bi
     __syncthreads();                // ... and so are the workgroup's
     if (threadIdx.x < npend) {  // one thread per shared unit: both arrivals in flight together
       const int p = threadIdx.x;
-      const int np = piece_count(pend_first[p], pend_n[p], I, NWG);
+      const int np = pend_np[p];
       const int old = __hip_atomic_fetch_add(a.ws_cnt + pend_u[p], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       const bool last = old == np - 1;
       if (last) __hip_atomic_store(a.ws_cnt + pend_u[p], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -732,7 +892,7 @@ __device__ __forceinline__ void decode_q4_body(const DecodeArgs& a, const int bi
       const int T = mg0 && mg1 ? 128 : 256;
       const int p = mg0 && mg1 ? (wv >> 1) : (mg0 ? 0 : 1);
       const int t = threadIdx.x & (T - 1);
-      const PieceInfo pi = piece_info<HG>(a, wg, pend_u[p], pend_first[p], pend_n[p], I, NWG);
+      const PieceInfo pi = pieces(pend_u[p], pend_wf[p], pend_np[p]);
       h16* out = a.out + ((size_t)pend_row[p] * a.Hq + (size_t)pend_kvh[p] * HG) * D;
       constexpr int NF4 = HG * D / 4;
       for (int f = t; f < NF4; f += T) {

@@ -989,6 +989,8 @@ int emx_paged_attention_affine(const void* queries, int num_tokens, int num_q_he
       hipLaunchKernelGGL(uf, dim3((unsigned)(pgrid + ndec)), dim3(256), 0, st, p, a, ndec);
       return check_launch(q4 ? "unified_q4" : "unified_affine");
     }
+    // two workgroups per compute unit: the second of each starts later (4-bit kernel's range balance)
+    a.first_slot = q4 ? nw / 8 : 0;
     hipLaunchKernelGGL(fn, dim3((unsigned)(nw / 4)), dim3(256), 0, st, a);
     return check_launch("decode_affine_d128");
   }
