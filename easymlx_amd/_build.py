@@ -23,6 +23,9 @@ HIPCC_FLAGS = [
     "-target-feature",
     "-Xclang",
     "-packed-fp32-ops",
+    # leading kernel arguments arrive in SGPRs with the wave (gfx950 kernel-argument preload)
+    "-mllvm",
+    "-amdgpu-kernarg-preload-count=16",
 ]
 
 

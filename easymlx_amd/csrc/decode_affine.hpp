@@ -61,6 +61,7 @@ struct DecodeArgs {
   int window;                 // sliding window, 0 = off
   int num_waves;              // waves of the persistent decode grid
   int nt;                     // tokens per work item (64 at 4-bit, 32 at 8-bit and FP8)
+  int* plan = nullptr;        // 4-bit kernel, pure decode: the workspace's plan cache (decode_q4.hpp)
   int first_slot = 0;         // 4-bit kernel: workgroups that start in the first slot of a compute unit
                               // (the rest start later; 0 = all start together)
   const float* kps;           // FP8 pages only: key / value scale per page [nb]

@@ -358,6 +358,30 @@ __device__ __forceinline__ int wg_of_lanes(const Q4Balance& bl, const long long 
   return bl.wg_of(X);
 }
 
+// Plan cache.  A decode step runs the same batch through every layer: the same
+// kv_lens, so the same item counts, workgroup ranges and first items.  A pure
+// decode call (no mixed batch) keeps, in a region of the caller's workspace, the
+// plan it computed: per workgroup {g0, g1, pk_first, pk_last, first sequence,
+// kv head, token base, -, page of each 64-token slice of the first item}, plus a
+// copy of kv_lens and a header {generation, S, Hkv, NWG, window, first_slot,
+// kernel kind, kv_len cap}.  The next call on the workspace loads its entry,
+// the header and the copy in its first memory round trip, sends the first
+// item's query and page loads out at once, and uses the cached ranges when the
+// header matches its shape and the copy matches kv_lens (compared during the
+// table scan); its first item's pages are checked against the block table
+// (which may change under the same kv_lens) and loaded again if they differ.
+// Otherwise it computes the ranges itself and writes its own plan into the
+// other slot; the workgroup counted last on header[15] then publishes it (every
+// workgroup of the call has read the old header by then, so none of them reads a
+// slot while it is written).  Zero-filled: no plan (generation 0).
+constexpr int kPlanMaxWG = 1024;  // workgroup entries per slot
+constexpr int kPlanSlotInts = kMaxSeqs + 16 * kPlanMaxWG;
+constexpr int kPlanInts = 16 + 2 * kPlanSlotInts;
+__host__ __device__ constexpr int q4_plan_kvl(const int slot) { return 16 + slot * kPlanSlotInts; }
+__host__ __device__ constexpr int q4_plan_entry(const int slot, const int w) {
+  return q4_plan_kvl(slot) + kMaxSeqs + 16 * w;
+}
+
 constexpr int kTableCache = 4096;  // block-table entries a workgroup keeps in LDS
 constexpr int kSnapItems = 2;     // unit length (items) up to which ranges end on unit starts ...
 constexpr int kSnapRange = 4;     // ... when the ranges average at most this many items
@@ -365,7 +389,9 @@ constexpr int kSnapRange = 4;     // ... when the ranges average at most this ma
 // The kernel body as workgroup `bid` of `nblocks` (a grid of its own, or the
 // decode part of a mixed batch's single launch, unified_q4).
 template <int GS, int HG>
-__device__ __forceinline__ void decode_q4_body(const DecodeArgs& a, const int bid, const int nblocks) {
+__device__ __forceinline__ void decode_q4_body(const DecodeArgs& a, const int bid, const int nblocks, int* const plan,
+                                               const int32_t* const kv_lens, const int32_t* const block_tables,
+                                               const int S, const int max_blocks) {
   using Geo = Q4Geom<HG>;
   constexpr int HQ = Geo::HQ, NSL = Geo::NSL, TW = Geo::TW;
   constexpr int D = 128, G = Q4Cfg<GS, 1>::G;
@@ -380,7 +406,7 @@ __device__ __forceinline__ void decode_q4_body(const DecodeArgs& a, const int bi
   constexpr int oSo = lds_next(oQrw, 4 * kMaxSeqs), oSml = lds_next(oSo, 4 * 2 * 4 * 4 * D);
   constexpr int oSlast = lds_next(oSml, 4 * 2 * 4 * 4 * 2), oSbt = lds_next(oSlast, 4 * 2);
   constexpr int oSst = lds_next(oSbt, 4 * kTableCache), oXb = lds_next(oSst, 8 * 4 * 16 * 4 * G);
-  constexpr int oEnd = lds_next(oXb, 24);
+  constexpr int oEnd = lds_next(oXb, 64);
   static_assert(oEnd <= kArenaBytes, "LDS arena too small");
   int(&cum)[kMaxSeqs + 1] = lds_at<int[kMaxSeqs + 1]>(oCum);
   int(&kvl)[kMaxSeqs] = lds_at<int[kMaxSeqs]>(oKvl);
@@ -391,50 +417,227 @@ __device__ __forceinline__ void decode_q4_body(const DecodeArgs& a, const int bi
   // Block tables of up to kTableCache entries are read into LDS together with
   // kv_lens (one memory round trip for both), larger ones from global memory.
   int(&sbt)[kTableCache] = lds_at<int[kTableCache]>(oSbt);
-  const int nbt = a.S * a.max_blocks;
+  const int Hkv = a.Hkv;
+  // LDS table entries read at a wave-uniform index are moved to SGPRs (uru), so the
+  // per-item scheduling arithmetic stays scalar
+  auto uru = [](int v) { return __builtin_amdgcn_readfirstlane(v); };
+  const int nbt = S * max_blocks;
   const bool bt_lds = nbt <= kTableCache;
+
+  // ---- query operand of a unit (this wave's head quad).  Lane L (head 4*quad + L%4,
+  // 16-lane group n = L/16) holds, in VGPR pair r, the operand of k-step 4r + n: K word
+  // m = 2r + n/2, dims 8m + (n even ? {0,4,1,5} : {2,6,3,7}), the last two / 16.
+  const int n16 = lane >> 4;
+  const int qhalf = n16 & 1;
+  uint32_t qraw[8][2];
+  auto issue_q = [&](int row, int kh) {
+    const uint32_t* qp = reinterpret_cast<const uint32_t*>(
+        a.q + ((size_t)row * a.Hq + (size_t)kh * HG + (hl < HG ? hl : 0)) * D);
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      const int m = 2 * r + (n16 >> 1);
+      qraw[r][0] = qp[4 * m + qhalf];      // dims 8m + 2*qhalf + {0, 1}
+      qraw[r][1] = qp[4 * m + qhalf + 2];  // dims 8m + 2*qhalf + {4, 5}
+    }
+  };
+  h16x4 qB[1][8];
+  float qs[1][2];
+  auto build_q = [&]() {
+    const bool ok = hl < HG;
+    float gsum[2] = {0.f, 0.f};
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      const int m = 2 * r + (n16 >> 1);
+      const h16 d0 = __builtin_bit_cast(h16, (uint16_t)(qraw[r][0] & 0xFFFFu));
+      const h16 d1 = __builtin_bit_cast(h16, (uint16_t)(qraw[r][0] >> 16));
+      const h16 d4 = __builtin_bit_cast(h16, (uint16_t)(qraw[r][1] & 0xFFFFu));
+      const h16 d5 = __builtin_bit_cast(h16, (uint16_t)(qraw[r][1] >> 16));
+      // element order (nibble 0,4 | 1,5) of the word pair; with qhalf the dims are offset by 2
+      const h16x4 v = {d0, d4, (h16)((float)d1 * 0.0625f), (h16)((float)d5 * 0.0625f)};
+      qB[0][r] = ok ? v : h16x4{(h16)0.f, (h16)0.f, (h16)0.f, (h16)0.f};
+      const float sum = ok ? ((float)d0 + (float)d1) + ((float)d4 + (float)d5) : 0.f;
+      if (G == 1 || (8 * m) / GS == 0)
+        gsum[0] += sum;
+      else
+        gsum[1] += sum;
+    }
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      float x = gsum[g];
+      x += __shfl_xor(x, 16, 64);
+      x += __shfl_xor(x, 32, 64);
+      qs[0][g] = x * (1.0f / kTwo24);  // bias term in the 2^-24 units of the MFMA output
+    }
+  };
+
+
+  // descriptors of this wave's slice at token t of page b (zero-size, reading nothing, when b is
+  // invalid), and the element offset of the page-head's scales (page 0 when b is invalid)
+  auto tile_of = [&](int b, int kh, int t, size_t& soff) {
+    const bool ok = (unsigned)b < (unsigned)a.nb;
+    const int off = t & (a.bs - 1) & ~127;  // page sizes are powers of two here
+    const size_t ph = (size_t)(ok ? b : 0) * a.Hkv + kh;
+    const int RW = a.bs * 4 / 32;
+    TileRsrc r;
+    r.k = uniform_rsrc(a.kc + (ph * a.bs + off) * 16, ok ? 128 * 16 * 4 : 0);
+    r.v = uniform_rsrc(a.vc + ph * D * RW + (off / 64) * D * 8, ok ? (D * RW - (off / 64) * D * 8) * 4 : 0);
+    soff = ph * G * a.bs + off;
+    return r;
+  };
+  // LDS reads are per lane to the compiler: 64-bit values go back to scalar registers
+  auto uru64 = [](long long v) {
+    return (long long)(((unsigned long long)(unsigned)__builtin_amdgcn_readfirstlane((int)(v >> 32)) << 32) |
+                       (unsigned)__builtin_amdgcn_readfirstlane((int)v));
+  };
+
+  // ---- the plan cache (Q4Plan): lanes 0-15 load this workgroup's entry in slot 0, lanes
+  // 16-31 its entry in slot 1, lanes 32-47 the header -- in the memory round trip that
+  // also brings kv_lens and the block tables.
+  int pl = 0;
+  if (plan) pl = plan[lane < 32 ? q4_plan_entry(lane >> 4, bid) + (lane & 15) : (lane & 15)];
+  // Block tables of up to kTableCache entries are read into LDS together with
+  // kv_lens (one memory round trip for both), larger ones from global memory.
   int btv[kTableCache / 256];
   if (bt_lds) {
 #pragma unroll
     for (int k = 0; k < kTableCache / 256; ++k) {
       const int i = threadIdx.x + 256 * k;
-      btv[k] = i < nbt ? a.block_tables[i] : -1;
+      btv[k] = i < nbt ? block_tables[i] : -1;
     }
   }
-  seq_table(a, cum, kvl, qrw);
-  if (bt_lds) {
+  // per-sequence loads (sequences ch*t .. ch*t+ch-1 of thread t): kv_len, the mixed
+  // batch's query row, and the plan's copies of kv_lens
+  constexpr int kSeqPT = kMaxSeqs / 256;
+  const int ch = (S + 255) / 256;
+  const int sq0 = threadIdx.x * ch;
+  // (A load whose destination another path writes with a plain move makes the
+  // compiler wait for every load in flight there, so the optional query_start_loc is
+  // loaded into registers of its own and selected afterwards.)
+  int klr[kSeqPT], qlo[kSeqPT] = {}, qhi[kSeqPT] = {}, kc[2][kSeqPT] = {};
+  const bool mixed = a.qsl != nullptr;
 #pragma unroll
-    for (int k = 0; k < kTableCache / 256; ++k) sbt[threadIdx.x + 256 * k] = btv[k];
+  for (int i = 0; i < kSeqPT; ++i) {
+    const int si = sq0 + i;
+    if (i < ch && si < S) {
+      klr[i] = kv_lens[si];
+      if (mixed) {
+        qlo[i] = a.qsl[si];
+        qhi[i] = a.qsl[si + 1];
+      }
+      if (plan) {
+        kc[0][i] = plan[q4_plan_kvl(0) + si];
+        kc[1][i] = plan[q4_plan_kvl(1) + si];
+      }
+    }
+  }
+
+  // ---- header and entry: when a plan is committed for this shape, the first item's
+  // query and pages go out now, before the tables are scanned (checked below)
+  Q4Loads<GS, 1> bufA, bufB;
+  const Q4ScalePtrs<GS> sptr = q4_scale_ptrs<GS>(a, lane);
+  const int pgen = plan ? uru(__builtin_amdgcn_readlane(pl, 32)) : 0;
+  const int kind = GS | (HG << 8) | (__builtin_ctz(a.bs) << 16);
+  const int kv_cap = max_blocks * a.bs;
+  const bool hdr_ok = pgen > 0 && __builtin_amdgcn_readlane(pl, 33) == S && __builtin_amdgcn_readlane(pl, 34) == Hkv &&
+                      __builtin_amdgcn_readlane(pl, 36) == a.window &&
+                      __builtin_amdgcn_readlane(pl, 37) == a.first_slot && __builtin_amdgcn_readlane(pl, 38) == kind &&
+                      __builtin_amdgcn_readlane(pl, 39) == kv_cap;
+  const int pslot = pgen & 1;  // the committed slot
+  auto pe = [&](const int k) { return uru(__builtin_amdgcn_readlane(pl, 16 * pslot + k)); };
+  const int spec_s = pe(4), spec_kvh = pe(5), spec_tb = pe(6) + 64 * slice, spec_blk = pe(8 + slice);
+  // Only entries below the header's NWG belong to the committed plan (the others are
+  // left from older plans); the sequence and kv head are bounds-checked as well, so the
+  // loads stay inside q and the pools whatever the entry holds (pages: tile_of).
+  const bool spec = hdr_ok && bid < __builtin_amdgcn_readlane(pl, 35) && pe(0) < pe(1) &&
+                    (unsigned)spec_s < (unsigned)S && (unsigned)spec_kvh < (unsigned)Hkv && spec_tb >= 0;
+  if (spec) {
+    issue_q(spec_s, spec_kvh);  // a plan exists only for pure decode calls: row = sequence
+    size_t so;
+    const TileRsrc rs = tile_of(spec_blk, spec_kvh, spec_tb, so);
+    q4_issue_loads(bufA, rs, sptr, so, (spec_tb & 127) / 64, lane, a.bs);
+  }
+
+  // ---- block-wide exclusive prefix of the live item counts (cum[s]), clamped
+  // kv_lens (kvl[s], -1 for rows a mixed batch runs elsewhere), query rows (qrw[s]),
+  // and whether kv_lens differ from the committed plan's copy
+  int tsum = 0, mis = 0;
+#pragma unroll
+  for (int i = 0; i < kSeqPT; ++i) {
+    const int si = sq0 + i;
+    if (i < ch && si < S) {
+      const int kl = max(min(klr[i], kv_cap), 0);
+      const bool dec = !mixed || qhi[i] - qlo[i] == 1;  // in a mixed batch only single-token rows decode here
+      qrw[si] = mixed ? qlo[i] : si;
+      kvl[si] = dec ? kl : -1;
+      int n = 0;
+      if (dec && kl > 0) {
+        const int sk = a.window > 0 ? max(0, kl - a.window) : 0;
+        n = (kl - 1) / TW - sk / TW + 1;
+      }
+      cum[si] = n;  // temporarily the count
+      tsum += n;
+      mis |= plan && kc[pslot][i] != klr[i];
+    }
+  }
+  {
+    int x = tsum;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int y = __shfl_up(x, o, 64);
+      if (lane >= o) x += y;
+    }
+    int(&wsum)[8] = lds_at<int[8]>(oXb + 32);
+    if (lane == 63) wsum[wv] = x;
+    if (lane == 0) wsum[4 + wv] = __ballot(mis) != 0ull;
+    __syncthreads();
+    int base = 0;
+    for (int w = 0; w < wv; ++w) base += wsum[w];
+    mis = wsum[4] | wsum[5] | wsum[6] | wsum[7];
+    int run = base + x - tsum;
+#pragma unroll
+    for (int i = 0; i < kSeqPT; ++i) {
+      const int si = sq0 + i;
+      if (i < ch && si < S) {
+        const int n = cum[si];
+        cum[si] = run;
+        run += n;
+      }
+    }
+    if (threadIdx.x == 255) cum[S] = base + x;
+    if (bt_lds) {
+#pragma unroll
+      for (int k = 0; k < kTableCache / 256; ++k) sbt[threadIdx.x + 256 * k] = btv[k];
+    }
     __syncthreads();
   }
   if (wv >= 2) {  // decoded sequences without a live token produce zeros (the reference's l == 0 case);
                   // waves 2-3, while waves 0-1 find the workgroup's range (below)
     const int per_seq = a.Hq * D / 8;
-    for (int i = bid * 128 + threadIdx.x - 128; i < a.S * per_seq; i += nblocks * 128) {
+    for (int i = bid * 128 + threadIdx.x - 128; i < S * per_seq; i += nblocks * 128) {
       const int si = i / per_seq;
       if (kvl[si] >= 0 && cum[si + 1] == cum[si])
         reinterpret_cast<u32x4*>(a.out)[(size_t)qrw[si] * per_seq + i % per_seq] = u32x4{0u, 0u, 0u, 0u};
     }
   }
 
-  const int S = a.S, Hkv = a.Hkv;
-  // LDS table entries read at a wave-uniform index are moved to SGPRs (uru), so the
-  // per-item scheduling arithmetic stays scalar
-  auto uru = [](int v) { return __builtin_amdgcn_readfirstlane(v); };
   const long long I = (long long)Hkv * uru(cum[S]);
   const int NWG = (int)min((long long)nblocks, I);  // every range non-empty (before snapping, below)
   const int wg = bid;
   if (wg >= NWG) return;
-  // Ranges of equal item counts; when ranges are short (at most kSnapRange items
-  // on average) and so is every unit (at most kSnapItems items), the boundaries
-  // move to the next unit start instead, so no unit is shared between workgroups
-  // and no split-K partial, arrival or merge is left (batch 64, contexts 64..512:
-  // 17.3 -> 15.1 us).  A range may then be empty.
-  // ---- cost-balanced range [g0, g1) of this workgroup (see Q4Balance).  Wave 0 finds
-  // the start, wave 1 the end, each with the pieces of the unit the boundary cuts
-  // (if any); they meet in LDS.  One wave per boundary: the workgroup's waves share one
-  // scalar unit per compute unit, and eight waves each repeating the search cost ~5 us.
-  long long(&xb)[2] = lds_at<long long[2]>(oXb);
+  // The committed plan holds when its shape and its copy of kv_lens match this call's.
+  const bool pvalid = hdr_ok && __builtin_amdgcn_readlane(pl, 35) == NWG && uru(mis) == 0;
+  const bool pwrite = plan && !pvalid;  // otherwise this call commits its own plan (slot pgen + 1)
+  const int wslot = (pgen + 1) & 1;
+  long long g0, g1;
+  int pk_first, pk_last;  // pieces (wf | np << 16, both below kMaxWaves) of the units the range
+                          // shares: its first (begun before g0) and its last (going on past g1)
+  if (pvalid) {
+    g0 = pe(0);
+    g1 = pe(1);
+    pk_first = pe(2);
+    pk_last = pe(3);
+  } else {
+    long long(&xb)[2] = lds_at<long long[2]>(oXb);
   int(&xpk)[2] = lds_at<int[2]>(oXb + 16);
   if (wv < 2) {
     int ne_tot = 0;  // sequences with items
@@ -522,17 +725,10 @@ __device__ __forceinline__ void decode_q4_body(const DecodeArgs& a, const int bi
     }
   }
   __syncthreads();
-  // LDS reads are per lane to the compiler: the boundaries go back to scalar registers
-  auto uru64 = [](long long v) {
-    return (long long)(((unsigned long long)(unsigned)__builtin_amdgcn_readfirstlane((int)(v >> 32)) << 32) |
-                       (unsigned)__builtin_amdgcn_readfirstlane((int)v));
-  };
-  long long g0 = uru64(xb[0]);
-  long long g1 = uru64(xb[1]);
-  // pieces (wf | np << 16, both below kMaxWaves) of the units the range shares: its first
-  // (begun before g0) and its last (going on past g1)
-  int pk_first = uru(xpk[0]), pk_last = uru(xpk[1]);
-  if (g0 >= g1) return;
+    g0 = uru64(xb[0]);
+    g1 = uru64(xb[1]);
+    pk_first = uru(xpk[0]);
+    pk_last = uru(xpk[1]);
   int max_items = kSnapItems + 1;
   if (I <= (long long)kSnapRange * NWG) {  // longest unit, by every wave for itself (no barrier)
     max_items = 0;
@@ -556,9 +752,26 @@ __device__ __forceinline__ void decode_q4_body(const DecodeArgs& a, const int bi
     };
     g0 = uru64(wg == 0 ? 0 : unit_start(g0));
     g1 = uru64(wg + 1 == NWG ? I : unit_start(g1));
-    if (g0 >= g1) return;
   }
 
+  const int bs_log2 = __builtin_ctz(a.bs);
+
+  }
+  if (pwrite && wv == 0 && lane == 0) {  // this workgroup's range into the plan being written
+    int* e = plan + q4_plan_entry(wslot, wg);
+    e[0] = (int)g0;
+    e[1] = (int)g1;
+    e[2] = pk_first;
+    e[3] = pk_last;
+  }
+  if (pwrite && wg == 0) {  // kv_lens as this call saw them
+#pragma unroll
+    for (int i = 0; i < kSeqPT; ++i) {
+      const int si = sq0 + i;
+      if (i < ch && si < S) plan[q4_plan_kvl(wslot) + si] = klr[i];
+    }
+  }
+  if (g0 < g1) {
   const int bs_log2 = __builtin_ctz(a.bs);
 
   // ---- item g -> (sequence, kv_head, item j of the unit)
@@ -586,59 +799,13 @@ __device__ __forceinline__ void decode_q4_body(const DecodeArgs& a, const int bi
       const int jn = (int)(g - (long long)Hkv * cum[si]) % n;
       const int t = (lo_of(si) + jn) * TW + 64 * slice;
       if (t < kvl[si]) {
-        const size_t bi = (size_t)si * a.max_blocks + (t >> bs_log2);
-        b = bt_lds ? sbt[bi] : a.block_tables[bi];
+        const size_t bi = (size_t)si * max_blocks + (t >> bs_log2);
+        b = bt_lds ? sbt[bi] : block_tables[bi];
       }
     }
     return b;
   };
   int blkv = blk_chunk(g0);
-
-  // ---- query operand of a unit (this wave's head quad).  Lane L (head 4*quad + L%4,
-  // 16-lane group n = L/16) holds, in VGPR pair r, the operand of k-step 4r + n: K word
-  // m = 2r + n/2, dims 8m + (n even ? {0,4,1,5} : {2,6,3,7}), the last two / 16.
-  const int n16 = lane >> 4;
-  const int qhalf = n16 & 1;
-  uint32_t qraw[8][2];
-  auto issue_q = [&](int seq, int kh) {
-    const uint32_t* qp = reinterpret_cast<const uint32_t*>(
-        a.q + ((size_t)uru(qrw[seq]) * a.Hq + (size_t)kh * HG + (hl < HG ? hl : 0)) * D);
-#pragma unroll
-    for (int r = 0; r < 8; ++r) {
-      const int m = 2 * r + (n16 >> 1);
-      qraw[r][0] = qp[4 * m + qhalf];      // dims 8m + 2*qhalf + {0, 1}
-      qraw[r][1] = qp[4 * m + qhalf + 2];  // dims 8m + 2*qhalf + {4, 5}
-    }
-  };
-  h16x4 qB[1][8];
-  float qs[1][2];
-  auto build_q = [&]() {
-    const bool ok = hl < HG;
-    float gsum[2] = {0.f, 0.f};
-#pragma unroll
-    for (int r = 0; r < 8; ++r) {
-      const int m = 2 * r + (n16 >> 1);
-      const h16 d0 = __builtin_bit_cast(h16, (uint16_t)(qraw[r][0] & 0xFFFFu));
-      const h16 d1 = __builtin_bit_cast(h16, (uint16_t)(qraw[r][0] >> 16));
-      const h16 d4 = __builtin_bit_cast(h16, (uint16_t)(qraw[r][1] & 0xFFFFu));
-      const h16 d5 = __builtin_bit_cast(h16, (uint16_t)(qraw[r][1] >> 16));
-      // element order (nibble 0,4 | 1,5) of the word pair; with qhalf the dims are offset by 2
-      const h16x4 v = {d0, d4, (h16)((float)d1 * 0.0625f), (h16)((float)d5 * 0.0625f)};
-      qB[0][r] = ok ? v : h16x4{(h16)0.f, (h16)0.f, (h16)0.f, (h16)0.f};
-      const float sum = ok ? ((float)d0 + (float)d1) + ((float)d4 + (float)d5) : 0.f;
-      if (G == 1 || (8 * m) / GS == 0)
-        gsum[0] += sum;
-      else
-        gsum[1] += sum;
-    }
-#pragma unroll
-    for (int g = 0; g < 2; ++g) {
-      float x = gsum[g];
-      x += __shfl_xor(x, 16, 64);
-      x += __shfl_xor(x, 32, 64);
-      qs[0][g] = x * (1.0f / kTwo24);  // bias term in the 2^-24 units of the MFMA output
-    }
-  };
 
   int n_s = uru(cum[s + 1]) - uru(cum[s]);
   int kvh, j;
@@ -647,35 +814,31 @@ __device__ __forceinline__ void decode_q4_body(const DecodeArgs& a, const int bi
     kvh = r / n_s;
     j = r % n_s;
   }
-  issue_q(s, kvh);
   int kv_len = uru(kvl[s]);
   int start_k = a.window > 0 ? max(0, kv_len - a.window) : 0;
   int it_lo = start_k / TW;
   const float sc_l2 = a.scale_log2 * kTwo24;
-
-  // descriptors of this wave's slice at token t of page b (zero-size, reading nothing, when b is
-  // invalid), and the element offset of the page-head's scales (page 0 when b is invalid)
-  auto tile_of = [&](int b, int kh, int t, size_t& soff) {
-    const bool ok = (unsigned)b < (unsigned)a.nb;
-    const int off = t & (a.bs - 1) & ~127;  // page sizes are powers of two here
-    const size_t ph = (size_t)(ok ? b : 0) * a.Hkv + kh;
-    const int RW = a.bs * 4 / 32;
-    TileRsrc r;
-    r.k = uniform_rsrc(a.kc + (ph * a.bs + off) * 16, ok ? 128 * 16 * 4 : 0);
-    r.v = uniform_rsrc(a.vc + ph * D * RW + (off / 64) * D * 8, ok ? (D * RW - (off / 64) * D * 8) * 4 : 0);
-    soff = ph * G * a.bs + off;
-    return r;
-  };
-  const Q4ScalePtrs<GS> sptr = q4_scale_ptrs<GS>(a, lane);
   u32x2(&sst)[4][16 * 4 * G] = lds_at<u32x2[4][16 * 4 * G]>(oSst);  // per wave: scale staging [16 quads][4 * G segments]
 
-  // ---- first item's loads (its query is already in flight)
+  // ---- first item's query and pages: already in flight when the plan held and its
+  // pages are this call's (the block tables may have changed under the same kv_lens)
   int tb = (it_lo + j) * TW + 64 * slice;
   int blk = __builtin_amdgcn_readfirstlane(__builtin_amdgcn_readlane(blkv, 0));
-  Q4Loads<GS, 1> bufA, bufB;
-  size_t soff0;
-  const TileRsrc rs0 = tile_of(blk, kvh, tb, soff0);
-  q4_issue_loads(bufA, rs0, sptr, soff0, (tb & 127) / 64, lane, a.bs);
+  if (pwrite && lane == 0) {
+    int* e = plan + q4_plan_entry(wslot, wg);
+    if (wv == 0) {
+      e[4] = s;
+      e[5] = kvh;
+      e[6] = (it_lo + j) * TW;
+    }
+    if (wv % HQ == 0) e[8 + slice] = blk;
+  }
+  if (!(spec && pvalid && s == spec_s && kvh == spec_kvh && tb == spec_tb && blk == spec_blk)) {
+    issue_q(uru(qrw[s]), kvh);  // the query first: loads return in order
+    size_t soff0;
+    const TileRsrc rs0 = tile_of(blk, kvh, tb, soff0);
+    q4_issue_loads(bufA, rs0, sptr, soff0, (tb & 127) / 64, lane, a.bs);
+  }
   build_q();
 
   Q4State st[1];
@@ -738,7 +901,7 @@ __device__ __forceinline__ void decode_q4_body(const DecodeArgs& a, const int bi
     }
     // The next unit's query first: loads return in order, so building its
     // operand at this unit's end does not wait for the next item's pages.
-    if (has_next && unit_end) issue_q(s1, kvh1);
+    if (has_next && unit_end) issue_q(uru(qrw[s1]), kvh1);
     // Issued on every path (an empty descriptor returns zeros without touching
     // memory), so the wait before this item's compute leaves them in flight.
     size_t soff1;
@@ -928,11 +1091,35 @@ __device__ __forceinline__ void decode_q4_body(const DecodeArgs& a, const int bi
       }
     }
   }
+  }  // g0 < g1
+
+  // ---- a call that wrote a plan commits it: the workgroup counted last (every
+  // workgroup of the call has read the old header by then) publishes the header,
+  // which the next call on this workspace reads
+  if (pwrite && threadIdx.x == 0) {
+    const int old = __hip_atomic_fetch_add(plan + 15, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (old == NWG - 1) {
+      plan[1] = S;
+      plan[2] = Hkv;
+      plan[3] = NWG;
+      plan[4] = a.window;
+      plan[5] = a.first_slot;
+      plan[6] = kind;
+      plan[7] = kv_cap;
+      plan[0] = pgen + 1;
+      __hip_atomic_store(plan + 15, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
 }
 
+// The values the first loads need lead the argument list: the library is built with
+// kernel-argument preloading, so they arrive in SGPRs with the wave instead of
+// after a scalar load from the kernel-argument buffer.
 template <int GS, int HG>
-__global__ __launch_bounds__(256, 2) void decode_q4_d128(DecodeArgs a) {
-  decode_q4_body<GS, HG>(a, blockIdx.x, gridDim.x);
+__global__ __launch_bounds__(256, 2) void decode_q4_d128(int* plan, const int32_t* kv_lens,
+                                                         const int32_t* block_tables, int S, int max_blocks,
+                                                         DecodeArgs a) {
+  decode_q4_body<GS, HG>(a, blockIdx.x, gridDim.x, plan, kv_lens, block_tables, S, max_blocks);
 }
 
 }  // namespace emx

@@ -76,6 +76,8 @@ int decode_max_waves() { return std::max(decode_num_waves(), decode_q4_num_waves
 // Unit counters, then per-group counters indexed by partial slot (< kMaxWaves + kMaxUnits).
 // Then the prefill key-split counters.
 constexpr size_t kCounterInts = 2 * (size_t)emx::kMaxUnits + emx::kMaxWaves + emx::kPrefillCounters;
+// The 4-bit decode's plan cache follows the counters; the split-K partials follow it.
+constexpr size_t kPartialsInt = kCounterInts + emx::kPlanInts;
 constexpr size_t kPrefillCounterOff = 2 * (size_t)emx::kMaxUnits + emx::kMaxWaves;
 
 // Prefill tiles per kv head a call with num_tokens query rows can have: a
@@ -126,8 +128,10 @@ DecodeFn pick_decode_hg(int hg) {
 
 // 4-bit pages, group 64 / 128, GQA ratio 1, 2, 4 or 16: the 4x4x4 MFMA decode kernel.
 // GQA 8 with groups of 64 fills all 16 columns of the 16x16x32 kernel, which serves it.
+typedef void (*Q4Fn)(int*, const int32_t*, const int32_t*, int, int, emx::DecodeArgs);
+
 template <int GS>
-DecodeFn pick_decode_q4_hg(int hg) {
+Q4Fn pick_decode_q4_hg(int hg) {
   switch (hg) {
     case 1: return emx::decode_q4_d128<GS, 1>;
     case 2: return emx::decode_q4_d128<GS, 2>;
@@ -137,7 +141,7 @@ DecodeFn pick_decode_q4_hg(int hg) {
   return nullptr;
 }
 
-DecodeFn pick_decode_q4(int gs, int hg) {
+Q4Fn pick_decode_q4(int gs, int hg) {
   if (gs == 64) return pick_decode_q4_hg<64>(hg);
   if (gs == 128) return pick_decode_q4_hg<128>(hg);
   return nullptr;
@@ -854,7 +858,7 @@ size_t emx_paged_workspace_bytes(int num_seqs, int num_q_heads, int num_kv_heads
   const size_t slots = (size_t)decode_max_waves() + (size_t)num_seqs * num_kv_heads;
   if (decode_max_waves() > emx::kMaxWaves) return 0;
   // arrival counters at a fixed offset (so every call finds them zeroed), then the partials
-  return kCounterInts * sizeof(int) + slots * hg * (head_dim + 2) * sizeof(float);
+  return kPartialsInt * sizeof(int) + slots * hg * (head_dim + 2) * sizeof(float);
 }
 
 int emx_paged_attention_affine(const void* queries, int num_tokens, int num_q_heads, int head_dim,
@@ -939,11 +943,11 @@ int emx_paged_attention_affine(const void* queries, int num_tokens, int num_q_he
       }
     }
     // the 4-bit kernel addresses pages with shifts: power-of-two page sizes
-    DecodeFn fn = bits == 4 && (page_size & (page_size - 1)) == 0 ? pick_decode_q4(group_size, hg) : nullptr;
-    const bool q4 = fn != nullptr;
+    const Q4Fn q4fn = bits == 4 && (page_size & (page_size - 1)) == 0 ? pick_decode_q4(group_size, hg) : nullptr;
+    const bool q4 = q4fn != nullptr;
     const int nw = q4 ? decode_q4_num_waves() : decode_num_waves();
-    if (!fn) fn = bits == 4 ? pick_decode_gs<4>(group_size, hg) : pick_decode_gs<8>(group_size, hg);
-    if (!fn)
+    const DecodeFn fn = q4 ? nullptr : bits == 4 ? pick_decode_gs<4>(group_size, hg) : pick_decode_gs<8>(group_size, hg);
+    if (!q4 && !fn)
       return fail(EMX_ERR_UNSUPPORTED, "no decode kernel for bits=%d group_size=%d gqa=%d", bits, group_size, hg);
     emx::DecodeArgs a;
     a.q = reinterpret_cast<const emx::h16*>(queries);
@@ -960,7 +964,7 @@ int emx_paged_attention_affine(const void* queries, int num_tokens, int num_q_he
     const size_t slots = (size_t)decode_max_waves() + (size_t)num_seqs * num_kv_heads;
     a.ws_cnt = reinterpret_cast<int*>(workspace);
     a.ws_cnt_grp = a.ws_cnt + emx::kMaxUnits;
-    a.ws_o = reinterpret_cast<float*>(a.ws_cnt + kCounterInts);
+    a.ws_o = reinterpret_cast<float*>(a.ws_cnt + kPartialsInt);
     a.ws_ml = a.ws_o + slots * hg * head_dim;
     a.S = num_seqs;
     a.Hq = num_q_heads;
@@ -991,6 +995,13 @@ int emx_paged_attention_affine(const void* queries, int num_tokens, int num_q_he
     }
     // two workgroups per compute unit: the second of each starts later (4-bit kernel's range balance)
     a.first_slot = q4 ? nw / 8 : 0;
+    // pure decode on the 4-bit kernel: the plan cache in the workspace
+    a.plan = q4 && single_token_decode && nw / 4 <= emx::kPlanMaxWG ? a.ws_cnt + kCounterInts : nullptr;
+    if (q4) {
+      hipLaunchKernelGGL(q4fn, dim3((unsigned)(nw / 4)), dim3(256), 0, st, a.plan, a.kv_lens, a.block_tables, a.S,
+                         a.max_blocks, a);
+      return check_launch("decode_q4_d128");
+    }
     hipLaunchKernelGGL(fn, dim3((unsigned)(nw / 4)), dim3(256), 0, st, a);
     return check_launch("decode_affine_d128");
   }
@@ -1367,7 +1378,7 @@ int emx_paged_attention_fp8(const void* queries, int num_tokens, int num_q_heads
     const size_t slots = (size_t)decode_max_waves() + (size_t)num_seqs * num_kv_heads;
     a.ws_cnt = reinterpret_cast<int*>(workspace);
     a.ws_cnt_grp = a.ws_cnt + emx::kMaxUnits;
-    a.ws_o = reinterpret_cast<float*>(a.ws_cnt + kCounterInts);
+    a.ws_o = reinterpret_cast<float*>(a.ws_cnt + kPartialsInt);
     a.ws_ml = a.ws_o + slots * hg * head_dim;
     a.S = num_seqs;
     a.Hq = num_q_heads;

@@ -20,7 +20,7 @@ namespace emx {
 template <int GS, int HG>
 __global__ __launch_bounds__(256, 2) void unified_q4(PrefillArgs p, DecodeArgs d, int ndec) {
   if ((int)blockIdx.x < ndec)
-    decode_q4_body<GS, HG>(d, blockIdx.x, ndec);
+    decode_q4_body<GS, HG>(d, blockIdx.x, ndec, d.plan, d.kv_lens, d.block_tables, d.S, d.max_blocks);
   else
     prefill_body<4, GS, HG>(p, (int)blockIdx.x - ndec);
 }

@@ -278,7 +278,11 @@ int emx_rope_rows(void* x, int rows, int heads, int head_dim, const int32_t* pos
  * workspace must be zero-filled before its first use; every call leaves its
  * counter region zeroed again, so one workspace serves any sequence of calls
  * (of any shape) that are ordered on one stream.  Calls sharing a workspace
- * must not overlap.
+ * must not overlap.  The workspace also carries the 4-bit decode's plan cache:
+ * a pure decode call keeps its work split there, keyed by its shape and the
+ * contents of kv_lens, and the next call with the same kv_lens (the next
+ * layer of the same decode step) starts from it; a call with other kv_lens
+ * or another shape computes its own.  Results are the same either way.
  * No direct reference counterpart: replaces the tmp_out/exp_sums/max_logits
  * allocation of lib/python/easymlx/operations/kernels/page_attention.py:2205-2272.
  */
