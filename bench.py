@@ -46,6 +46,8 @@ def parse():
     p.add_argument("--no-aux", action="store_true", help="skip the c3 / c4 / quantize-on-write measurements")
     p.add_argument("--aux-only", choices=("c3", "c4", "write", "op", "fp8"),
                    help="run one auxiliary measurement alone and print its JSON (for profiler runs)")
+    p.add_argument("--layers", type=int, default=32,
+                   help="decode calls per model step: kv_lens change at every step's first call (Llama-3-8B: 32)")
     p.add_argument("--cpu-seqs", type=int, default=0, help="sequences in the CPU baseline sample (0 = auto)")
     p.add_argument("--copy-probe-mib", type=int, default=0,
                    help="after the timed region, run 5 plain device copies of this size (counter calibration)")
@@ -223,6 +225,28 @@ class Setup:
             torch.cuda.synchronize()
             assert torch.equal(out, eager), f"C-ABI call differs from paged_attention ({wl.name})"
 
+        # The same batch one step later in a model's decode: kv_lens of other contents (sequence 0
+        # one token shorter; its pages hold that token too).  Alternating the two every `layers`
+        # calls gives each model step's first layer a decode without a cached plan, as in serving.
+        lens_b = wl.kv_lens.copy()
+        if wl.single_token_decode and lens_b[0] > 1:
+            lens_b[0] -= 1
+        self.kv_lens_b = torch.from_numpy(lens_b).to(dev)
+        self.bytes_b = int(wl.kv_bytes() * (int(lens_b.sum()) / max(1, int(wl.kv_lens.sum()))))
+        ikl = 18  # position of kv_lens in the argument tuple
+        self.args_b = [a[:ikl] + (self.kv_lens_b.data_ptr(),) + a[ikl + 1:] for a in self.args]
+        out_b = torch.empty_like(out)
+        paged_attention(q, base.k_codes, base.v_codes, base.block_tables, self.kv_lens_b, qsl,
+                        k_scales=base.k_scales, k_biases=base.k_biases, v_scales=base.v_scales,
+                        v_biases=base.v_biases, bits=wl.bits, group_size=wl.group_size,
+                        single_token_decode=bool(wl.single_token_decode), out=out_b)
+        torch.cuda.synchronize()
+        eager_b = out_b.clone()
+        out.zero_()
+        self.call(0, alt=True)
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager_b), f"C-ABI call differs from paged_attention ({wl.name}, kv_lens b)"
+
         # the page-read probe over the same pools: exactly the slices this call reads, loads only
         self._probe = lib.emx_probe_page_read
         self.sink = torch.zeros(2048, dtype=torch.int32, device=dev)
@@ -237,10 +261,15 @@ class Setup:
         per_tok = 2 * wl.head_dim * wl.bits // 8 + 4 * (wl.head_dim // wl.group_size) * 2
         self.probe_bytes = int(((lens + 63) // 64).sum()) * 64 * wl.num_kv_heads * per_tok
 
-    def call(self, i):
-        rc = self._fn(*self.args[i % self.n_pools])
+    def call(self, i, alt=False):
+        rc = self._fn(*(self.args_b if alt else self.args)[i % self.n_pools])
         if rc:
             self._check(rc)
+
+    def step_call(self, i, layers):
+        """Call i of a run of model decode steps of `layers` layer calls each: kv_lens change at
+        every step's first layer (the two contents alternate), the other layers repeat them."""
+        self.call(i, alt=(i // layers) % 2 == 1)
 
     def set_probe_grid(self, words):
         self.probe_args = [a[:17] + (int(words),) + a[18:] for a in self.probe_args]
@@ -614,26 +643,34 @@ def main():
     wl = config("c2")
     bytes_per_step = wl.kv_bytes()
     st = Setup(wl, args.pool_gib, dev)
+    layers = max(1, args.layers)
+    step_call = lambda i: st.step_call(i, layers)  # noqa: E731
     for i in range(args.warmup):
-        st.call(i)
-    warm(st.call, 1.0)
+        step_call(i)
+    warm(step_call, 1.0)
 
-    # ---- timed region: exactly `steps` decode calls, bracketed by HIP events on the launch stream
+    # ---- timed region: exactly `steps` decode calls (layer calls of consecutive model steps: kv_lens
+    # change at every step's first layer), bracketed by HIP events on the launch stream
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     ev0.record()
     for i in range(args.steps):
-        st.call(i)
+        step_call(i)
     ev1.record()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
+    n_alt = sum(1 for i in range(args.steps) if (i // layers) % 2 == 1)
+    bytes_per_step = ((args.steps - n_alt) * wl.kv_bytes() + n_alt * st.bytes_b) / args.steps
     ms_per_step = elapsed / args.steps * 1e3
     call_us = ev0.elapsed_time(ev1) * 1e3 / args.steps  # device time per call, back to back
     achieved = bytes_per_step / (call_us * 1e-6) / 1e9
+    # the two kinds of call apart: kv_lens as the previous call's (cached plan) / new every call
+    us_cached = b2b_us(st.call, 200)
+    us_new = b2b_us(lambda i: st.call(i, alt=i % 2 == 1), 200)
 
     # ---- per-call times with events around each call (includes each launch's dispatch gap)
-    kt = event_us(st.call, min(args.steps, 200))
+    kt = event_us(step_call, min(args.steps, 200))
     k_avg_us = float(kt.mean())
 
     # ---- measured read-stream peak: the page-read probe over the same rotated pools (same page slices,
@@ -700,6 +737,11 @@ def main():
         "tokens_per_s_attention_32_layers": round(wl.num_seqs / (ms_per_step * 1e-3 * 32), 1),
         "us_per_layer_step": round(ms_per_step * 1e3, 3),
         "call_us_back_to_back": round(call_us, 3),
+        "plan_cache": {"layers_per_step": layers, "us_same_kv_lens": round(us_cached, 3),
+                       "us_new_kv_lens_every_call": round(us_new, 3),
+                       "what": "the decode keeps its work split in the workspace, keyed by kv_lens: a model "
+                               "step's first layer computes it, the other layers reuse it; the timed calls "
+                               "change kv_lens every `layers_per_step` calls"},
         "kernel_us": {"mean": round(k_avg_us, 3), "p10": round(float(np.percentile(kt, 10)), 3),
                       "p50": round(float(np.percentile(kt, 50)), 3), "p90": round(float(np.percentile(kt, 90)), 3)},
         "roofline": {

@@ -257,30 +257,34 @@ __device__ __forceinline__ void compute_iteration(IterLoads<BITS, GS, HG>& L, co
     }
   }
 
-  // ---- O += P V: B = p * v_scale as fp16 hi + lo (~22 bits; one fp16 rounding
-  // alone, 2^-12 relative, shows on outputs near zero where sum P' * code cancels
-  // against the bias term), bias term accumulated on the side
+  // ---- O += P V: B = P' = p * v_scale rounded once to fp16, bias term accumulated on
+  // the side in fp32.  The rounding error e of P' is folded into the bias term at the
+  // centre code 2^(BITS-1): sum P' * c = sum fp16(P') * c + sum e * C0 + sum e * (c - C0),
+  // so only e * (c - C0), |c - C0| <= 2^(BITS-1), is lost instead of e * c.  (One fp16
+  // P' alone put outputs near zero, where sum P' * c cancels against the bias term,
+  // up to 1.14x the tolerance on short-context batches; with the centre at most 0.45x,
+  // measured by a float64 model of this arithmetic on the same seeds; a second MFMA
+  // pass over the lo part of P' gave ~1e-4x at twice the matrix work.)
   const h16* svs = stage + (2 * G + gg) * NT + TPL * jj;
   const h16* svb = stage + (3 * G + gg) * NT + TPL * jj;
 #pragma unroll
   for (int w = 0; w < NWS; ++w) {
     const h16x8 vs8 = *reinterpret_cast<const h16x8*>(svs + 8 * w);
     const h16x8 vb8 = *reinterpret_cast<const h16x8*>(svb + 8 * w);
-    h16x8 pB, pL;
+    h16x8 pB;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int j = 8 * w + i;  // unpacked value element i is token i of the word
       const float p = sc[j >> 2][j & 3];
       const float x = col_ok ? p * (float)vs8[i] : 0.f;
       pB[i] = (h16)x;
-      pL[i] = (h16)(x - (float)pB[i]);
       pb = fmaf(p, (float)vb8[i], pb);
+      pb = fmaf(x - (float)pB[i], (float)(1 << (BITS - 1)), pb);
     }
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) {
       const h16x8 A = BITS == 4 ? unpack4(L.vw[dt][w]) : unpack8(L.vw[dt][0], L.vw[dt][1]);
       acc[dt] = mfma16x16x32(A, pB, acc[dt]);
-      acc[dt] = mfma16x16x32(A, pL, acc[dt]);
     }
   }
 }

@@ -18,7 +18,8 @@
 //            s = sum_g scale[t,g] * C_g + bias[t,g] * sum_{d in g} q_d
 //   softmax: online, base 2, fp32; the per-head max and sum run over the 16
 //          lanes of a head (DPP row rotations, then two cross-row shuffles).
-//   PV   : A = P' = p * v_scale[t, g] as fp16 hi + lo (two MFMAs), lane layout exactly as the QK
+//   PV   : A = P' = p * v_scale[t, g] in fp16 (its rounding error folded into the fp32 bias term at the
+//          centre code 8), lane layout exactly as the QK
 //          output; block tau of A is broadcast to all blocks (cbsz 4, abid
 //          tau), so no transpose is needed.  B = V codes, lane L holds dims L
 //          and 64 + L (one group half each).  Output: lane L holds dims L and
@@ -259,11 +260,14 @@ __device__ __forceinline__ void q4_compute(Q4Loads<GS, HQ>& L, const bool full, 
       st[hq].l += p[i];
     }
     // ---- O += P' V, P' = p * v_scale (elements 2, 3 of each quad / 16: their codes enter * 16)
-    // P' = p * v_scale as fp16 hi + lo (P' ~= hi + lo to ~22 bits): with a large
-    // v_bias the sum over P' * code cancels against sum p * v_bias, and one fp16
-    // rounding of P' alone (2^-12 relative) reached ~2e-3 absolute on outputs
-    // near zero (a 36-token context, scales of -1.4, biases of -9).
-    h16x4 pv[G], pvl[G];
+    // rounded once to fp16; its rounding error e is folded into the fp32 bias term at
+    // the centre code 8 (sum P' * c = sum fp16(P') * c + sum e * 8 + sum e * (c - 8)),
+    // so the loss is e * (c - 8), |c - 8| <= 8, instead of e * c.  One fp16 P' alone put
+    // outputs near zero (sum P' * code cancelling sum p * v_bias) up to 1.02x the
+    // tolerance on short-context batches; with the centre 0.44x (float64 model of this
+    // arithmetic on the same seeds); a second MFMA pass over the lo part of P' gave
+    // ~1e-4x at twice the PV matrix work.
+    h16x4 pv[G];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
 #pragma unroll
@@ -271,7 +275,7 @@ __device__ __forceinline__ void q4_compute(Q4Loads<GS, HQ>& L, const bool full, 
         st[hq].pb[g] = fmaf(p[i], half_of(L.s[3][g], i), st[hq].pb[g]);
         const float x = (i < 2 ? p[i] : p[i] * 0.0625f) * half_of(L.s[2][g], i);
         pv[g][i] = (h16)x;
-        pvl[g][i] = (h16)(x - (float)pv[g][i]);
+        st[hq].pb[g] = fmaf(x - (float)pv[g][i], i < 2 ? 8.f : 128.f, st[hq].pb[g]);
       }
     }
     static_for<8>([&](auto Wd) {
@@ -282,8 +286,6 @@ __device__ __forceinline__ void q4_compute(Q4Loads<GS, HQ>& L, const bool full, 
         const int g = (64 * c) / GS;
         st[hq].o[c] = mfma4<4, 2 * w, 0>(pv[g], nib_pairs(x), st[hq].o[c]);
         st[hq].o[c] = mfma4<4, 2 * w + 1, 0>(pv[g], nib_pairs(x >> 8), st[hq].o[c]);
-        st[hq].o[c] = mfma4<4, 2 * w, 0>(pvl[g], nib_pairs(x), st[hq].o[c]);
-        st[hq].o[c] = mfma4<4, 2 * w + 1, 0>(pvl[g], nib_pairs(x >> 8), st[hq].o[c]);
       }
     });
   }
