@@ -45,7 +45,8 @@ SIGNATURES: dict[str, tuple] = {
         _I, [_P, _P, _I, _P, _I, _P, _I, _I, _P, _P] + [_I] * 4 + [_P] * 5 + [_I, _I, _P, _P, _I, _P]),
     "emx_cache_slots": (_I, [_P, _P, _I, _I, _P, _I, _I, _I, _P, _P, _P, _P]),
     "emx_dense_cache_write": (_I, [_P, _P, _I, _P, _I, _I, _I, _I, _I, _P, _P, _P]),
-    "emx_copy_blocks": (_I, [_I, _P, _P, _I, _P, _I, _P]),
+    "emx_copy_blocks": (_I, [_I, _P, _P, _I, _P, _I, _P, _SZ, _P]),
+    "emx_copy_blocks_workspace_bytes": (_SZ, [_I, _P, _I]),
     "emx_gather_kv_affine": (_I, [_P] * 6 + [_I] * 6 + [_P, _I, _I, _P, _I, _I, _P, _P, _P]),
     "emx_affine_pages_from_logical": (_I, [_P] * 6 + [_I] * 6 + [_P] * 7),
     "emx_affine_logical_from_pages": (_I, [_P] * 6 + [_I] * 6 + [_P] * 7),

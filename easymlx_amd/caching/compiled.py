@@ -142,8 +142,11 @@ class CompiledPagedCacheProxy:
         if not (isinstance(c, (AffinePageCacheView, Fp8PageCacheView)) and isinstance(rope, RotaryEmbedding)
                 and rope.dims <= c.head_dim and queries.dtype == torch.float16 and c.block_tables.is_contiguous()):
             return None
-        if c.__dict__.get("_counter") is None and torch.cuda.is_current_stream_capturing():
-            raise RuntimeError("CompiledPagedCacheProxy: run one eager step before capture")
+        counter = self.__dict__.get("_counter")  # the proxy's own (its steps are ordered on the capturing stream)
+        if counter is None:
+            if torch.cuda.is_current_stream_capturing():
+                raise RuntimeError("CompiledPagedCacheProxy: run one eager step before capture")
+            counter = self._counter = torch.zeros(1, dtype=torch.int32, device=c.block_tables.device)
         q_in = queries.contiguous()
         q_out = torch.empty_like(q_in)
         bt = c.block_tables
@@ -155,7 +158,7 @@ class CompiledPagedCacheProxy:
             k, v = keys.contiguous(), values.contiguous()
             rc = lib.emx_fp8_cache_append_rope(
                 k.data_ptr(), v.data_ptr(), codes[k.dtype], slots_d.data_ptr(), int(k.shape[0]), bt.data_ptr(),
-                int(bt.shape[0]), int(bt.shape[1]), c.kv_lens.data_ptr(), c._append_counter().data_ptr(),
+                int(bt.shape[0]), int(bt.shape[1]), c.kv_lens.data_ptr(), counter.data_ptr(),
                 c.num_kv_heads, c.head_dim, c.block_size, c.num_blocks, c.key_cache.data_ptr(),
                 c.value_cache.data_ptr(), c.k_scales.data_ptr(), c.v_scales.data_ptr(),
                 rope.inv_freq(k.device).data_ptr(), rope.dims, int(rope.traditional), q_in.data_ptr(),
@@ -168,7 +171,7 @@ class CompiledPagedCacheProxy:
         v = values if values.dtype == torch.float16 and values.is_contiguous() else values.to(torch.float16).contiguous()
         rc = lib.emx_affine_cache_append_rope(
             k.data_ptr(), v.data_ptr(), slots_d.data_ptr(), int(k.shape[0]), bt.data_ptr(), int(bt.shape[0]),
-            int(bt.shape[1]), c.kv_lens.data_ptr(), c._append_counter().data_ptr(), c.num_kv_heads, c.head_dim,
+            int(bt.shape[1]), c.kv_lens.data_ptr(), counter.data_ptr(), c.num_kv_heads, c.head_dim,
             c.group_size, c.bits, c.block_size, c.num_blocks, c.key_cache.data_ptr(), c.k_scales.data_ptr(),
             c.k_biases.data_ptr(), c.value_cache.data_ptr(), c.v_scales.data_ptr(), c.v_biases.data_ptr(),
             rope.inv_freq(k.device).data_ptr(), rope.dims, int(rope.traditional), q_in.data_ptr(), q_out.data_ptr(),
@@ -221,11 +224,13 @@ class CompiledPagedCacheProxy:
                         positions.data_ptr(), inv.data_ptr(), rope.dims, int(rope.traditional), q_in.data_ptr(),
                         q_out.data_ptr(), int(q_out.shape[1]), stream))
                     return q_out
-                # no workspace: the library's own scratch (a decode step's append takes one launch anyway)
-                _native.check(lib.emx_fp8_cache_write_noalloc(
+                # the proxy's own workspace (the library's process-wide scratch would race with a
+                # write on another stream)
+                ws = self._fp8_workspace(lib, k.device)
+                _native.check(lib.emx_fp8_cache_write(
                     k.data_ptr(), v.data_ptr(), codes[k.dtype], mapping.data_ptr(), n, c.num_kv_heads, c.head_dim,
                     c.block_size, c.num_blocks, c.key_cache.data_ptr(), c.value_cache.data_ptr(),
-                    c.k_scales.data_ptr(), c.v_scales.data_ptr(), stream))
+                    c.k_scales.data_ptr(), c.v_scales.data_ptr(), ws.data_ptr(), ws.numel(), stream))
                 return queries
         elif rope is None:
             c._write(keys, values, mapping)

@@ -79,17 +79,11 @@ def _torch_float_dtype(dtype) -> torch.dtype:
 
 
 def block_mapping_on_device(block_mapping, device) -> torch.Tensor:
-    """``[num_pairs, 2]`` (src, dst) rows as an int32 device tensor; host data is checked not to chain copies
-    (a destination that is also a source would read a block the same call overwrites)."""
-    on_device = isinstance(block_mapping, torch.Tensor) and block_mapping.is_cuda
+    """``[num_pairs, 2]`` (src, dst) rows as an int32 device tensor (the reference's shape check,
+    ``cache.py:953-954``)."""
     m = block_mapping if isinstance(block_mapping, torch.Tensor) else torch.as_tensor(block_mapping)
     if m.ndim != 2 or m.shape[1] != 2:
         raise ValueError("block_mapping must be rank-2 with shape [num_pairs, 2]")
-    if not on_device and m.shape[0]:
-        pairs = [(int(a), int(b)) for a, b in m.tolist() if int(a) != int(b)]
-        srcs = {a for a, _ in pairs}
-        if any(b in srcs for _, b in pairs):
-            raise ValueError("block_mapping chains copies: a destination block is also a source")
     return m.to(device=device, dtype=torch.int32).contiguous()
 
 
@@ -374,11 +368,13 @@ class PageCacheView:
             t = cache[slot_ids] = torch.tensor(slot_ids, dtype=torch.int32, device=self.block_tables.device)
         return t
 
-    def _append_counter(self) -> torch.Tensor:
-        """One device int the decode append counts its workgroups on (zero between calls)."""
-        c = self.__dict__.get("_counter")
+    def _append_counter(self, stream: int) -> torch.Tensor:
+        """The device int the decode append counts its workgroups on (zero between calls), one per stream:
+        appends ordered on one stream share it, appends issued on another stream never do."""
+        counters = self.__dict__.setdefault("_counters", {})
+        c = counters.get(stream)
         if c is None:
-            c = self._counter = torch.zeros(1, dtype=torch.int32, device=self.block_tables.device)
+            c = counters[stream] = torch.zeros(1, dtype=torch.int32, device=self.block_tables.device)
         return c
 
     def _concatenate_rope_fused(self, queries, keys, values, cache_metadata, rope, slot_ids, query_lens, write,
@@ -399,8 +395,9 @@ class PageCacheView:
             q_in = queries.contiguous()
             q_out = torch.empty_like(q_in)
             slots = self._slot_ids_device(slot_ids)
-            rc = append(keys, values, slots, rope.inv_freq(q_in.device), rope, _stream_ptr(q_in.device), q_in, q_out,
-                        self._append_counter())
+            stream = _stream_ptr(q_in.device)
+            rc = append(keys, values, slots, rope.inv_freq(q_in.device), rope, stream, q_in, q_out,
+                        self._append_counter(stream))
             if rc == _native.EMX_OK:
                 return q_out, self.key_cache, self.value_cache, self._resolved(cache_metadata, slots, single,
                                                                                slot_ids)
@@ -451,7 +448,7 @@ class PageCacheView:
         """Every array of the cache indexed by block first (codes, then scales / biases where present)."""
         return [self.key_cache, self.value_cache]
 
-    def _page_call(self, fn, ids: torch.Tensor, count: int) -> None:
+    def _page_call(self, fn, ids: torch.Tensor, count: int, staging: bool = False) -> None:
         import ctypes
 
         arrays = self.page_arrays()
@@ -460,7 +457,12 @@ class PageCacheView:
                 raise RuntimeError("page arrays must be contiguous device tensors with num_blocks rows")
         ptrs = (ctypes.c_void_p * len(arrays))(*[t.data_ptr() for t in arrays])
         sizes = (ctypes.c_int64 * len(arrays))(*[t[0].numel() * t.element_size() for t in arrays])
-        _native.check(fn(len(arrays), ptrs, sizes, self.num_blocks, ids.data_ptr(), count,
+        extra = ()
+        if staging:  # copy_blocks: the pairs' source blocks are staged before any destination is written
+            nbytes = int(_native.load().emx_copy_blocks_workspace_bytes(len(arrays), sizes, count))
+            ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=arrays[0].device)
+            extra = (ws.data_ptr(), ws.numel())
+        _native.check(fn(len(arrays), ptrs, sizes, self.num_blocks, ids.data_ptr(), count, *extra,
                          _stream_ptr(arrays[0].device)))
 
     def zero_pages(self, page_ids) -> None:
@@ -474,11 +476,12 @@ class PageCacheView:
     def copy_blocks(self, block_mapping) -> None:
         """Copy-on-write block copies (``cache.py:944-972``): rows ``(src, dst)`` of ``[num_pairs, 2]``.
 
-        Host mappings are checked not to chain (a destination that is also a
-        source); a device tensor is used as given."""
+        Every destination receives its source block as it was before the call
+        (the reference's kernel reads its inputs), so swapped and chained pairs
+        are well defined; of several pairs with one destination the last counts."""
         m = block_mapping_on_device(block_mapping, self.key_cache.device)
         if m.shape[0]:
-            self._page_call(_native.load().emx_copy_blocks, m, int(m.shape[0]))
+            self._page_call(_native.load().emx_copy_blocks, m, int(m.shape[0]), staging=True)
 
     def gather_kv_cache(self, block_table, cu_seq_lens, *, out_dtype: torch.dtype | None = None):
         """Dense ``(k, v)`` ``[total_tokens, Hkv, D]`` of a ragged batch from the pages (``cache.py:974-1027``).

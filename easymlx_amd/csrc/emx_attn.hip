@@ -23,14 +23,17 @@
 #include "probe.hpp"
 #include "pages.hpp"
 
-constexpr int kNoallocScratchFloats = 2 * emx::kFp8Parts;  // 2 KiB
+constexpr int kNoallocScratchFloats = 2 * emx::kFp8Parts;  // 2 KiB per stream slot
+constexpr int kNoallocSlots = 8;                            // streams with a slot of their own
 
 // Scratch of emx_fp8_cache_write_noalloc: the two-launch FP8 write's
 // per-workgroup maxima (written by fp8_amax before fp8_write reads them, so it
-// needs no clearing).  Each GPU holds its own copy until the process ends.  In
-// host code `scratch` is only a symbol: kernels get the device address that
+// needs no clearing), one 2 KiB slot per stream that calls it (up to
+// kNoallocSlots streams per GPU), so calls on different streams never share
+// one.  Each GPU holds its own copy until the process ends.  In host code
+// `scratch` is only a symbol: kernels get the device address that
 // hipGetSymbolAddress returns for the current device (noalloc_scratch()).
-static __device__ __align__(256) float scratch[kNoallocScratchFloats];
+static __device__ __align__(256) float scratch[kNoallocSlots][kNoallocScratchFloats];
 
 
 namespace {
@@ -288,11 +291,16 @@ int launch_generic(const emx::GenericArgs& ga, const KV& kv, hipStream_t st) {
 constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
 void* g_scratch_ptr[kMaxDevices] = {};
+void* g_scratch_stream[kMaxDevices][kNoallocSlots] = {};  // the stream holding each slot
+int g_scratch_used[kMaxDevices] = {};
 
-// Device address of `scratch` on the current device, looked up once per device
-// (with that device current).  Null, with the last error set, on failure.
-void* noalloc_scratch() {
+// Device address of the scratch slot of `stream` on the current device: the
+// symbol's address is looked up once per device (with that device current), a
+// slot is given to each new stream, up to kNoallocSlots per device.  Null, with
+// the last error set, on failure (*rc: the status to return).
+void* noalloc_scratch(void* stream, int* rc) {
   int dev = 0;
+  *rc = EMX_ERR_HIP;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
     fail(EMX_ERR_HIP, "emx_fp8_cache_write_noalloc: no current device (or device id >= %d)", kMaxDevices);
     return nullptr;
@@ -307,7 +315,23 @@ void* noalloc_scratch() {
     }
     g_scratch_ptr[dev] = p;
   }
-  return g_scratch_ptr[dev];
+  int slot = -1;
+  for (int i = 0; i < g_scratch_used[dev]; ++i)
+    if (g_scratch_stream[dev][i] == stream) slot = i;
+  if (slot < 0) {
+    if (g_scratch_used[dev] == kNoallocSlots) {
+      *rc = EMX_ERR_UNSUPPORTED;
+      fail(EMX_ERR_UNSUPPORTED,
+           "emx_fp8_cache_write_noalloc: more than %d streams on this device (each holds a scratch slot); "
+           "use emx_fp8_cache_write with a workspace",
+           kNoallocSlots);
+      return nullptr;
+    }
+    slot = g_scratch_used[dev]++;
+    g_scratch_stream[dev][slot] = stream;
+  }
+  *rc = EMX_OK;
+  return static_cast<char*>(g_scratch_ptr[dev]) + (size_t)slot * sizeof(float) * kNoallocScratchFloats;
 }
 
 template <typename KV>
@@ -593,16 +617,41 @@ static int page_arrays(int num_arrays, void* const* arrays, const int64_t* block
   return EMX_OK;
 }
 
+size_t emx_copy_blocks_workspace_bytes(int num_arrays, const int64_t* block_bytes, int num_pairs) {
+  if (num_arrays <= 0 || num_arrays > emx::kMaxPageArrays || !block_bytes || num_pairs <= 0) return 0;
+  size_t total = 0;
+  for (int k = 0; k < num_arrays; ++k) {
+    if (block_bytes[k] <= 0) return 0;
+    total += (((size_t)block_bytes[k] * (size_t)num_pairs) + 255) & ~(size_t)255;
+  }
+  return total;
+}
+
 int emx_copy_blocks(int num_arrays, void* const* arrays, const int64_t* block_bytes, int num_blocks,
-                    const int32_t* block_mapping, int num_pairs, void* stream) {
+                    const int32_t* block_mapping, int num_pairs, void* workspace, size_t workspace_bytes,
+                    void* stream) {
   if (num_pairs < 0) return fail(EMX_ERR_INVALID, "num_pairs must be >= 0");
   emx::PageArrays pa{};
   if (int rc = page_arrays(num_arrays, arrays, block_bytes, num_blocks, pa)) return rc;
   if (num_pairs == 0) return EMX_OK;
   if (!block_mapping) return fail(EMX_ERR_INVALID, "null block_mapping");
-  hipLaunchKernelGGL(emx::copy_blocks, dim3((unsigned)num_pairs, (unsigned)num_arrays), dim3(256), 0,
-                     reinterpret_cast<hipStream_t>(stream), pa, block_mapping);
-  return check_launch("copy_blocks");
+  const size_t need = emx_copy_blocks_workspace_bytes(num_arrays, block_bytes, num_pairs);
+  if (!workspace || workspace_bytes < need || (reinterpret_cast<uintptr_t>(workspace) & 15))
+    return fail(EMX_ERR_INVALID, "copy_blocks staging workspace: need %zu bytes (16-byte aligned), got %zu", need,
+                workspace_bytes);
+  pa.stage = static_cast<char*>(workspace);
+  size_t off = 0;
+  for (int k = 0; k < num_arrays; ++k) {
+    pa.stage_off[k] = (long long)off;
+    off += (((size_t)block_bytes[k] * (size_t)num_pairs) + 255) & ~(size_t)255;
+  }
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(emx::copy_blocks_gather, dim3((unsigned)num_pairs, (unsigned)num_arrays), dim3(256), 0, st, pa,
+                     block_mapping);
+  if (int rc = check_launch("copy_blocks_gather")) return rc;
+  hipLaunchKernelGGL(emx::copy_blocks_scatter, dim3((unsigned)num_pairs, (unsigned)num_arrays), dim3(256), 0, st, pa,
+                     block_mapping, num_pairs);
+  return check_launch("copy_blocks_scatter");
 }
 
 int emx_zero_blocks(int num_arrays, void* const* arrays, const int64_t* block_bytes, int num_blocks,
@@ -1200,8 +1249,9 @@ int emx_fp8_cache_write_noalloc(const void* keys, const void* values, int dtype,
                 "scratch holds the FP8 write's per-workgroup maxima");
   // the scratch is a fixed 2 KiB whatever the call's size; the size limit is the
   // FP8 write's own (fewer than 2^33 values per tensor, checked by fp8_write_impl)
-  void* ws = num_tokens > 0 ? noalloc_scratch() : nullptr;
-  if (num_tokens > 0 && ws == nullptr) return EMX_ERR_HIP;
+  int rc = EMX_OK;
+  void* ws = num_tokens > 0 ? noalloc_scratch(stream, &rc) : nullptr;
+  if (num_tokens > 0 && ws == nullptr) return rc;
   return fp8_write_impl(keys, values, dtype, slot_mapping, num_tokens, num_kv_heads, head_dim, page_size, num_blocks,
                         key_cache, value_cache, k_scales, v_scales, ws, sizeof(float) * kNoallocScratchFloats,
                         emx::RopeArgs{nullptr, nullptr, 0, 0}, nullptr, nullptr, 0, stream);

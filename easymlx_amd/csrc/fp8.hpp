@@ -123,12 +123,14 @@ __device__ __forceinline__ void k_turn(const Fp8WriteArgs& a, const uint32_t e, 
 template <typename T>
 __device__ __forceinline__ void k_word(const Fp8WriteArgs& a, const T* k, const uint32_t e, float (&x)[4],
                                        const float2* tab = nullptr) {
-  const uint32_t pe = k_partner(a, e);
-  float p[4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    x[j] = to_f32(k[4 * (size_t)e + j]);
-    p[j] = to_f32(k[4 * (size_t)pe + j]);
+  for (int j = 0; j < 4; ++j) x[j] = to_f32(k[4 * (size_t)e + j]);
+  if (a.rope.inv_freq == nullptr) return;  // unturned keys
+  const uint32_t pe = k_partner(a, e);
+  float p[4] = {x[0], x[1], x[2], x[3]};
+  if (pe != e) {  // the partner word is loaded only where the rotation pairs two words
+#pragma unroll
+    for (int j = 0; j < 4; ++j) p[j] = to_f32(k[4 * (size_t)pe + j]);
   }
   k_turn<T>(a, e, x, p, tab);
 }
@@ -261,12 +263,18 @@ __global__ __launch_bounds__(SELF ? 1024 : 256) void fp8_write(Fp8WriteArgs a, i
         const int sl = e < n4 ? a.slot[e / row4] : -1;
         live[u] = sl >= 0 && sl / a.bs < a.nb;  // as the write loop: a page outside the pool is skipped
         ee[u] = e < n4 ? e : e0;
-        const uint32_t pe = k_partner(a, ee[u]);
+        const uint32_t pe = k_partner(a, ee[u]);  // ee[u] itself without a pairing rotation
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           x[u][j] = to_f32(k[4 * (size_t)ee[u] + j]);
-          p[u][j] = to_f32(k[4 * (size_t)pe + j]);
           y[u][j] = to_f32(v[4 * (size_t)ee[u] + j]);
+        }
+        if (pe != ee[u]) {  // the partner word only where the rotation pairs two words
+#pragma unroll
+          for (int j = 0; j < 4; ++j) p[u][j] = to_f32(k[4 * (size_t)pe + j]);
+        } else {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) p[u][j] = x[u][j];
         }
       }
 #pragma unroll

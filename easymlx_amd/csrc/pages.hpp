@@ -4,12 +4,16 @@
 // copy_blocks follows PageCacheView.copy_blocks
 // (lib/python/easymlx/caching/paged/cache.py:944-972; Metal kernel :95-136):
 // for each pair (src, dst) of block_mapping [num_pairs, 2], block dst of every
-// array becomes a copy of block src.  zero_blocks follows the runner's
-// _zero_pages (lib/python/easymlx/inference/esurge/runners/model_runner.py:
-// 1058-1094) and PageCacheView.reset (cache.py:874-906, pages addressed by id):
-// the listed blocks of every array become zero.  Block ids outside
-// [0, num_blocks) are skipped.  One workgroup per (pair or page, array);
-// 16-byte words when a block's bytes allow it, else 4-byte words.
+// array becomes a copy of block src as it was before the call (the reference
+// kernel reads its input arrays and writes separate outputs), so swapped and
+// chained pairs are well defined; of several pairs with one destination the
+// last one counts.  Two launches through a staging buffer: every pair's source
+// blocks are gathered, then scattered to the destinations.  zero_blocks
+// follows the runner's _zero_pages (lib/python/easymlx/inference/esurge/
+// runners/model_runner.py:1058-1094) and PageCacheView.reset (cache.py:874-906,
+// pages addressed by id): the listed blocks of every array become zero.  Block
+// ids outside [0, num_blocks) are skipped.  One workgroup per (pair or page,
+// array); 16-byte words when a block's bytes allow it, else 4-byte words.
 #pragma once
 
 #include "common.hpp"
@@ -21,6 +25,8 @@ constexpr int kMaxPageArrays = 8;
 struct PageArrays {
   void* base[kMaxPageArrays];
   long long block_bytes[kMaxPageArrays];  // bytes of one block of the array (a multiple of 4)
+  long long stage_off[kMaxPageArrays];    // copy_blocks: byte offset of the array's staged blocks
+  char* stage;                            // copy_blocks: staging buffer (16-byte aligned)
   int n;
   int nb;
 };
@@ -40,18 +46,40 @@ __device__ __forceinline__ void zero_words(char* dst, long long bytes) {
   for (long long i = threadIdx.x; i < n; i += blockDim.x) d[i] = W{};
 }
 
-// grid (num_pairs, n arrays)
-__global__ __launch_bounds__(256) void copy_blocks(PageArrays a, const int32_t* mapping) {
+template <typename W>
+__device__ __forceinline__ void copy_block(const char* s, char* d, const long long bb, const bool w16) {
+  if (w16)
+    copy_words<u32x4>(s, d, bb);
+  else
+    copy_words<uint32_t>(s, d, bb);
+}
+
+// grid (num_pairs, n arrays): staged block p of array k <- block src of pair p
+__global__ __launch_bounds__(256) void copy_blocks_gather(PageArrays a, const int32_t* mapping) {
   const int p = blockIdx.x, k = blockIdx.y;
   const int src = mapping[2 * p], dst = mapping[2 * p + 1];
   if (src < 0 || src >= a.nb || dst < 0 || dst >= a.nb || src == dst) return;
   const long long bb = a.block_bytes[k];
-  const char* s = static_cast<const char*>(a.base[k]) + (long long)src * bb;
-  char* d = static_cast<char*>(a.base[k]) + (long long)dst * bb;
-  if (bb % 16 == 0 && (reinterpret_cast<uintptr_t>(a.base[k]) & 15) == 0)
-    copy_words<u32x4>(s, d, bb);
-  else
-    copy_words<uint32_t>(s, d, bb);
+  const bool w16 = bb % 16 == 0 && (reinterpret_cast<uintptr_t>(a.base[k]) & 15) == 0;
+  copy_block<int>(static_cast<const char*>(a.base[k]) + (long long)src * bb, a.stage + a.stage_off[k] + p * bb, bb,
+                  w16);
+}
+
+// grid (num_pairs, n arrays): block dst of pair p <- staged block p, unless a later
+// pair has the same destination
+__global__ __launch_bounds__(256) void copy_blocks_scatter(PageArrays a, const int32_t* mapping, const int num_pairs) {
+  const int p = blockIdx.x, k = blockIdx.y;
+  const int src = mapping[2 * p], dst = mapping[2 * p + 1];
+  if (src < 0 || src >= a.nb || dst < 0 || dst >= a.nb || src == dst) return;
+  int later = 0;
+  for (int q = p + 1 + (int)threadIdx.x; q < num_pairs; q += blockDim.x) {
+    const int s2 = mapping[2 * q], d2 = mapping[2 * q + 1];
+    later |= d2 == dst && s2 >= 0 && s2 < a.nb && s2 != d2;
+  }
+  if (__syncthreads_or(later)) return;
+  const long long bb = a.block_bytes[k];
+  const bool w16 = bb % 16 == 0 && (reinterpret_cast<uintptr_t>(a.base[k]) & 15) == 0;
+  copy_block<int>(a.stage + a.stage_off[k] + p * bb, static_cast<char*>(a.base[k]) + (long long)dst * bb, bb, w16);
 }
 
 // grid (num_pages, n arrays)

@@ -100,7 +100,11 @@ int emx_affine_cache_write_rope(const void* keys, const void* values, const int3
  * at that position and quantized into the pages, queries_in rotated into
  * queries, and kv_lens[s] advances by one.  `counter` is one int of device
  * memory, zero before the first call; every call leaves it zero (calls that
- * share it must not overlap).  head_dim and group_size multiples of 16,
+ * share it must not overlap: give each stream its own, as the Python views do;
+ * a counter left nonzero, e.g. by a launch that never ran to its end, makes the
+ * later calls advance kv_lens at the wrong workgroup, so a caller that aborts a
+ * launch zeroes it again).  A cache must not be appended to from two streams at
+ * once (the pages and kv_lens would race).  head_dim and group_size multiples of 16,
  * group_size <= 64; otherwise EMX_ERR_UNSUPPORTED (use the two calls).
  * Replaces the decode branch of PageCacheView.concatenate_to_cache
  *   lib/python/easymlx/caching/paged/cache.py:1126-1190 (RoPE :1161-1166)
@@ -168,14 +172,27 @@ int emx_dense_cache_write(const void* keys, const void* values, int dtype, const
  * num_blocks blocks of block_bytes[k] bytes each (a positive multiple of 4;
  * host arrays of num_arrays <= 8 entries, e.g. codes, scales and biases of K
  * and V).  For each row (src, dst) of block_mapping int32 [num_pairs, 2] on the
- * device, block dst of every array becomes a copy of block src; ids outside
- * [0, num_blocks) are skipped.  No destination may also be a source of another
- * pair in the same call (copy-on-write mappings never chain).
+ * device, block dst of every array becomes a copy of block src as it was
+ * before the call, as the reference kernel reads its inputs and writes
+ * separate outputs: swapped and chained pairs are well defined; of several
+ * pairs with one destination the last counts.  Ids outside [0, num_blocks) are
+ * skipped.  workspace: device staging of at least
+ * emx_copy_blocks_workspace_bytes(...) bytes, 16-byte aligned (no zero-fill
+ * needed); two launches (gather the sources, scatter to the destinations).
  * Replaces PageCacheView.copy_blocks / PageCache.copy_blocks
  *   lib/python/easymlx/caching/paged/cache.py:944-972, 1438-1445 (Metal kernel :95-136).
  */
 int emx_copy_blocks(int num_arrays, void* const* arrays, const int64_t* block_bytes, int num_blocks,
-                    const int32_t* block_mapping, int num_pairs, void* stream);
+                    const int32_t* block_mapping, int num_pairs, void* workspace, size_t workspace_bytes,
+                    void* stream);
+
+/*
+ * Staging bytes emx_copy_blocks needs for num_pairs pairs over these arrays
+ * (0 for an invalid description or no pairs).
+ * No direct reference counterpart: the reference's kernel allocates whole
+ * output arrays (cache.py:95-136).
+ */
+size_t emx_copy_blocks_workspace_bytes(int num_arrays, const int64_t* block_bytes, int num_pairs);
 
 /*
  * Zero the blocks page_ids int32 [num_pages] (device) of every array of a cache
@@ -361,11 +378,13 @@ int emx_fp8_cache_write(const void* keys, const void* values, int dtype, const i
 
 /*
  * emx_fp8_cache_write that allocates nothing and takes no workspace: the
- * two-launch path keeps its per-workgroup maxima in a fixed 2 KiB device array
- * of the library (one per GPU, held until the process ends).  Same arguments,
- * results and limits as emx_fp8_cache_write otherwise; calls no hipMalloc,
- * hipFree or allocating library routine.  Calls that overlap in time on one GPU
- * share that array and race: order them on one stream.
+ * two-launch path keeps its per-workgroup maxima in a fixed device array of the
+ * library, 8 slots of 2 KiB per GPU (held until the process ends), one slot per
+ * stream that calls it: calls on one stream are ordered, calls on different
+ * streams use different slots.  A ninth stream on one GPU is refused
+ * (EMX_ERR_UNSUPPORTED).  Same arguments, results and limits as
+ * emx_fp8_cache_write otherwise; calls no hipMalloc, hipFree or allocating
+ * library routine.
  * No counterpart in the reference.  For callers that cannot allocate device
  * memory or hold a workspace: code under HIP graph capture, tight serving
  * loops, harnesses that forbid allocation.

@@ -113,15 +113,17 @@ def test_append_rejects_unsupported_geometry(cuda):
     assert rc == _native.EMX_ERR_UNSUPPORTED
 
 
-@pytest.mark.parametrize("bs,trad", [(128, False), (16, True)])
-def test_fp8_append_matches_the_two_launch_write(cuda, bs, trad):
+@pytest.mark.parametrize("bs,trad,S,hkv", [(128, False, 12, 4), (16, True, 12, 4), (128, False, 80, 1),
+                                            (16, True, 80, 1)])
+def test_fp8_append_matches_the_two_launch_write(cuda, bs, trad, S, hkv):
     """``emx_fp8_cache_append_rope`` against ``emx_cache_slots`` + ``emx_fp8_cache_write_rope``: codes, page
-    scales, kv_lens and the turned queries bit for bit."""
-    print(f"[fp8 append bs={bs} traditional={trad}]", flush=True)
+    scales, kv_lens and the turned queries bit for bit.  80 one-head tokens: more (token, pair) angles than
+    the one-launch write's LDS table holds (each value turned with its own sincosf)."""
+    print(f"[fp8 append bs={bs} traditional={trad} S={S} hkv={hkv}]", flush=True)
     from easymlx_amd import Fp8PageCacheView
 
-    rng = np.random.default_rng(500 + bs)
-    S, hkv, hq, d, mb = 12, 4, 16, 128, 5
+    rng = np.random.default_rng(500 + bs + S)
+    hq, d, mb = 16, 128, 5
     nb = S * mb + 3
     tables = rng.permutation(nb)[:S * mb].astype(np.int32).reshape(S, mb)
     lens = rng.integers(0, mb * bs, S).astype(np.int32)

@@ -78,6 +78,31 @@ def test_copy_blocks_and_zero_pages_match_oracle(cuda, kind):
         np.testing.assert_array_equal(t.cpu().numpy(), a)
 
 
+@pytest.mark.parametrize("kind", ["dense", "fp8", "affine4"])
+def test_copy_blocks_swaps_and_chains(cuda, kind):
+    """Swapped, chained and repeated destinations: every destination gets its source as it was before the call
+    (cache.py:95-136 reads its inputs); of two pairs with one destination the later counts."""
+    print(f"[copy swaps / chains {kind}]", flush=True)
+    rng = np.random.default_rng(40 + len(kind))
+    view = _filled(kind, cuda, rng)
+    arrays = [t.cpu().numpy() for t in view.page_arrays()]
+    for mapping in ([[0, 1], [1, 0]],                      # swap
+                    [[2, 3], [3, 4], [4, 5], [5, 2]],      # a 4-cycle
+                    [[6, 7], [7, 8], [8, 9]],              # a chain
+                    [[10, 11], [12, 11], [11, 13], [1, 99], [-1, 3]]):  # repeated destination, skipped ids
+        view.copy_blocks(mapping)
+        ocw.copy_blocks(arrays, mapping)
+        torch.cuda.synchronize()
+        for t, a in zip(view.page_arrays(), arrays):
+            np.testing.assert_array_equal(t.cpu().numpy(), a, err_msg=str(mapping))
+        dm = torch.tensor(mapping[::-1], dtype=torch.int32, device=cuda)  # and as a device tensor
+        view.copy_blocks(dm)
+        ocw.copy_blocks(arrays, mapping[::-1])
+        torch.cuda.synchronize()
+        for t, a in zip(view.page_arrays(), arrays):
+            np.testing.assert_array_equal(t.cpu().numpy(), a, err_msg=f"device {mapping[::-1]}")
+
+
 @pytest.mark.parametrize("kind", ["dense", "affine4"])
 def test_reset_and_clear(cuda, kind):
     print(f"[reset / clear {kind}]", flush=True)

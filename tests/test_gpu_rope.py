@@ -139,15 +139,18 @@ def test_concatenate_fused_vs_callable(cuda):
         assert views[0].kv_lens.cpu().tolist() == views[1].kv_lens.cpu().tolist()
 
 
-@pytest.mark.parametrize("traditional,T", [(False, 200), (True, 200), (False, 24)])
-def test_fp8_fused_write_equals_rotate_then_write(cuda, traditional, T):
+@pytest.mark.parametrize("traditional,T,hkv", [(False, 200, 8), (True, 200, 8), (False, 24, 8), (False, 300, 1),
+                                                (True, 300, 1)])
+def test_fp8_fused_write_equals_rotate_then_write(cuda, traditional, T, hkv):
     """FP8 cache: the call's scale and the codes over the turned keys, in the write kernels == emx_rope_rows on K,
-    then the plain FP8 write: every byte of the pages and every page scale."""
+    then the plain FP8 write: every byte of the pages and every page scale.  T = 24 (8 heads) and T = 300 (one
+    head): the one-launch write, the latter with too many (token, pair) angles for its LDS table, so every
+    value is turned with its own sincosf."""
     from easymlx_amd import Fp8PageCacheView
 
-    print(f"[fp8 fused rope write traditional={traditional} T={T}]", flush=True)
+    print(f"[fp8 fused rope write traditional={traditional} T={T} hkv={hkv}]", flush=True)
     rng = np.random.default_rng(11 + traditional + T)
-    hkv, d, bs, nb = 8, 128, 32, 64  # T = 24: the one-launch write (queries turned by its extra workgroups)
+    d, bs, nb = 128, 32, 64  # T = 24: the one-launch write (queries turned by its extra workgroups)
     rope = RotaryEmbedding.llama3(128, base=500000.0, traditional=traditional)
     k = torch.from_numpy((rng.standard_normal((T, hkv, d)) * 2).astype(np.float16)).to(cuda)
     v = torch.from_numpy((rng.standard_normal((T, hkv, d)) * 2).astype(np.float16)).to(cuda)

@@ -327,6 +327,16 @@ def test_block_mapping_checks():
 
     with pytest.raises(ValueError, match="rank-2"):
         block_mapping_on_device([1, 2, 3], "cpu")
-    with pytest.raises(ValueError, match="chains"):
-        block_mapping_on_device([[0, 1], [1, 2]], "cpu")
+    # chained / swapped pairs are valid (the kernel stages every source block before writing)
+    assert block_mapping_on_device([[0, 1], [1, 2], [2, 0]], "cpu").tolist() == [[0, 1], [1, 2], [2, 0]]
     assert block_mapping_on_device([[0, 1], [2, 3], [4, 4]], "cpu").dtype == torch.int32
+
+
+def test_copy_blocks_oracle_simultaneous_semantics():
+    """The oracle reads every source as it was before the call (the reference kernel's separate outputs)."""
+    from oracle import cache_write as ocw
+
+    a = np.arange(5)[:, None].repeat(3, 1).astype(np.int32)
+    ocw.copy_blocks([a], [[0, 1], [1, 0], [2, 3], [3, 4], [4, 2], [1, 4]])
+    # swap 0<->1; 2->3, 3->4 then 1->4 (the later pair wins), 4->2: all from the old contents
+    np.testing.assert_array_equal(a[:, 0], [1, 0, 4, 2, 1])
