@@ -44,7 +44,7 @@ def parse():
     p.add_argument("--pool-gib", type=float, default=1.5, help="total size of the rotated page pools")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-aux", action="store_true", help="skip the c3 / c4 / quantize-on-write measurements")
-    p.add_argument("--aux-only", choices=("c3", "c4", "write", "op", "fp8"),
+    p.add_argument("--aux-only", choices=("c3", "c4", "write", "op", "fp8", "shapes"),
                    help="run one auxiliary measurement alone and print its JSON (for profiler runs)")
     p.add_argument("--layers", type=int, default=32,
                    help="decode calls per model step: kv_lens change at every step's first call (Llama-3-8B: 32)")
@@ -376,6 +376,30 @@ def aux_c4(dev):
             "timing": "us_p50: events around each call (launch gap included); kv_GBs and frac: back to back"}
 
 
+def aux_shapes(dev):
+    """The c2 batch (seed 2 lengths, 4-bit, group 64) at other page sizes and head sizes: page 16 (the
+    reference's PageCacheConfig default), 32 and 64, and head_dim 256, each over its own rotated pools."""
+    from easymlx_amd.workloads import decode_workload
+
+    res = {}
+    for name, kw in (("page16", dict(block_size=16)), ("page32", dict(block_size=32)),
+                     ("page64", dict(block_size=64)), ("d256", dict(head_dim=256))):
+        wl = decode_workload(name, seed=2, bits=4, **kw)
+        st = Setup(wl, 1.0, dev)
+        warm(st.call, 0.3)
+        us = b2b_us(st.call, 100)
+        nbytes = wl.kv_bytes()
+        res[name] = {"block_size": wl.block_size, "head_dim": wl.head_dim, "us_back_to_back": round(us, 2),
+                     "kv_bytes": int(nbytes), "kv_GBs": round(nbytes / (us * 1e3), 1),
+                     "frac": round(nbytes / (us * 1e3) / HBM_PEAK_GBS, 4)}
+        del st
+        import torch
+
+        torch.cuda.empty_cache()
+    res["workload"] = "c2 batch (32 seqs, ctx U[512,4096], seed 2), 4-bit group 64, Hq 32 / Hkv 8; back to back"
+    return res
+
+
 def aux_fp8(dev):
     """FP8 (E4M3, per-page scale) cache: c2-shaped decode (batch 32, ctx U[512,4096]) and a 32-token write.
 
@@ -637,7 +661,7 @@ def main():
     dev = torch.device("cuda", 0)
     if args.aux_only:
         fn = {"c3": aux_c3, "c4": aux_c4, "write": aux_quantize_on_write, "op": aux_op_layer_step,
-              "fp8": aux_fp8}[args.aux_only]
+              "fp8": aux_fp8, "shapes": aux_shapes}[args.aux_only]
         print(json.dumps({args.aux_only: fn(dev)}))
         return
     wl = config("c2")
@@ -707,6 +731,8 @@ def main():
         aux["quantize_on_write"] = aux_quantize_on_write(dev)
         aux["op_layer_step"] = aux_op_layer_step(dev)
         aux["fp8_cache"] = aux_fp8(dev)
+        torch.cuda.empty_cache()
+        aux["other_shapes"] = aux_shapes(dev)
 
     value = bytes_per_step / (ms_per_step * 1e-3) / 1e9
     traffic, traffic_src = measured_traffic()

@@ -159,6 +159,63 @@ __device__ __forceinline__ void q4_issue_loads(Q4Loads<GS, HQ>& L, const TileRsr
     L.sraw[i] = *reinterpret_cast<const u32x4*>(sp.p[i] + soff + it * 64);
 }
 
+// One wave-item's loads over pages of PS = 16, 32 or 64 tokens: the 64-token slice
+// spans NSUB = 64 / PS pages pg[0 .. NSUB-1] (an invalid id reads page 0; its tokens
+// are masked by the compute).  K: lane L holds token L's row from page pg[L / PS]
+// (per-lane address).  V: a page holds one tile of PS tokens per dim (PS / 8 words,
+// v_word_index), so dim lane d takes PS / 8 words from each page.  Scales: piece
+// 64i + L (8 tokens of one (array, group) run) from the page of its tokens.  The
+// register image is the big-page one (q4_issue_loads).
+template <int GS, int PS>
+__device__ __forceinline__ void q4_issue_loads_small(Q4Loads<GS, 1>& L, const DecodeArgs& a, const int (&pg)[64 / PS],
+                                                     const int kh, const int lane) {
+  constexpr int NSUB = 64 / PS, G = Q4Cfg<GS, 1>::G, D = 128, VW = PS / 8;
+  auto page = [&](int j) { return (unsigned)pg[j] < (unsigned)a.nb ? pg[j] : 0; };
+  {
+    int pl = page(0);
+#pragma unroll
+    for (int j = 1; j < NSUB; ++j) pl = lane / PS == j ? page(j) : pl;
+    const uint32_t* kp = a.kc + ((size_t)pl * a.Hkv + kh) * (PS * 16) + (lane % PS) * 16;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const u32x4 x = *reinterpret_cast<const u32x4*>(kp + 4 * v);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) L.k[4 * v + e] = x[e];
+    }
+  }
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+#pragma unroll
+    for (int j = 0; j < NSUB; ++j) {
+      const uint32_t* vp = a.vc + (((size_t)page(j) * a.Hkv + kh) * D + 64 * c + lane) * VW;
+      if constexpr (VW == 2) {
+        const u32x2 x = *reinterpret_cast<const u32x2*>(vp);
+        L.v[c][2 * j] = x[0];
+        L.v[c][2 * j + 1] = x[1];
+      } else {
+#pragma unroll
+        for (int h = 0; h < VW / 4; ++h) {
+          const u32x4 x = *reinterpret_cast<const u32x4*>(vp + 4 * h);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) L.v[c][VW * j + 4 * h + e] = x[e];
+        }
+      }
+    }
+  }
+  using LD = Q4Loads<GS, 1>;
+  const h16* sb[4] = {a.ks, a.kb, a.vs, a.vb};
+#pragma unroll
+  for (int i = 0; i < LD::SNI; ++i) {
+    const int P = (64 * i + lane) % (LD::NSEG * 8);
+    const int seg = P / 8, arr = seg / G, g = seg % G, t0 = 8 * (P % 8);
+    int pj = page(0);
+#pragma unroll
+    for (int j = 1; j < NSUB; ++j) pj = t0 / PS == j ? page(j) : pj;
+    const h16* base = arr == 0 ? sb[0] : arr == 1 ? sb[1] : arr == 2 ? sb[2] : sb[3];
+    L.sraw[i] = *reinterpret_cast<const u32x4*>(base + (((size_t)pj * a.Hkv + kh) * G + g) * PS + t0 % PS);
+  }
+}
+
 // Per-lane softmax / accumulator state of one head quad.
 struct Q4State {
   f32x4 o[2];   // dims L, 64 + L of the quad's 4 heads (2^-24 units)
@@ -186,10 +243,12 @@ __device__ __forceinline__ float head_max(float v) {
 }
 
 // One 64-token item.  `full`: every token of the item is inside [start_k, kv_len).
-template <int GS, int HQ>
+// sub_ok (small pages, PS tokens each): bit j set when page j of the slice is valid.
+template <int GS, int HQ, int PS = 0>
 __device__ __forceinline__ void q4_compute(Q4Loads<GS, HQ>& L, const bool full, const int lane, const int tok_base,
                                            const int start_k, const int kv_len, const h16x4 (&qB)[HQ][8],
-                                           const float (&qs)[HQ][2], const float sc_l2, Q4State (&st)[HQ]) {
+                                           const float (&qs)[HQ][2], const float sc_l2, Q4State (&st)[HQ],
+                                           const int sub_ok = 1) {
   constexpr int G = Q4Cfg<GS, HQ>::G;
 
   // ---- S = K Q^T, one accumulator per (head quad, group)
@@ -215,7 +274,10 @@ __device__ __forceinline__ void q4_compute(Q4Loads<GS, HQ>& L, const bool full, 
   bool live[4] = {true, true, true, true};
   if (!full) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) live[i] = t0 + i >= start_k && t0 + i < kv_len;
+    for (int i = 0; i < 4; ++i) {
+      live[i] = t0 + i >= start_k && t0 + i < kv_len;
+      if constexpr (PS != 0) live[i] = live[i] && ((sub_ok >> ((t0 + i - tok_base) / PS)) & 1);
+    }
 #pragma unroll
     for (int w = 0; w < 2; ++w) {
       const uint32_t keep = (live[2 * w] ? 0x0000FFFFu : 0u) | (live[2 * w + 1] ? 0xFFFF0000u : 0u);
@@ -390,13 +452,16 @@ constexpr int kSnapRange = 4;     // ... when the ranges average at most this ma
 
 // The kernel body as workgroup `bid` of `nblocks` (a grid of its own, or the
 // decode part of a mixed batch's single launch, unified_q4).
-template <int GS, int HG>
+template <int GS, int HG, int PS = 0>
 __device__ __forceinline__ void decode_q4_body(const DecodeArgs& a, const int bid, const int nblocks, int* const plan,
                                                const int32_t* const kv_lens, const int32_t* const block_tables,
                                                const int S, const int max_blocks) {
   using Geo = Q4Geom<HG>;
   constexpr int HQ = Geo::HQ, NSL = Geo::NSL, TW = Geo::TW;
   constexpr int D = 128, G = Q4Cfg<GS, 1>::G;
+  // pages of a 64-token slice: one (big pages, a multiple of 128 tokens) or 64 / PS
+  static_assert(PS == 0 || PS == 16 || PS == 32 || PS == 64, "small pages of 16, 32 or 64 tokens");
+  constexpr int NSUB = PS ? 64 / PS : 1;
 
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -550,7 +615,7 @@ __device__ __forceinline__ void decode_q4_body(const DecodeArgs& a, const int bi
   // Only entries below the header's NWG belong to the committed plan (the others are
   // left from older plans); the sequence and kv head are bounds-checked as well, so the
   // loads stay inside q and the pools whatever the entry holds (pages: tile_of).
-  const bool spec = hdr_ok && bid < __builtin_amdgcn_readlane(pl, 35) && pe(0) < pe(1) &&
+  const bool spec = PS == 0 && hdr_ok && bid < __builtin_amdgcn_readlane(pl, 35) && pe(0) < pe(1) &&
                     (unsigned)spec_s < (unsigned)S && (unsigned)spec_kvh < (unsigned)Hkv && spec_tb >= 0;
   if (spec) {
     issue_q(spec_s, spec_kvh);  // a plan exists only for pure decode calls: row = sequence
@@ -755,9 +820,6 @@ __device__ __forceinline__ void decode_q4_body(const DecodeArgs& a, const int bi
     g0 = uru64(wg == 0 ? 0 : unit_start(g0));
     g1 = uru64(wg + 1 == NWG ? I : unit_start(g1));
   }
-
-  const int bs_log2 = __builtin_ctz(a.bs);
-
   }
   if (pwrite && wv == 0 && lane == 0) {  // this workgroup's range into the plan being written
     int* e = plan + q4_plan_entry(wslot, wg);
@@ -792,22 +854,28 @@ __device__ __forceinline__ void decode_q4_body(const DecodeArgs& a, const int bi
 
   // ---- page of this wave's slice for every item of the range, one item per lane
   // (64 items per chunk); -1 where the slice holds no token below kv_len
-  auto blk_chunk = [&](long long gb) {
+  // (small pages: the NSUB pages of the slice; -1 past kv_len or past the table row)
+  auto blk_chunk = [&](long long gb, int (&b)[NSUB]) {
     const long long g = gb + lane;
-    int b = -1;
+#pragma unroll
+    for (int q = 0; q < NSUB; ++q) b[q] = -1;
     if (g < g1) {
       const int si = seq_of(g, s);
       const int n = cum[si + 1] - cum[si];
       const int jn = (int)(g - (long long)Hkv * cum[si]) % n;
       const int t = (lo_of(si) + jn) * TW + 64 * slice;
-      if (t < kvl[si]) {
-        const size_t bi = (size_t)si * max_blocks + (t >> bs_log2);
-        b = bt_lds ? sbt[bi] : block_tables[bi];
+#pragma unroll
+      for (int q = 0; q < NSUB; ++q) {
+        const int tq = t + q * (PS ? PS : 0);
+        if (tq < kvl[si] && (tq >> bs_log2) < max_blocks) {
+          const size_t bi = (size_t)si * max_blocks + (tq >> bs_log2);
+          b[q] = bt_lds ? sbt[bi] : block_tables[bi];
+        }
       }
     }
-    return b;
   };
-  int blkv = blk_chunk(g0);
+  int blkv[NSUB];
+  blk_chunk(g0, blkv);
 
   int n_s = uru(cum[s + 1]) - uru(cum[s]);
   int kvh, j;
@@ -825,7 +893,9 @@ __device__ __forceinline__ void decode_q4_body(const DecodeArgs& a, const int bi
   // ---- first item's query and pages: already in flight when the plan held and its
   // pages are this call's (the block tables may have changed under the same kv_lens)
   int tb = (it_lo + j) * TW + 64 * slice;
-  int blk = __builtin_amdgcn_readfirstlane(__builtin_amdgcn_readlane(blkv, 0));
+  int blk[NSUB];
+#pragma unroll
+  for (int q = 0; q < NSUB; ++q) blk[q] = __builtin_amdgcn_readfirstlane(__builtin_amdgcn_readlane(blkv[q], 0));
   if (pwrite && lane == 0) {
     int* e = plan + q4_plan_entry(wslot, wg);
     if (wv == 0) {
@@ -833,13 +903,21 @@ __device__ __forceinline__ void decode_q4_body(const DecodeArgs& a, const int bi
       e[5] = kvh;
       e[6] = (it_lo + j) * TW;
     }
-    if (wv % HQ == 0) e[8 + slice] = blk;
+    if (wv % HQ == 0) e[8 + slice] = blk[0];
   }
-  if (!(spec && pvalid && s == spec_s && kvh == spec_kvh && tb == spec_tb && blk == spec_blk)) {
+  // this wave's slice of one item: loads of pages blk_ at token base t_
+  auto issue_item = [&](Q4Loads<GS, 1>& buf, const int (&blk_)[NSUB], const int kh, const int t_) {
+    if constexpr (PS == 0) {
+      size_t so;
+      const TileRsrc rs = tile_of(blk_[0], kh, t_, so);
+      q4_issue_loads(buf, rs, sptr, so, (t_ & 127) / 64, lane, a.bs);
+    } else {
+      q4_issue_loads_small<GS, PS>(buf, a, blk_, kh, lane);
+    }
+  };
+  if (!(spec && pvalid && s == spec_s && kvh == spec_kvh && tb == spec_tb && blk[0] == spec_blk)) {
     issue_q(uru(qrw[s]), kvh);  // the query first: loads return in order
-    size_t soff0;
-    const TileRsrc rs0 = tile_of(blk, kvh, tb, soff0);
-    q4_issue_loads(bufA, rs0, sptr, soff0, (tb & 127) / 64, lane, a.bs);
+    issue_item(bufA, blk, kvh, tb);
   }
   build_q();
 
@@ -894,21 +972,23 @@ __device__ __forceinline__ void decode_q4_body(const DecodeArgs& a, const int bi
     }
     const bool has_next = g + 1 < g1;
     const bool unit_end = !has_next || s1 != s || kvh1 != kvh;
-    int blk1 = -1;
+    int blk1[NSUB];
+#pragma unroll
+    for (int q = 0; q < NSUB; ++q) blk1[q] = -1;
     const int tb1 = (lo1 + j1) * TW + 64 * slice;
     if (has_next) {
       const int k1 = (int)(g + 1 - g0);
-      if ((k1 & 63) == 0) blkv = blk_chunk(g + 1);
-      blk1 = __builtin_amdgcn_readfirstlane(__builtin_amdgcn_readlane(blkv, k1 & 63));
+      if ((k1 & 63) == 0) blk_chunk(g + 1, blkv);
+#pragma unroll
+      for (int q = 0; q < NSUB; ++q)
+        blk1[q] = __builtin_amdgcn_readfirstlane(__builtin_amdgcn_readlane(blkv[q], k1 & 63));
     }
     // The next unit's query first: loads return in order, so building its
     // operand at this unit's end does not wait for the next item's pages.
     if (has_next && unit_end) issue_q(uru(qrw[s1]), kvh1);
     // Issued on every path (an empty descriptor returns zeros without touching
     // memory), so the wait before this item's compute leaves them in flight.
-    size_t soff1;
-    const TileRsrc rs1 = tile_of(blk1, kvh1, tb1, soff1);
-    q4_issue_loads(nxt, rs1, sptr, soff1, (tb1 & 127) / 64, lane, a.bs);
+    issue_item(nxt, blk1, kvh1, tb1);
 
     // ---- compute this wave's slice of the item.  A slice without a live token or
     // with an invalid page (skipped by the reference's Metal kernel) is computed
@@ -916,10 +996,13 @@ __device__ __forceinline__ void decode_q4_body(const DecodeArgs& a, const int bi
     // compiler unable to order this item's loads against the next item's, and
     // it waited for all of them before issuing the next page loads.
     {
-      const bool ok = (unsigned)blk < (unsigned)a.nb;
+      int sub_ok = 0;
+#pragma unroll
+      for (int q = 0; q < NSUB; ++q) sub_ok |= ((unsigned)blk[q] < (unsigned)a.nb) << q;
+      const bool ok = sub_ok != 0;
       q4_stage_scales<GS, 1>(cur, sst[wv], lane);
-      const bool full = ok && tb >= start_k && tb + 64 <= kv_len;
-      q4_compute<GS, 1>(cur, full, lane, tb, start_k, ok ? kv_len : 0, qB, qs, sc_l2, st);
+      const bool full = sub_ok == (1 << NSUB) - 1 && tb >= start_k && tb + 64 <= kv_len;
+      q4_compute<GS, 1, PS>(cur, full, lane, tb, start_k, ok ? kv_len : 0, qB, qs, sc_l2, st, sub_ok);
     }
 
     // ---- unit finished (or range ends): the waves' (o, m, l) meet in LDS and, after one
@@ -1027,7 +1110,8 @@ __device__ __forceinline__ void decode_q4_body(const DecodeArgs& a, const int bi
     n_s = n1;
     it_lo = lo1;
     tb = tb1;
-    blk = blk1;
+#pragma unroll
+    for (int q = 0; q < NSUB; ++q) blk[q] = blk1[q];
   };
   for (long long g = g0; g < g1; g += 2) {
     step(bufA, bufB, g);
@@ -1117,11 +1201,11 @@ __device__ __forceinline__ void decode_q4_body(const DecodeArgs& a, const int bi
 // The values the first loads need lead the argument list: the library is built with
 // kernel-argument preloading, so they arrive in SGPRs with the wave instead of
 // after a scalar load from the kernel-argument buffer.
-template <int GS, int HG>
+template <int GS, int HG, int PS = 0>
 __global__ __launch_bounds__(256, 2) void decode_q4_d128(int* plan, const int32_t* kv_lens,
                                                          const int32_t* block_tables, int S, int max_blocks,
                                                          DecodeArgs a) {
-  decode_q4_body<GS, HG>(a, blockIdx.x, gridDim.x, plan, kv_lens, block_tables, S, max_blocks);
+  decode_q4_body<GS, HG, PS>(a, blockIdx.x, gridDim.x, plan, kv_lens, block_tables, S, max_blocks);
 }
 
 }  // namespace emx

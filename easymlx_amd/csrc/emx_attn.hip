@@ -106,8 +106,18 @@ void prefill_split(emx::PrefillArgs& p, int num_tokens, int num_q_heads, int num
   p.ws_part = reinterpret_cast<float*>(static_cast<char*>(workspace) + base);
 }
 
-bool decode_fast_path(int head_dim, int page_size, int bits, int group_size, int hg, int num_seqs) {
-  if (head_dim != 128 || page_size % 128 != 0 || num_seqs > emx::kMaxSeqs) return false;
+// Pages of 16, 32 or 64 tokens (the reference's PageCacheConfig default is 16): pure
+// decode calls over 4-bit pages with group 64 and GQA 1, 2, 4 or 16 (decode_q4_d128's
+// small-page variant).
+bool small_page_q4(int page_size, int bits, int group_size, int hg, int single_token_decode) {
+  return (page_size == 16 || page_size == 32 || page_size == 64) && bits == 4 && group_size == 64 &&
+         (hg == 1 || hg == 2 || hg == 4 || hg == 16) && single_token_decode;
+}
+
+bool decode_fast_path(int head_dim, int page_size, int bits, int group_size, int hg, int num_seqs,
+                      int single_token_decode) {
+  if (head_dim != 128 || num_seqs > emx::kMaxSeqs) return false;
+  if (page_size % 128 != 0) return small_page_q4(page_size, bits, group_size, hg, single_token_decode);
   if (bits != 4 && bits != 8) return false;
   if (group_size != 32 && group_size != 64 && group_size != 128) return false;
   if (hg < 1 || hg > 16 || (hg & (hg - 1)) != 0) return false;
@@ -133,18 +143,26 @@ DecodeFn pick_decode_hg(int hg) {
 // GQA 8 with groups of 64 fills all 16 columns of the 16x16x32 kernel, which serves it.
 typedef void (*Q4Fn)(int*, const int32_t*, const int32_t*, int, int, emx::DecodeArgs);
 
-template <int GS>
+template <int GS, int PS = 0>
 Q4Fn pick_decode_q4_hg(int hg) {
   switch (hg) {
-    case 1: return emx::decode_q4_d128<GS, 1>;
-    case 2: return emx::decode_q4_d128<GS, 2>;
-    case 4: return emx::decode_q4_d128<GS, 4>;
-    case 16: return emx::decode_q4_d128<GS, 16>;
+    case 1: return emx::decode_q4_d128<GS, 1, PS>;
+    case 2: return emx::decode_q4_d128<GS, 2, PS>;
+    case 4: return emx::decode_q4_d128<GS, 4, PS>;
+    case 16: return emx::decode_q4_d128<GS, 16, PS>;
   }
   return nullptr;
 }
 
-Q4Fn pick_decode_q4(int gs, int hg) {
+// page_size a multiple of 128, or 16 / 32 / 64 (group 64 only)
+Q4Fn pick_decode_q4(int gs, int hg, int page_size) {
+  if (page_size < 128) {
+    if (gs != 64) return nullptr;
+    if (page_size == 16) return pick_decode_q4_hg<64, 16>(hg);
+    if (page_size == 32) return pick_decode_q4_hg<64, 32>(hg);
+    if (page_size == 64) return pick_decode_q4_hg<64, 64>(hg);
+    return nullptr;
+  }
   if (gs == 64) return pick_decode_q4_hg<64>(hg);
   if (gs == 128) return pick_decode_q4_hg<128>(hg);
   return nullptr;
@@ -900,7 +918,7 @@ size_t emx_paged_prefill_workspace_bytes(int num_tokens, int num_seqs, int num_q
 size_t emx_paged_workspace_bytes(int num_seqs, int num_q_heads, int num_kv_heads, int head_dim,
                                  int max_blocks_per_seq, int page_size) {
   if (num_seqs <= 0 || num_kv_heads <= 0 || num_q_heads <= 0 || max_blocks_per_seq <= 0 || page_size <= 0 ||
-      head_dim != 128 || page_size % 32 != 0 || num_seqs > emx::kMaxSeqs ||
+      head_dim != 128 || page_size % 16 != 0 || num_seqs > emx::kMaxSeqs ||
       (long)num_seqs * num_kv_heads > emx::kMaxUnits)
     return 0;
   const int hg = num_q_heads / num_kv_heads;
@@ -942,7 +960,7 @@ int emx_paged_attention_affine(const void* queries, int num_tokens, int num_q_he
       emx_paged_workspace_bytes(num_seqs, num_q_heads, num_kv_heads, head_dim, max_blocks_per_seq, page_size);
   // MFMA paths: decode rows (one query token) on the split-K decode kernel, rows of
   // longer queries on the prefill kernel; anything else on the generic kernel.
-  if (need > 0 && decode_fast_path(head_dim, page_size, bits, group_size, hg, num_seqs) &&
+  if (need > 0 && decode_fast_path(head_dim, page_size, bits, group_size, hg, num_seqs, single_token_decode) &&
       (single_token_decode || prefill_fast_path(hg))) {
     if (!aligned16(queries) || !aligned16(k_codes) || !aligned16(v_codes) || !aligned16(k_scales) ||
         !aligned16(k_biases) || !aligned16(v_scales) || !aligned16(v_biases))
@@ -982,7 +1000,7 @@ int emx_paged_attention_affine(const void* queries, int num_tokens, int num_q_he
       pgrid = (long)((num_tokens + tokb - 1) / tokb + num_seqs) * num_kv_heads * p.nparts;
       // prefill and decode rows go out as one launch (below) when a unified kernel
       // pairs this prefill with the decode kernel picked for the rows
-      const bool q4u = bits == 4 && (page_size & (page_size - 1)) == 0 && pick_decode_q4(group_size, hg);
+      const bool q4u = bits == 4 && (page_size & (page_size - 1)) == 0 && pick_decode_q4(group_size, hg, page_size);
       uf = q4u ? pick_unified_q4(group_size, hg)
                : bits == 4 ? pick_unified_affine<4>(group_size, hg) : pick_unified_affine<8>(group_size, hg);
       if (!uf) {
@@ -992,7 +1010,8 @@ int emx_paged_attention_affine(const void* queries, int num_tokens, int num_q_he
       }
     }
     // the 4-bit kernel addresses pages with shifts: power-of-two page sizes
-    const Q4Fn q4fn = bits == 4 && (page_size & (page_size - 1)) == 0 ? pick_decode_q4(group_size, hg) : nullptr;
+    const Q4Fn q4fn =
+        bits == 4 && (page_size & (page_size - 1)) == 0 ? pick_decode_q4(group_size, hg, page_size) : nullptr;
     const bool q4 = q4fn != nullptr;
     const int nw = q4 ? decode_q4_num_waves() : decode_num_waves();
     const DecodeFn fn = q4 ? nullptr : bits == 4 ? pick_decode_gs<4>(group_size, hg) : pick_decode_gs<8>(group_size, hg);

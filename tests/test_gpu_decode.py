@@ -158,3 +158,48 @@ def test_decode_repeat_reuses_workspace(cuda):
     first = _run(wl, view, cuda)
     for _ in range(3):
         np.testing.assert_array_equal(_run(wl, view, cuda), first)
+
+
+SMALL_PAGE_CASES = [
+    # (page, Hq, Hkv, ctx range, seqs, window)
+    (16, 32, 8, (512, 4096), 32, 0),   # the c2 batch at the reference's default page size
+    (16, 8, 8, (1, 700), 9, 0),        # GQA 1, lengths not a multiple of the page
+    (32, 16, 8, (60, 3000), 6, 0),     # GQA 2
+    (64, 64, 4, (200, 2500), 4, 0),    # GQA 16
+    (16, 32, 8, (100, 2000), 7, 333),  # sliding window inside a page
+    (32, 32, 8, (1, 300), 80, 0),      # many one-item units
+]
+
+
+@pytest.mark.parametrize("case", SMALL_PAGE_CASES, ids=[f"p{c[0]}hq{c[1]}hkv{c[2]}w{c[5]}" for c in SMALL_PAGE_CASES])
+def test_decode_small_pages(cuda, case):
+    """4-bit decode over pages of 16 / 32 / 64 tokens (a 64-token slice spans several pages) vs the oracle,
+    and a repeat on the cached plan bit for bit."""
+    bs, hq, hkv, ctx, seqs, window = case
+    print(f"[decode small pages {case}]", flush=True)
+    wl = decode_workload(seed=600 + bs + seqs, num_seqs=seqs, num_q_heads=hq, num_kv_heads=hkv, ctx_range=ctx,
+                         bits=4, group_size=64, block_size=bs)
+    view = gpu_cache(wl, cuda)
+    kw = {"sliding_window": window} if window else {}
+    got = _run(wl, view, cuda, **kw)
+    assert_attention_close(got, oracle_expected(wl, sliding_window=window), f"small pages {case}")
+    assert np.array_equal(_run(wl, view, cuda, **kw), got), "repeat differs"
+
+
+def test_decode_small_pages_invalid_pages(cuda):
+    """Page 16: an unassigned page (-1) and one past the pool inside a slice are skipped, as the Metal kernel
+    skips block < 0; kv_len 0 gives zeros."""
+    print("[decode small pages invalid]", flush=True)
+    wl = decode_workload(seed=77, num_seqs=5, ctx_range=(300, 1200), bits=4, block_size=16)
+    view = gpu_cache(wl, cuda)
+    lens = wl.kv_lens.copy()
+    lens[1] = 0
+    tables = wl.block_tables.copy()
+    tables[2, 3] = -1
+    tables[3, 5] = wl.num_blocks + 7
+    view.kv_lens.copy_(torch.from_numpy(lens))
+    view.block_tables.copy_(torch.from_numpy(tables))
+    got = _run(wl, view, cuda)
+    exp = oracle_expected(wl, block_tables=tables, kv_lens=lens)
+    assert_attention_close(got, exp, "small pages invalid")
+    assert not got[1].any()
