@@ -63,7 +63,7 @@ SIGNATURES: dict[str, tuple] = {
     ),
     "emx_paged_attention_dense": (
         _I,
-        [_P, _I, _I, _I, _I, _P, _P, _I, _I, _I, _P, _I, _I, _P, _P, _F, _I, _I, _P, _P],
+        [_P, _I, _I, _I, _I, _P, _P, _I, _I, _I, _P, _I, _I, _P, _P, _F, _I, _I, _P, _SZ, _P, _P],
     ),
     "emx_fp8_write_workspace_bytes": (_SZ, []),
     "emx_fp8_cache_write": (_I, [_P, _P, _I, _P, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _SZ, _P]),

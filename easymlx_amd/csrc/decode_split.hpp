@@ -1,0 +1,287 @@
+// Split-K single-token decode for the shapes outside the MFMA decode kernels:
+// any head_dim that is a multiple of 32 up to 256, pages of a multiple of 8
+// tokens, affine pages with group sizes that are multiples of 32, dense
+// fp16/bf16/fp32 caches and FP8 pages, fp16/bf16/fp32 queries.
+//
+// Replaces the reference's per-(seq, q_head) serial key loop
+// (lib/python/easymlx/operations/kernels/unified_attention.py:467-609, and the
+// head-256 variants :611-775, :1103-1268) with its split-K form
+// (page_attention.py:1718-2059: partitions, then a reduce).
+//
+//   decode_split: one wave per (sequence, kv head, <= 16 query heads, chunk of
+//     kSplitChunk keys).  The query rows sit in LDS; per 64-key step lane L
+//     takes key L: its K row 32 dims at a time through the cache's loader
+//     (vector loads of the packed codes, the group's scale and bias) against
+//     every query head of the GQA group, an online softmax in base 2 over the
+//     wave, then lane L takes dims L, L + 64, .. and walks the 64 keys in
+//     groups of 8 (one value word of 4-bit pages) with the probabilities from
+//     LDS.  The chunk's (acc, m, l) go to the workspace.
+//   decode_split_merge: one workgroup per (sequence, kv head, head chunk)
+//     combines the chunks: O = sum 2^(m_c - M) acc_c, L = sum 2^(m_c - M) l_c,
+//     out = O / L (page_attention.py:2006-2059); zero rows for empty sequences.
+//
+// Chunks start on 64-key boundaries (the first one at the window start rounded
+// down); keys outside [start_k, kv_len) or on pages with an invalid id are
+// masked, as the reference skips block < 0.
+#pragma once
+
+#include "paged_generic.hpp"
+
+namespace emx {
+
+constexpr int kSplitChunk = 256;  // keys per wave
+
+struct SplitArgs {
+  const void* q;               // [S, Hq, D]
+  void* out;                   // [S, Hq, D]
+  const int32_t* block_tables; // [S, max_blocks]
+  const int32_t* kv_lens;      // [S]
+  float* part;                 // [S, Hkv * nhc, nchunk, hc, D + 2]: acc, then (m, l)
+  int S, Hq, Hkv, D, bs, nb, max_blocks;
+  int hc;                      // query heads per wave (<= 16)
+  int nchunk;                  // chunk slots per (sequence, kv head): ceil(max_blocks * bs / kSplitChunk) + 1
+  float scale_log2;
+  int window;
+};
+
+__device__ __forceinline__ size_t split_part_index(const SplitArgs& a, int s, int y, int c) {
+  return (((size_t)s * gridDim.y + y) * a.nchunk + c) * (size_t)a.hc * (a.D + 2);
+}
+
+// --- row loaders: 32 K dims of one key, 8 keys' values of one dim
+
+template <typename Tag>
+__device__ __forceinline__ void key32(const DenseKV<Tag>& kv, int blk, int off, int h, int d0, float (&x)[32]) {
+  const typename Tag::T* p = kv.k + (((size_t)blk * kv.bs + off) * kv.Hkv + h) * kv.D + d0;
+#pragma unroll
+  for (int j = 0; j < 32; ++j) x[j] = to_f32(p[j]);
+}
+template <typename Tag>
+__device__ __forceinline__ void val8(const DenseKV<Tag>& kv, int blk, int off8, int h, int d, float (&v)[8]) {
+  const typename Tag::T* p = kv.v + (((size_t)blk * kv.bs + off8) * kv.Hkv + h) * kv.D + d;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) v[j] = to_f32(p[(size_t)j * kv.Hkv * kv.D]);
+}
+
+template <int BITS>
+__device__ __forceinline__ void key32(const AffineKV<BITS>& kv, int blk, int off, int h, int d0, float (&x)[32]) {
+  constexpr int PW = 32 / BITS;
+  const size_t ph = (size_t)blk * kv.Hkv + h;
+  const uint32_t* w = kv.kc + (ph * kv.bs + off) * (kv.D / PW) + d0 / PW;
+  const size_t si = (ph * (kv.D / kv.gs) + d0 / kv.gs) * kv.bs + off;  // 32 dims lie in one group
+  const float sc = (float)kv.ks[si], bi = (float)kv.kb[si];
+#pragma unroll
+  for (int i = 0; i < BITS; ++i) {
+    const uint32_t x4 = w[i];
+#pragma unroll
+    for (int j = 0; j < PW; ++j) x[PW * i + j] = fmaf(sc, (float)((x4 >> (j * BITS)) & ((1u << BITS) - 1u)), bi);
+  }
+}
+template <int BITS>
+__device__ __forceinline__ void val8(const AffineKV<BITS>& kv, int blk, int off8, int h, int d, float (&v)[8]) {
+  constexpr int PW = 32 / BITS;
+  const size_t ph = (size_t)blk * kv.Hkv + h;
+  const size_t si = (ph * (kv.D / kv.gs) + d / kv.gs) * kv.bs + off8;
+  const u32x4 s4 = *reinterpret_cast<const u32x4*>(kv.vs + si);  // 8 fp16 scales (off8 % 8 == 0)
+  const u32x4 b4 = *reinterpret_cast<const u32x4*>(kv.vb + si);
+#pragma unroll
+  for (int k = 0; k < 8 / PW; ++k) {
+    const uint32_t w = kv.vc[v_word_index<BITS>(ph, off8 + PW * k, d, kv.D, kv.bs)];
+#pragma unroll
+    for (int j = 0; j < PW; ++j) {
+      const int t = PW * k + j;
+      const float sc = (float)__builtin_bit_cast(h16, (uint16_t)(s4[t >> 1] >> (16 * (t & 1))));
+      const float bi = (float)__builtin_bit_cast(h16, (uint16_t)(b4[t >> 1] >> (16 * (t & 1))));
+      v[t] = fmaf(sc, (float)((w >> v_shift<BITS>(t)) & ((1u << BITS) - 1u)), bi);
+    }
+  }
+}
+
+__device__ __forceinline__ void key32(const Fp8KV& kv, int blk, int off, int h, int d0, float (&x)[32]) {
+  const uint32_t* p = reinterpret_cast<const uint32_t*>(kv.k + (((size_t)blk * kv.bs + off) * kv.Hkv + h) * kv.D + d0);
+  const float sc = kv.ks[blk];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t w = p[i];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) x[4 * i + j] = e4m3_to_f32((w >> (8 * j)) & 0xFFu) * sc;
+  }
+}
+__device__ __forceinline__ void val8(const Fp8KV& kv, int blk, int off8, int h, int d, float (&v)[8]) {
+  const uint8_t* p = kv.v + (((size_t)blk * kv.bs + off8) * kv.Hkv + h) * kv.D + d;
+  const float sc = kv.vs[blk];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) v[j] = e4m3_to_f32(p[(size_t)j * kv.Hkv * kv.D]) * sc;
+}
+
+// Loaders this kernel can use: 32 K dims must lie in one quantization group.
+template <typename Tag>
+__host__ __device__ inline bool split_kv_ok(const DenseKV<Tag>&) { return true; }
+template <int BITS>
+__host__ __device__ inline bool split_kv_ok(const AffineKV<BITS>& kv) { return kv.gs % 32 == 0; }
+__host__ __device__ inline bool split_kv_ok(const Fp8KV&) { return true; }
+
+// grid (nchunk, Hkv * head chunks, S), 64 threads; dynamic LDS: q rows [hc][D], p [hc][64]
+template <typename QT, typename KV>
+__global__ __launch_bounds__(64) void decode_split(SplitArgs a, KV kv) {
+  constexpr int MAXH = 16, MAXD = 256;
+  extern __shared__ float dyn_lds[];
+  const int lane = threadIdx.x;
+  const int c = blockIdx.x, s = blockIdx.z;
+  const int HG = a.Hq / a.Hkv, nhc = (HG + a.hc - 1) / a.hc;
+  const int kvh = blockIdx.y / nhc, h0 = (blockIdx.y % nhc) * a.hc;
+  const int nh = min(a.hc, HG - h0), D = a.D;
+  const int kl = max(min(a.kv_lens[s], a.max_blocks * a.bs), 0);
+  const int start_k = a.window > 0 ? max(0, kl - a.window) : 0;
+  const int c0 = (start_k & ~63) + c * kSplitChunk;
+  const int c1 = min(kl, c0 + kSplitChunk);
+  float* part = a.part + split_part_index(a, s, blockIdx.y, c);
+  if (c0 >= kl) return;  // no chunk here (the merge reads only the chunks that exist)
+
+  float* qs = dyn_lds;          // [hc][D]
+  float* ps = dyn_lds + a.hc * D;  // [hc][64]
+  const QT* q = reinterpret_cast<const QT*>(a.q) + ((size_t)s * a.Hq + (size_t)kvh * HG + h0) * D;
+  for (int i = lane; i < nh * D; i += 64) qs[i] = to_f32(q[i]);
+  __syncthreads();
+
+  float m[MAXH], l[MAXH], acc[MAXH][MAXD / 64];
+#pragma unroll
+  for (int h = 0; h < MAXH; ++h) {
+    m[h] = -INFINITY;
+    l[h] = 0.f;
+#pragma unroll
+    for (int i = 0; i < MAXD / 64; ++i) acc[h][i] = 0.f;
+  }
+  const int32_t* bt = a.block_tables + (size_t)s * a.max_blocks;
+
+  for (int base = c0; base < c1; base += 64) {
+    // ---- scores: lane L takes key base + L
+    const int pos = base + lane;
+    const bool in = pos >= start_k && pos < c1;
+    const int blk = pos < kl ? bt[pos / a.bs] : -1;
+    const bool ok = in && blk >= 0 && blk < a.nb;
+    float sc[MAXH];
+#pragma unroll
+    for (int h = 0; h < MAXH; ++h) sc[h] = 0.f;
+    if (ok) {
+      const int off = pos % a.bs;
+      for (int d0 = 0; d0 < D; d0 += 32) {
+        float x[32];
+        key32(kv, blk, off, kvh, d0, x);
+#pragma unroll
+        for (int h = 0; h < MAXH; ++h) {
+          if (h < nh) {
+            const float4* qv = reinterpret_cast<const float4*>(qs + h * D + d0);
+            float t = sc[h];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+              const float4 q4 = qv[j];
+              t = fmaf(q4.x, x[4 * j], t);
+              t = fmaf(q4.y, x[4 * j + 1], t);
+              t = fmaf(q4.z, x[4 * j + 2], t);
+              t = fmaf(q4.w, x[4 * j + 3], t);
+            }
+            sc[h] = t;
+          }
+        }
+      }
+    }
+    // ---- online softmax (base 2) over the wave, one head at a time
+#pragma unroll
+    for (int h = 0; h < MAXH; ++h) {
+      if (h < nh) {
+        const float x = ok ? sc[h] * a.scale_log2 : -INFINITY;
+        const float m_new = fmaxf(m[h], wave_max(x));
+        float p = 0.f, alpha = 1.f;
+        if (m_new != -INFINITY) {
+          p = ok ? exp2f(x - m_new) : 0.f;
+          alpha = exp2f(m[h] - m_new);
+        }
+        l[h] = l[h] * alpha + wave_sum(p);
+        m[h] = m_new;
+        ps[h * 64 + lane] = p;
+#pragma unroll
+        for (int i = 0; i < MAXD / 64; ++i) acc[h][i] *= alpha;
+      }
+    }
+    __syncthreads();
+    // ---- values: lane takes dims lane + 64 i; keys in groups of 8 (one page each)
+    const int nk = min(64, c1 - base);
+    for (int t8 = 0; t8 < nk; t8 += 8) {
+      const int pt = base + t8;
+      const int b = pt < kl ? bt[pt / a.bs] : -1;
+      if (b < 0 || b >= a.nb) continue;  // its probabilities are zero
+      const int off8 = pt % a.bs;
+#pragma unroll
+      for (int i = 0; i < MAXD / 64; ++i) {
+        const int d = lane + 64 * i;
+        if (d < D) {
+          float v[8];
+          val8(kv, b, off8, kvh, d, v);
+#pragma unroll
+          for (int h = 0; h < MAXH; ++h) {
+            if (h < nh) {
+              float t = acc[h][i];
+#pragma unroll
+              for (int j = 0; j < 8; ++j) t = fmaf(ps[h * 64 + t8 + j], v[j], t);
+              acc[h][i] = t;
+            }
+          }
+        }
+      }
+    }
+    __syncthreads();
+  }
+
+  // ---- this chunk's partial state
+#pragma unroll
+  for (int h = 0; h < MAXH; ++h) {
+    if (h < nh) {
+      float* ph = part + (size_t)h * (D + 2);
+#pragma unroll
+      for (int i = 0; i < MAXD / 64; ++i) {
+        const int d = lane + 64 * i;
+        if (d < D) ph[d] = acc[h][i];
+      }
+      if (lane == 0) {
+        ph[D] = m[h];
+        ph[D + 1] = l[h];
+      }
+    }
+  }
+}
+
+// grid (Hkv * head chunks, S), 256 threads
+template <typename QT>
+__global__ __launch_bounds__(256) void decode_split_merge(SplitArgs a) {
+  const int s = blockIdx.y;
+  const int HG = a.Hq / a.Hkv, nhc = (HG + a.hc - 1) / a.hc;
+  const int kvh = blockIdx.x / nhc, h0 = (blockIdx.x % nhc) * a.hc;
+  const int nh = min(a.hc, HG - h0), D = a.D;
+  const int kl = max(min(a.kv_lens[s], a.max_blocks * a.bs), 0);
+  const int start_k = a.window > 0 ? max(0, kl - a.window) : 0;
+  const int first = start_k & ~63;
+  const int nc = kl > first ? (kl - first + kSplitChunk - 1) / kSplitChunk : 0;
+  QT* out = reinterpret_cast<QT*>(a.out) + ((size_t)s * a.Hq + (size_t)kvh * HG + h0) * D;
+  const float* part = a.part + (((size_t)s * gridDim.x + blockIdx.x) * a.nchunk) * (size_t)a.hc * (D + 2);
+  const size_t stride = (size_t)a.hc * (D + 2);
+  for (int e = threadIdx.x; e < nh * D; e += 256) {
+    const int h = e / D, d = e % D;
+    float M = -INFINITY;
+    for (int c = 0; c < nc; ++c) M = fmaxf(M, part[c * stride + (size_t)h * (D + 2) + D]);
+    float O = 0.f, L = 0.f;
+    if (M != -INFINITY) {
+      for (int c = 0; c < nc; ++c) {
+        const float* ph = part + c * stride + (size_t)h * (D + 2);
+        const float mc = ph[D];
+        if (mc == -INFINITY) continue;  // a chunk without a live key
+        const float f = exp2f(mc - M);
+        O = fmaf(f, ph[d], O);
+        L = fmaf(f, ph[D + 1], L);
+      }
+    }
+    from_f32(L > 0.f ? O / L : 0.f, out + (size_t)h * D + d);
+  }
+}
+
+}  // namespace emx

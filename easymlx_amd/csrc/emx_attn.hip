@@ -13,6 +13,7 @@
 #include "../../include/emx_attn.h"
 #include "decode_affine.hpp"
 #include "paged_generic.hpp"
+#include "decode_split.hpp"
 #include "prefill_affine.hpp"
 #include "decode_q4.hpp"
 #include "unified.hpp"
@@ -298,8 +299,77 @@ int validate_common(const void* q, int num_tokens, int hq, int d, int hkv, int n
   return EMX_OK;
 }
 
+// Single-token decode outside the MFMA kernels: the split-K kernel (decode_split.hpp)
+// when the shape allows it (head_dim a multiple of 32 up to 256, pages of a multiple
+// of 8 tokens) and the workspace holds its partials.
+bool split_shape_ok(int head_dim, int page_size) {
+  return head_dim % 32 == 0 && head_dim <= 256 && page_size % 8 == 0;
+}
+
+void split_geometry(int num_q_heads, int num_kv_heads, int max_blocks, int page_size, int& hc, int& nhc,
+                    int& nchunk) {
+  const int hg = num_q_heads / num_kv_heads;
+  hc = std::min(hg, 16);
+  nhc = (hg + hc - 1) / hc;
+  nchunk = (int)(((long long)max_blocks * page_size + emx::kSplitChunk - 1) / emx::kSplitChunk) + 1;
+}
+
+size_t split_workspace_bytes(int num_seqs, int num_q_heads, int num_kv_heads, int head_dim, int max_blocks,
+                             int page_size) {
+  if (!split_shape_ok(head_dim, page_size) || num_seqs <= 0 || num_kv_heads <= 0 || num_q_heads <= 0 ||
+      max_blocks <= 0 || num_q_heads % num_kv_heads)
+    return 0;
+  int hc, nhc, nchunk;
+  split_geometry(num_q_heads, num_kv_heads, max_blocks, page_size, hc, nhc, nchunk);
+  return (size_t)num_seqs * num_kv_heads * nhc * nchunk * hc * (head_dim + 2) * sizeof(float);
+}
+
 template <typename QT, typename KV>
-int launch_generic(const emx::GenericArgs& ga, const KV& kv, hipStream_t st) {
+int launch_split(const emx::GenericArgs& ga, const KV& kv, float* part, hipStream_t st) {
+  emx::SplitArgs sa;
+  sa.q = ga.q;
+  sa.out = ga.out;
+  sa.block_tables = ga.block_tables;
+  sa.kv_lens = ga.kv_lens;
+  sa.part = part;
+  sa.S = ga.S;
+  sa.Hq = ga.Hq;
+  sa.Hkv = ga.Hkv;
+  sa.D = ga.D;
+  sa.bs = ga.bs;
+  sa.nb = ga.nb;
+  sa.max_blocks = ga.max_blocks;
+  sa.scale_log2 = ga.scale_log2;
+  sa.window = ga.window;
+  int nhc;
+  split_geometry(ga.Hq, ga.Hkv, ga.max_blocks, ga.bs, sa.hc, nhc, sa.nchunk);
+  const size_t lds = (size_t)sa.hc * (ga.D + 64) * sizeof(float);
+  hipLaunchKernelGGL((emx::decode_split<QT, KV>), dim3((unsigned)sa.nchunk, (unsigned)(ga.Hkv * nhc), (unsigned)ga.S),
+                     dim3(64), lds, st, sa, kv);
+  if (int r = check_launch("decode_split")) return r;
+  hipLaunchKernelGGL((emx::decode_split_merge<QT>), dim3((unsigned)(ga.Hkv * nhc), (unsigned)ga.S), dim3(256), 0, st,
+                     sa);
+  return check_launch("decode_split_merge");
+}
+
+template <typename QT, typename KV>
+int launch_generic_only(const emx::GenericArgs& ga, const KV& kv, hipStream_t st);
+
+// The generic kernel, or the split-K decode for single-token calls it covers
+// (ws: the caller's workspace, or null).
+template <typename QT, typename KV>
+int launch_generic(const emx::GenericArgs& ga, const KV& kv, hipStream_t st, void* ws = nullptr,
+                   size_t ws_bytes = 0) {
+  if (ga.decode && ws && ga.S == ga.T && emx::split_kv_ok(kv) &&
+      ws_bytes >= (size_t)kPartialsInt * sizeof(int) +
+                      split_workspace_bytes(ga.S, ga.Hq, ga.Hkv, ga.D, ga.max_blocks, ga.bs) &&
+      split_workspace_bytes(ga.S, ga.Hq, ga.Hkv, ga.D, ga.max_blocks, ga.bs) > 0)
+    return launch_split<QT>(ga, kv, reinterpret_cast<float*>(static_cast<int*>(ws) + kPartialsInt), st);
+  return launch_generic_only<QT>(ga, kv, st);
+}
+
+template <typename QT, typename KV>
+int launch_generic_only(const emx::GenericArgs& ga, const KV& kv, hipStream_t st) {
   const int hg = ga.Hq / ga.Hkv;
   dim3 grid(ga.T, ga.Hkv, (hg + 15) / 16);
   hipLaunchKernelGGL((emx::paged_generic<QT, KV>), grid, dim3(64), 0, st, ga, kv);
@@ -918,14 +988,20 @@ size_t emx_paged_prefill_workspace_bytes(int num_tokens, int num_seqs, int num_q
 size_t emx_paged_workspace_bytes(int num_seqs, int num_q_heads, int num_kv_heads, int head_dim,
                                  int max_blocks_per_seq, int page_size) {
   if (num_seqs <= 0 || num_kv_heads <= 0 || num_q_heads <= 0 || max_blocks_per_seq <= 0 || page_size <= 0 ||
-      head_dim != 128 || page_size % 16 != 0 || num_seqs > emx::kMaxSeqs ||
-      (long)num_seqs * num_kv_heads > emx::kMaxUnits)
+      num_seqs > emx::kMaxSeqs || (long)num_seqs * num_kv_heads > emx::kMaxUnits || num_q_heads % num_kv_heads)
     return 0;
+  size_t fast = 0;
   const int hg = num_q_heads / num_kv_heads;
-  const size_t slots = (size_t)decode_max_waves() + (size_t)num_seqs * num_kv_heads;
-  if (decode_max_waves() > emx::kMaxWaves) return 0;
-  // arrival counters at a fixed offset (so every call finds them zeroed), then the partials
-  return kPartialsInt * sizeof(int) + slots * hg * (head_dim + 2) * sizeof(float);
+  if (head_dim == 128 && page_size % 16 == 0 && decode_max_waves() <= emx::kMaxWaves) {
+    // arrival counters and the plan cache at fixed offsets (so every call finds them as
+    // the last call left them), then the split-K partials
+    const size_t slots = (size_t)decode_max_waves() + (size_t)num_seqs * num_kv_heads;
+    fast = kPartialsInt * sizeof(int) + slots * hg * (head_dim + 2) * sizeof(float);
+  }
+  // the split-K decode of the other shapes keeps its chunks' partials after the same offset
+  const size_t split = split_workspace_bytes(num_seqs, num_q_heads, num_kv_heads, head_dim, max_blocks_per_seq,
+                                             page_size);
+  return std::max(fast, split ? kPartialsInt * sizeof(int) + split : 0);
 }
 
 int emx_paged_attention_affine(const void* queries, int num_tokens, int num_q_heads, int head_dim,
@@ -1103,7 +1179,7 @@ int emx_paged_attention_affine(const void* queries, int num_tokens, int num_q_he
                         head_dim,
                         page_size,
                         group_size};
-    return launch_generic<emx::h16>(ga, kv, st);
+    return launch_generic<emx::h16>(ga, kv, st, workspace, workspace_bytes);
   }
   emx::AffineKV<8> kv{k_codes,
                       reinterpret_cast<const emx::h16*>(k_scales),
@@ -1115,14 +1191,15 @@ int emx_paged_attention_affine(const void* queries, int num_tokens, int num_q_he
                       head_dim,
                       page_size,
                       group_size};
-  return launch_generic<emx::h16>(ga, kv, st);
+  return launch_generic<emx::h16>(ga, kv, st, workspace, workspace_bytes);
 }
 
 int emx_paged_attention_dense(const void* queries, int num_tokens, int num_q_heads, int head_dim, int dtype,
                               const void* key_cache, const void* value_cache, int num_blocks, int page_size,
                               int num_kv_heads, const int32_t* block_tables, int num_seqs, int max_blocks_per_seq,
                               const int32_t* kv_lens, const int32_t* query_start_loc, float softmax_scale,
-                              int sliding_window, int single_token_decode, void* out, void* stream) {
+                              int sliding_window, int single_token_decode, void* workspace, size_t workspace_bytes,
+                              void* out, void* stream) {
   int rc = validate_common(queries, num_tokens, num_q_heads, head_dim, num_kv_heads, num_blocks, page_size,
                            block_tables, num_seqs, max_blocks_per_seq, kv_lens, query_start_loc, single_token_decode,
                            out);
@@ -1152,17 +1229,17 @@ int emx_paged_attention_dense(const void* queries, int num_tokens, int num_q_hea
     case EMX_DTYPE_F16: {
       emx::DenseKV<emx::F16> kv{reinterpret_cast<const emx::h16*>(key_cache),
                                 reinterpret_cast<const emx::h16*>(value_cache), num_kv_heads, head_dim, page_size};
-      return launch_generic<emx::h16>(ga, kv, st);
+      return launch_generic<emx::h16>(ga, kv, st, workspace, workspace_bytes);
     }
     case EMX_DTYPE_BF16: {
       emx::DenseKV<emx::BF16> kv{reinterpret_cast<const uint16_t*>(key_cache),
                                  reinterpret_cast<const uint16_t*>(value_cache), num_kv_heads, head_dim, page_size};
-      return launch_generic<uint16_t>(ga, kv, st);
+      return launch_generic<uint16_t>(ga, kv, st, workspace, workspace_bytes);
     }
     case EMX_DTYPE_F32: {
       emx::DenseKV<emx::F32> kv{reinterpret_cast<const float*>(key_cache),
                                 reinterpret_cast<const float*>(value_cache), num_kv_heads, head_dim, page_size};
-      return launch_generic<float>(ga, kv, st);
+      return launch_generic<float>(ga, kv, st, workspace, workspace_bytes);
     }
   }
   return fail(EMX_ERR_UNSUPPORTED, "unknown dtype code %d", dtype);
@@ -1479,9 +1556,9 @@ int emx_paged_attention_fp8(const void* queries, int num_tokens, int num_q_heads
   if (pf && query_start_loc) return launch_prefill(1);
   const emx::Fp8KV kv{key_cache, value_cache, k_scale, v_scale, num_kv_heads, head_dim, page_size};
   switch (dtype) {
-    case EMX_DTYPE_F16: return launch_generic<emx::h16>(ga, kv, st);
-    case EMX_DTYPE_BF16: return launch_generic<uint16_t>(ga, kv, st);
-    case EMX_DTYPE_F32: return launch_generic<float>(ga, kv, st);
+    case EMX_DTYPE_F16: return launch_generic<emx::h16>(ga, kv, st, workspace, workspace_bytes);
+    case EMX_DTYPE_BF16: return launch_generic<uint16_t>(ga, kv, st, workspace, workspace_bytes);
+    case EMX_DTYPE_F32: return launch_generic<float>(ga, kv, st, workspace, workspace_bytes);
   }
   return fail(EMX_ERR_INVALID, "unknown dtype %d", dtype);
 }

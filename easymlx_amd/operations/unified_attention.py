@@ -255,13 +255,18 @@ def paged_attention(
     key_cache = key_cache.contiguous()
     value_cache = value_cache.contiguous()
     nb, bs, hkv = int(key_cache.shape[0]), int(key_cache.shape[1]), int(key_cache.shape[2])
+    need = int(lib.emx_paged_workspace_bytes(S, hq, hkv, d, max_blocks, bs)) if single_token_decode else 0
+    if need and workspace is None:
+        workspace = _workspace(dev, stream, need)
+    ws_ptr = workspace.data_ptr() if workspace is not None else None
+    ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
     _native.check(
         lib.emx_paged_attention_dense(
             queries.data_ptr(), total, hq, d, _DTYPE_CODE[queries.dtype],
             key_cache.data_ptr(), value_cache.data_ptr(), nb, bs, hkv,
             block_tables.data_ptr(), S, max_blocks, kv_lens.data_ptr(), query_start_loc.data_ptr(),
             float(softmax_scale), int(sliding_window), int(bool(single_token_decode)),
-            out.data_ptr(), stream,
+            ws_ptr, ws_bytes, out.data_ptr(), stream,
         )
     )
     return out

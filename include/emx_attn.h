@@ -341,13 +341,20 @@ int emx_paged_attention_affine(const void* queries, int num_tokens, int num_q_he
 /*
  * Paged attention over an unquantized cache in the reference layout
  * key/value [num_blocks, page_size, Hkv, head_dim] (dtype = queries' dtype).
- * Replaces: paged_attention(...) unified_attention.py:1377-1512 for fp16/bf16/fp32 caches.
+ * Single-token decode calls (head_dim a multiple of 32 up to 256, page_size a
+ * multiple of 8) run split-K over chunks of keys when the workspace holds
+ * emx_paged_workspace_bytes(...) bytes (same rules as
+ * emx_paged_attention_affine); otherwise, or with a null workspace, one
+ * wave per (token, kv head) walks the keys.
+ * Replaces: paged_attention(...) unified_attention.py:1377-1512 for fp16/bf16/fp32 caches
+ *   (decode kernels :467-775, split-K precedent page_attention.py:1718-2059).
  */
 int emx_paged_attention_dense(const void* queries, int num_tokens, int num_q_heads, int head_dim, int dtype,
                               const void* key_cache, const void* value_cache, int num_blocks, int page_size,
                               int num_kv_heads, const int32_t* block_tables, int num_seqs, int max_blocks_per_seq,
                               const int32_t* kv_lens, const int32_t* query_start_loc, float softmax_scale,
-                              int sliding_window, int single_token_decode, void* out, void* stream);
+                              int sliding_window, int single_token_decode, void* workspace, size_t workspace_bytes,
+                              void* out, void* stream);
 
 /*
  * Bytes of device workspace emx_fp8_cache_write needs (per-workgroup maxima;

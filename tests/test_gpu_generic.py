@@ -83,3 +83,48 @@ def test_decode_odd_shapes_generic(cuda, shape):
                           group_size=gs, single_token_decode=True)
     torch.cuda.synchronize()
     assert_attention_close(out.float().cpu().numpy(), oracle_expected(wl), str(shape))
+
+
+SPLIT_CASES = [
+    # (kind, D, page, Hq, Hkv, bits, group, ctx, seqs, window)
+    ("affine", 256, 128, 32, 8, 4, 64, (512, 4096), 6, 0),   # head-256 decode
+    ("affine", 256, 16, 16, 8, 4, 64, (1, 1500), 7, 0),
+    ("affine", 256, 64, 16, 4, 8, 128, (100, 2500), 4, 700),
+    ("affine", 64, 8, 8, 2, 8, 32, (1, 900), 9, 0),
+    ("affine", 96, 32, 24, 8, 4, 32, (60, 1200), 5, 0),      # GQA 3
+    ("affine", 128, 128, 64, 2, 4, 64, (300, 2000), 3, 0),   # GQA 32: two head chunks per kv head
+    ("dense", 256, 16, 32, 8, None, 64, (1, 2000), 6, 0),
+    ("dense", 96, 32, 12, 4, None, 64, (1, 700), 5, 99),
+]
+
+
+@pytest.mark.parametrize("case", SPLIT_CASES, ids=[f"{c[0]}d{c[1]}p{c[2]}hq{c[3]}hkv{c[4]}b{c[5]}g{c[6]}w{c[9]}"
+                                                  for c in SPLIT_CASES])
+def test_split_decode_shapes(cuda, case):
+    """Single-token decode outside the MFMA kernels (head_dim 64..256, pages of 8..128 tokens, any GQA): the
+    split-K kernel (chunks of 256 keys + a merge launch) against the oracle, and a repeat bit for bit."""
+    kind, d, bs, hq, hkv, bits, gs, ctx, seqs, window = case
+    print(f"[split decode {case}]", flush=True)
+    wl = decode_workload(seed=900 + d + bs + seqs, num_seqs=seqs, num_q_heads=hq, num_kv_heads=hkv, head_dim=d,
+                         block_size=bs, ctx_range=ctx, bits=bits, group_size=gs)
+    q = torch.from_numpy(wl.q).to(cuda)
+    qsl = torch.from_numpy(wl.query_start_loc).to(cuda)
+    kw = {"sliding_window": window} if window else {}
+    if kind == "affine":
+        view = gpu_cache(wl, cuda)
+
+        def run():
+            return paged_attention(q, view.k_codes, view.v_codes, view.block_tables, view.kv_lens, qsl,
+                                   k_scales=view.k_scales, k_biases=view.k_biases, v_scales=view.v_scales,
+                                   v_biases=view.v_biases, bits=bits, group_size=gs, single_token_decode=True, **kw)
+    else:
+        kc, vc = wl.logical_cache()
+        t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(cuda)  # noqa: E731
+        kct, vct, bt, kl = t(kc), t(vc), t(wl.block_tables), t(wl.kv_lens)
+
+        def run():
+            return paged_attention(q, kct, vct, bt, kl, qsl, single_token_decode=True, **kw)
+    got = run().float().cpu().numpy()
+    torch.cuda.synchronize()
+    assert_attention_close(got, oracle_expected(wl, sliding_window=window), f"split decode {case}")
+    assert np.array_equal(run().float().cpu().numpy(), got), "repeat differs"
