@@ -18,6 +18,7 @@ EMX_OK = 0
 EMX_ERR_INVALID = -1
 EMX_ERR_UNSUPPORTED = -2
 EMX_ERR_HIP = -3
+APPEND_COUNTER_INTS = 4  # EMX_APPEND_COUNTER_INTS: the device ints a decode append counts on
 
 DTYPE_F16 = 0
 DTYPE_BF16 = 1

@@ -146,7 +146,8 @@ class CompiledPagedCacheProxy:
         if counter is None:
             if torch.cuda.is_current_stream_capturing():
                 raise RuntimeError("CompiledPagedCacheProxy: run one eager step before capture")
-            counter = self._counter = torch.zeros(1, dtype=torch.int32, device=c.block_tables.device)
+            counter = self._counter = torch.zeros(_native.APPEND_COUNTER_INTS, dtype=torch.int32,
+                                                  device=c.block_tables.device)
         q_in = queries.contiguous()
         q_out = torch.empty_like(q_in)
         bt = c.block_tables

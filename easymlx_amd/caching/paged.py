@@ -369,12 +369,13 @@ class PageCacheView:
         return t
 
     def _append_counter(self, stream: int) -> torch.Tensor:
-        """The device int the decode append counts its workgroups on (zero between calls), one per stream:
-        appends ordered on one stream share it, appends issued on another stream never do."""
+        """The device ints the decode append counts its workgroups on (zero between calls), one set per
+        stream: appends ordered on one stream share it, appends issued on another stream never do."""
         counters = self.__dict__.setdefault("_counters", {})
         c = counters.get(stream)
         if c is None:
-            c = counters[stream] = torch.zeros(1, dtype=torch.int32, device=self.block_tables.device)
+            c = counters[stream] = torch.zeros(_native.APPEND_COUNTER_INTS, dtype=torch.int32,
+                                               device=self.block_tables.device)
         return c
 
     def _concatenate_rope_fused(self, queries, keys, values, cache_metadata, rope, slot_ids, query_lens, write,

@@ -159,13 +159,27 @@ struct RopeArgs {
   int traditional;
 };
 
-// (y0, y1) = (x0, x1) turned by theta; fp32 products and sums rounded one by
-// one (no contraction), so every kernel that rotates gets the same bits.
+// sin and cos of a RoPE angle: the rotations below and the (token, pair) tables
+// that the fused writes build all take them from here.
+__device__ __forceinline__ void rope_sincos(const float theta, float* sn, float* cs) { sincosf(theta, sn, cs); }
+
+// (x0, x1) turned by the angle whose sine and cosine are given: fp32 products
+// and sums rounded one by one, so every kernel that rotates gets the same bits.
+// (HIP's __fmul_rn and __fadd_rn are plain operators compiled under the
+// header's -ffp-contract=fast, which fused a product into the following sum at
+// some call sites and not at others; the operators are written here with
+// contraction off.)
+__device__ __forceinline__ void rope_rotate_sc(const float x0, const float x1, const float2 sc, float& y0, float& y1) {
+#pragma clang fp contract(off)
+  y0 = x0 * sc.y - x1 * sc.x;
+  y1 = x0 * sc.x + x1 * sc.y;
+}
+
+// (y0, y1) = (x0, x1) turned by theta (rope_rotate_sc on rope_sincos(theta)).
 __device__ __forceinline__ void rope_rotate(const float x0, const float x1, const float theta, float& y0, float& y1) {
   float sn, cs;
-  sincosf(theta, &sn, &cs);
-  y0 = __fsub_rn(__fmul_rn(x0, cs), __fmul_rn(x1, sn));
-  y1 = __fadd_rn(__fmul_rn(x0, sn), __fmul_rn(x1, cs));
+  rope_sincos(theta, &sn, &cs);
+  rope_rotate_sc(x0, x1, float2{sn, cs}, y0, y1);
 }
 
 // Max / sum over the lanes i, i^16, i^32, i^48 (one column of the four 16-lane

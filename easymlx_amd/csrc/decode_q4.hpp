@@ -423,17 +423,22 @@ __device__ __forceinline__ int wg_of_lanes(const Q4Balance& bl, const long long 
 }
 
 // Plan cache.  A decode step runs the same batch through every layer: the same
-// kv_lens, so the same item counts, workgroup ranges and first items.  A pure
+// kv_lens, so the same item counts, workgroup ranges and first items; and from
+// one step to the next each kv_len grows by one token, which leaves a
+// sequence's item count unchanged except when it crosses a TW boundary.  The
+// ranges are a function of the item counts alone (and of the shape).  A pure
 // decode call (no mixed batch) keeps, in a region of the caller's workspace, the
 // plan it computed: per workgroup {g0, g1, pk_first, pk_last, first sequence,
 // kv head, token base, -, page of each 64-token slice of the first item}, plus a
-// copy of kv_lens and a header {generation, S, Hkv, NWG, window, first_slot,
-// kernel kind, kv_len cap}.  The next call on the workspace loads its entry,
-// the header and the copy in its first memory round trip, sends the first
-// item's query and page loads out at once, and uses the cached ranges when the
-// header matches its shape and the copy matches kv_lens (compared during the
-// table scan); its first item's pages are checked against the block table
-// (which may change under the same kv_lens) and loaded again if they differ.
+// copy of the per-sequence item counts and a header {generation, S, Hkv, NWG,
+// window, first_slot, kernel kind, kv_len cap}.  The next call on the workspace
+// loads its entry, the header and the copy in its first memory round trip, sends
+// the first item's query and page loads out at once, and uses the cached ranges
+// when the header matches its shape and the copy matches its item counts
+// (compared during the table scan); its first item's sequence, head, token base
+// and pages are checked against this call's own (the block table may change
+// under the same counts, a sliding window moves the first item) and loaded
+// again if they differ.  Tokens past kv_len are masked from this call's kv_lens.
 // Otherwise it computes the ranges itself and writes its own plan into the
 // other slot; the workgroup counted last on header[15] then publishes it (every
 // workgroup of the call has read the old header by then, so none of them reads a
@@ -573,7 +578,7 @@ __device__ __forceinline__ void decode_q4_body(const DecodeArgs& a, const int bi
     }
   }
   // per-sequence loads (sequences ch*t .. ch*t+ch-1 of thread t): kv_len, the mixed
-  // batch's query row, and the plan's copies of kv_lens
+  // batch's query row, and the plan's copies of the item counts
   constexpr int kSeqPT = kMaxSeqs / 256;
   const int ch = (S + 255) / 256;
   const int sq0 = threadIdx.x * ch;
@@ -626,7 +631,7 @@ __device__ __forceinline__ void decode_q4_body(const DecodeArgs& a, const int bi
 
   // ---- block-wide exclusive prefix of the live item counts (cum[s]), clamped
   // kv_lens (kvl[s], -1 for rows a mixed batch runs elsewhere), query rows (qrw[s]),
-  // and whether kv_lens differ from the committed plan's copy
+  // and whether the item counts differ from the committed plan's copy
   int tsum = 0, mis = 0;
 #pragma unroll
   for (int i = 0; i < kSeqPT; ++i) {
@@ -643,7 +648,7 @@ __device__ __forceinline__ void decode_q4_body(const DecodeArgs& a, const int bi
       }
       cum[si] = n;  // temporarily the count
       tsum += n;
-      mis |= plan && kc[pslot][i] != klr[i];
+      mis |= plan && kc[pslot][i] != n;
     }
   }
   {
@@ -654,8 +659,9 @@ __device__ __forceinline__ void decode_q4_body(const DecodeArgs& a, const int bi
       if (lane >= o) x += y;
     }
     int(&wsum)[8] = lds_at<int[8]>(oXb + 32);
+    const bool wmis = __ballot(mis) != 0ull;  // every lane votes (not under the lane test below)
     if (lane == 63) wsum[wv] = x;
-    if (lane == 0) wsum[4 + wv] = __ballot(mis) != 0ull;
+    if (lane == 0) wsum[4 + wv] = wmis;
     __syncthreads();
     int base = 0;
     for (int w = 0; w < wv; ++w) base += wsum[w];
@@ -691,7 +697,7 @@ __device__ __forceinline__ void decode_q4_body(const DecodeArgs& a, const int bi
   const int NWG = (int)min((long long)nblocks, I);  // every range non-empty (before snapping, below)
   const int wg = bid;
   if (wg >= NWG) return;
-  // The committed plan holds when its shape and its copy of kv_lens match this call's.
+  // The committed plan holds when its shape and its copy of the item counts match this call's.
   const bool pvalid = hdr_ok && __builtin_amdgcn_readlane(pl, 35) == NWG && uru(mis) == 0;
   const bool pwrite = plan && !pvalid;  // otherwise this call commits its own plan (slot pgen + 1)
   const int wslot = (pgen + 1) & 1;
@@ -828,11 +834,11 @@ __device__ __forceinline__ void decode_q4_body(const DecodeArgs& a, const int bi
     e[2] = pk_first;
     e[3] = pk_last;
   }
-  if (pwrite && wg == 0) {  // kv_lens as this call saw them
+  if (pwrite && wg == 0) {  // the item counts of this call
 #pragma unroll
     for (int i = 0; i < kSeqPT; ++i) {
       const int si = sq0 + i;
-      if (i < ch && si < S) plan[q4_plan_kvl(wslot) + si] = klr[i];
+      if (i < ch && si < S) plan[q4_plan_kvl(wslot) + si] = cum[si + 1] - cum[si];
     }
   }
   if (g0 < g1) {
@@ -891,7 +897,7 @@ __device__ __forceinline__ void decode_q4_body(const DecodeArgs& a, const int bi
   u32x2(&sst)[4][16 * 4 * G] = lds_at<u32x2[4][16 * 4 * G]>(oSst);  // per wave: scale staging [16 quads][4 * G segments]
 
   // ---- first item's query and pages: already in flight when the plan held and its
-  // pages are this call's (the block tables may have changed under the same kv_lens)
+  // pages are this call's (the block tables may have changed under the same item counts)
   int tb = (it_lo + j) * TW + 64 * slice;
   int blk[NSUB];
 #pragma unroll

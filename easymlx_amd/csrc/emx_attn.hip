@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <type_traits>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -483,6 +484,21 @@ int emx_affine_quantize(const void* x, long rows, int head_dim, int group_size, 
   return check_launch("affine_quantize");
 }
 
+// The lane-per-8-dims fused-RoPE write (affine_write_rope_lanes: one workgroup per
+// kv head plus workgroups for the queries) when the call fits it; false: the
+// caller launches affine_cache_write_small.
+static bool launch_affine_lanes(const emx::WriteArgs& a, int bits, hipStream_t st) {
+  if (a.rope.inv_freq == nullptr || !emx::affine_lanes_fit(a.T, a.D, a.gs, a.rope.rot, a.rope.traditional))
+    return false;
+  const int tpw = emx::affine_lanes_tpw(a.D);
+  const int nt = (tpw * (a.D / 8) + 63) / 64 * 64;       // threads per workgroup
+  const int nwg = a.Hkv * ((a.T + tpw - 1) / tpw) + (a.q != nullptr ? a.T : 0);  // + one per query token
+  typedef void (*Fn)(emx::WriteArgs);
+  const Fn fn = bits == 4 ? emx::affine_write_rope_lanes<4> : emx::affine_write_rope_lanes<8>;
+  hipLaunchKernelGGL(fn, dim3((unsigned)nwg), dim3((unsigned)nt), 0, st, a);
+  return true;
+}
+
 static int affine_write_impl(const void* keys, const void* values, const int32_t* slot_mapping, int num_tokens,
                       int num_kv_heads, int head_dim, int group_size, int bits, int page_size, int num_blocks,
                       uint32_t* k_codes, void* k_scales, void* k_biases, uint32_t* v_codes, void* v_scales,
@@ -532,6 +548,7 @@ static int affine_write_impl(const void* keys, const void* values, const int32_t
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (num_tokens <= emx::kSmallWrite && head_dim % 16 == 0 && group_size % 16 == 0 &&
       group_size <= emx::kSmallMaxGroup) {
+    if (launch_affine_lanes(a, bits, st)) return check_launch("affine_write_rope_lanes");
     const bool r = rope.inv_freq != nullptr;
     // with RoPE and queries: kQRopeBlocks more rows of workgroups turn the queries in the same launch
     const dim3 sgrid((unsigned)num_kv_heads,
@@ -642,10 +659,12 @@ int emx_affine_cache_append_rope(const void* keys, const void* values, const int
   a.S = num_seqs;
   a.max_blocks = max_blocks_per_seq;
   a.counter = counter;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (launch_affine_lanes(a, bits, st)) return check_launch("affine_write_rope_lanes (append)");
   const dim3 sgrid((unsigned)num_kv_heads, (unsigned)(head_dim / 16 + (queries ? emx::kQRopeBlocks : 0)));
   typedef void (*SmallFn)(emx::WriteArgs);
   SmallFn fn = bits == 4 ? emx::affine_cache_write_small<4, true> : emx::affine_cache_write_small<8, true>;
-  hipLaunchKernelGGL(fn, sgrid, dim3(256), 0, reinterpret_cast<hipStream_t>(stream), a);
+  hipLaunchKernelGGL(fn, sgrid, dim3(256), 0, st, a);
   return check_launch("affine_cache_write_small (append)");
 }
 
@@ -1247,6 +1266,45 @@ int emx_paged_attention_dense(const void* queries, int num_tokens, int num_q_hea
 
 size_t emx_fp8_write_workspace_bytes(void) { return sizeof(float) * 2 * emx::kFp8Parts; }
 
+// The one-workgroup write (fp8_write_one, plus workgroups for the queries) when
+// the call fits it and its pointers allow 16-byte loads and 8-byte stores; false:
+// the caller launches the general kernels.
+static bool launch_fp8_one(const emx::Fp8WriteArgs& a, int dtype, bool turn_q, hipStream_t st) {
+  const int rot = a.rope.inv_freq ? a.rope.rot : 0, trad = a.rope.traditional;
+  auto fits_as = [&](auto big) {
+    constexpr bool B = decltype(big)::value;
+    return dtype == EMX_DTYPE_F16    ? emx::fp8_one_fits<emx::h16, B>(a.T, a.Hkv, a.D, rot, trad)
+           : dtype == EMX_DTYPE_BF16 ? emx::fp8_one_fits<uint16_t, B>(a.T, a.Hkv, a.D, rot, trad)
+                                     : emx::fp8_one_fits<float, B>(a.T, a.Hkv, a.D, rot, trad);
+  };
+  const bool small = fits_as(std::false_type{}), fits = small || fits_as(std::true_type{});
+  const uintptr_t in16 = reinterpret_cast<uintptr_t>(a.k) | reinterpret_cast<uintptr_t>(a.v) |
+                         (turn_q ? reinterpret_cast<uintptr_t>(a.q) | reinterpret_cast<uintptr_t>(a.q_in) : 0);
+  const uintptr_t out8 = reinterpret_cast<uintptr_t>(a.kc) | reinterpret_cast<uintptr_t>(a.vc);
+  if (!fits || (in16 & 15) || (out8 & 7) || (turn_q && (rot <= 0 || a.Hq <= 0))) return false;
+  const int nk = emx::fp8_one_ktasks(a.T, a.Hkv, a.D, rot, trad), nv = a.T * a.Hkv * (a.D / 8);
+  const int ue = small ? 1 : 2;  // Fp8OneCfg::UE
+  const int nw = (nk + nv + ue * 1024 - 1) / (ue * 1024);  // write workgroups
+  int nq = 0;  // query workgroups: two 16-byte tasks per thread
+  if (turn_q) {
+    const long qt = (long)emx::fp8_one_ktasks(a.T, a.Hq, a.D, rot, trad);
+    nq = (int)std::min<long>(8, std::max<long>(1, (qt + 2047) / 2048));
+  }
+  const dim3 g((unsigned)(nw + nq));
+  emx::Fp8WriteArgs b = a;
+  b.nwg = nw;
+  if (!turn_q) b.q = nullptr;
+  typedef void (*Fn)(emx::Fp8WriteArgs);
+  Fn fn;
+  switch (dtype) {
+    case EMX_DTYPE_F16: fn = small ? emx::fp8_write_one<emx::F16, false> : emx::fp8_write_one<emx::F16, true>; break;
+    case EMX_DTYPE_BF16: fn = small ? emx::fp8_write_one<emx::BF16, false> : emx::fp8_write_one<emx::BF16, true>; break;
+    default: fn = small ? emx::fp8_write_one<emx::F32, false> : emx::fp8_write_one<emx::F32, true>; break;
+  }
+  hipLaunchKernelGGL(fn, g, dim3(1024), 0, st, b);
+  return true;
+}
+
 static int fp8_write_impl(const void* keys, const void* values, int dtype, const int32_t* slot_mapping, int num_tokens,
                           int num_kv_heads, int head_dim, int page_size, int num_blocks, uint8_t* key_cache,
                           uint8_t* value_cache, float* k_scales, float* v_scales, void* workspace,
@@ -1295,6 +1353,7 @@ static int fp8_write_impl(const void* keys, const void* values, int dtype, const
   const int nwrite = (int)std::min<size_t>(1024, (n / 4 + 255) / 256);
   const bool turn_q = rope.inv_freq != nullptr && queries != nullptr;
   if (n <= (size_t)emx::kFp8SelfMax) {  // one launch: each workgroup takes the maxima itself
+    if (launch_fp8_one(a, dtype, turn_q, st)) return check_launch("fp8_write_one");
     a.nwg = (int)((n / 4 + 1023) / 1024);
     const dim3 g1((unsigned)(a.nwg + (turn_q ? 4 : 0)));  // + workgroups that turn the queries
     switch (dtype) {
@@ -1421,9 +1480,26 @@ int emx_fp8_cache_append_rope(const void* keys, const void* values, int dtype, c
   a.S = num_seqs;
   a.max_blocks = max_blocks_per_seq;
   a.counter = counter;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const uintptr_t in16 = reinterpret_cast<uintptr_t>(keys) | reinterpret_cast<uintptr_t>(values) |
+                         reinterpret_cast<uintptr_t>(queries) | reinterpret_cast<uintptr_t>(a.q_in);
+  const uintptr_t out8 = reinterpret_cast<uintptr_t>(key_cache) | reinterpret_cast<uintptr_t>(value_cache);
+  if (emx::fp8_grid_fits(num_tokens, num_kv_heads, head_dim, rot_dims, traditional ? 1 : 0) && !(in16 & 15) &&
+      !(out8 & 7)) {
+    const long tasks = (long)emx::fp8_one_ktasks(num_tokens, num_kv_heads, head_dim, rot_dims, traditional ? 1 : 0) +
+                       (long)num_tokens * num_kv_heads * (head_dim / 8);
+    a.nwg = (int)((tasks + 255) / 256);
+    const dim3 g((unsigned)(a.nwg + (queries ? num_tokens : 0)));  // + one workgroup per query token
+    switch (dtype) {
+      case EMX_DTYPE_F16: hipLaunchKernelGGL(emx::fp8_append_grid<emx::F16>, g, dim3(256), 0, st, a); break;
+      case EMX_DTYPE_BF16: hipLaunchKernelGGL(emx::fp8_append_grid<emx::BF16>, g, dim3(256), 0, st, a); break;
+      default: hipLaunchKernelGGL(emx::fp8_append_grid<emx::F32>, g, dim3(256), 0, st, a); break;
+    }
+    return check_launch("fp8_append_grid");
+  }
+  if (launch_fp8_one(a, dtype, queries != nullptr, st)) return check_launch("fp8_write_one (append)");
   a.nwg = (int)((n / 4 + 1023) / 1024);
   const dim3 g1((unsigned)(a.nwg + (queries ? 4 : 0)));  // + workgroups that turn the queries
-  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   switch (dtype) {
     case EMX_DTYPE_F16: hipLaunchKernelGGL((emx::fp8_write<emx::F16, true>), g1, dim3(1024), 0, st, a, 0); break;
     case EMX_DTYPE_BF16: hipLaunchKernelGGL((emx::fp8_write<emx::BF16, true>), g1, dim3(1024), 0, st, a, 0); break;

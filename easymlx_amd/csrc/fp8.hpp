@@ -179,6 +179,15 @@ __global__ __launch_bounds__(SELF ? 1024 : 256) void fp8_write(Fp8WriteArgs a, i
   // its end, so no workgroup reads an advanced length.
   const bool app = SELF && a.slot_ids != nullptr;
   int arrived = 0;
+  // workgroups past a.nwg turn the queries: 16-byte pieces, loads sent before the
+  // positions are derived
+  constexpr int QU = 2;
+  const bool qwg = SELF && (int)blockIdx.x >= a.nwg;
+  const bool qvec = qwg && turn_rows_vec_ok(a.D, a.rope.rot, a.rope.traditional);
+  TurnRowsVec<QU> tv(a.T, a.Hq, a.D, a.rope);
+  const int qstride = (int)(gridDim.x - a.nwg) * NTH;
+  const int qfirst = (int)(blockIdx.x - a.nwg) * NTH + threadIdx.x;
+  if (qvec) tv.issue(a.q_in, a.D, a.rope, qfirst, qstride);
   if constexpr (SELF) {
     __shared__ int fslot[kFp8AppendMax], fpos[kFp8AppendMax], fseq[kFp8AppendMax];
     if (app) {
@@ -231,7 +240,7 @@ __global__ __launch_bounds__(SELF ? 1024 : 256) void fp8_write(Fp8WriteArgs a, i
     if (a.rope.inv_freq != nullptr && (int)blockIdx.x < a.nwg && a.T * half <= kFp8RopeTab) {
       for (int i = threadIdx.x; i < a.T * half; i += NTH) {
         float sn, cs;
-        sincosf((float)a.rope.positions[i / half] * a.rope.inv_freq[i % half], &sn, &cs);
+        rope_sincos((float)a.rope.positions[i / half] * a.rope.inv_freq[i % half], &sn, &cs);
         rsc[i] = float2{sn, cs};
       }
       __syncthreads();
@@ -239,9 +248,16 @@ __global__ __launch_bounds__(SELF ? 1024 : 256) void fp8_write(Fp8WriteArgs a, i
     }
   }
   if constexpr (SELF) {
-    if ((int)blockIdx.x >= a.nwg) {  // the query rotation rides in the same launch
-      turn_rows(a.q, a.q_in, a.T, a.Hq, a.D, a.rope, (long)(blockIdx.x - a.nwg) * NTH + threadIdx.x,
-                (long)(gridDim.x - a.nwg) * NTH);
+    if (qwg) {  // the query rotation rides in the same launch
+      if (qvec) {
+        tv.finish(a.q, a.Hq, a.D, a.rope);
+        for (int i0 = qfirst + QU * qstride; i0 < tv.n; i0 += QU * qstride) {
+          tv.issue(a.q_in, a.D, a.rope, i0, qstride);
+          tv.finish(a.q, a.Hq, a.D, a.rope);
+        }
+      } else {
+        turn_rows(a.q, a.q_in, a.T, a.Hq, a.D, a.rope, (long)qfirst, (long)qstride);
+      }
       finish();
       return;
     }
@@ -351,6 +367,547 @@ __global__ __launch_bounds__(SELF ? 1024 : 256) void fp8_write(Fp8WriteArgs a, i
     }
   }
   finish();
+}
+
+
+// ---- One-launch write of a small call (decode appends, small writes), in
+// workgroups of 1024 threads.  Each of the a.nwg write workgroups loads every
+// value of the call into registers -- K in the row tasks of TurnRowsVec (a piece
+// of 8 values and, where the rotation pairs it with the piece half a rotation
+// on, that piece too), V in pieces of 8 -- plus its own share of the tasks to
+// encode, all in one round trip that goes out before the slots and positions
+// are known.  It derives slots and positions into LDS, builds the (sin, cos)
+// table of the call's (token, pair) angles, turns K from it and takes both
+// maxima in one block reduction (the call's single scale pair, the same in
+// every workgroup: a maximum is exact), then encodes and stores 8 codes per
+// piece of its share (spreading the encoder's work over workgroups; one
+// workgroup encoding a 32-sequence append took ~30 us).  Workgroups a.nwg..
+// turn the queries from their own copy of the table.  The bits are fp8_write's:
+// the same turned values (rope_rotate_sc on rope_sincos of the same angles,
+// rounded to the input dtype), maxima over the same live values, the same
+// encoder.  Fits when D % 8 == 0, the RoPE (if any) meets turn_rows_vec_ok,
+// T * rot / 2 <= kFp8RopeTab, and the tasks fit the registers (fp8_one_fits;
+// BIG: twice the tasks per thread).
+template <typename T>
+struct Fp8Piece {  // 8 values of T, raw
+  u32x4 w[sizeof(T) / 2];
+  __device__ __forceinline__ void load(const T* p) {
+#pragma unroll
+    for (int i = 0; i < (int)(sizeof(T) / 2); ++i) w[i] = reinterpret_cast<const u32x4*>(p)[i];
+  }
+  __device__ __forceinline__ float at(const int j) const {
+    if constexpr (sizeof(T) == 4) {
+      return __uint_as_float(w[j / 4][j % 4]);
+    } else {
+      const uint16_t b = (uint16_t)(w[0][j / 2] >> (16 * (j & 1)));
+      if constexpr (__is_same(T, h16))
+        return (float)__builtin_bit_cast(h16, b);
+      else
+        return bf16_to_f32(b);
+    }
+  }
+};
+
+template <typename T, bool BIG>
+struct Fp8OneCfg {
+  static constexpr int NTH = 1024;
+  static constexpr int UK = (sizeof(T) == 4 ? 1 : 2) * (BIG ? 2 : 1);  // K tasks per thread
+  static constexpr int UV = 2 * UK;                  // V pieces per thread
+  static constexpr int UE = BIG ? 2 : 1;             // tasks each thread encodes
+  static constexpr int UQ = 2;                       // query tasks per thread and pass
+  static constexpr int UTAB = kFp8RopeTab / NTH;     // table entries per thread
+};
+
+__host__ __device__ inline int fp8_one_ktasks(const int T, const int Hkv, const int D, const int rot, const int trad) {
+  const int nrot = rot <= 0 ? 0 : (trad ? rot / 8 : rot / 16);
+  return T * Hkv * (nrot + (D - (rot > 0 ? rot : 0)) / 8);
+}
+
+template <typename T, bool BIG>
+__host__ __device__ inline bool fp8_one_fits(const int nT, const int Hkv, const int D, const int rot, const int trad) {
+  typedef Fp8OneCfg<T, BIG> C;
+  if (nT > kFp8AppendMax || D % 8 != 0) return false;
+  if (rot > 0 && (!turn_rows_vec_ok(D, rot, trad) || nT * (rot / 2) > kFp8RopeTab)) return false;
+  return fp8_one_ktasks(nT, Hkv, D, rot, trad) <= C::UK * C::NTH && nT * Hkv * (D / 8) <= C::UV * C::NTH;
+}
+
+template <typename Tag, bool BIG>
+__global__ __launch_bounds__(1024) void fp8_write_one(Fp8WriteArgs a) {
+  typedef typename Tag::T T;
+  typedef Fp8OneCfg<T, BIG> C;
+  constexpr int NTH = C::NTH, UK = C::UK, UV = C::UV, UE = C::UE, UQ = C::UQ, UTAB = C::UTAB;
+  const int tid = threadIdx.x;
+  const RopeArgs& r = a.rope;
+  const bool rope = r.inv_freq != nullptr;
+  const int rot = rope ? r.rot : 0, half = rot / 2;
+  const int nwg = a.nwg;
+  const bool qwg = (int)blockIdx.x >= nwg;  // workgroups a.nwg.. turn the queries
+  const bool app = a.slot_ids != nullptr;
+  const T* k = reinterpret_cast<const T*>(a.k);
+  const T* v = reinterpret_cast<const T*>(a.v);
+  const int nrot = rope ? (r.traditional ? rot / 8 : rot / 16) : 0;
+  const int per = nrot + (a.D - rot) / 8;  // K tasks per (token, head) row
+  const int nk = a.T * a.Hkv * per, nv = a.T * a.Hkv * (a.D / 8);
+
+  // ---- loads that depend on nothing: values (or queries), the table's inv_freq
+  Fp8Piece<T> klo[UK], khi[UK], vp[UV], elo[UE], ehi[UE];
+  TurnRowsVec<UQ> tq(a.T, a.Hq, a.D, r);
+  const int qstride = (int)(gridDim.x - nwg) * NTH, qfirst = (int)(blockIdx.x - nwg) * NTH + tid;
+  auto k_piece_off = [&](const int c) { return c < nrot ? 8 * c : rot + 8 * (c - nrot); };
+  if (qwg) {
+    tq.issue(a.q_in, a.D, r, qfirst, qstride);
+  } else {
+    // this thread's share of the codes (tasks j < nk: K, then V pieces)
+#pragma unroll
+    for (int e = 0; e < UE; ++e) {
+      const int j = (int)blockIdx.x * NTH + tid + e * nwg * NTH;
+      if (j < nk) {
+        const int rr = j / per, c = j % per;
+        const T* row = k + (size_t)rr * a.D;
+        elo[e].load(row + k_piece_off(c));
+        if (c < nrot && !r.traditional) ehi[e].load(row + half + 8 * c);
+      } else if (j < nk + nv) {
+        elo[e].load(v + 8 * (size_t)(j - nk));
+      }
+    }
+    // every value of the call, for the maxima
+#pragma unroll
+    for (int u = 0; u < UK; ++u) {
+      const int i = tid + u * NTH;
+      if (i < nk) {
+        const int rr = i / per, c = i % per;
+        const T* row = k + (size_t)rr * a.D;
+        klo[u].load(row + k_piece_off(c));
+        if (c < nrot && !r.traditional) khi[u].load(row + half + 8 * c);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < UV; ++u) {
+      const int i = tid + u * NTH;
+      if (i < nv) vp[u].load(v + 8 * (size_t)i);
+    }
+  }
+  float invr[UTAB];
+#pragma unroll
+  for (int u = 0; u < UTAB; ++u) {
+    const int i = tid + u * NTH;
+    invr[u] = rope && i < a.T * half ? r.inv_freq[i % half] : 0.f;
+  }
+
+  // ---- slots and positions (decode append: derived as cache_slots does) into LDS
+  __shared__ int fslot[kFp8AppendMax], fpos[kFp8AppendMax], fseq[kFp8AppendMax];
+  if (tid < a.T) {
+    int sl = -1, pos = 0, sq = -1;
+    if (app) {
+      const int s = a.slot_ids[tid];
+      if (s >= 0 && s < a.S) {
+        sq = s;
+        pos = a.kv_lens[s];
+        const int col = pos / a.bs;
+        if (pos >= 0 && col < a.max_blocks) {
+          const int b = a.bt[(size_t)s * a.max_blocks + col];
+          if (b >= 0) sl = b * a.bs + pos % a.bs;
+        }
+      }
+    } else {
+      sl = a.slot[tid];
+      pos = rope ? r.positions[tid] : 0;
+    }
+    fslot[tid] = sl >= 0 && sl / a.bs < a.nb ? sl : -1;  // a page outside the pool: skipped
+    fpos[tid] = pos;
+    fseq[tid] = sq;
+  }
+  __syncthreads();  // every kv_lens read of the workgroup has returned
+  int arrived = 0;
+  if (app && tid == 0) arrived = __hip_atomic_fetch_add(a.counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+  // ---- (sin, cos) of every (token, pair) angle
+  __shared__ float2 rsc[kFp8RopeTab];
+  if (rope) {
+#pragma unroll
+    for (int u = 0; u < UTAB; ++u) {
+      const int i = tid + u * NTH;
+      if (i < a.T * half) {
+        float sn, cs;
+        rope_sincos((float)fpos[i / half] * invr[u], &sn, &cs);
+        rsc[i] = float2{sn, cs};
+      }
+    }
+  }
+  __syncthreads();
+
+  auto finish = [&]() {  // the end of the workgroup: the last one counted advances kv_lens
+    if (!app) return;
+    __shared__ int slast;
+    if (tid == 0) {
+      slast = arrived == (int)gridDim.x - 1;
+      if (arrived == (int)gridDim.x - 1) __hip_atomic_store(a.counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (slast && tid < a.T && fseq[tid] >= 0) a.kv_lens[fseq[tid]] = fpos[tid] + 1;
+  };
+  if (qwg) {
+    tq.finish(a.q, a.Hq, a.D, r, rope ? rsc : nullptr);
+    for (int i0 = qfirst + UQ * qstride; i0 < tq.n; i0 += UQ * qstride) {
+      tq.issue(a.q_in, a.D, r, i0, qstride);
+      tq.finish(a.q, a.Hq, a.D, r, rope ? rsc : nullptr);
+    }
+    finish();
+    return;
+  }
+
+  // ---- K turned (rounded to T; turned again for the codes rather than held),
+  // maxima over the live tokens
+  auto turned = [&](const Fp8Piece<T>& lo, const Fp8Piece<T>& hi, const int c, const int t, float (&kx)[8],
+                    float (&ky)[8]) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      kx[j] = lo.at(j);
+      ky[j] = 0.f;
+    }
+    if (c >= nrot) return;
+    const float2* tt = rsc + t * half;
+    if (r.traditional) {
+#pragma unroll
+      for (int j = 0; j < 8; j += 2) {
+        float y0, y1;
+        rope_rotate_sc(kx[j], kx[j + 1], tt[4 * c + j / 2], y0, y1);
+        kx[j] = round_to(y0, (T*)nullptr);
+        kx[j + 1] = round_to(y1, (T*)nullptr);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        float y0, y1;
+        rope_rotate_sc(kx[j], hi.at(j), tt[8 * c + j], y0, y1);
+        kx[j] = round_to(y0, (T*)nullptr);
+        ky[j] = round_to(y1, (T*)nullptr);
+      }
+    }
+  };
+  float mk = 0.f, mv = 0.f;
+#pragma unroll
+  for (int u = 0; u < UK; ++u) {
+    const int i = tid + u * NTH;
+    if (i >= nk) continue;
+    const int rr = i / per, c = i % per, t = rr / a.Hkv;
+    if (fslot[t] < 0) continue;
+    float kx[8], ky[8];
+    turned(klo[u], khi[u], c, t, kx, ky);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) mk = fmaxf(mk, fmaxf(fabsf(kx[j]), fabsf(ky[j])));
+  }
+#pragma unroll
+  for (int u = 0; u < UV; ++u) {
+    const int i = tid + u * NTH;
+    if (i < nv && fslot[i / (a.Hkv * (a.D / 8))] >= 0) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) mv = fmaxf(mv, fabsf(vp[u].at(j)));
+    }
+  }
+  mk = wave_max(mk);
+  mv = wave_max(mv);
+  __shared__ float sm[2][NTH / 64];
+  if ((tid & 63) == 0) {
+    sm[0][tid >> 6] = mk;
+    sm[1][tid >> 6] = mv;
+  }
+  __syncthreads();
+  float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+  for (int i = 0; i < NTH / 64; ++i) {
+    a0 = fmaxf(a0, sm[0][i]);
+    a1 = fmaxf(a1, sm[1][i]);
+  }
+  const float ksc = a0 / 240.0f, vsc = a1 / 240.0f;
+  const float kq = fmaxf(ksc, 1e-12f), vq = fmaxf(vsc, 1e-12f);
+
+  // ---- codes: 8 bytes per piece, [nb, bs, Hkv, D]
+  auto row_of = [&](const int rr, const int sl) {  // byte offset of (token row rr, its slot) in the pages
+    return ((size_t)sl * a.Hkv + rr % a.Hkv) * (size_t)a.D;
+  };
+  auto enc8 = [](const float (&x)[8], const float q) {
+    uint32_t lo = 0, hi = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      lo |= f32_to_e4m3(x[j] / q) << (8 * j);
+      hi |= f32_to_e4m3(x[j + 4] / q) << (8 * j);
+    }
+    return uint2{lo, hi};
+  };
+#pragma unroll
+  for (int e = 0; e < UE; ++e) {
+    const int j = (int)blockIdx.x * NTH + tid + e * nwg * NTH;
+    if (j < nk) {
+      const int rr = j / per, c = j % per, t = rr / a.Hkv;
+      const int sl = fslot[t];
+      if (sl < 0) continue;
+      float kx[8], ky[8];
+      turned(elo[e], ehi[e], c, t, kx, ky);
+      uint8_t* dst = a.kc + row_of(rr, sl);
+      *reinterpret_cast<uint2*>(dst + k_piece_off(c)) = enc8(kx, kq);
+      if (c < nrot && !r.traditional) *reinterpret_cast<uint2*>(dst + half + 8 * c) = enc8(ky, kq);
+      if (c == 0 && rr % a.Hkv == 0) {  // once per written token: the page keeps the larger scale
+        atomicMax(reinterpret_cast<unsigned int*>(a.ks) + sl / a.bs, __float_as_uint(ksc));
+        atomicMax(reinterpret_cast<unsigned int*>(a.vs) + sl / a.bs, __float_as_uint(vsc));
+      }
+    } else if (j < nk + nv) {
+      const int i = j - nk;
+      const int rr = i / (a.D / 8), c = i % (a.D / 8), t = rr / a.Hkv;
+      const int sl = fslot[t];
+      if (sl < 0) continue;
+      float x[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) x[q] = elo[e].at(q);
+      *reinterpret_cast<uint2*>(a.vc + row_of(rr, sl) + 8 * c) = enc8(x, vq);
+    }
+  }
+  finish();
+}
+
+
+// ---- Decode append by a grid that waits on itself once (fp8_append_grid).
+// The call's single scale pair needs the maxima of every value before any code
+// is written.  Workgroups of 256 threads each take 256 tasks of the call (K row
+// tasks as in fp8_write_one, then V pieces of 8), load them with the slots and
+// positions of every token, turn their K from a (sin, cos) table of their own
+// tokens, and reduce their maxima; thread 0 folds them into the call's maxima
+// (atomicMax on the bits of non-negative floats, counter[2] and [3]), counts the
+// workgroup on counter[1], and waits until all a.nwg write workgroups have
+// counted.  Then every workgroup encodes its own tasks with the call's scales.
+// The workgroups (at most kFp8GridMaxWG, each small) are all resident at once on
+// an otherwise busy GPU, so the wait ends; it is bounded all the same.  Workgroups
+// a.nwg.. turn the queries, one token each.  counter[0] counts every workgroup
+// at its end; the last one clears counter[0..3] and advances kv_lens, so the
+// four ints are zero between calls.  Same bits as fp8_write: the same turned
+// values, the same maxima (a maximum is exact in any order) and encoder.
+constexpr int kFp8GridMaxWG = 128;
+constexpr int kFp8GridTab = 4096;
+
+__host__ __device__ inline bool fp8_grid_fits(const int T, const int Hkv, const int D, const int rot,
+                                              const int trad) {
+  if (T <= 0 || T > kFp8AppendMax || D % 8 != 0 || D > 256 || rot <= 0 || !turn_rows_vec_ok(D, rot, trad))
+    return false;
+  const long tasks = (long)fp8_one_ktasks(T, Hkv, D, rot, trad) + (long)T * Hkv * (D / 8);
+  return (tasks + 255) / 256 <= kFp8GridMaxWG;
+}
+
+template <typename Tag>
+__global__ __launch_bounds__(256) void fp8_append_grid(Fp8WriteArgs a) {
+  typedef typename Tag::T T;
+  constexpr int NTH = 256, KT = kFp8AppendMax / NTH;
+  const int tid = threadIdx.x;
+  const int nwg = a.nwg;
+  const bool qwg = (int)blockIdx.x >= nwg;
+  const RopeArgs& r = a.rope;
+  const int rot = r.rot, half = rot / 2, trad = r.traditional;
+  const int nrot = trad ? rot / 8 : rot / 16;
+  const int per = nrot + (a.D - rot) / 8;  // K tasks per (token, head) row
+  const int nk = a.T * a.Hkv * per, nv = a.T * a.Hkv * (a.D / 8);
+  const T* k = reinterpret_cast<const T*>(a.k);
+  const T* v = reinterpret_cast<const T*>(a.v);
+  int* const cnt = a.counter;
+
+  // ---- loads that depend on nothing: this thread's task, or a query token's rows
+  const int j0 = (int)blockIdx.x * NTH, j = j0 + tid;
+  Fp8Piece<T> lo, hi;
+  auto k_piece_off = [&](const int c) { return c < nrot ? 8 * c : rot + 8 * (c - nrot); };
+  const int tq = (int)blockIdx.x - nwg;  // query workgroup: its token
+  TurnRowsVec<2> tv(1, a.Hq, a.D, r);
+  if (qwg) {
+    tv.issue(a.q_in + (size_t)tq * a.Hq * a.D, a.D, r, tid, NTH);
+  } else if (j < nk) {
+    const int rr = j / per, c = j % per;
+    const T* row = k + (size_t)rr * a.D;
+    lo.load(row + k_piece_off(c));
+    if (c < nrot && !trad) hi.load(row + half + 8 * c);
+  } else if (j < nk + nv) {
+    lo.load(v + 8 * (size_t)(j - nk));
+  }
+  const float inv_in = tid < half ? r.inv_freq[tid] : 0.f;  // half <= 128
+  // slots and positions of every token (as cache_slots derives them)
+  int sl[KT], pos[KT], sq[KT];
+#pragma unroll
+  for (int u = 0; u < KT; ++u) {
+    const int t = tid + u * NTH;
+    sl[u] = -1;
+    pos[u] = 0;
+    sq[u] = -1;
+    if (t < a.T) {
+      const int s = a.slot_ids[t];
+      if (s >= 0 && s < a.S) {
+        sq[u] = s;
+        pos[u] = a.kv_lens[s];
+        const int col = pos[u] / a.bs;
+        if (pos[u] >= 0 && col < a.max_blocks) {
+          const int b = a.bt[(size_t)s * a.max_blocks + col];
+          if (b >= 0) sl[u] = b * a.bs + pos[u] % a.bs;
+        }
+      }
+    }
+  }
+  __shared__ int fslot[kFp8AppendMax], fpos[kFp8AppendMax], fseq[kFp8AppendMax];
+  __shared__ float sinv[128];
+  __shared__ float2 stab[kFp8GridTab];
+  __shared__ unsigned int sred[2][NTH / 64];
+  __shared__ int sflag;
+#pragma unroll
+  for (int u = 0; u < KT; ++u) {
+    const int t = tid + u * NTH;
+    if (t < a.T) {
+      fslot[t] = sl[u] >= 0 && sl[u] / a.bs < a.nb ? sl[u] : -1;  // a page outside the pool: skipped
+      fpos[t] = pos[u];
+      fseq[t] = sq[u];
+    }
+  }
+  if (tid < half) sinv[tid] = inv_in;
+  __syncthreads();
+
+  // ---- the (sin, cos) table of this workgroup's tokens [t_lo, t_hi]
+  int t_lo = tq, t_hi = tq;
+  if (!qwg) {
+    const int k_end = min(j0 + NTH, nk);
+    t_lo = j0 < nk ? (j0 / per) / a.Hkv : 0;
+    t_hi = j0 < nk ? ((k_end - 1) / per) / a.Hkv : -1;
+  }
+  const int ntab = (t_hi - t_lo + 1) * half;  // <= kFp8GridTab (fp8_grid_fits)
+  for (int i = tid; i < ntab; i += NTH) {
+    float sn, cs;
+    rope_sincos((float)fpos[t_lo + i / half] * sinv[i % half], &sn, &cs);
+    stab[i] = float2{sn, cs};
+  }
+  __syncthreads();
+
+  auto count_and_finish = [&]() {  // every workgroup at its end, once
+    if (tid == 0) {
+      const int arrived = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+      sflag = arrived == (int)gridDim.x - 1;
+      if (sflag) {  // every workgroup has read the maxima and kv_lens: clear for the next call
+        __hip_atomic_store(cnt + 1, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(cnt + 2, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(cnt + 3, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+    __syncthreads();
+    if (sflag)
+      for (int t = tid; t < a.T; t += NTH)
+        if (fseq[t] >= 0) a.kv_lens[fseq[t]] = fpos[t] + 1;
+  };
+  if (qwg) {
+    h16* qo = a.q + (size_t)tq * a.Hq * a.D;
+    const h16* qi = a.q_in + (size_t)tq * a.Hq * a.D;
+    tv.finish(qo, a.Hq, a.D, r, stab);
+    for (int i0 = tid + 2 * NTH; i0 < tv.n; i0 += 2 * NTH) {
+      tv.issue(qi, a.D, r, i0, NTH);
+      tv.finish(qo, a.Hq, a.D, r, stab);
+    }
+    count_and_finish();
+    return;
+  }
+
+  // ---- this task's values (K turned and rounded to T), the workgroup's maxima
+  float x[8], y[8];
+  int kind = 0, rr = 0, c = 0, t = 0;  // kind 1: K task, 2: V piece
+  if (j < nk) {
+    kind = 1;
+    rr = j / per;
+    c = j % per;
+    t = rr / a.Hkv;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      x[q] = lo.at(q);
+      y[q] = 0.f;
+    }
+    if (c < nrot) {
+      const float2* tt = stab + (t - t_lo) * half;
+      if (trad) {
+#pragma unroll
+        for (int q = 0; q < 8; q += 2) {
+          float y0, y1;
+          rope_rotate_sc(x[q], x[q + 1], tt[4 * c + q / 2], y0, y1);
+          x[q] = round_to(y0, (T*)nullptr);
+          x[q + 1] = round_to(y1, (T*)nullptr);
+        }
+      } else {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          float y0, y1;
+          rope_rotate_sc(x[q], hi.at(q), tt[8 * c + q], y0, y1);
+          x[q] = round_to(y0, (T*)nullptr);
+          y[q] = round_to(y1, (T*)nullptr);
+        }
+      }
+    }
+  } else if (j < nk + nv) {
+    kind = 2;
+    rr = (j - nk) / (a.D / 8);
+    c = (j - nk) % (a.D / 8);
+    t = rr / a.Hkv;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      x[q] = lo.at(q);
+      y[q] = 0.f;
+    }
+  }
+  const int slot = kind ? fslot[t] : -1;
+  float m = 0.f;
+  if (slot >= 0) {
+#pragma unroll
+    for (int q = 0; q < 8; ++q) m = fmaxf(m, fmaxf(fabsf(x[q]), fabsf(y[q])));
+  }
+  float mk = wave_max(kind == 1 ? m : 0.f), mv = wave_max(kind == 2 ? m : 0.f);
+  if ((tid & 63) == 0) {
+    sred[0][tid >> 6] = __float_as_uint(mk);
+    sred[1][tid >> 6] = __float_as_uint(mv);
+  }
+  __syncthreads();
+  // ---- the call's maxima: fold, count, wait for every write workgroup (bounded)
+  if (tid == 0) {
+    unsigned int bk = 0u, bv = 0u;
+#pragma unroll
+    for (int w = 0; w < NTH / 64; ++w) {
+      bk = max(bk, sred[0][w]);
+      bv = max(bv, sred[1][w]);
+    }
+    __hip_atomic_fetch_max(reinterpret_cast<unsigned int*>(cnt + 2), bk, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_fetch_max(reinterpret_cast<unsigned int*>(cnt + 3), bv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_fetch_add(cnt + 1, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+    for (int it = 0; it < (1 << 22); ++it) {
+      if (__hip_atomic_load(cnt + 1, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) >= nwg) break;
+      __builtin_amdgcn_s_sleep(1);
+    }
+    sred[0][0] = __hip_atomic_load(reinterpret_cast<unsigned int*>(cnt + 2), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    sred[1][0] = __hip_atomic_load(reinterpret_cast<unsigned int*>(cnt + 3), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  const float ksc = __uint_as_float(sred[0][0]) / 240.0f, vsc = __uint_as_float(sred[1][0]) / 240.0f;
+  const float kq = fmaxf(ksc, 1e-12f), vq = fmaxf(vsc, 1e-12f);
+
+  // ---- codes: 8 bytes per piece, [nb, bs, Hkv, D]
+  if (slot >= 0) {
+    auto enc8 = [](const float (&z)[8], const float qd) {
+      uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        w0 |= f32_to_e4m3(z[q] / qd) << (8 * q);
+        w1 |= f32_to_e4m3(z[q + 4] / qd) << (8 * q);
+      }
+      return uint2{w0, w1};
+    };
+    const size_t rowb = ((size_t)slot * a.Hkv + rr % a.Hkv) * (size_t)a.D;
+    if (kind == 1) {
+      *reinterpret_cast<uint2*>(a.kc + rowb + k_piece_off(c)) = enc8(x, kq);
+      if (c < nrot && !trad) *reinterpret_cast<uint2*>(a.kc + rowb + half + 8 * c) = enc8(y, kq);
+      if (c == 0 && rr % a.Hkv == 0) {  // once per written token: the page keeps the larger scale
+        atomicMax(reinterpret_cast<unsigned int*>(a.ks) + slot / a.bs, __float_as_uint(ksc));
+        atomicMax(reinterpret_cast<unsigned int*>(a.vs) + slot / a.bs, __float_as_uint(vsc));
+      }
+    } else {
+      *reinterpret_cast<uint2*>(a.vc + rowb + 8 * c) = enc8(x, vq);
+    }
+  }
+  count_and_finish();
 }
 
 }  // namespace emx

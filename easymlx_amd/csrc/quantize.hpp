@@ -134,12 +134,92 @@ __device__ __forceinline__ void turn_rows(h16* x, const h16* src, const int rows
   }
 }
 
-// (x0, x1) turned by the angle whose sine and cosine are given: rope_rotate's
-// arithmetic on a precomputed sincosf, so both give the same bits.
-__device__ __forceinline__ void rope_rotate_sc(const float x0, const float x1, const float2 sc, float& y0, float& y1) {
-  y0 = __fsub_rn(__fmul_rn(x0, sc.y), __fmul_rn(x1, sc.x));
-  y1 = __fadd_rn(__fmul_rn(x0, sc.x), __fmul_rn(x1, sc.y));
+// turn_rows in 16-byte pieces, out of place (every dim of a row written): a task
+// is one piece of 4 adjacent pairs (traditional), 8 pairs of a piece and its
+// partner piece half a rotation on (neox order), or a piece past r.rot that is
+// copied.  rope_pair on each pair, so the bits are turn_rows'.  Applies when
+// D % 8 == 0 and r.rot is a multiple of 8 (traditional) or 16 (neox); the
+// caller checks (turn_rows_vec_ok).  The loads of a pass of U tasks per thread
+// go out together: issue() then finish(), with the positions needed only in
+// finish() (a caller may wait for them in between).
+__host__ __device__ inline bool turn_rows_vec_ok(const int D, const int rot, const int traditional) {
+  return D % 8 == 0 && rot % (traditional ? 8 : 16) == 0;
 }
+
+template <int U>
+struct TurnRowsVec {
+  h16x8 lo[U], hi[U];
+  int rh[U], c[U];
+  int nrot, per, n;
+
+  __device__ __forceinline__ TurnRowsVec(const int rows, const int heads, const int D, const RopeArgs& r) {
+    nrot = r.traditional ? r.rot / 8 : r.rot / 16;
+    per = nrot + (D - r.rot) / 8;
+    n = rows * heads * per;
+  }
+  __device__ __forceinline__ void issue(const h16* src, const int D, const RopeArgs& r, const int i0, const int stride) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int i = i0 + u * stride;
+      rh[u] = i < n ? i / per : -1;
+      c[u] = i < n ? i % per : 0;
+      if (rh[u] >= 0) {
+        const h16* row = src + (size_t)rh[u] * D;
+        const int off = c[u] < nrot ? 8 * c[u] : r.rot + 8 * (c[u] - nrot);
+        lo[u] = *reinterpret_cast<const h16x8*>(row + off);
+        if (c[u] < nrot && !r.traditional) hi[u] = *reinterpret_cast<const h16x8*>(row + r.rot / 2 + off);
+      }
+    }
+  }
+  // tab: null, or (sin, cos) of positions[t] * inv_freq[p] at t * (r.rot / 2) + p
+  // (rope_rotate_sc on it gives rope_pair's bits)
+  __device__ __forceinline__ void finish(h16* x, const int heads, const int D, const RopeArgs& r,
+                                         const float2* tab = nullptr) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (rh[u] < 0) continue;
+      h16* row = x + (size_t)rh[u] * D;
+      if (c[u] >= nrot) {
+        *reinterpret_cast<h16x8*>(row + r.rot + 8 * (c[u] - nrot)) = lo[u];
+        continue;
+      }
+      const int t = rh[u] / heads;
+      const float pos = tab ? 0.f : (float)r.positions[t];
+      const float2* tt = tab ? tab + (size_t)t * (r.rot / 2) : nullptr;
+      auto turn = [&](h16& a0, h16& a1, const int p) {
+        if (tab) {
+          float y0, y1;
+          rope_rotate_sc((float)a0, (float)a1, tt[p], y0, y1);
+          a0 = (h16)y0;
+          a1 = (h16)y1;
+        } else {
+          rope_pair(a0, a1, pos * r.inv_freq[p]);
+        }
+      };
+      if (r.traditional) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          h16 a0 = lo[u][2 * k], a1 = lo[u][2 * k + 1];
+          turn(a0, a1, 4 * c[u] + k);
+          lo[u][2 * k] = a0;
+          lo[u][2 * k + 1] = a1;
+        }
+        *reinterpret_cast<h16x8*>(row + 8 * c[u]) = lo[u];
+      } else {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          h16 a0 = lo[u][k], a1 = hi[u][k];
+          turn(a0, a1, 8 * c[u] + k);
+          lo[u][k] = a0;
+          hi[u][k] = a1;
+        }
+        *reinterpret_cast<h16x8*>(row + 8 * c[u]) = lo[u];
+        *reinterpret_cast<h16x8*>(row + r.rot / 2 + 8 * c[u]) = hi[u];
+      }
+    }
+  }
+};
+
 
 __global__ __launch_bounds__(256) void rope_rows(h16* x, const h16* src, int rows, int heads, int D, RopeArgs r) {
   turn_rows(x, src, rows, heads, D, r, (long)blockIdx.x * 256 + threadIdx.x, (long)gridDim.x * 256);
@@ -168,7 +248,8 @@ struct WriteArgs {
   int* counter;                // workgroups that have read kv_lens: zero before and after every launch
 };
 
-constexpr int kQRopeBlocks = 4;  // extra workgroup rows of the small write that turn the queries
+constexpr int kQRopeBlocks = 4;     // extra workgroup rows of the small write that turn the queries
+constexpr int kSmallRopeTab = 2048;  // (token, pair) angles the query workgroups tabulate
 
 // One workgroup per (32 consecutive tokens, kv head):
 //   1. per (token, group, K|V): min/max -> scale/bias (kept in LDS, stored as fp16);
@@ -339,6 +420,12 @@ __global__ __launch_bounds__(256) void affine_cache_write_small(WriteArgs a) {
   __shared__ int sseq[kSmallWrite];
   int sl_dev = -1, app_s = -1, app_pos = 0;
   RopeArgs rope = a.rope;
+  // with ROPE, the positions (when given) and inv_freq go to LDS with the first
+  // barrier: the rotation loops then read no global memory
+  __shared__ float sinv[kWriteMaxDim / 2];
+  const int half = ROPE ? rope.rot / 2 : 0;
+  const float inv_in = ROPE && tid < half ? rope.inv_freq[tid] : 0.f;
+  if (ROPE && !app && tid < a.T) app_pos = rope.positions[tid];
   if (app) {
     if (tid < a.T) {
       const int s = a.slot_ids[tid];
@@ -352,14 +439,18 @@ __global__ __launch_bounds__(256) void affine_cache_write_small(WriteArgs a) {
         }
       }
     }
+  }
+  if (ROPE) {
     rope.positions = spos;
+    rope.inv_freq = sinv;
   }
   int arrived = 0;
   auto publish = [&]() {  // before a barrier: this workgroup's positions and sequences to LDS
-    if (app && tid < a.T) {
+    if ((app || ROPE) && tid < a.T) {
       spos[tid] = app_pos;
       sseq[tid] = app_s;
     }
+    if (ROPE && tid < half) sinv[tid] = inv_in;
   };
   auto count = [&]() {  // after that barrier: every kv_lens read of the workgroup has returned
     if (app && tid == 0) arrived = __hip_atomic_fetch_add(a.counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -375,22 +466,45 @@ __global__ __launch_bounds__(256) void affine_cache_write_small(WriteArgs a) {
     __syncthreads();
     if (slast && tid < a.T && sseq[tid] >= 0) a.kv_lens[sseq[tid]] = spos[tid] + 1;
   };
+  const int T = a.T;
   if constexpr (ROPE) {
     // the extra rows of workgroups turn the queries (rows of gridDim.x * kQRopeBlocks workgroups)
     if (d0 >= a.D) {
+      const int nwg = gridDim.x * kQRopeBlocks;
+      const int wg = (blockIdx.y - a.D / DB) * gridDim.x + blockIdx.x;
+      // 16-byte pieces, the first pass's loads in flight while the positions arrive
+      const bool vec = a.q != nullptr && turn_rows_vec_ok(a.D, rope.rot, rope.traditional);
+      constexpr int U = 2;
+      TurnRowsVec<U> tv(a.T, a.Hq, a.D, rope);
+      const int stride = nwg * 256;
+      if (vec) tv.issue(a.q_in, a.D, rope, wg * 256 + tid, stride);
       publish();
-      if (app) __syncthreads();
+      __syncthreads();
       count();
-      if (a.q != nullptr) {
-        const int nwg = gridDim.x * kQRopeBlocks;
-        const int wg = (blockIdx.y - a.D / DB) * gridDim.x + blockIdx.x;
-        turn_rows(a.q, a.q_in, a.T, a.Hq, a.D, rope, (long)wg * 256 + tid, (long)nwg * 256);
+      // (sin, cos) of the call's (token, pair) angles once per workgroup, when they fit
+      __shared__ float2 stab[kSmallRopeTab];
+      const bool tab = vec && T * half <= kSmallRopeTab;
+      if (tab) {
+        for (int i = tid; i < T * half; i += 256) {
+          float sn, cs;
+          rope_sincos((float)spos[i / half] * sinv[i % half], &sn, &cs);
+          stab[i] = float2{sn, cs};
+        }
+        __syncthreads();
+      }
+      if (vec) {
+        tv.finish(a.q, a.Hq, a.D, rope, tab ? stab : nullptr);
+        for (int i0 = wg * 256 + tid + U * stride; i0 < tv.n; i0 += U * stride) {
+          tv.issue(a.q_in, a.D, rope, i0, stride);
+          tv.finish(a.q, a.Hq, a.D, rope, tab ? stab : nullptr);
+        }
+      } else if (a.q != nullptr) {
+        turn_rows(a.q, a.q_in, a.T, a.Hq, a.D, rope, (long)wg * 256 + tid, (long)stride);
       }
       finish();
       return;
     }
   }
-  const int T = a.T;
   const int G = a.D / a.gs;
   const float n_bins = (float)((1 << BITS) - 1);
   __shared__ float sp[2][kSmallWrite][2];  // [K|V][token] -> (scale, bias) of this block's group
@@ -414,26 +528,36 @@ __global__ __launch_bounds__(256) void affine_cache_write_small(WriteArgs a) {
   u32x4 piece[kPieces];
   if constexpr (ROPE) {
     __shared__ __attribute__((aligned(16))) h16 krow[kSmallWrite][kWriteMaxDim];
-    for (int i = tid; i < T * (a.D / 8); i += 256) {
-      const int t = i / (a.D / 8), c = i % (a.D / 8);
-      *reinterpret_cast<u32x4*>(&krow[t][8 * c]) =
-          *reinterpret_cast<const u32x4*>(a.keys + ((size_t)t * a.Hkv + h) * a.D + 8 * c);
-    }
 #pragma unroll
     for (int k = 0; k < kPieces / 2; ++k) {  // V only: K comes from the turned rows
       const int i = tid + 256 * k;
       piece[k] = __builtin_amdgcn_raw_buffer_load_b128(rval, i < T * per_tok ? goff(i / per_tok, i % per_tok) : kOob,
                                                        0, kLoadAux);
     }
+    // the head's K rows, four 16-byte pieces per thread in flight at a time
+    for (int i0 = tid; i0 < T * (a.D / 8); i0 += 4 * 256) {
+      u32x4 kp[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int i = i0 + 256 * u;
+        const int t = i / (a.D / 8), c = i % (a.D / 8);
+        kp[u] = __builtin_amdgcn_raw_buffer_load_b128(rkey, i < T * (a.D / 8) ? ((t * a.Hkv + h) * a.D + 8 * c) * 2 : kOob,
+                                                      0, kLoadAux);
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int i = i0 + 256 * u;
+        if (i < T * (a.D / 8)) *reinterpret_cast<u32x4*>(&krow[i / (a.D / 8)][8 * (i % (a.D / 8))]) = kp[u];
+      }
+    }
     publish();
     __syncthreads();
     count();
-    const RopeArgs& r = rope;  // positions: the device-derived ones in a decode append
-    const int half = r.rot / 2;
+    const RopeArgs& r = rope;  // positions and inv_freq in LDS
     for (int task = tid; task < T * half; task += 256) {
       const int t = task / half, p = task % half;
       const int i0 = r.traditional ? 2 * p : p, i1 = r.traditional ? 2 * p + 1 : p + half;
-      rope_pair(krow[t][i0], krow[t][i1], (float)r.positions[t] * r.inv_freq[p]);
+      rope_pair(krow[t][i0], krow[t][i1], (float)spos[t] * sinv[p]);
     }
     __syncthreads();
     for (int i = tid; i < T * per_tok; i += 256) {
@@ -469,7 +593,7 @@ __global__ __launch_bounds__(256) void affine_cache_write_small(WriteArgs a) {
   __syncthreads();
   if constexpr (!ROPE) count();
   constexpr int kVTasks = kSmallWrite * DB / 256;
-  // scale / bias (the first dim block of each group stores them)
+  // scale / bias of each (K|V, token) of this block's group, into LDS
   for (int task = tid; task < 2 * T; task += 256) {
     const int kv = task / T, t = task % T;
     const int sl = sslot[t];
@@ -479,14 +603,20 @@ __global__ __launch_bounds__(256) void affine_cache_write_small(WriteArgs a) {
     affine_params(wmin, wmax, n_bins, scale, bias);
     sp[kv][t][0] = scale;
     sp[kv][t][1] = bias;
-    if (d0 % a.gs == 0) {
-      const size_t ph = (size_t)(sl / a.bs) * a.Hkv + h;
-      const size_t si = (ph * G + g) * a.bs + sl % a.bs;
-      (kv ? a.vs : a.ks)[si] = (h16)scale;
-      (kv ? a.vb : a.kb)[si] = (h16)bias;
-    }
   }
   __syncthreads();
+  // (stored after the barrier: a barrier waits for the stores issued before it)
+  if (d0 % a.gs == 0) {  // the first dim block of each group stores them
+    for (int task = tid; task < 2 * T; task += 256) {
+      const int kv = task / T, t = task % T;
+      const int sl = sslot[t];
+      if (sl < 0) continue;
+      const size_t ph = (size_t)(sl / a.bs) * a.Hkv + h;
+      const size_t si = (ph * G + g) * a.bs + sl % a.bs;
+      (kv ? a.vs : a.ks)[si] = (h16)sp[kv][t][0];
+      (kv ? a.vb : a.kb)[si] = (h16)sp[kv][t][1];
+    }
+  }
   // K words of this block: DB / PW per token
   for (int task = tid; task < T * (DB / PW); task += 256) {
     const int t = task / (DB / PW), w = d0 / PW + task % (DB / PW);
@@ -524,5 +654,238 @@ __global__ __launch_bounds__(256) void affine_cache_write_small(WriteArgs a) {
 }
 
 #pragma clang fp contract(on)
+
+
+// ---- Fused-RoPE write of a small call by lanes (decode appends).  Workgroup
+// (kv head h, token chunk) of TPW = max(1, 64 / (D / 8)) tokens: thread i holds
+// the 8 dims 8c .. 8c+7 (c = i % (D/8)) of token t0 + i / (D/8), K and V, and --
+// where the rotation pairs them with the piece half a rotation on -- that K piece
+// too, loaded in one round trip before the slots and positions are known.  After
+// one barrier (slots, positions, inv_freq in LDS) and a second ((sin, cos) of its
+// tokens' (token, pair) angles) it has everything: it turns its K values, takes
+// each quantization group's minimum and maximum across the gs/8 lanes holding it
+// (lane shuffles, no LDS), and writes its K word(s), its V nibbles or bytes, and
+// -- the group's first lane -- the group's scale and bias.  Small workgroups
+// spread the V nibble atomics (8 per lane) over many CUs: with one 512-thread
+// workgroup per head they took ~6 us.  The last T workgroups turn the queries,
+// one token each, from their own table.  Same bits as
+// affine_cache_write_small<.., true> (the same turned fp16 values, group
+// extrema, affine_params and affine_code).  Fits when D % 8 == 0, D <= 512, gs / 8
+// a power of two dividing D / 8, the RoPE meets turn_rows_vec_ok and
+// T <= kLaneMaxTokens (affine_lanes_fit).
+constexpr int kLaneMaxTokens = 256;
+
+__host__ __device__ inline int affine_lanes_tpw(const int D) { return D / 8 >= 64 ? 1 : 64 / (D / 8); }
+
+__host__ __device__ inline bool affine_lanes_fit(const int T, const int D, const int gs, const int rot,
+                                                 const int trad) {
+  const int lanes = gs / 8;
+  return T > 0 && T <= kLaneMaxTokens && D % 8 == 0 && D <= kWriteMaxDim && gs % 8 == 0 && lanes <= 64 &&
+         (lanes & (lanes - 1)) == 0 && D % gs == 0 && turn_rows_vec_ok(D, rot, trad);
+}
+
+template <int BITS>
+__global__ __launch_bounds__(256) void affine_write_rope_lanes(WriteArgs a) {
+  constexpr int PW = 32 / BITS;
+  constexpr int UQ = 2;
+  const int tid = threadIdx.x, NT = blockDim.x;
+  const int T = a.T, D = a.D, per = D / 8;
+  const int tpw = affine_lanes_tpw(D), nch = (T + tpw - 1) / tpw;
+  const int bid = blockIdx.x;
+  const bool qwg = bid >= a.Hkv * nch;
+  const int h = bid % a.Hkv;
+  const int t0 = qwg ? bid - a.Hkv * nch : (bid / a.Hkv) * tpw;  // first token of the workgroup
+  const int nt = qwg ? 1 : min(tpw, T - t0);                     // its tokens
+  const bool app = a.slot_ids != nullptr;
+  const int rot = a.rope.rot, half = rot / 2, trad = a.rope.traditional;
+  const int nrp = rot / 8;  // pieces inside the rotation
+  const int tl = tid / per, c = tid % per;  // local token, piece
+  const bool mine = !qwg && tl < nt;
+  const bool rotp = c < nrp;
+  const bool lo_half = c < nrp / 2;  // neox: the piece holds the first element of its pairs
+
+  // ---- loads that depend on nothing
+  h16x8 klo = {}, khi = {}, vv = {};
+  TurnRowsVec<UQ> tq(1, a.Hq, D, a.rope);  // query workgroups: the heads of token t0
+  const h16* qin = a.q_in + (size_t)t0 * a.Hq * D;
+  if (qwg) {
+    tq.issue(qin, D, a.rope, tid, NT);
+  } else if (mine) {
+    const size_t ro = ((size_t)(t0 + tl) * a.Hkv + h) * D;
+    klo = *reinterpret_cast<const h16x8*>(a.keys + ro + 8 * c);
+    if (rotp && !trad) khi = *reinterpret_cast<const h16x8*>(a.keys + ro + 8 * (lo_half ? c + nrp / 2 : c - nrp / 2));
+    vv = *reinterpret_cast<const h16x8*>(a.values + ro + 8 * c);
+  }
+  float inv_in[2];  // half <= kWriteMaxDim / 2 = 128 <= 2 * NT
+#pragma unroll
+  for (int k = 0; k < 2; ++k) inv_in[k] = tid + k * NT < half ? a.rope.inv_freq[tid + k * NT] : 0.f;
+  // slots and positions of every token of the call (decode append: derived as
+  // cache_slots does): the workgroup's own, and the rest for the kv_lens update
+  // the last workgroup makes
+  constexpr int KT = kLaneMaxTokens / 64;
+  int sl[KT], pos[KT], sq[KT];
+#pragma unroll
+  for (int k = 0; k < KT; ++k) {
+    const int tg = tid + k * NT;
+    sl[k] = -1;
+    pos[k] = 0;
+    sq[k] = -1;
+    if (tg < T) {
+      if (app) {
+        const int s = a.slot_ids[tg];
+        if (s >= 0 && s < a.S) {
+          sq[k] = s;
+          pos[k] = a.kv_lens[s];
+          const int col = pos[k] / a.bs;
+          if (pos[k] >= 0 && col < a.max_blocks) {
+            const int b = a.bt[(size_t)s * a.max_blocks + col];
+            if (b >= 0) sl[k] = b * a.bs + pos[k] % a.bs;
+          }
+        }
+      } else if (tg >= t0 && tg < t0 + nt) {
+        sl[k] = a.slot_mapping[tg];
+        pos[k] = a.rope.positions[tg];
+      }
+    }
+  }
+  __shared__ int sslot[kLaneMaxTokens], spos[kLaneMaxTokens], sseq[kLaneMaxTokens];
+  __shared__ float sinv[kWriteMaxDim / 2];
+  __shared__ float2 stab[256];  // nt * half <= 4 * (tokens * D / 8) <= 256
+#pragma unroll
+  for (int k = 0; k < KT; ++k) {
+    const int tg = tid + k * NT;
+    if (tg < T) {
+      sslot[tg] = sl[k] >= 0 && sl[k] / a.bs < a.nb ? sl[k] : -1;  // a page outside the pool is not written
+      spos[tg] = pos[k];
+      sseq[tg] = sq[k];
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < 2; ++k)
+    if (tid + k * NT < half) sinv[tid + k * NT] = inv_in[k];
+  __syncthreads();  // every kv_lens read of the workgroup has returned
+  int arrived = 0;
+  if (app && tid == 0) arrived = __hip_atomic_fetch_add(a.counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  for (int i = tid; i < nt * half; i += NT) {
+    float sn, cs;
+    rope_sincos((float)spos[t0 + i / half] * sinv[i % half], &sn, &cs);
+    stab[i] = float2{sn, cs};
+  }
+  __syncthreads();
+
+  auto finish = [&]() {  // the end of the workgroup: the last one counted advances kv_lens
+    if (!app) return;
+    __shared__ int slast;
+    if (tid == 0) {
+      slast = arrived == (int)gridDim.x - 1;
+      if (arrived == (int)gridDim.x - 1) __hip_atomic_store(a.counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    // every token of the call (the last one counted may be a query workgroup), from the
+    // lengths read at the start (a sequence named twice gets the same length twice)
+    if (slast)
+      for (int i = tid; i < T; i += NT)
+        if (sseq[i] >= 0) a.kv_lens[sseq[i]] = spos[i] + 1;
+  };
+  if (qwg) {
+    h16* qout = a.q + (size_t)t0 * a.Hq * D;
+    tq.finish(qout, a.Hq, D, a.rope, stab);
+    for (int i0 = tid + UQ * NT; i0 < tq.n; i0 += UQ * NT) {
+      tq.issue(qin, D, a.rope, i0, NT);
+      tq.finish(qout, a.Hq, D, a.rope, stab);
+    }
+    finish();
+    return;
+  }
+
+  // ---- this lane's K values, turned and rounded to fp16 (rope_pair's values)
+  float kx[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) kx[j] = (float)klo[j];
+  if (rotp && mine) {
+    const float2* tt = stab + tl * half;
+    if (trad) {
+#pragma unroll
+      for (int j = 0; j < 8; j += 2) {
+        float y0, y1;
+        rope_rotate_sc(kx[j], kx[j + 1], tt[4 * c + j / 2], y0, y1);
+        kx[j] = (float)(h16)y0;
+        kx[j + 1] = (float)(h16)y1;
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        float y0, y1;
+        if (lo_half) {
+          rope_rotate_sc(kx[j], (float)khi[j], tt[8 * c + j], y0, y1);
+          kx[j] = (float)(h16)y0;
+        } else {
+          rope_rotate_sc((float)khi[j], kx[j], tt[8 * (c - nrp / 2) + j], y0, y1);
+          kx[j] = (float)(h16)y1;
+        }
+      }
+    }
+  }
+  float vx[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) vx[j] = (float)vv[j];
+
+  // ---- group extrema across the gs / 8 lanes of a group (aligned: a row is D / 8 lanes)
+  const int lanes = a.gs / 8;
+  float kmin = kx[0], kmax = kx[0], vmin = vx[0], vmax = vx[0];
+#pragma unroll
+  for (int j = 1; j < 8; ++j) {
+    kmin = fminf(kmin, kx[j]);
+    kmax = fmaxf(kmax, kx[j]);
+    vmin = fminf(vmin, vx[j]);
+    vmax = fmaxf(vmax, vx[j]);
+  }
+  for (int o = 1; o < lanes; o <<= 1) {
+    kmin = fminf(kmin, __shfl_xor(kmin, o, 64));
+    kmax = fmaxf(kmax, __shfl_xor(kmax, o, 64));
+    vmin = fminf(vmin, __shfl_xor(vmin, o, 64));
+    vmax = fmaxf(vmax, __shfl_xor(vmax, o, 64));
+  }
+  const int slot = mine ? sslot[t0 + tl] : -1;
+  if (slot >= 0) {
+  const float n_bins = (float)((1 << BITS) - 1);
+  float ksc, kbi, vsc, vbi;
+  affine_params(kmin, kmax, n_bins, ksc, kbi);
+  affine_params(vmin, vmax, n_bins, vsc, vbi);
+  const int off = slot % a.bs;
+  const size_t ph = (size_t)(slot / a.bs) * a.Hkv + h;
+  // K codes: 8 dims are 8 / PW words
+#pragma unroll
+  for (int w = 0; w < 8 / PW; ++w) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int k = 0; k < PW; ++k) word |= affine_code(kx[w * PW + k], ksc, kbi, n_bins) << (k * BITS);
+    a.kc[(ph * a.bs + off) * (size_t)(D / PW) + (8 * c) / PW + w] = word;
+  }
+  // V codes: each dim's value goes to its own word (the word holds consecutive tokens)
+  constexpr uint32_t M = (1u << BITS) - 1u;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const uint32_t code = affine_code(vx[j], vsc, vbi, n_bins);
+    uint32_t* wp = a.vc + v_word_index<BITS>(ph, off, 8 * c + j, D, a.bs);
+    if (BITS == 8) {
+      reinterpret_cast<uint8_t*>(wp)[off % 4] = (uint8_t)code;
+    } else {  // the nibble by two atomics that return nothing (tokens of the call may share the word)
+      const int sh = v_shift<BITS>(off % PW);
+      atomicAnd(wp, ~(M << sh));
+      atomicOr(wp, code << sh);
+    }
+  }
+  if (c % lanes == 0) {  // the group's first lane: scale and bias
+    const int G = D / a.gs;
+    const size_t si = (ph * G + (8 * c) / a.gs) * a.bs + off;
+    a.ks[si] = (h16)ksc;
+    a.kb[si] = (h16)kbi;
+    a.vs[si] = (h16)vsc;
+    a.vb[si] = (h16)vbi;
+  }
+  }  // slot >= 0
+  finish();  // every thread, once (it holds a barrier)
+}
 
 }  // namespace emx

@@ -29,6 +29,9 @@
 extern "C" {
 #endif
 
+/* Device ints the decode appends (emx_*_cache_append_rope) take as `counter`. */
+#define EMX_APPEND_COUNTER_INTS 4
+
 #define EMX_OK 0
 #define EMX_ERR_INVALID (-1)     /* bad argument / shape (Python: ValueError) */
 #define EMX_ERR_UNSUPPORTED (-2) /* valid but unsupported configuration (NotImplementedError) */
@@ -98,12 +101,12 @@ int emx_affine_cache_write_rope(const void* keys, const void* values, const int3
  * page_size + position % page_size (not written for a slot id outside
  * [0, num_seqs), a column past the table or a negative page id), K is rotated
  * at that position and quantized into the pages, queries_in rotated into
- * queries, and kv_lens[s] advances by one.  `counter` is one int of device
- * memory, zero before the first call; every call leaves it zero (calls that
- * share it must not overlap: give each stream its own, as the Python views do;
- * a counter left nonzero, e.g. by a launch that never ran to its end, makes the
- * later calls advance kv_lens at the wrong workgroup, so a caller that aborts a
- * launch zeroes it again).  A cache must not be appended to from two streams at
+ * queries, and kv_lens[s] advances by one.  `counter` is EMX_APPEND_COUNTER_INTS
+ * ints of device memory, zero before the first call; every call leaves them zero
+ * (calls that share them must not overlap: give each stream its own, as the
+ * Python views do; counters left nonzero, e.g. by a launch that never ran to its
+ * end, make the later calls advance kv_lens at the wrong workgroup, so a caller
+ * that aborts a launch zeroes them again).  A cache must not be appended to from two streams at
  * once (the pages and kv_lens would race).  head_dim and group_size multiples of 16,
  * group_size <= 64; otherwise EMX_ERR_UNSUPPORTED (use the two calls).
  * Replaces the decode branch of PageCacheView.concatenate_to_cache
@@ -124,8 +127,12 @@ int emx_affine_cache_append_rope(const void* keys, const void* values, const int
  * emx_fp8_cache_write_rope together for one token per sequence, with the
  * positions, slots and kv_lens rule of emx_affine_cache_append_rope
  * (num_tokens <= 1024 and at most 65536 values per tensor; otherwise
- * EMX_ERR_UNSUPPORTED).  `counter`: one device int, zero before the first call,
- * left zero by every call (calls sharing it must not overlap).
+ * EMX_ERR_UNSUPPORTED).  `counter`: EMX_APPEND_COUNTER_INTS device ints, zero
+ * before the first call, left zero by every call (calls sharing them must not
+ * overlap).  Besides the workgroup count they carry the call's K and V maxima
+ * while its workgroups exchange them: the write workgroups wait (a bounded wait)
+ * until every one of them has folded its maxima in, so all encode with the same
+ * scales; their number is small (at most 128) and they are all resident at once.
  * Replaces the FP8 decode write of PageCacheView.concatenate_to_cache
  *   lib/python/easymlx/caching/paged/cache.py:1126-1184 (RoPE :1161-1166).
  */
@@ -297,9 +304,12 @@ int emx_rope_rows(void* x, int rows, int heads, int head_dim, const int32_t* pos
  * (of any shape) that are ordered on one stream.  Calls sharing a workspace
  * must not overlap.  The workspace also carries the 4-bit decode's plan cache:
  * a pure decode call keeps its work split there, keyed by its shape and the
- * contents of kv_lens, and the next call with the same kv_lens (the next
- * layer of the same decode step) starts from it; a call with other kv_lens
- * or another shape computes its own.  Results are the same either way.
+ * per-sequence counts of work items that kv_lens gives (an item: 256 tokens up
+ * to GQA 4, 128 up to 8, 64 up to 16), and the next call with the same counts
+ * (the next layer of the same decode step, and most next steps: a kv_len that
+ * grows by one token keeps its count unless it crosses an item boundary)
+ * starts from it; a call with other counts or another shape
+ * computes its own.  Results are the same either way.
  * No direct reference counterpart: replaces the tmp_out/exp_sums/max_logits
  * allocation of lib/python/easymlx/operations/kernels/page_attention.py:2205-2272.
  */

@@ -86,7 +86,7 @@ def test_append_matches_the_two_launch_write(cuda, bits, bs, gs, trad):
     lens[5] = lens[4] + 1     # ... and the neighbouring slots of one value word
     rope = RotaryEmbedding(d, traditional=trad, base=10000.0)
     base = _view(rng, cuda, nb, bs, hkv, d, bits, gs, tables, lens)
-    counter = torch.zeros(1, dtype=torch.int32, device=cuda)
+    counter = torch.zeros(_native.APPEND_COUNTER_INTS, dtype=torch.int32, device=cuda)
     for slots in (tuple(range(S)), (7, 3, 11, 4, 5, 0, 2, 1), (6, -1, 9, S + 2, 10)):
         a, b = _clone(base, cuda), _clone(base, cuda)
         for rep in range(2):  # two calls in a row: the counter is back at zero
@@ -101,7 +101,7 @@ def test_append_matches_the_two_launch_write(cuda, bits, bs, gs, trad):
             assert torch.equal(a.kv_lens, b.kv_lens), (slots, rep)
             for x, y in zip(a.page_arrays(), b.page_arrays()):
                 assert torch.equal(x, y), (slots, rep)
-            assert int(counter.item()) == 0
+            assert not counter.any()
 
 
 def test_append_rejects_unsupported_geometry(cuda):
@@ -144,7 +144,7 @@ def test_fp8_append_matches_the_two_launch_write(cuda, bs, trad, S, hkv):
                                 head_dim=d)
 
     base = view()
-    counter = torch.zeros(1, dtype=torch.int32, device=cuda)
+    counter = torch.zeros(_native.APPEND_COUNTER_INTS, dtype=torch.int32, device=cuda)
     ws = torch.empty(int(lib.emx_fp8_write_workspace_bytes()), dtype=torch.uint8, device=cuda)
     inv = rope.inv_freq(cuda)
     for slots in (tuple(range(S)), (7, 3, 11, 4, 0, 2), (6, -1, 9, S + 2, 10)):
@@ -176,4 +176,4 @@ def test_fp8_append_matches_the_two_launch_write(cuda, bs, trad, S, hkv):
             assert torch.equal(qa, qb), (slots, rep)
             for x, y in zip(a, b):
                 assert torch.equal(x, y), (slots, rep)
-            assert int(counter.item()) == 0
+            assert not counter.any()

@@ -118,3 +118,46 @@ def test_plan_shapes_interleaved(cuda):
     win_fresh = _call(w, v, cuda, torch.zeros(size, dtype=torch.uint8, device=cuda), window=300)
     assert torch.equal(win, win_fresh)
     assert_attention_close(win.float().cpu().numpy(), oracle_expected(w, sliding_window=300), "window")
+
+
+def test_plan_kept_across_token_growth(cuda):
+    """kv_lens that grow by a token per call keep their item counts (the plan holds) until a
+    sequence crosses an item boundary; the token masks and, under a sliding window, the first
+    items follow this call's kv_lens, not the plan's."""
+    print("[plan token growth]", flush=True)
+    wl = _wl(38, 24, ctx=(1400, 3000))
+    view = gpu_cache(wl, cuda)
+    ws = _workspace(wl, cuda)
+    base = (np.maximum(wl.kv_lens - 12, 1)).astype(np.int32)
+    base[0] = 256 * 3 - 2  # crosses an item boundary within the calls below
+    base[1] = 256 * 5
+    for window in (None, 300, 512):
+        for step in range(6):
+            lens = (base + step).astype(np.int32)
+            kl = torch.from_numpy(lens).to(cuda)
+            got = _call(wl, view, cuda, ws, kv_lens=kl, window=window)
+            fresh = _call(wl, view, cuda, _workspace(wl, cuda), kv_lens=kl, window=window)
+            assert torch.equal(got, fresh), f"window {window} step {step}"
+            if step in (0, 3, 5):
+                assert_attention_close(got.float().cpu().numpy(), oracle_expected(wl, kv_lens=lens,
+                                                                                   sliding_window=window or 0),
+                                       f"window {window} step {step}")
+
+
+def test_plan_one_sequence_changes(cuda):
+    """A change of one sequence's item count, at any position of the batch, invalidates the plan
+    (every lane of every wave votes on the mismatch)."""
+    print("[plan one sequence]", flush=True)
+    wl = _wl(39, 150, ctx=(300, 1500))
+    view = gpu_cache(wl, cuda)
+    ws = _workspace(wl, cuda)
+    _call(wl, view, cuda, ws)
+    for si in (1, 37, 63, 64, 100, 149):
+        lens = wl.kv_lens.copy()
+        lens[si] = max(1, int(lens[si]) - 256)  # one item fewer
+        kl = torch.from_numpy(lens.astype(np.int32)).to(cuda)
+        got = _call(wl, view, cuda, ws, kv_lens=kl)
+        fresh = _call(wl, view, cuda, _workspace(wl, cuda), kv_lens=kl)
+        assert torch.equal(got, fresh), f"sequence {si}"
+        back = _call(wl, view, cuda, ws)
+        assert torch.equal(back, _call(wl, view, cuda, _workspace(wl, cuda))), f"sequence {si} back"

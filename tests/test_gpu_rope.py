@@ -62,14 +62,16 @@ def test_rope_rows_vs_float64(cuda, traditional, kind):
     assert np.array_equal(got[..., rope.dims:], x[..., rope.dims:])
 
 
-@pytest.mark.parametrize("bits,T,rot", [(4, 300, 128), (4, 32, 128), (8, 77, 128), (4, 32, 64), (4, 300, 64)])
-def test_fused_write_equals_rotate_then_write(cuda, bits, T, rot):
+@pytest.mark.parametrize("bits,T,rot,trad", [(4, 300, 128, 0), (4, 32, 128, 0), (8, 77, 128, 0), (4, 32, 64, 0),
+                                             (4, 300, 64, 0), (8, 32, 128, 0), (4, 32, 128, 1), (8, 40, 64, 1),
+                                             (4, 7, 32, 0)])
+def test_fused_write_equals_rotate_then_write(cuda, bits, T, rot, trad):
     """One launch (rotate K in LDS, quantize) == emx_rope_rows on K, then emx_affine_cache_write: every byte.
     The queries come out turned into a separate tensor (dims past rot copied), or turned in place."""
-    print(f"[fused rope write bits={bits} T={T} rot={rot}]", flush=True)
+    print(f"[fused rope write bits={bits} T={T} rot={rot} traditional={trad}]", flush=True)
     rng = np.random.default_rng(9 + bits + T)
     hkv, d, bs, nb = 8, 128, 128, 16
-    rope = RotaryEmbedding.llama3(rot, base=500000.0)
+    rope = RotaryEmbedding.llama3(rot, base=500000.0, traditional=bool(trad))
     k = torch.from_numpy((rng.standard_normal((T, hkv, d)) * 2).astype(np.float16)).to(cuda)
     v = torch.from_numpy((rng.standard_normal((T, hkv, d)) * 2).astype(np.float16)).to(cuda)
     slots = torch.from_numpy(rng.permutation(nb * bs)[:T].astype(np.int32)).to(cuda)
@@ -92,7 +94,7 @@ def test_fused_write_equals_rotate_then_write(cuda, bits, T, rot):
         _native.check(lib.emx_affine_cache_write_rope(
             k.data_ptr(), v.data_ptr(), slots.data_ptr(), T, hkv, d, 64, bits, bs, nb, a.key_cache.data_ptr(),
             a.k_scales.data_ptr(), a.k_biases.data_ptr(), a.value_cache.data_ptr(), a.v_scales.data_ptr(),
-            a.v_biases.data_ptr(), pos.data_ptr(), inv.data_ptr(), rope.dims, 0, q_in, q_out.data_ptr(), 32, st))
+            a.v_biases.data_ptr(), pos.data_ptr(), inv.data_ptr(), rope.dims, trad, q_in, q_out.data_ptr(), 32, st))
 
     call(q.data_ptr(), qo)
     call(None, qa)  # the same write again: the pages come out the same

@@ -232,9 +232,12 @@ def test_abi_argument_errors(lib):
         _native.check(_native.EMX_ERR_UNSUPPORTED)
     with pytest.raises(RuntimeError):
         _native.check(_native.EMX_ERR_HIP)
-    # decode workspace size is pure host arithmetic; 0 where the split-K path does not apply
+    # decode workspace size is pure host arithmetic; 0 where neither the MFMA decode nor the split-K
+    # path applies (head_dim not a multiple of 32, or pages not a multiple of 8 tokens)
     assert lib.emx_paged_workspace_bytes(32, 32, 8, 128, 32, 128) > 0
-    assert lib.emx_paged_workspace_bytes(32, 32, 8, 64, 32, 128) == 0
+    assert lib.emx_paged_workspace_bytes(32, 32, 8, 64, 32, 128) > 0  # split-K
+    assert lib.emx_paged_workspace_bytes(32, 32, 8, 48, 32, 128) == 0
+    assert lib.emx_paged_workspace_bytes(32, 32, 8, 64, 32, 12) == 0
 
 
 def test_abi_rope_and_prefill_split_arguments(lib):
