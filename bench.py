@@ -567,11 +567,12 @@ def aux_quantize_on_write(dev):
     return res
 
 
-def aux_op_layer_step(dev, steps=100):
+def aux_op_layer_step(dev, steps=100, layers=8):
     """The public op as a runner calls it, per layer-step of c2: ``concatenate_to_cache`` (quantize-on-write of
-    one token per sequence, Llama-3 RoPE fused) then ``UnifiedAttention.forward_native``.  Wall clock per step:
-    eager Python calls, and the same step captured once in a HIP graph through ``CompiledPagedCacheProxy``
-    (the counterpart of the reference's compiled decode) and replayed."""
+    one token per sequence, Llama-3 RoPE fused) then ``UnifiedAttention.forward_native``, over ``layers``
+    layers with a cache each (one decode step).  Wall clock per layer-step: eager Python calls, and the decode
+    step captured once in a HIP graph through ``CompiledPagedCacheProxy`` (the counterpart of the reference's
+    compiled decode, which compiles the whole model step) and replayed."""
     import torch
 
     from easymlx_amd import CompiledPagedCacheProxy, Fp8PageCacheView, PageMetadata, RotaryEmbedding, UnifiedAttention
@@ -592,33 +593,40 @@ def aux_op_layer_step(dev, steps=100):
     q = torch.randn((S, hq, d), device=dev, generator=g).half()
     k = torch.randn((S, hkv, d), device=dev, generator=g).half()
     v = torch.randn((S, hkv, d), device=dev, generator=g).half()
-    res = {}
+    res = {"layers_per_step": layers}
     for mode in ("eager", "graph", "fp8_eager", "fp8_graph"):
         nbp = wl.num_blocks + extra * S
-        if mode.startswith("fp8"):  # the reference's FP8 cache on the same pages
-            shape = (nbp, bs, hkv, d)
-            view = Fp8PageCacheView(key_cache=torch.zeros(shape, dtype=torch.uint8, device=dev),
-                                    value_cache=torch.zeros(shape, dtype=torch.uint8, device=dev),
-                                    k_scales=torch.zeros(nbp, device=dev), v_scales=torch.zeros(nbp, device=dev),
-                                    block_tables=torch.from_numpy(tables).to(dev),
-                                    kv_lens=torch.from_numpy(wl.kv_lens).to(dev), block_size=bs, num_kv_heads=hkv,
-                                    head_dim=d)
-        else:
-            view = affine_pool(num_blocks=nbp, num_kv_heads=hkv, head_dim=d, block_size=bs, bits=4, group_size=64,
-                               block_tables=torch.from_numpy(tables).to(dev),
-                               kv_lens=torch.from_numpy(wl.kv_lens).to(dev))
-        view.write_slots(torch.from_numpy(wl.k).to(dev), torch.from_numpy(wl.v).to(dev),
-                         torch.from_numpy(wl.slot.astype(np.int32)).to(dev))
+
+        def make_view():
+            if mode.startswith("fp8"):  # the reference's FP8 cache on the same pages
+                shape = (nbp, bs, hkv, d)
+                view = Fp8PageCacheView(key_cache=torch.zeros(shape, dtype=torch.uint8, device=dev),
+                                        value_cache=torch.zeros(shape, dtype=torch.uint8, device=dev),
+                                        k_scales=torch.zeros(nbp, device=dev), v_scales=torch.zeros(nbp, device=dev),
+                                        block_tables=torch.from_numpy(tables).to(dev),
+                                        kv_lens=torch.from_numpy(wl.kv_lens).to(dev), block_size=bs,
+                                        num_kv_heads=hkv, head_dim=d)
+            else:
+                view = affine_pool(num_blocks=nbp, num_kv_heads=hkv, head_dim=d, block_size=bs, bits=4,
+                                   group_size=64, block_tables=torch.from_numpy(tables).to(dev),
+                                   kv_lens=torch.from_numpy(wl.kv_lens).to(dev))
+            view.write_slots(torch.from_numpy(wl.k).to(dev), torch.from_numpy(wl.v).to(dev),
+                             torch.from_numpy(wl.slot.astype(np.int32)).to(dev))
+            return view
+
+        views = [make_view() for _ in range(layers)]
         md0 = PageMetadata(query_start_loc=torch.arange(S + 1, dtype=torch.int32, device=dev),
                            slot_ids=tuple(range(S)))
         qlens = (1,) * S
-        cache = CompiledPagedCacheProxy(view) if mode.endswith("graph") else view
+        caches = [CompiledPagedCacheProxy(w) if mode.endswith("graph") else w for w in views]
         outs = []
 
         def step():
-            q2, kc, vc, md = cache.concatenate_to_cache(q, k, v, cache_metadata=md0, rope=rope, query_lens=qlens)
-            outs[:] = [op.forward_native(query=q2, key=kc, value=vc, cache_metadata=md,
-                                         cache_view=view).attention_outputs]
+            x = q
+            for cache, view in zip(caches, views):
+                q2, kc, vc, md = cache.concatenate_to_cache(x, k, v, cache_metadata=md0, rope=rope, query_lens=qlens)
+                x = op.forward_native(query=q2, key=kc, value=vc, cache_metadata=md, cache_view=view).attention_outputs
+            outs[:] = [x]
 
         side = torch.cuda.Stream(dev)
         side.wait_stream(torch.cuda.current_stream(dev))
@@ -640,13 +648,14 @@ def aux_op_layer_step(dev, steps=100):
             for _ in range(steps):
                 run()
             side.synchronize()
-            res[f"{mode}_us_per_layer_step"] = round((time.perf_counter() - t0) / steps * 1e6, 2)
-        del view
-    res["workload"] = ("c2 layer-step through the public op: concatenate_to_cache (1 token x 32 seqs, Llama-3 "
-                       "RoPE fused) + UnifiedAttention.forward_native, wall clock; fp8_*: the same over an FP8 "
-                       "(E4M3, per-page scale) cache")
+            res[f"{mode}_us_per_layer_step"] = round((time.perf_counter() - t0) / (steps * layers) * 1e6, 2)
+        del views, caches
+    res["workload"] = (f"c2 decode step through the public op over {layers} layers (a cache each): per layer "
+                       "concatenate_to_cache (1 token x 32 seqs, Llama-3 RoPE fused) + "
+                       "UnifiedAttention.forward_native (its output is the next layer's query); wall clock per "
+                       "layer-step; graph: the whole step in one HIP graph, replayed; fp8_*: the same over an "
+                       "FP8 (E4M3, per-page scale) cache")
     return res
-
 
 def main():
     args = parse()

@@ -484,21 +484,6 @@ int emx_affine_quantize(const void* x, long rows, int head_dim, int group_size, 
   return check_launch("affine_quantize");
 }
 
-// The lane-per-8-dims fused-RoPE write (affine_write_rope_lanes: one workgroup per
-// kv head plus workgroups for the queries) when the call fits it; false: the
-// caller launches affine_cache_write_small.
-static bool launch_affine_lanes(const emx::WriteArgs& a, int bits, hipStream_t st) {
-  if (a.rope.inv_freq == nullptr || !emx::affine_lanes_fit(a.T, a.D, a.gs, a.rope.rot, a.rope.traditional))
-    return false;
-  const int tpw = emx::affine_lanes_tpw(a.D);
-  const int nt = (tpw * (a.D / 8) + 63) / 64 * 64;       // threads per workgroup
-  const int nwg = a.Hkv * ((a.T + tpw - 1) / tpw) + (a.q != nullptr ? a.T : 0);  // + one per query token
-  typedef void (*Fn)(emx::WriteArgs);
-  const Fn fn = bits == 4 ? emx::affine_write_rope_lanes<4> : emx::affine_write_rope_lanes<8>;
-  hipLaunchKernelGGL(fn, dim3((unsigned)nwg), dim3((unsigned)nt), 0, st, a);
-  return true;
-}
-
 static int affine_write_impl(const void* keys, const void* values, const int32_t* slot_mapping, int num_tokens,
                       int num_kv_heads, int head_dim, int group_size, int bits, int page_size, int num_blocks,
                       uint32_t* k_codes, void* k_scales, void* k_biases, uint32_t* v_codes, void* v_scales,
@@ -548,7 +533,6 @@ static int affine_write_impl(const void* keys, const void* values, const int32_t
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (num_tokens <= emx::kSmallWrite && head_dim % 16 == 0 && group_size % 16 == 0 &&
       group_size <= emx::kSmallMaxGroup) {
-    if (launch_affine_lanes(a, bits, st)) return check_launch("affine_write_rope_lanes");
     const bool r = rope.inv_freq != nullptr;
     // with RoPE and queries: kQRopeBlocks more rows of workgroups turn the queries in the same launch
     const dim3 sgrid((unsigned)num_kv_heads,
@@ -660,7 +644,6 @@ int emx_affine_cache_append_rope(const void* keys, const void* values, const int
   a.max_blocks = max_blocks_per_seq;
   a.counter = counter;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  if (launch_affine_lanes(a, bits, st)) return check_launch("affine_write_rope_lanes (append)");
   const dim3 sgrid((unsigned)num_kv_heads, (unsigned)(head_dim / 16 + (queries ? emx::kQRopeBlocks : 0)));
   typedef void (*SmallFn)(emx::WriteArgs);
   SmallFn fn = bits == 4 ? emx::affine_cache_write_small<4, true> : emx::affine_cache_write_small<8, true>;
@@ -1486,8 +1469,7 @@ int emx_fp8_cache_append_rope(const void* keys, const void* values, int dtype, c
   const uintptr_t out8 = reinterpret_cast<uintptr_t>(key_cache) | reinterpret_cast<uintptr_t>(value_cache);
   if (emx::fp8_grid_fits(num_tokens, num_kv_heads, head_dim, rot_dims, traditional ? 1 : 0) && !(in16 & 15) &&
       !(out8 & 7)) {
-    const long tasks = (long)emx::fp8_one_ktasks(num_tokens, num_kv_heads, head_dim, rot_dims, traditional ? 1 : 0) +
-                       (long)num_tokens * num_kv_heads * (head_dim / 8);
+    const long tasks = 2L * num_tokens * num_kv_heads * (head_dim / 8);  // K pieces, then V pieces
     a.nwg = (int)((tasks + 255) / 256);
     const dim3 g((unsigned)(a.nwg + (queries ? num_tokens : 0)));  // + one workgroup per query token
     switch (dtype) {

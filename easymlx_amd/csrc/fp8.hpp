@@ -668,8 +668,9 @@ __global__ __launch_bounds__(1024) void fp8_write_one(Fp8WriteArgs a) {
 
 // ---- Decode append by a grid that waits on itself once (fp8_append_grid).
 // The call's single scale pair needs the maxima of every value before any code
-// is written.  Workgroups of 256 threads each take 256 tasks of the call (K row
-// tasks as in fp8_write_one, then V pieces of 8), load them with the slots and
+// is written.  Workgroups of 256 threads each take 256 pieces of 8 values of the
+// call (K pieces, then V pieces; a rotated K piece also loads the piece it pairs
+// with), load them with the slots and
 // positions of every token, turn their K from a (sin, cos) table of their own
 // tokens, and reduce their maxima; thread 0 folds them into the call's maxima
 // (atomicMax on the bits of non-negative floats, counter[2] and [3]), counts the
@@ -688,7 +689,7 @@ __host__ __device__ inline bool fp8_grid_fits(const int T, const int Hkv, const 
                                               const int trad) {
   if (T <= 0 || T > kFp8AppendMax || D % 8 != 0 || D > 256 || rot <= 0 || !turn_rows_vec_ok(D, rot, trad))
     return false;
-  const long tasks = (long)fp8_one_ktasks(T, Hkv, D, rot, trad) + (long)T * Hkv * (D / 8);
+  const long tasks = 2L * T * Hkv * (D / 8);  // K pieces, then V pieces
   return (tasks + 255) / 256 <= kFp8GridMaxWG;
 }
 
@@ -701,9 +702,8 @@ __global__ __launch_bounds__(256) void fp8_append_grid(Fp8WriteArgs a) {
   const bool qwg = (int)blockIdx.x >= nwg;
   const RopeArgs& r = a.rope;
   const int rot = r.rot, half = rot / 2, trad = r.traditional;
-  const int nrot = trad ? rot / 8 : rot / 16;
-  const int per = nrot + (a.D - rot) / 8;  // K tasks per (token, head) row
-  const int nk = a.T * a.Hkv * per, nv = a.T * a.Hkv * (a.D / 8);
+  const int pr = a.D / 8, nrp = rot / 8;  // pieces per (token, head) row, of them rotated
+  const int nk = a.T * a.Hkv * pr, nv = nk;
   const T* k = reinterpret_cast<const T*>(a.k);
   const T* v = reinterpret_cast<const T*>(a.v);
   int* const cnt = a.counter;
@@ -711,16 +711,15 @@ __global__ __launch_bounds__(256) void fp8_append_grid(Fp8WriteArgs a) {
   // ---- loads that depend on nothing: this thread's task, or a query token's rows
   const int j0 = (int)blockIdx.x * NTH, j = j0 + tid;
   Fp8Piece<T> lo, hi;
-  auto k_piece_off = [&](const int c) { return c < nrot ? 8 * c : rot + 8 * (c - nrot); };
   const int tq = (int)blockIdx.x - nwg;  // query workgroup: its token
   TurnRowsVec<2> tv(1, a.Hq, a.D, r);
   if (qwg) {
     tv.issue(a.q_in + (size_t)tq * a.Hq * a.D, a.D, r, tid, NTH);
   } else if (j < nk) {
-    const int rr = j / per, c = j % per;
-    const T* row = k + (size_t)rr * a.D;
-    lo.load(row + k_piece_off(c));
-    if (c < nrot && !trad) hi.load(row + half + 8 * c);
+    const int c = j % pr;
+    const T* row = k + (size_t)(j / pr) * a.D;
+    lo.load(row + 8 * c);
+    if (c < nrp && !trad) hi.load(row + 8 * (c < nrp / 2 ? c + nrp / 2 : c - nrp / 2));
   } else if (j < nk + nv) {
     lo.load(v + 8 * (size_t)(j - nk));
   }
@@ -767,8 +766,8 @@ __global__ __launch_bounds__(256) void fp8_append_grid(Fp8WriteArgs a) {
   int t_lo = tq, t_hi = tq;
   if (!qwg) {
     const int k_end = min(j0 + NTH, nk);
-    t_lo = j0 < nk ? (j0 / per) / a.Hkv : 0;
-    t_hi = j0 < nk ? ((k_end - 1) / per) / a.Hkv : -1;
+    t_lo = j0 < nk ? (j0 / pr) / a.Hkv : 0;
+    t_hi = j0 < nk ? ((k_end - 1) / pr) / a.Hkv : -1;
   }
   const int ntab = (t_hi - t_lo + 1) * half;  // <= kFp8GridTab (fp8_grid_fits)
   for (int i = tid; i < ntab; i += NTH) {
@@ -780,7 +779,7 @@ __global__ __launch_bounds__(256) void fp8_append_grid(Fp8WriteArgs a) {
 
   auto count_and_finish = [&]() {  // every workgroup at its end, once
     if (tid == 0) {
-      const int arrived = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+      const int arrived = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       sflag = arrived == (int)gridDim.x - 1;
       if (sflag) {  // every workgroup has read the maxima and kv_lens: clear for the next call
         __hip_atomic_store(cnt + 1, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -806,55 +805,49 @@ __global__ __launch_bounds__(256) void fp8_append_grid(Fp8WriteArgs a) {
     return;
   }
 
-  // ---- this task's values (K turned and rounded to T), the workgroup's maxima
-  float x[8], y[8];
-  int kind = 0, rr = 0, c = 0, t = 0;  // kind 1: K task, 2: V piece
-  if (j < nk) {
-    kind = 1;
-    rr = j / per;
-    c = j % per;
+  // ---- this piece's values (K turned and rounded to T), the workgroup's maxima
+  float x[8];
+  int kind = 0, rr = 0, c = 0, t = 0;  // kind 1: K piece, 2: V piece
+  if (j < nk + nv) {
+    kind = j < nk ? 1 : 2;
+    const int i = kind == 1 ? j : j - nk;
+    rr = i / pr;
+    c = i % pr;
     t = rr / a.Hkv;
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      x[q] = lo.at(q);
-      y[q] = 0.f;
-    }
-    if (c < nrot) {
-      const float2* tt = stab + (t - t_lo) * half;
-      if (trad) {
+    for (int q = 0; q < 8; ++q) x[q] = lo.at(q);
+  }
+  if (kind == 1 && c < nrp) {
+    const float2* tt = stab + (t - t_lo) * half;
+    if (trad) {
 #pragma unroll
-        for (int q = 0; q < 8; q += 2) {
-          float y0, y1;
-          rope_rotate_sc(x[q], x[q + 1], tt[4 * c + q / 2], y0, y1);
-          x[q] = round_to(y0, (T*)nullptr);
-          x[q + 1] = round_to(y1, (T*)nullptr);
-        }
-      } else {
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-          float y0, y1;
-          rope_rotate_sc(x[q], hi.at(q), tt[8 * c + q], y0, y1);
-          x[q] = round_to(y0, (T*)nullptr);
-          y[q] = round_to(y1, (T*)nullptr);
-        }
+      for (int q = 0; q < 8; q += 2) {
+        float y0, y1;
+        rope_rotate_sc(x[q], x[q + 1], tt[4 * c + q / 2], y0, y1);
+        x[q] = round_to(y0, (T*)nullptr);
+        x[q + 1] = round_to(y1, (T*)nullptr);
       }
-    }
-  } else if (j < nk + nv) {
-    kind = 2;
-    rr = (j - nk) / (a.D / 8);
-    c = (j - nk) % (a.D / 8);
-    t = rr / a.Hkv;
+    } else if (c < nrp / 2) {  // the first elements of their pairs
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      x[q] = lo.at(q);
-      y[q] = 0.f;
+      for (int q = 0; q < 8; ++q) {
+        float y0, y1;
+        rope_rotate_sc(x[q], hi.at(q), tt[8 * c + q], y0, y1);
+        x[q] = round_to(y0, (T*)nullptr);
+      }
+    } else {  // the second elements
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        float y0, y1;
+        rope_rotate_sc(hi.at(q), x[q], tt[8 * (c - nrp / 2) + q], y0, y1);
+        x[q] = round_to(y1, (T*)nullptr);
+      }
     }
   }
   const int slot = kind ? fslot[t] : -1;
   float m = 0.f;
   if (slot >= 0) {
 #pragma unroll
-    for (int q = 0; q < 8; ++q) m = fmaxf(m, fmaxf(fabsf(x[q]), fabsf(y[q])));
+    for (int q = 0; q < 8; ++q) m = fmaxf(m, fabsf(x[q]));
   }
   float mk = wave_max(kind == 1 ? m : 0.f), mv = wave_max(kind == 2 ? m : 0.f);
   if ((tid & 63) == 0) {
@@ -870,11 +863,18 @@ __global__ __launch_bounds__(256) void fp8_append_grid(Fp8WriteArgs a) {
       bk = max(bk, sred[0][w]);
       bv = max(bv, sred[1][w]);
     }
-    __hip_atomic_fetch_max(reinterpret_cast<unsigned int*>(cnt + 2), bk, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_fetch_max(reinterpret_cast<unsigned int*>(cnt + 3), bv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_fetch_add(cnt + 1, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+    // Only atomics touch counter[1..3], and an agent-scope atomic is performed where
+    // every XCD sees it, so relaxed order suffices once the two maxima have returned
+    // before the count goes out (the empty asm makes the count wait for them); release
+    // and acquire fences would write back and invalidate whole L2s for nothing.
+    const unsigned int ok = __hip_atomic_fetch_max(reinterpret_cast<unsigned int*>(cnt + 2), bk, __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT);
+    const unsigned int ov = __hip_atomic_fetch_max(reinterpret_cast<unsigned int*>(cnt + 3), bv, __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT);
+    asm volatile("" ::"v"(ok), "v"(ov));
+    __hip_atomic_fetch_add(cnt + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     for (int it = 0; it < (1 << 22); ++it) {
-      if (__hip_atomic_load(cnt + 1, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) >= nwg) break;
+      if (__hip_atomic_load(cnt + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= nwg) break;
       __builtin_amdgcn_s_sleep(1);
     }
     sred[0][0] = __hip_atomic_load(reinterpret_cast<unsigned int*>(cnt + 2), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -897,8 +897,7 @@ __global__ __launch_bounds__(256) void fp8_append_grid(Fp8WriteArgs a) {
     };
     const size_t rowb = ((size_t)slot * a.Hkv + rr % a.Hkv) * (size_t)a.D;
     if (kind == 1) {
-      *reinterpret_cast<uint2*>(a.kc + rowb + k_piece_off(c)) = enc8(x, kq);
-      if (c < nrot && !trad) *reinterpret_cast<uint2*>(a.kc + rowb + half + 8 * c) = enc8(y, kq);
+      *reinterpret_cast<uint2*>(a.kc + rowb + 8 * c) = enc8(x, kq);
       if (c == 0 && rr % a.Hkv == 0) {  // once per written token: the page keeps the larger scale
         atomicMax(reinterpret_cast<unsigned int*>(a.ks) + slot / a.bs, __float_as_uint(ksc));
         atomicMax(reinterpret_cast<unsigned int*>(a.vs) + slot / a.bs, __float_as_uint(vsc));

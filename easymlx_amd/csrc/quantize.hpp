@@ -656,236 +656,4 @@ __global__ __launch_bounds__(256) void affine_cache_write_small(WriteArgs a) {
 #pragma clang fp contract(on)
 
 
-// ---- Fused-RoPE write of a small call by lanes (decode appends).  Workgroup
-// (kv head h, token chunk) of TPW = max(1, 64 / (D / 8)) tokens: thread i holds
-// the 8 dims 8c .. 8c+7 (c = i % (D/8)) of token t0 + i / (D/8), K and V, and --
-// where the rotation pairs them with the piece half a rotation on -- that K piece
-// too, loaded in one round trip before the slots and positions are known.  After
-// one barrier (slots, positions, inv_freq in LDS) and a second ((sin, cos) of its
-// tokens' (token, pair) angles) it has everything: it turns its K values, takes
-// each quantization group's minimum and maximum across the gs/8 lanes holding it
-// (lane shuffles, no LDS), and writes its K word(s), its V nibbles or bytes, and
-// -- the group's first lane -- the group's scale and bias.  Small workgroups
-// spread the V nibble atomics (8 per lane) over many CUs: with one 512-thread
-// workgroup per head they took ~6 us.  The last T workgroups turn the queries,
-// one token each, from their own table.  Same bits as
-// affine_cache_write_small<.., true> (the same turned fp16 values, group
-// extrema, affine_params and affine_code).  Fits when D % 8 == 0, D <= 512, gs / 8
-// a power of two dividing D / 8, the RoPE meets turn_rows_vec_ok and
-// T <= kLaneMaxTokens (affine_lanes_fit).
-constexpr int kLaneMaxTokens = 256;
-
-__host__ __device__ inline int affine_lanes_tpw(const int D) { return D / 8 >= 64 ? 1 : 64 / (D / 8); }
-
-__host__ __device__ inline bool affine_lanes_fit(const int T, const int D, const int gs, const int rot,
-                                                 const int trad) {
-  const int lanes = gs / 8;
-  return T > 0 && T <= kLaneMaxTokens && D % 8 == 0 && D <= kWriteMaxDim && gs % 8 == 0 && lanes <= 64 &&
-         (lanes & (lanes - 1)) == 0 && D % gs == 0 && turn_rows_vec_ok(D, rot, trad);
-}
-
-template <int BITS>
-__global__ __launch_bounds__(256) void affine_write_rope_lanes(WriteArgs a) {
-  constexpr int PW = 32 / BITS;
-  constexpr int UQ = 2;
-  const int tid = threadIdx.x, NT = blockDim.x;
-  const int T = a.T, D = a.D, per = D / 8;
-  const int tpw = affine_lanes_tpw(D), nch = (T + tpw - 1) / tpw;
-  const int bid = blockIdx.x;
-  const bool qwg = bid >= a.Hkv * nch;
-  const int h = bid % a.Hkv;
-  const int t0 = qwg ? bid - a.Hkv * nch : (bid / a.Hkv) * tpw;  // first token of the workgroup
-  const int nt = qwg ? 1 : min(tpw, T - t0);                     // its tokens
-  const bool app = a.slot_ids != nullptr;
-  const int rot = a.rope.rot, half = rot / 2, trad = a.rope.traditional;
-  const int nrp = rot / 8;  // pieces inside the rotation
-  const int tl = tid / per, c = tid % per;  // local token, piece
-  const bool mine = !qwg && tl < nt;
-  const bool rotp = c < nrp;
-  const bool lo_half = c < nrp / 2;  // neox: the piece holds the first element of its pairs
-
-  // ---- loads that depend on nothing
-  h16x8 klo = {}, khi = {}, vv = {};
-  TurnRowsVec<UQ> tq(1, a.Hq, D, a.rope);  // query workgroups: the heads of token t0
-  const h16* qin = a.q_in + (size_t)t0 * a.Hq * D;
-  if (qwg) {
-    tq.issue(qin, D, a.rope, tid, NT);
-  } else if (mine) {
-    const size_t ro = ((size_t)(t0 + tl) * a.Hkv + h) * D;
-    klo = *reinterpret_cast<const h16x8*>(a.keys + ro + 8 * c);
-    if (rotp && !trad) khi = *reinterpret_cast<const h16x8*>(a.keys + ro + 8 * (lo_half ? c + nrp / 2 : c - nrp / 2));
-    vv = *reinterpret_cast<const h16x8*>(a.values + ro + 8 * c);
-  }
-  float inv_in[2];  // half <= kWriteMaxDim / 2 = 128 <= 2 * NT
-#pragma unroll
-  for (int k = 0; k < 2; ++k) inv_in[k] = tid + k * NT < half ? a.rope.inv_freq[tid + k * NT] : 0.f;
-  // slots and positions of every token of the call (decode append: derived as
-  // cache_slots does): the workgroup's own, and the rest for the kv_lens update
-  // the last workgroup makes
-  constexpr int KT = kLaneMaxTokens / 64;
-  int sl[KT], pos[KT], sq[KT];
-#pragma unroll
-  for (int k = 0; k < KT; ++k) {
-    const int tg = tid + k * NT;
-    sl[k] = -1;
-    pos[k] = 0;
-    sq[k] = -1;
-    if (tg < T) {
-      if (app) {
-        const int s = a.slot_ids[tg];
-        if (s >= 0 && s < a.S) {
-          sq[k] = s;
-          pos[k] = a.kv_lens[s];
-          const int col = pos[k] / a.bs;
-          if (pos[k] >= 0 && col < a.max_blocks) {
-            const int b = a.bt[(size_t)s * a.max_blocks + col];
-            if (b >= 0) sl[k] = b * a.bs + pos[k] % a.bs;
-          }
-        }
-      } else if (tg >= t0 && tg < t0 + nt) {
-        sl[k] = a.slot_mapping[tg];
-        pos[k] = a.rope.positions[tg];
-      }
-    }
-  }
-  __shared__ int sslot[kLaneMaxTokens], spos[kLaneMaxTokens], sseq[kLaneMaxTokens];
-  __shared__ float sinv[kWriteMaxDim / 2];
-  __shared__ float2 stab[256];  // nt * half <= 4 * (tokens * D / 8) <= 256
-#pragma unroll
-  for (int k = 0; k < KT; ++k) {
-    const int tg = tid + k * NT;
-    if (tg < T) {
-      sslot[tg] = sl[k] >= 0 && sl[k] / a.bs < a.nb ? sl[k] : -1;  // a page outside the pool is not written
-      spos[tg] = pos[k];
-      sseq[tg] = sq[k];
-    }
-  }
-#pragma unroll
-  for (int k = 0; k < 2; ++k)
-    if (tid + k * NT < half) sinv[tid + k * NT] = inv_in[k];
-  __syncthreads();  // every kv_lens read of the workgroup has returned
-  int arrived = 0;
-  if (app && tid == 0) arrived = __hip_atomic_fetch_add(a.counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  for (int i = tid; i < nt * half; i += NT) {
-    float sn, cs;
-    rope_sincos((float)spos[t0 + i / half] * sinv[i % half], &sn, &cs);
-    stab[i] = float2{sn, cs};
-  }
-  __syncthreads();
-
-  auto finish = [&]() {  // the end of the workgroup: the last one counted advances kv_lens
-    if (!app) return;
-    __shared__ int slast;
-    if (tid == 0) {
-      slast = arrived == (int)gridDim.x - 1;
-      if (arrived == (int)gridDim.x - 1) __hip_atomic_store(a.counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    __syncthreads();
-    // every token of the call (the last one counted may be a query workgroup), from the
-    // lengths read at the start (a sequence named twice gets the same length twice)
-    if (slast)
-      for (int i = tid; i < T; i += NT)
-        if (sseq[i] >= 0) a.kv_lens[sseq[i]] = spos[i] + 1;
-  };
-  if (qwg) {
-    h16* qout = a.q + (size_t)t0 * a.Hq * D;
-    tq.finish(qout, a.Hq, D, a.rope, stab);
-    for (int i0 = tid + UQ * NT; i0 < tq.n; i0 += UQ * NT) {
-      tq.issue(qin, D, a.rope, i0, NT);
-      tq.finish(qout, a.Hq, D, a.rope, stab);
-    }
-    finish();
-    return;
-  }
-
-  // ---- this lane's K values, turned and rounded to fp16 (rope_pair's values)
-  float kx[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) kx[j] = (float)klo[j];
-  if (rotp && mine) {
-    const float2* tt = stab + tl * half;
-    if (trad) {
-#pragma unroll
-      for (int j = 0; j < 8; j += 2) {
-        float y0, y1;
-        rope_rotate_sc(kx[j], kx[j + 1], tt[4 * c + j / 2], y0, y1);
-        kx[j] = (float)(h16)y0;
-        kx[j + 1] = (float)(h16)y1;
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        float y0, y1;
-        if (lo_half) {
-          rope_rotate_sc(kx[j], (float)khi[j], tt[8 * c + j], y0, y1);
-          kx[j] = (float)(h16)y0;
-        } else {
-          rope_rotate_sc((float)khi[j], kx[j], tt[8 * (c - nrp / 2) + j], y0, y1);
-          kx[j] = (float)(h16)y1;
-        }
-      }
-    }
-  }
-  float vx[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) vx[j] = (float)vv[j];
-
-  // ---- group extrema across the gs / 8 lanes of a group (aligned: a row is D / 8 lanes)
-  const int lanes = a.gs / 8;
-  float kmin = kx[0], kmax = kx[0], vmin = vx[0], vmax = vx[0];
-#pragma unroll
-  for (int j = 1; j < 8; ++j) {
-    kmin = fminf(kmin, kx[j]);
-    kmax = fmaxf(kmax, kx[j]);
-    vmin = fminf(vmin, vx[j]);
-    vmax = fmaxf(vmax, vx[j]);
-  }
-  for (int o = 1; o < lanes; o <<= 1) {
-    kmin = fminf(kmin, __shfl_xor(kmin, o, 64));
-    kmax = fmaxf(kmax, __shfl_xor(kmax, o, 64));
-    vmin = fminf(vmin, __shfl_xor(vmin, o, 64));
-    vmax = fmaxf(vmax, __shfl_xor(vmax, o, 64));
-  }
-  const int slot = mine ? sslot[t0 + tl] : -1;
-  if (slot >= 0) {
-  const float n_bins = (float)((1 << BITS) - 1);
-  float ksc, kbi, vsc, vbi;
-  affine_params(kmin, kmax, n_bins, ksc, kbi);
-  affine_params(vmin, vmax, n_bins, vsc, vbi);
-  const int off = slot % a.bs;
-  const size_t ph = (size_t)(slot / a.bs) * a.Hkv + h;
-  // K codes: 8 dims are 8 / PW words
-#pragma unroll
-  for (int w = 0; w < 8 / PW; ++w) {
-    uint32_t word = 0;
-#pragma unroll
-    for (int k = 0; k < PW; ++k) word |= affine_code(kx[w * PW + k], ksc, kbi, n_bins) << (k * BITS);
-    a.kc[(ph * a.bs + off) * (size_t)(D / PW) + (8 * c) / PW + w] = word;
-  }
-  // V codes: each dim's value goes to its own word (the word holds consecutive tokens)
-  constexpr uint32_t M = (1u << BITS) - 1u;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const uint32_t code = affine_code(vx[j], vsc, vbi, n_bins);
-    uint32_t* wp = a.vc + v_word_index<BITS>(ph, off, 8 * c + j, D, a.bs);
-    if (BITS == 8) {
-      reinterpret_cast<uint8_t*>(wp)[off % 4] = (uint8_t)code;
-    } else {  // the nibble by two atomics that return nothing (tokens of the call may share the word)
-      const int sh = v_shift<BITS>(off % PW);
-      atomicAnd(wp, ~(M << sh));
-      atomicOr(wp, code << sh);
-    }
-  }
-  if (c % lanes == 0) {  // the group's first lane: scale and bias
-    const int G = D / a.gs;
-    const size_t si = (ph * G + (8 * c) / a.gs) * a.bs + off;
-    a.ks[si] = (h16)ksc;
-    a.kb[si] = (h16)kbi;
-    a.vs[si] = (h16)vsc;
-    a.vb[si] = (h16)vbi;
-  }
-  }  // slot >= 0
-  finish();  // every thread, once (it holds a barrier)
-}
-
 }  // namespace emx

@@ -64,7 +64,7 @@ def test_rope_rows_vs_float64(cuda, traditional, kind):
 
 @pytest.mark.parametrize("bits,T,rot,trad", [(4, 300, 128, 0), (4, 32, 128, 0), (8, 77, 128, 0), (4, 32, 64, 0),
                                              (4, 300, 64, 0), (8, 32, 128, 0), (4, 32, 128, 1), (8, 40, 64, 1),
-                                             (4, 7, 32, 0)])
+                                             (4, 7, 32, 0), (4, 24, 128, 0)])
 def test_fused_write_equals_rotate_then_write(cuda, bits, T, rot, trad):
     """One launch (rotate K in LDS, quantize) == emx_rope_rows on K, then emx_affine_cache_write: every byte.
     The queries come out turned into a separate tensor (dims past rot copied), or turned in place."""
@@ -75,6 +75,8 @@ def test_fused_write_equals_rotate_then_write(cuda, bits, T, rot, trad):
     k = torch.from_numpy((rng.standard_normal((T, hkv, d)) * 2).astype(np.float16)).to(cuda)
     v = torch.from_numpy((rng.standard_normal((T, hkv, d)) * 2).astype(np.float16)).to(cuda)
     slots = torch.from_numpy(rng.permutation(nb * bs)[:T].astype(np.int32)).to(cuda)
+    if T == 24:  # consecutive slots: tokens of the call share value words
+        slots = torch.arange(100, 100 + T, dtype=torch.int32, device=cuda)
     pos = torch.from_numpy(rng.integers(0, 30000, T).astype(np.int32)).to(cuda)
     tables = torch.zeros((1, 1), dtype=torch.int32, device=cuda)
     lens = torch.zeros(1, dtype=torch.int32, device=cuda)
