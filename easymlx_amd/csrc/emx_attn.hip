@@ -1249,45 +1249,6 @@ int emx_paged_attention_dense(const void* queries, int num_tokens, int num_q_hea
 
 size_t emx_fp8_write_workspace_bytes(void) { return sizeof(float) * 2 * emx::kFp8Parts; }
 
-// The one-workgroup write (fp8_write_one, plus workgroups for the queries) when
-// the call fits it and its pointers allow 16-byte loads and 8-byte stores; false:
-// the caller launches the general kernels.
-static bool launch_fp8_one(const emx::Fp8WriteArgs& a, int dtype, bool turn_q, hipStream_t st) {
-  const int rot = a.rope.inv_freq ? a.rope.rot : 0, trad = a.rope.traditional;
-  auto fits_as = [&](auto big) {
-    constexpr bool B = decltype(big)::value;
-    return dtype == EMX_DTYPE_F16    ? emx::fp8_one_fits<emx::h16, B>(a.T, a.Hkv, a.D, rot, trad)
-           : dtype == EMX_DTYPE_BF16 ? emx::fp8_one_fits<uint16_t, B>(a.T, a.Hkv, a.D, rot, trad)
-                                     : emx::fp8_one_fits<float, B>(a.T, a.Hkv, a.D, rot, trad);
-  };
-  const bool small = fits_as(std::false_type{}), fits = small || fits_as(std::true_type{});
-  const uintptr_t in16 = reinterpret_cast<uintptr_t>(a.k) | reinterpret_cast<uintptr_t>(a.v) |
-                         (turn_q ? reinterpret_cast<uintptr_t>(a.q) | reinterpret_cast<uintptr_t>(a.q_in) : 0);
-  const uintptr_t out8 = reinterpret_cast<uintptr_t>(a.kc) | reinterpret_cast<uintptr_t>(a.vc);
-  if (!fits || (in16 & 15) || (out8 & 7) || (turn_q && (rot <= 0 || a.Hq <= 0))) return false;
-  const int nk = emx::fp8_one_ktasks(a.T, a.Hkv, a.D, rot, trad), nv = a.T * a.Hkv * (a.D / 8);
-  const int ue = small ? 1 : 2;  // Fp8OneCfg::UE
-  const int nw = (nk + nv + ue * 1024 - 1) / (ue * 1024);  // write workgroups
-  int nq = 0;  // query workgroups: two 16-byte tasks per thread
-  if (turn_q) {
-    const long qt = (long)emx::fp8_one_ktasks(a.T, a.Hq, a.D, rot, trad);
-    nq = (int)std::min<long>(8, std::max<long>(1, (qt + 2047) / 2048));
-  }
-  const dim3 g((unsigned)(nw + nq));
-  emx::Fp8WriteArgs b = a;
-  b.nwg = nw;
-  if (!turn_q) b.q = nullptr;
-  typedef void (*Fn)(emx::Fp8WriteArgs);
-  Fn fn;
-  switch (dtype) {
-    case EMX_DTYPE_F16: fn = small ? emx::fp8_write_one<emx::F16, false> : emx::fp8_write_one<emx::F16, true>; break;
-    case EMX_DTYPE_BF16: fn = small ? emx::fp8_write_one<emx::BF16, false> : emx::fp8_write_one<emx::BF16, true>; break;
-    default: fn = small ? emx::fp8_write_one<emx::F32, false> : emx::fp8_write_one<emx::F32, true>; break;
-  }
-  hipLaunchKernelGGL(fn, g, dim3(1024), 0, st, b);
-  return true;
-}
-
 static int fp8_write_impl(const void* keys, const void* values, int dtype, const int32_t* slot_mapping, int num_tokens,
                           int num_kv_heads, int head_dim, int page_size, int num_blocks, uint8_t* key_cache,
                           uint8_t* value_cache, float* k_scales, float* v_scales, void* workspace,
@@ -1336,7 +1297,6 @@ static int fp8_write_impl(const void* keys, const void* values, int dtype, const
   const int nwrite = (int)std::min<size_t>(1024, (n / 4 + 255) / 256);
   const bool turn_q = rope.inv_freq != nullptr && queries != nullptr;
   if (n <= (size_t)emx::kFp8SelfMax) {  // one launch: each workgroup takes the maxima itself
-    if (launch_fp8_one(a, dtype, turn_q, st)) return check_launch("fp8_write_one");
     a.nwg = (int)((n / 4 + 1023) / 1024);
     const dim3 g1((unsigned)(a.nwg + (turn_q ? 4 : 0)));  // + workgroups that turn the queries
     switch (dtype) {
@@ -1479,7 +1439,6 @@ int emx_fp8_cache_append_rope(const void* keys, const void* values, int dtype, c
     }
     return check_launch("fp8_append_grid");
   }
-  if (launch_fp8_one(a, dtype, queries != nullptr, st)) return check_launch("fp8_write_one (append)");
   a.nwg = (int)((n / 4 + 1023) / 1024);
   const dim3 g1((unsigned)(a.nwg + (queries ? 4 : 0)));  // + workgroups that turn the queries
   switch (dtype) {

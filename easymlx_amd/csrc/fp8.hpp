@@ -11,8 +11,9 @@
 //     neither written nor counted in the call's maxima.
 // Two launches: per-workgroup maxima into a small workspace, then every
 // workgroup reduces them and quantizes its share (4 values per thread).  Writes
-// of up to kFp8SelfMax values per tensor (decode appends) take one launch in
-// which every workgroup computes the maxima itself.
+// of up to kFp8SelfMax values per tensor take one launch in which every
+// workgroup computes the maxima itself; the decode append (fp8_append_grid)
+// spreads the call over small workgroups that exchange their maxima once.
 #pragma once
 
 #include "common.hpp"
@@ -370,26 +371,9 @@ __global__ __launch_bounds__(SELF ? 1024 : 256) void fp8_write(Fp8WriteArgs a, i
 }
 
 
-// ---- One-launch write of a small call (decode appends, small writes), in
-// workgroups of 1024 threads.  Each of the a.nwg write workgroups loads every
-// value of the call into registers -- K in the row tasks of TurnRowsVec (a piece
-// of 8 values and, where the rotation pairs it with the piece half a rotation
-// on, that piece too), V in pieces of 8 -- plus its own share of the tasks to
-// encode, all in one round trip that goes out before the slots and positions
-// are known.  It derives slots and positions into LDS, builds the (sin, cos)
-// table of the call's (token, pair) angles, turns K from it and takes both
-// maxima in one block reduction (the call's single scale pair, the same in
-// every workgroup: a maximum is exact), then encodes and stores 8 codes per
-// piece of its share (spreading the encoder's work over workgroups; one
-// workgroup encoding a 32-sequence append took ~30 us).  Workgroups a.nwg..
-// turn the queries from their own copy of the table.  The bits are fp8_write's:
-// the same turned values (rope_rotate_sc on rope_sincos of the same angles,
-// rounded to the input dtype), maxima over the same live values, the same
-// encoder.  Fits when D % 8 == 0, the RoPE (if any) meets turn_rows_vec_ok,
-// T * rot / 2 <= kFp8RopeTab, and the tasks fit the registers (fp8_one_fits;
-// BIG: twice the tasks per thread).
+// 8 values of T, raw (16-byte loads; 32 bytes for fp32).
 template <typename T>
-struct Fp8Piece {  // 8 values of T, raw
+struct Fp8Piece {
   u32x4 w[sizeof(T) / 2];
   __device__ __forceinline__ void load(const T* p) {
 #pragma unroll
@@ -407,264 +391,6 @@ struct Fp8Piece {  // 8 values of T, raw
     }
   }
 };
-
-template <typename T, bool BIG>
-struct Fp8OneCfg {
-  static constexpr int NTH = 1024;
-  static constexpr int UK = (sizeof(T) == 4 ? 1 : 2) * (BIG ? 2 : 1);  // K tasks per thread
-  static constexpr int UV = 2 * UK;                  // V pieces per thread
-  static constexpr int UE = BIG ? 2 : 1;             // tasks each thread encodes
-  static constexpr int UQ = 2;                       // query tasks per thread and pass
-  static constexpr int UTAB = kFp8RopeTab / NTH;     // table entries per thread
-};
-
-__host__ __device__ inline int fp8_one_ktasks(const int T, const int Hkv, const int D, const int rot, const int trad) {
-  const int nrot = rot <= 0 ? 0 : (trad ? rot / 8 : rot / 16);
-  return T * Hkv * (nrot + (D - (rot > 0 ? rot : 0)) / 8);
-}
-
-template <typename T, bool BIG>
-__host__ __device__ inline bool fp8_one_fits(const int nT, const int Hkv, const int D, const int rot, const int trad) {
-  typedef Fp8OneCfg<T, BIG> C;
-  if (nT > kFp8AppendMax || D % 8 != 0) return false;
-  if (rot > 0 && (!turn_rows_vec_ok(D, rot, trad) || nT * (rot / 2) > kFp8RopeTab)) return false;
-  return fp8_one_ktasks(nT, Hkv, D, rot, trad) <= C::UK * C::NTH && nT * Hkv * (D / 8) <= C::UV * C::NTH;
-}
-
-template <typename Tag, bool BIG>
-__global__ __launch_bounds__(1024) void fp8_write_one(Fp8WriteArgs a) {
-  typedef typename Tag::T T;
-  typedef Fp8OneCfg<T, BIG> C;
-  constexpr int NTH = C::NTH, UK = C::UK, UV = C::UV, UE = C::UE, UQ = C::UQ, UTAB = C::UTAB;
-  const int tid = threadIdx.x;
-  const RopeArgs& r = a.rope;
-  const bool rope = r.inv_freq != nullptr;
-  const int rot = rope ? r.rot : 0, half = rot / 2;
-  const int nwg = a.nwg;
-  const bool qwg = (int)blockIdx.x >= nwg;  // workgroups a.nwg.. turn the queries
-  const bool app = a.slot_ids != nullptr;
-  const T* k = reinterpret_cast<const T*>(a.k);
-  const T* v = reinterpret_cast<const T*>(a.v);
-  const int nrot = rope ? (r.traditional ? rot / 8 : rot / 16) : 0;
-  const int per = nrot + (a.D - rot) / 8;  // K tasks per (token, head) row
-  const int nk = a.T * a.Hkv * per, nv = a.T * a.Hkv * (a.D / 8);
-
-  // ---- loads that depend on nothing: values (or queries), the table's inv_freq
-  Fp8Piece<T> klo[UK], khi[UK], vp[UV], elo[UE], ehi[UE];
-  TurnRowsVec<UQ> tq(a.T, a.Hq, a.D, r);
-  const int qstride = (int)(gridDim.x - nwg) * NTH, qfirst = (int)(blockIdx.x - nwg) * NTH + tid;
-  auto k_piece_off = [&](const int c) { return c < nrot ? 8 * c : rot + 8 * (c - nrot); };
-  if (qwg) {
-    tq.issue(a.q_in, a.D, r, qfirst, qstride);
-  } else {
-    // this thread's share of the codes (tasks j < nk: K, then V pieces)
-#pragma unroll
-    for (int e = 0; e < UE; ++e) {
-      const int j = (int)blockIdx.x * NTH + tid + e * nwg * NTH;
-      if (j < nk) {
-        const int rr = j / per, c = j % per;
-        const T* row = k + (size_t)rr * a.D;
-        elo[e].load(row + k_piece_off(c));
-        if (c < nrot && !r.traditional) ehi[e].load(row + half + 8 * c);
-      } else if (j < nk + nv) {
-        elo[e].load(v + 8 * (size_t)(j - nk));
-      }
-    }
-    // every value of the call, for the maxima
-#pragma unroll
-    for (int u = 0; u < UK; ++u) {
-      const int i = tid + u * NTH;
-      if (i < nk) {
-        const int rr = i / per, c = i % per;
-        const T* row = k + (size_t)rr * a.D;
-        klo[u].load(row + k_piece_off(c));
-        if (c < nrot && !r.traditional) khi[u].load(row + half + 8 * c);
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < UV; ++u) {
-      const int i = tid + u * NTH;
-      if (i < nv) vp[u].load(v + 8 * (size_t)i);
-    }
-  }
-  float invr[UTAB];
-#pragma unroll
-  for (int u = 0; u < UTAB; ++u) {
-    const int i = tid + u * NTH;
-    invr[u] = rope && i < a.T * half ? r.inv_freq[i % half] : 0.f;
-  }
-
-  // ---- slots and positions (decode append: derived as cache_slots does) into LDS
-  __shared__ int fslot[kFp8AppendMax], fpos[kFp8AppendMax], fseq[kFp8AppendMax];
-  if (tid < a.T) {
-    int sl = -1, pos = 0, sq = -1;
-    if (app) {
-      const int s = a.slot_ids[tid];
-      if (s >= 0 && s < a.S) {
-        sq = s;
-        pos = a.kv_lens[s];
-        const int col = pos / a.bs;
-        if (pos >= 0 && col < a.max_blocks) {
-          const int b = a.bt[(size_t)s * a.max_blocks + col];
-          if (b >= 0) sl = b * a.bs + pos % a.bs;
-        }
-      }
-    } else {
-      sl = a.slot[tid];
-      pos = rope ? r.positions[tid] : 0;
-    }
-    fslot[tid] = sl >= 0 && sl / a.bs < a.nb ? sl : -1;  // a page outside the pool: skipped
-    fpos[tid] = pos;
-    fseq[tid] = sq;
-  }
-  __syncthreads();  // every kv_lens read of the workgroup has returned
-  int arrived = 0;
-  if (app && tid == 0) arrived = __hip_atomic_fetch_add(a.counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-
-  // ---- (sin, cos) of every (token, pair) angle
-  __shared__ float2 rsc[kFp8RopeTab];
-  if (rope) {
-#pragma unroll
-    for (int u = 0; u < UTAB; ++u) {
-      const int i = tid + u * NTH;
-      if (i < a.T * half) {
-        float sn, cs;
-        rope_sincos((float)fpos[i / half] * invr[u], &sn, &cs);
-        rsc[i] = float2{sn, cs};
-      }
-    }
-  }
-  __syncthreads();
-
-  auto finish = [&]() {  // the end of the workgroup: the last one counted advances kv_lens
-    if (!app) return;
-    __shared__ int slast;
-    if (tid == 0) {
-      slast = arrived == (int)gridDim.x - 1;
-      if (arrived == (int)gridDim.x - 1) __hip_atomic_store(a.counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    __syncthreads();
-    if (slast && tid < a.T && fseq[tid] >= 0) a.kv_lens[fseq[tid]] = fpos[tid] + 1;
-  };
-  if (qwg) {
-    tq.finish(a.q, a.Hq, a.D, r, rope ? rsc : nullptr);
-    for (int i0 = qfirst + UQ * qstride; i0 < tq.n; i0 += UQ * qstride) {
-      tq.issue(a.q_in, a.D, r, i0, qstride);
-      tq.finish(a.q, a.Hq, a.D, r, rope ? rsc : nullptr);
-    }
-    finish();
-    return;
-  }
-
-  // ---- K turned (rounded to T; turned again for the codes rather than held),
-  // maxima over the live tokens
-  auto turned = [&](const Fp8Piece<T>& lo, const Fp8Piece<T>& hi, const int c, const int t, float (&kx)[8],
-                    float (&ky)[8]) {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      kx[j] = lo.at(j);
-      ky[j] = 0.f;
-    }
-    if (c >= nrot) return;
-    const float2* tt = rsc + t * half;
-    if (r.traditional) {
-#pragma unroll
-      for (int j = 0; j < 8; j += 2) {
-        float y0, y1;
-        rope_rotate_sc(kx[j], kx[j + 1], tt[4 * c + j / 2], y0, y1);
-        kx[j] = round_to(y0, (T*)nullptr);
-        kx[j + 1] = round_to(y1, (T*)nullptr);
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        float y0, y1;
-        rope_rotate_sc(kx[j], hi.at(j), tt[8 * c + j], y0, y1);
-        kx[j] = round_to(y0, (T*)nullptr);
-        ky[j] = round_to(y1, (T*)nullptr);
-      }
-    }
-  };
-  float mk = 0.f, mv = 0.f;
-#pragma unroll
-  for (int u = 0; u < UK; ++u) {
-    const int i = tid + u * NTH;
-    if (i >= nk) continue;
-    const int rr = i / per, c = i % per, t = rr / a.Hkv;
-    if (fslot[t] < 0) continue;
-    float kx[8], ky[8];
-    turned(klo[u], khi[u], c, t, kx, ky);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) mk = fmaxf(mk, fmaxf(fabsf(kx[j]), fabsf(ky[j])));
-  }
-#pragma unroll
-  for (int u = 0; u < UV; ++u) {
-    const int i = tid + u * NTH;
-    if (i < nv && fslot[i / (a.Hkv * (a.D / 8))] >= 0) {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) mv = fmaxf(mv, fabsf(vp[u].at(j)));
-    }
-  }
-  mk = wave_max(mk);
-  mv = wave_max(mv);
-  __shared__ float sm[2][NTH / 64];
-  if ((tid & 63) == 0) {
-    sm[0][tid >> 6] = mk;
-    sm[1][tid >> 6] = mv;
-  }
-  __syncthreads();
-  float a0 = 0.f, a1 = 0.f;
-#pragma unroll
-  for (int i = 0; i < NTH / 64; ++i) {
-    a0 = fmaxf(a0, sm[0][i]);
-    a1 = fmaxf(a1, sm[1][i]);
-  }
-  const float ksc = a0 / 240.0f, vsc = a1 / 240.0f;
-  const float kq = fmaxf(ksc, 1e-12f), vq = fmaxf(vsc, 1e-12f);
-
-  // ---- codes: 8 bytes per piece, [nb, bs, Hkv, D]
-  auto row_of = [&](const int rr, const int sl) {  // byte offset of (token row rr, its slot) in the pages
-    return ((size_t)sl * a.Hkv + rr % a.Hkv) * (size_t)a.D;
-  };
-  auto enc8 = [](const float (&x)[8], const float q) {
-    uint32_t lo = 0, hi = 0;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      lo |= f32_to_e4m3(x[j] / q) << (8 * j);
-      hi |= f32_to_e4m3(x[j + 4] / q) << (8 * j);
-    }
-    return uint2{lo, hi};
-  };
-#pragma unroll
-  for (int e = 0; e < UE; ++e) {
-    const int j = (int)blockIdx.x * NTH + tid + e * nwg * NTH;
-    if (j < nk) {
-      const int rr = j / per, c = j % per, t = rr / a.Hkv;
-      const int sl = fslot[t];
-      if (sl < 0) continue;
-      float kx[8], ky[8];
-      turned(elo[e], ehi[e], c, t, kx, ky);
-      uint8_t* dst = a.kc + row_of(rr, sl);
-      *reinterpret_cast<uint2*>(dst + k_piece_off(c)) = enc8(kx, kq);
-      if (c < nrot && !r.traditional) *reinterpret_cast<uint2*>(dst + half + 8 * c) = enc8(ky, kq);
-      if (c == 0 && rr % a.Hkv == 0) {  // once per written token: the page keeps the larger scale
-        atomicMax(reinterpret_cast<unsigned int*>(a.ks) + sl / a.bs, __float_as_uint(ksc));
-        atomicMax(reinterpret_cast<unsigned int*>(a.vs) + sl / a.bs, __float_as_uint(vsc));
-      }
-    } else if (j < nk + nv) {
-      const int i = j - nk;
-      const int rr = i / (a.D / 8), c = i % (a.D / 8), t = rr / a.Hkv;
-      const int sl = fslot[t];
-      if (sl < 0) continue;
-      float x[8];
-#pragma unroll
-      for (int q = 0; q < 8; ++q) x[q] = elo[e].at(q);
-      *reinterpret_cast<uint2*>(a.vc + row_of(rr, sl) + 8 * c) = enc8(x, vq);
-    }
-  }
-  finish();
-}
-
 
 // ---- Decode append by a grid that waits on itself once (fp8_append_grid).
 // The call's single scale pair needs the maxima of every value before any code
