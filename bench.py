@@ -225,12 +225,13 @@ class Setup:
             torch.cuda.synchronize()
             assert torch.equal(out, eager), f"C-ABI call differs from paged_attention ({wl.name})"
 
-        # The same batch one step later in a model's decode: kv_lens of other contents (sequence 0
-        # one token shorter; its pages hold that token too).  Alternating the two every `layers`
-        # calls gives each model step's first layer a decode without a cached plan, as in serving.
+        # The same batch one decode step earlier: every sequence one token shorter (its pages hold
+        # the token too).  Alternating the two every `layers` calls gives each model step's first
+        # layer new kv_lens, as in serving; the decode's plan is keyed by the per-sequence item
+        # counts, which a one-token step changes only where a sequence crosses an item boundary.
         lens_b = wl.kv_lens.copy()
-        if wl.single_token_decode and lens_b[0] > 1:
-            lens_b[0] -= 1
+        if wl.single_token_decode:
+            lens_b = np.maximum(lens_b - 1, np.minimum(lens_b, 1)).astype(lens_b.dtype)
         self.kv_lens_b = torch.from_numpy(lens_b).to(dev)
         self.bytes_b = int(wl.kv_bytes() * (int(lens_b.sum()) / max(1, int(wl.kv_lens.sum()))))
         ikl = 18  # position of kv_lens in the argument tuple
@@ -774,9 +775,11 @@ def main():
         "call_us_back_to_back": round(call_us, 3),
         "plan_cache": {"layers_per_step": layers, "us_same_kv_lens": round(us_cached, 3),
                        "us_new_kv_lens_every_call": round(us_new, 3),
-                       "what": "the decode keeps its work split in the workspace, keyed by kv_lens: a model "
-                               "step's first layer computes it, the other layers reuse it; the timed calls "
-                               "change kv_lens every `layers_per_step` calls"},
+                       "what": "the decode keeps its work split in the workspace, keyed by the per-sequence "
+                               "counts of 256-token items: the other layers of a step reuse it, and so does "
+                               "the next step unless a sequence crosses an item boundary; the timed calls "
+                               "alternate kv_lens one decode step apart (every sequence one token longer) every "
+                               "`layers_per_step` calls, and every call for us_new_kv_lens_every_call"},
         "kernel_us": {"mean": round(k_avg_us, 3), "p10": round(float(np.percentile(kt, 10)), 3),
                       "p50": round(float(np.percentile(kt, 50)), 3), "p90": round(float(np.percentile(kt, 90)), 3)},
         "roofline": {
