@@ -565,6 +565,43 @@ def aux_quantize_on_write(dev):
     warm(call_rope, 0.3)
     res["append_1_token_x32_seqs_rope_q_and_k"] = {"tokens": n,
                                                    "us_p50": round(float(np.median(event_us(call_rope, 200))), 2)}
+    # the reference's logical layout at the op: the c2 decode given codes [nb, bs, Hkv, W] and scales
+    # [nb, bs, Hkv, G] converts the whole pool to pages for the call
+    from easymlx_amd import paged_attention
+    from easymlx_amd.caching.paged import pages_from_logical
+
+    view.write_slots(torch.from_numpy(wl.k).to(dev), torch.from_numpy(wl.v).to(dev),
+                     torch.from_numpy(wl.slot.astype(np.int32)).to(dev))
+    lg = view.to_logical()
+    qd = torch.from_numpy(wl.q).to(dev)
+    qsl = torch.from_numpy(wl.query_start_loc).to(dev)
+    pages = pages_from_logical(lg["k_codes"], lg["k_scales"], lg["k_biases"], lg["v_codes"], lg["v_scales"],
+                               lg["v_biases"], 4, 64)
+
+    def convert(i):
+        pages_from_logical(lg["k_codes"], lg["k_scales"], lg["k_biases"], lg["v_codes"], lg["v_scales"],
+                           lg["v_biases"], 4, 64, out=pages)
+
+    def decode_pages(i):
+        paged_attention(qd, view.k_codes, view.v_codes, view.block_tables, view.kv_lens, qsl, k_scales=view.k_scales,
+                        k_biases=view.k_biases, v_scales=view.v_scales, v_biases=view.v_biases, bits=4, group_size=64,
+                        single_token_decode=True)
+
+    def decode_logical(i):
+        paged_attention(qd, lg["k_codes"], lg["v_codes"], view.block_tables, view.kv_lens, qsl,
+                        k_scales=lg["k_scales"], k_biases=lg["k_biases"], v_scales=lg["v_scales"],
+                        v_biases=lg["v_biases"], bits=4, group_size=64, single_token_decode=True)
+
+    lay = {"pool_bytes": int(sum(t.numel() * t.element_size() for t in pages))}
+    for name, fn_ in (("convert_pool", convert), ("decode_on_pages", decode_pages),
+                      ("decode_from_logical_layout", decode_logical)):
+        warm(fn_, 0.3)
+        lay[name + "_us_p50"] = round(float(np.median(event_us(fn_, 50))), 2)
+    lay["what"] = ("the c2 batch through paged_attention given the reference's logical affine layout: the op "
+                   "converts the whole pool to pages for the call (a caller that keeps the cache converts it once, "
+                   "AffinePageCacheView.from_logical); one pool, so the decode is partly served by the Infinity "
+                   "Cache here")
+    res["logical_layout_at_the_op"] = lay
     return res
 
 

@@ -848,25 +848,13 @@ class AffinePageCacheView(PageCacheView):
         """A view over pages converted on the device from the logical layout (``emx_affine_pages_from_logical``):
         codes ``[nb, bs, Hkv, D*bits/32]`` (int32/uint32 words), scales/biases ``[nb, bs, Hkv, D/group_size]``
         fp16 -- ``mlx.core.quantize`` of the reference's dense cache ``[nb, bs, Hkv, D]`` (``cache.py:790-791``)."""
-        dev = k_codes.device
-        if dev.type != "cuda":
-            raise RuntimeError("layout conversion runs on the GPU only")
         nb, bs, hkv, w = (int(x) for x in k_codes.shape)
         d = w * 32 // int(bits)
-        G = d // int(group_size)
-        for name, t, shape in (("v_codes", v_codes, (nb, bs, hkv, w)), ("k_scales", k_scales, (nb, bs, hkv, G)),
-                               ("k_biases", k_biases, (nb, bs, hkv, G)), ("v_scales", v_scales, (nb, bs, hkv, G)),
-                               ("v_biases", v_biases, (nb, bs, hkv, G))):
-            if tuple(t.shape) != shape:
-                raise ValueError(f"{name} must be {list(shape)} in the logical layout, got {list(t.shape)}")
         view = affine_pool(num_blocks=nb, num_kv_heads=hkv, head_dim=d, block_size=bs, bits=int(bits),
-                           group_size=int(group_size), block_tables=block_tables.to(dev), kv_lens=kv_lens.to(dev))
-        src = [x.contiguous() for x in (k_codes, v_codes)]
-        par = [x.to(torch.float16).contiguous() for x in (k_scales, k_biases, v_scales, v_biases)]
-        _native.check(_native.load().emx_affine_pages_from_logical(
-            src[0].data_ptr(), src[1].data_ptr(), *(x.data_ptr() for x in par), nb, bs, hkv, d, int(bits),
-            int(group_size), view.key_cache.data_ptr(), view.value_cache.data_ptr(), view.k_scales.data_ptr(),
-            view.k_biases.data_ptr(), view.v_scales.data_ptr(), view.v_biases.data_ptr(), _stream_ptr(dev)))
+                           group_size=int(group_size), block_tables=block_tables.to(k_codes.device),
+                           kv_lens=kv_lens.to(k_codes.device))
+        pages_from_logical(k_codes, k_scales, k_biases, v_codes, v_scales, v_biases, bits, group_size,
+                           out=view.page_arrays())
         return view
 
     def to_logical(self) -> dict[str, torch.Tensor]:
@@ -891,6 +879,37 @@ class AffinePageCacheView(PageCacheView):
             self.v_scales.data_ptr(), self.v_biases.data_ptr(), self.num_blocks, self.block_size, self.num_kv_heads,
             self.head_dim, self.bits, self.group_size, bt.data_ptr(), int(bt.shape[0]), int(bt.shape[1]),
             cu.data_ptr(), total, out_code, k_out.data_ptr(), v_out.data_ptr(), _stream_ptr(k_out.device)))
+
+
+def pages_from_logical(k_codes, k_scales, k_biases, v_codes, v_scales, v_biases, bits, group_size, out=None):
+    """Affine pages ``[key codes, value codes, k_scales, k_biases, v_scales, v_biases]`` in this library's
+    layout (``AffinePageCacheView``), converted on the device from the logical layout: codes
+    ``[nb, bs, Hkv, D*bits/32]``, scales/biases ``[nb, bs, Hkv, D/group_size]`` (``emx_affine_pages_from_logical``).
+    ``out``: the six page tensors to fill (new ones when None)."""
+    dev = k_codes.device
+    if dev.type != "cuda":
+        raise RuntimeError("layout conversion runs on the GPU only")
+    if k_codes.ndim != 4:
+        raise ValueError("logical-layout codes must be rank-4: [num_blocks, block_size, num_kv_heads, W]")
+    nb, bs, hkv, w = (int(x) for x in k_codes.shape)
+    bits, group_size = int(bits), int(group_size)
+    d = w * 32 // bits
+    G = d // group_size
+    for name, t, shape in (("v_codes", v_codes, (nb, bs, hkv, w)), ("k_scales", k_scales, (nb, bs, hkv, G)),
+                           ("k_biases", k_biases, (nb, bs, hkv, G)), ("v_scales", v_scales, (nb, bs, hkv, G)),
+                           ("v_biases", v_biases, (nb, bs, hkv, G))):
+        if tuple(t.shape) != shape:
+            raise ValueError(f"{name} must be {list(shape)} in the logical layout, got {list(t.shape)}")
+    if out is None:
+        out = [torch.empty((nb, hkv, bs, w), dtype=torch.int32, device=dev),
+               torch.empty(_v_shape(nb, hkv, d, bs, bits), dtype=torch.int32, device=dev)]
+        out += [torch.empty((nb, hkv, G, bs), dtype=torch.float16, device=dev) for _ in range(4)]
+    src = [x.contiguous() for x in (k_codes, v_codes)]
+    par = [x.to(torch.float16).contiguous() for x in (k_scales, k_biases, v_scales, v_biases)]
+    _native.check(_native.load().emx_affine_pages_from_logical(
+        src[0].data_ptr(), src[1].data_ptr(), *(x.data_ptr() for x in par), nb, bs, hkv, d, bits, group_size,
+        *(t.data_ptr() for t in out), _stream_ptr(dev)))
+    return out
 
 
 def affine_pool(

@@ -56,10 +56,6 @@ def _validate_inputs(queries, key_cache, value_cache, block_tables, kv_lens, que
         raise ValueError("queries must be rank-3: [total_tokens, num_q_heads, head_dim]")
     if not affine and (key_cache.ndim != 4 or value_cache.ndim != 4):
         raise ValueError("key_cache/value_cache must be rank-4: [num_blocks, block_size, num_kv_heads, head_dim]")
-    if affine and key_cache.ndim == 4 and value_cache.ndim == 4:
-        # mlx.core.quantize of the reference's dense [num_blocks, block_size, Hkv, D] caches: the logical layout
-        raise ValueError("affine caches in the logical layout [num_blocks, block_size, num_kv_heads, W] must be "
-                         "converted to pages once (AffinePageCacheView.from_logical / emx_affine_pages_from_logical)")
     if affine and (key_cache.ndim != 4 or value_cache.ndim != 5):
         raise ValueError("affine pages must be key codes [num_blocks, num_kv_heads, block_size, W] and value codes "
                          "[num_blocks, num_kv_heads, block_size/T, head_dim, T*bits/32]")
@@ -153,7 +149,9 @@ def paged_attention(
 ) -> torch.Tensor:
     """Execute paged attention over block-tabled KV caches.
 
-    Dense caches use the reference layout ``[num_blocks, block_size, Hkv, D]``;
+    Dense caches use the reference layout ``[num_blocks, block_size, Hkv, D]``; affine caches may also come in
+    the reference's logical layout (``mlx.core.quantize`` of that dense cache: codes ``[nb, bs, Hkv, W]``,
+    scales / biases ``[nb, bs, Hkv, D/group_size]``), converted to pages for the call;
     an FP8 (E4M3) cache is that layout in ``uint8`` with per-page fp32 scales
     ``k_scale/v_scale [num_blocks]`` (``unified_attention.py:1431``).
     Affine caches (``k_scales`` given) use the page layout of
@@ -168,6 +166,17 @@ def paged_attention(
     if affine and (k_biases is None or v_scales is None or v_biases is None or bits is None or group_size is None):
         raise ValueError("affine caches need k_scales, k_biases, v_scales, v_biases, bits and group_size")
     dev = queries.device
+    if affine and key_cache.ndim == 4 and value_cache.ndim == 4:
+        # the reference's layout: mlx.core.quantize of its dense [num_blocks, block_size, Hkv, D] caches,
+        # codes [nb, bs, Hkv, W] and scales / biases [nb, bs, Hkv, D/group_size].  Converted to pages for
+        # this call, on the device (a whole-pool pass: a caller that keeps the cache converts it once,
+        # AffinePageCacheView.from_logical, and passes the pages)
+        from ..caching.paged import pages_from_logical
+
+        if key_cache.device.type != "cuda":
+            raise RuntimeError("paged_attention runs on the GPU only; the cache is on " + str(key_cache.device))
+        key_cache, value_cache, k_scales, k_biases, v_scales, v_biases = pages_from_logical(
+            key_cache, k_scales, k_biases, value_cache, v_scales, v_biases, bits, group_size)
     block_tables = _i32(block_tables, dev)
     kv_lens = _i32(kv_lens, dev)
     query_start_loc = _i32(query_start_loc, dev)

@@ -65,3 +65,34 @@ def test_attention_over_converted_pages(cuda, bits):
                           group_size=wl.group_size, single_token_decode=True)
     torch.cuda.synchronize()
     assert_attention_close(out.float().cpu().numpy(), oracle_expected(wl), f"converted pages, {bits}-bit")
+
+
+@pytest.mark.parametrize("bits,decode", [(4, True), (8, True), (4, False)])
+def test_op_takes_the_logical_layout(cuda, bits, decode):
+    """``paged_attention`` given the reference's logical layout (rank-4 value codes) converts the pages for the
+    call: the same bits as on pages converted once, and the oracle's attention."""
+    print(f"[op logical layout bits={bits} decode={decode}]", flush=True)
+    if decode:
+        wl = decode_workload("lay", seed=21 + bits, num_seqs=5, ctx_range=(40, 900), bits=bits)
+    else:
+        from easymlx_amd.workloads import unified_workload
+        wl = unified_workload("lay", seed=23, num_prefill=2, chunk=40, prior_range=(0, 300), num_decode=3,
+                              decode_ctx=(50, 600), bits=bits)
+    lp = oracle_logical_pages(wl)
+    t = lambda a: torch.from_numpy(a.view(np.int32) if a.dtype == np.uint32 else a).to(cuda)  # noqa: E731
+    logical = dict(k_codes=t(lp["k"][0]), k_scales=t(lp["k"][1]), k_biases=t(lp["k"][2]), v_codes=t(lp["v"][0]),
+                   v_scales=t(lp["v"][1]), v_biases=t(lp["v"][2]))
+    view = AffinePageCacheView.from_logical(**logical, block_tables=torch.from_numpy(wl.block_tables),
+                                            kv_lens=torch.from_numpy(wl.kv_lens), bits=bits,
+                                            group_size=wl.group_size)
+    q = torch.from_numpy(wl.q).to(cuda)
+    qsl = torch.from_numpy(wl.query_start_loc).to(cuda)
+    a = paged_attention(q, view.key_cache, view.value_cache, view.block_tables, view.kv_lens, qsl,
+                        k_scales=view.k_scales, k_biases=view.k_biases, v_scales=view.v_scales,
+                        v_biases=view.v_biases, bits=bits, group_size=wl.group_size)
+    b = paged_attention(q, logical["k_codes"], logical["v_codes"], view.block_tables, view.kv_lens, qsl,
+                        k_scales=logical["k_scales"], k_biases=logical["k_biases"], v_scales=logical["v_scales"],
+                        v_biases=logical["v_biases"], bits=bits, group_size=wl.group_size)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+    assert_attention_close(b.float().cpu().numpy(), oracle_expected(wl), f"logical layout, {bits}-bit")
