@@ -152,9 +152,9 @@ def test_validation_messages():
         paged_attention(q, k, v, bt, kl, qsl[:-1])
     with pytest.raises(ValueError, match="affine caches need"):
         paged_attention(q, k, v, bt, kl, qsl, k_scales=torch.zeros(1))
-    # affine codes in the logical (mlx.core.quantize) layout: told how to convert them
+    # affine codes in the logical (mlx.core.quantize) layout are converted on the device: no CPU path
     z = torch.zeros(1)
-    with pytest.raises(ValueError, match="from_logical"):
+    with pytest.raises(RuntimeError, match="GPU only"):
         paged_attention(q, k.int(), v.int(), bt, kl, qsl, k_scales=z, k_biases=z, v_scales=z, v_biases=z, bits=4,
                         group_size=8)
     # zero tokens -> zeros without touching a device (unified_attention.py:1425-1426)
