@@ -390,8 +390,12 @@ struct Q4Geom {
 // 64-bit division.  c2: equal item ranges 27.2 us, these 26.1 us (kCostUnit 20..32
 // and kCostLag 31..48 all within 0.2 us of each other); the same ranges handed in
 // from the host measured 24.9-25.1 us, the difference being this search on every
-// workgroup's critical path (~2 us from kv_lens to the boundaries).
-constexpr int kCostItem = 16, kCostUnit = 24, kCostLag = 48;
+// workgroup's critical path (~2 us from kv_lens to the boundaries).  The weights:
+// per-workgroup end clocks of the c2 decode (s_memrealtime, 40 launches) fit
+// end = 1.0 + 2.02 items + 2.54 units + 5.31 (second slot) us, i.e. a unit ~1.26
+// items and the second slot's lag ~2.6 items; unit 16 / lag 40 measured 24.17 us
+// against 24.58 for 24 / 48 (20 / 42: 24.23; 12 / 40: 24.19; 16 / 36: 24.31).
+constexpr int kCostItem = 16, kCostUnit = 16, kCostLag = 40;
 
 struct Q4Balance {
   long long P, Q;
