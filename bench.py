@@ -605,7 +605,7 @@ def aux_quantize_on_write(dev):
     return res
 
 
-def aux_op_layer_step(dev, steps=100, layers=8):
+def aux_op_layer_step(dev, steps=100, layers=32):
     """The public op as a runner calls it, per layer-step of c2: ``concatenate_to_cache`` (quantize-on-write of
     one token per sequence, Llama-3 RoPE fused) then ``UnifiedAttention.forward_native``, over ``layers``
     layers with a cache each (one decode step).  Wall clock per layer-step: eager Python calls, and the decode
