@@ -113,13 +113,17 @@ def test_append_rejects_unsupported_geometry(cuda):
     assert rc == _native.EMX_ERR_UNSUPPORTED
 
 
-@pytest.mark.parametrize("bs,trad,S,hkv", [(128, False, 12, 4), (16, True, 12, 4), (128, False, 80, 1),
-                                            (16, True, 80, 1)])
-def test_fp8_append_matches_the_two_launch_write(cuda, bs, trad, S, hkv):
+@pytest.mark.parametrize("bs,trad,S,hkv,dt,rot", [(128, False, 12, 4, "f16", 128), (16, True, 12, 4, "f16", 128),
+                                                  (128, False, 80, 1, "f16", 128), (16, True, 80, 1, "f16", 128),
+                                                  (128, False, 12, 4, "bf16", 64), (16, True, 12, 4, "f32", 64),
+                                                  (32, False, 12, 2, "f32", 128), (128, True, 12, 4, "bf16", 32)])
+def test_fp8_append_matches_the_two_launch_write(cuda, bs, trad, S, hkv, dt, rot):
     """``emx_fp8_cache_append_rope`` against ``emx_cache_slots`` + ``emx_fp8_cache_write_rope``: codes, page
     scales, kv_lens and the turned queries bit for bit.  80 one-head tokens: more (token, pair) angles than
     the one-launch write's LDS table holds (each value turned with its own sincosf)."""
-    print(f"[fp8 append bs={bs} traditional={trad} S={S} hkv={hkv}]", flush=True)
+    print(f"[fp8 append bs={bs} traditional={trad} S={S} hkv={hkv} dtype={dt} rot={rot}]", flush=True)
+    tdt = {"f16": torch.float16, "bf16": torch.bfloat16, "f32": torch.float32}[dt]
+    code = {"f16": _native.DTYPE_F16, "bf16": _native.DTYPE_BF16, "f32": _native.DTYPE_F32}[dt]
     from easymlx_amd import Fp8PageCacheView
 
     rng = np.random.default_rng(500 + bs + S)
@@ -130,7 +134,7 @@ def test_fp8_append_matches_the_two_launch_write(cuda, bs, trad, S, hkv):
     lens[1] = bs
     lens[2] = mb * bs
     tables[3, lens[3] // bs] = -1
-    rope = RotaryEmbedding(d, traditional=trad, base=10000.0)
+    rope = RotaryEmbedding(rot, traditional=trad, base=10000.0)
     lib = _native.load()
     st = torch.cuda.current_stream(cuda).cuda_stream
 
@@ -153,8 +157,8 @@ def test_fp8_append_matches_the_two_launch_write(cuda, bs, trad, S, hkv):
         bt = base.block_tables
         for rep in range(2):
             n = len(slots)
-            k = torch.from_numpy(rng.standard_normal((n, hkv, d)).astype(np.float16) * 3).to(cuda)
-            v = torch.from_numpy(rng.standard_normal((n, hkv, d)).astype(np.float16) * 3).to(cuda)
+            k = torch.from_numpy(rng.standard_normal((n, hkv, d)).astype(np.float32) * 3).to(cuda).to(tdt)
+            v = torch.from_numpy(rng.standard_normal((n, hkv, d)).astype(np.float32) * 3).to(cuda).to(tdt)
             q = torch.from_numpy(rng.standard_normal((n, hq, d)).astype(np.float16)).to(cuda)
             meta = torch.tensor(list(slots) + list(range(n + 1)), dtype=torch.int32, device=cuda)
             mapping = torch.empty(n, dtype=torch.int32, device=cuda)
@@ -163,12 +167,12 @@ def test_fp8_append_matches_the_two_launch_write(cuda, bs, trad, S, hkv):
                                               bs, a[4].data_ptr(), mapping.data_ptr(), pos.data_ptr(), st))
             qa = torch.empty_like(q)
             _native.check(lib.emx_fp8_cache_write_rope(
-                k.data_ptr(), v.data_ptr(), _native.DTYPE_F16, mapping.data_ptr(), n, hkv, d, bs, nb,
+                k.data_ptr(), v.data_ptr(), code, mapping.data_ptr(), n, hkv, d, bs, nb,
                 a[0].data_ptr(), a[1].data_ptr(), a[2].data_ptr(), a[3].data_ptr(), ws.data_ptr(), ws.numel(),
                 pos.data_ptr(), inv.data_ptr(), rope.dims, int(trad), q.data_ptr(), qa.data_ptr(), hq, st))
             qb = torch.empty_like(q)
             _native.check(lib.emx_fp8_cache_append_rope(
-                k.data_ptr(), v.data_ptr(), _native.DTYPE_F16, meta[:n].data_ptr(), n, bt.data_ptr(), S, mb,
+                k.data_ptr(), v.data_ptr(), code, meta[:n].data_ptr(), n, bt.data_ptr(), S, mb,
                 b[4].data_ptr(), counter.data_ptr(), hkv, d, bs, nb, b[0].data_ptr(), b[1].data_ptr(),
                 b[2].data_ptr(), b[3].data_ptr(), inv.data_ptr(), rope.dims, int(trad), q.data_ptr(), qb.data_ptr(),
                 hq, st))
