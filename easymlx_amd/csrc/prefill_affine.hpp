@@ -283,8 +283,14 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a, const int bid
     if (tid < P::SEGS * PER) {
       const int seg = tid / PER, piece = tid % PER;
       const int arr = seg / G, g = seg % G;
-      const h16* base = arr == 0 ? a.ks : arr == 1 ? a.kb : arr == 2 ? a.vs : a.vb;
-      rsc = *reinterpret_cast<const u32x4*>(base + (ph * G + g) * a.bs + off + 8 * piece);
+      // the four bases as scalar values: a per-lane pick among the struct's fields would
+      // be a vector load of the chosen pointer, and its wait would also wait for the
+      // page loads issued just above
+      const h16 *b_ks = a.ks, *b_kb = a.kb, *b_vs = a.vs, *b_vb = a.vb;
+      asm("" : "+s"(b_ks), "+s"(b_kb), "+s"(b_vs), "+s"(b_vb));
+      const h16* base = arr == 0 ? b_ks : arr == 1 ? b_kb : arr == 2 ? b_vs : b_vb;
+      typedef const __attribute__((address_space(1))) u32x4* gu32x4;  // a global load, not a flat one
+      rsc = *(gu32x4)(base + (ph * G + g) * a.bs + off + 8 * piece);
       // positions past kv_len may hold anything: zero their scales so that p = 0 contributes 0
       const int live = kv_len - (pos0 + 8 * piece);
       if (live < 8) {
