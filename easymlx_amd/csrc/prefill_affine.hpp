@@ -402,12 +402,14 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a, const int bid
     }
     // K scales of the step in fp32, times 2^24 (the codes enter the MFMA as code * 2^-24), and
     // the K biases as the bias MFMA's A rows
-    for (int i = tid; i < G * NT; i += 256) ksf[i / NT][i % NT] = (float)raw_s[i] * kTwo24;
-    if (tid < NT) {
+    // (by waves 1 .. 3: wave 0 also loads the scales)
+    for (int i = tid - 64; i >= 0 && i < G * NT; i += 192) ksf[i / NT][i % NT] = (float)raw_s[i] * kTwo24;
+    if (tid >= 256 - NT) {
+      const int k = tid - (256 - NT);
       h16x8 b = {(h16)0.f, (h16)0.f, (h16)0.f, (h16)0.f, (h16)0.f, (h16)0.f, (h16)0.f, (h16)0.f};
 #pragma unroll
-      for (int g = 0; g < G; ++g) b[2 * g] = b[2 * g + 1] = raw_s[(G + g) * NT + tid];
-      kbe[tid] = b;
+      for (int g = 0; g < G; ++g) b[2 * g] = b[2 * g + 1] = raw_s[(G + g) * NT + k];
+      kbe[k] = b;
     }
   };
 
@@ -452,12 +454,10 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a, const int bid
             cg[(32 * w) / GS] = mfma16x16x32(A, qB[ct][w], cg[(32 * w) / GS]);
           }
           // bias term sum_g kb[t,g] * sum_{d in g} q_d on the matrix core (FP8: no biases)
+          // (every lane reads the key's biases: the B operand is zero outside lane group 0, and
+          // the biases are finite, so the other lane groups add exact zeros)
           f32x4 cb = {0.f, 0.f, 0.f, 0.f};
-          if constexpr (!FP8) {
-            const h16x8 zero8 = {(h16)0.f, (h16)0.f, (h16)0.f, (h16)0.f, (h16)0.f, (h16)0.f, (h16)0.f, (h16)0.f};
-            const h16x8 Ab = jj == 0 ? kbe[16 * at + col] : zero8;
-            cb = mfma16x16x32(Ab, qbias[ct], cb);
-          }
+          if constexpr (!FP8) cb = mfma16x16x32(kbe[16 * at + col], qbias[ct], cb);
           float v[4] = {cb[0], cb[1], cb[2], cb[3]};
 #pragma unroll
           for (int g = 0; g < G; ++g) {
@@ -470,12 +470,13 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a, const int bid
         }
       }
 
-      // ---- mask (causal / window / kv_len) where the half is not fully visible to every column
+      // ---- mask (causal / window / kv_len) where the half is not fully visible to every
+      // column (one branch for both query tiles)
       const int kpos0 = pos0 + 32 * h;
+      const bool full = kpos0 >= start[0] && kpos0 + 31 <= limit[0] && kpos0 >= start[1] && kpos0 + 31 <= limit[1];
+      if (!full) {
 #pragma unroll
-      for (int ct = 0; ct < 2; ++ct) {
-        const bool full = kpos0 >= start[ct] && kpos0 + 31 <= limit[ct];
-        if (!full) {
+        for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
           for (int t = 0; t < 2; ++t)
 #pragma unroll
@@ -483,10 +484,14 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a, const int bid
               const int p = kpos0 + 16 * t + 4 * jj + r;
               if (p < start[ct] || p > limit[ct]) sc[ct][t][r] = -INFINITY;
             }
-        }
       }
 
-      // ---- online softmax per column (base 2)
+      // ---- online softmax per column (base 2).  The reference maximum m_run moves only when
+      // a score passes it by more than kLazyMax (log2 units), so the accumulator is rescaled
+      // rarely (one branch for both query tiles); p <= 2^kLazyMax otherwise, well inside
+      // fp16.  The result does not depend on the reference.
+      float m_new[2];
+      bool grow[2];
 #pragma unroll
       for (int ct = 0; ct < 2; ++ct) {
         float tmax = -INFINITY;
@@ -495,19 +500,22 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a, const int bid
 #pragma unroll
           for (int r = 0; r < 4; ++r) tmax = fmaxf(tmax, sc[ct][t][r]);
         tmax = rows4_max(tmax);
-        // The reference maximum m_run moves only when a score passes it by more than
-        // kLazyMax (log2 units), so the accumulator is rescaled rarely; p <= 2^kLazyMax
-        // otherwise, well inside fp16.  The result does not depend on the reference.
-        const float m_new = fmaxf(m_run[ct], tmax * sc_l2);
-        const bool grow = m_new > m_run[ct] + kLazyMax;  // also the first finite maximum
-        if (__any(grow)) {
-          const float m_ref = grow ? m_new : m_run[ct];
-          const float alpha = grow ? __builtin_amdgcn_exp2f(m_run[ct] - m_ref) : 1.f;
+        m_new[ct] = fmaxf(m_run[ct], tmax * sc_l2);
+        grow[ct] = m_new[ct] > m_run[ct] + kLazyMax;  // also the first finite maximum
+      }
+      if (__any(grow[0] || grow[1])) {
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) {
+          const float m_ref = grow[ct] ? m_new[ct] : m_run[ct];
+          const float alpha = grow[ct] ? __builtin_amdgcn_exp2f(m_run[ct] - m_ref) : 1.f;
           l_part[ct] *= alpha;
 #pragma unroll
           for (int dt = 0; dt < 8; ++dt) acc[ct][dt] *= alpha;
           m_run[ct] = m_ref;
         }
+      }
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct) {
         // nothing visible yet (m_run = -inf): every score is -inf and p = 0
         const float m_sub = fmaxf(m_run[ct], -3.0e38f);
 #pragma unroll
