@@ -307,7 +307,12 @@ __device__ __forceinline__ void decode_fp8_body(const DecodeArgs& a, const int b
     // an invalid page is skipped like the reference's Metal kernel
     if (bok) {
       const bool full = tb >= start_k && tb + NT <= kv_len;
-      fp8_compute<HG>(cur, full, jj, tb, start_k, kv_len, qB, kl2 * ksc, 256.0f * vsc, m_run, l_part, acc);
+      // the page scales enter their products here, at the item that uses them: a product hoisted
+      // to where the scale was loaded (the previous item) would wait there for every load in
+      // flight, the next item's pages included
+      float ks_ = ksc, vs_ = vsc;
+      asm volatile("" : "+v"(ks_), "+v"(vs_));
+      fp8_compute<HG>(cur, full, jj, tb, start_k, kv_len, qB, kl2 * ks_, 256.0f * vs_, m_run, l_part, acc);
     }
 
     if (unit_end) {
