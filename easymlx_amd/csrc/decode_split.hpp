@@ -121,10 +121,12 @@ template <int BITS>
 __host__ __device__ inline bool split_kv_ok(const AffineKV<BITS>& kv) { return kv.gs % 32 == 0; }
 __host__ __device__ inline bool split_kv_ok(const Fp8KV&) { return true; }
 
-// grid (nchunk, Hkv * head chunks, S), 64 threads; dynamic LDS: q rows [hc][D], p [hc][64]
-template <typename QT, typename KV>
+// grid (nchunk, Hkv * head chunks, S), 64 threads; dynamic LDS: q rows [hc][D], p [hc][64].
+// MAXH >= hc: the per-head registers (scores, maxima, sums, 4 accumulators per head) are
+// sized by it, so a GQA group of 4 holds a quarter of what 16 heads need (more waves in flight).
+template <typename QT, typename KV, int MAXH>
 __global__ __launch_bounds__(64) void decode_split(SplitArgs a, KV kv) {
-  constexpr int MAXH = 16, MAXD = 256;
+  constexpr int MAXD = 256;
   extern __shared__ float dyn_lds[];
   const int lane = threadIdx.x;
   const int c = blockIdx.x, s = blockIdx.z;

@@ -345,8 +345,11 @@ int launch_split(const emx::GenericArgs& ga, const KV& kv, float* part, hipStrea
   int nhc;
   split_geometry(ga.Hq, ga.Hkv, ga.max_blocks, ga.bs, sa.hc, nhc, sa.nchunk);
   const size_t lds = (size_t)sa.hc * (ga.D + 64) * sizeof(float);
-  hipLaunchKernelGGL((emx::decode_split<QT, KV>), dim3((unsigned)sa.nchunk, (unsigned)(ga.Hkv * nhc), (unsigned)ga.S),
-                     dim3(64), lds, st, sa, kv);
+  const dim3 grid((unsigned)sa.nchunk, (unsigned)(ga.Hkv * nhc), (unsigned)ga.S);
+  if (sa.hc <= 4)
+    hipLaunchKernelGGL((emx::decode_split<QT, KV, 4>), grid, dim3(64), lds, st, sa, kv);
+  else
+    hipLaunchKernelGGL((emx::decode_split<QT, KV, 16>), grid, dim3(64), lds, st, sa, kv);
   if (int r = check_launch("decode_split")) return r;
   hipLaunchKernelGGL((emx::decode_split_merge<QT>), dim3((unsigned)(ga.Hkv * nhc), (unsigned)ga.S), dim3(256), 0, st,
                      sa);
