@@ -97,6 +97,44 @@ __device__ __forceinline__ void val8(const AffineKV<BITS>& kv, int blk, int off8
   }
 }
 
+// Affine pages, loads apart from their use: the raw words, scale and bias of one 32-dim K
+// piece (key32 split in two, so that every piece's loads can leave before the first is
+// decoded).
+template <int BITS>
+struct KPieceRaw {
+  uint32_t w[BITS];
+  h16 sc, bi;
+};
+template <int BITS>
+__device__ __forceinline__ void key32_load(const AffineKV<BITS>& kv, int blk, int off, int h, int d0,
+                                           KPieceRaw<BITS>& r) {
+  constexpr int PW = 32 / BITS;
+  const size_t ph = (size_t)blk * kv.Hkv + h;
+  const uint32_t* w = kv.kc + (ph * kv.bs + off) * (kv.D / PW) + d0 / PW;
+  const size_t si = (ph * (kv.D / kv.gs) + d0 / kv.gs) * kv.bs + off;
+#pragma unroll
+  for (int i = 0; i < BITS; ++i) r.w[i] = w[i];
+  r.sc = kv.ks[si];
+  r.bi = kv.kb[si];
+}
+template <int BITS>
+__device__ __forceinline__ void key32_decode(const KPieceRaw<BITS>& r, float (&x)[32]) {
+  constexpr int PW = 32 / BITS;
+  const float sc = (float)r.sc, bi = (float)r.bi;
+#pragma unroll
+  for (int i = 0; i < BITS; ++i)
+#pragma unroll
+    for (int j = 0; j < PW; ++j) x[PW * i + j] = fmaf(sc, (float)((r.w[i] >> (j * BITS)) & ((1u << BITS) - 1u)), bi);
+}
+template <typename KV>
+struct AffineBits {
+  static constexpr int value = 0;
+};
+template <int BITS>
+struct AffineBits<AffineKV<BITS>> {
+  static constexpr int value = BITS;
+};
+
 __device__ __forceinline__ void key32(const Fp8KV& kv, int blk, int off, int h, int d0, float (&x)[32]) {
   const uint32_t* p = reinterpret_cast<const uint32_t*>(kv.k + (((size_t)blk * kv.bs + off) * kv.Hkv + h) * kv.D + d0);
   const float sc = kv.ks[blk];
@@ -165,27 +203,48 @@ __global__ __launch_bounds__(64) void decode_split(SplitArgs a, KV kv) {
     float sc[MAXH];
 #pragma unroll
     for (int h = 0; h < MAXH; ++h) sc[h] = 0.f;
-    if (ok) {
+    auto dot32 = [&](const float (&x)[32], const int d0) {
+#pragma unroll
+      for (int h = 0; h < MAXH; ++h) {
+        if (h < nh) {
+          const float4* qv = reinterpret_cast<const float4*>(qs + h * D + d0);
+          float t = sc[h];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const float4 q4 = qv[j];
+            t = fmaf(q4.x, x[4 * j], t);
+            t = fmaf(q4.y, x[4 * j + 1], t);
+            t = fmaf(q4.z, x[4 * j + 2], t);
+            t = fmaf(q4.w, x[4 * j + 3], t);
+          }
+          sc[h] = t;
+        }
+      }
+    };
+    if constexpr (AffineBits<KV>::value > 0) {
+      // every piece's loads first (one round trip for the key), then decode and dot
+      constexpr int BITS = AffineBits<KV>::value;
+      const int off = pos % a.bs;
+      KPieceRaw<BITS> raw[MAXD / 32];
+      if (ok) {
+#pragma unroll
+        for (int pc = 0; pc < MAXD / 32; ++pc)
+          if (32 * pc < D) key32_load(kv, blk, off, kvh, 32 * pc, raw[pc]);
+#pragma unroll
+        for (int pc = 0; pc < MAXD / 32; ++pc) {
+          if (32 * pc < D) {
+            float x[32];
+            key32_decode(raw[pc], x);
+            dot32(x, 32 * pc);
+          }
+        }
+      }
+    } else if (ok) {
       const int off = pos % a.bs;
       for (int d0 = 0; d0 < D; d0 += 32) {
         float x[32];
         key32(kv, blk, off, kvh, d0, x);
-#pragma unroll
-        for (int h = 0; h < MAXH; ++h) {
-          if (h < nh) {
-            const float4* qv = reinterpret_cast<const float4*>(qs + h * D + d0);
-            float t = sc[h];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-              const float4 q4 = qv[j];
-              t = fmaf(q4.x, x[4 * j], t);
-              t = fmaf(q4.y, x[4 * j + 1], t);
-              t = fmaf(q4.z, x[4 * j + 2], t);
-              t = fmaf(q4.w, x[4 * j + 3], t);
-            }
-            sc[h] = t;
-          }
-        }
+        dot32(x, d0);
       }
     }
     // ---- online softmax (base 2) over the wave, one head at a time
@@ -208,27 +267,34 @@ __global__ __launch_bounds__(64) void decode_split(SplitArgs a, KV kv) {
     }
     __syncthreads();
     // ---- values: lane takes dims lane + 64 i; keys in groups of 8 (one page each)
+    // (the page of key group t8 is lane t8's page from the score pass, not a second table read)
     const int nk = min(64, c1 - base);
+    auto pv8 = [&](const float (&v)[8], const int t8, const int i) {
+#pragma unroll
+      for (int h = 0; h < MAXH; ++h) {
+        if (h < nh) {
+          float t = acc[h][i];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) t = fmaf(ps[h * 64 + t8 + j], v[j], t);
+          acc[h][i] = t;
+        }
+      }
+    };
+    auto group_page = [&](const int t8) {  // -1: no live page (its probabilities are zero)
+      const int b = __builtin_amdgcn_readlane(pos < kl ? blk : -1, t8);
+      return b >= 0 && b < a.nb ? b : -1;
+    };
     for (int t8 = 0; t8 < nk; t8 += 8) {
-      const int pt = base + t8;
-      const int b = pt < kl ? bt[pt / a.bs] : -1;
-      if (b < 0 || b >= a.nb) continue;  // its probabilities are zero
-      const int off8 = pt % a.bs;
+      const int b = group_page(t8);
+      if (b < 0) continue;
+      const int off8 = (base + t8) % a.bs;
 #pragma unroll
       for (int i = 0; i < MAXD / 64; ++i) {
         const int d = lane + 64 * i;
         if (d < D) {
           float v[8];
           val8(kv, b, off8, kvh, d, v);
-#pragma unroll
-          for (int h = 0; h < MAXH; ++h) {
-            if (h < nh) {
-              float t = acc[h][i];
-#pragma unroll
-              for (int j = 0; j < 8; ++j) t = fmaf(ps[h * 64 + t8 + j], v[j], t);
-              acc[h][i] = t;
-            }
-          }
+          pv8(v, t8, i);
         }
       }
     }
@@ -267,21 +333,48 @@ __global__ __launch_bounds__(256) void decode_split_merge(SplitArgs a) {
   QT* out = reinterpret_cast<QT*>(a.out) + ((size_t)s * a.Hq + (size_t)kvh * HG + h0) * D;
   const float* part = a.part + (((size_t)s * gridDim.x + blockIdx.x) * a.nchunk) * (size_t)a.hc * (D + 2);
   const size_t stride = (size_t)a.hc * (D + 2);
+  // every chunk's (m, l) into LDS at once (one round of loads), then each head's maximum and
+  // the chunk weights 2^(m_c - M) there; the per-dim sums below are independent loads
+  extern __shared__ float mlw[];  // [hc][nchunk]: m, then the weight; [hc][nchunk]: l; [hc]: L
+  float* wt = mlw;
+  float* lt = mlw + a.hc * a.nchunk;
+  float* Lh = lt + a.hc * a.nchunk;
+  for (int e = threadIdx.x; e < nh * nc; e += 256) {
+    const int h = e / nc, c = e % nc;
+    const float* ph = part + c * stride + (size_t)h * (D + 2);
+    wt[h * a.nchunk + c] = ph[D];
+    lt[h * a.nchunk + c] = ph[D + 1];
+  }
+  __syncthreads();
+  if (threadIdx.x < nh) {
+    const int h = threadIdx.x;
+    float M = -INFINITY;
+    for (int c = 0; c < nc; ++c) M = fmaxf(M, wt[h * a.nchunk + c]);
+    float L = 0.f;
+    for (int c = 0; c < nc; ++c) {
+      const float mc = wt[h * a.nchunk + c];
+      const float f = M == -INFINITY || mc == -INFINITY ? 0.f : exp2f(mc - M);  // a chunk without a live key: 0
+      wt[h * a.nchunk + c] = f;
+      L = fmaf(f, lt[h * a.nchunk + c], L);
+    }
+    Lh[h] = L;
+  }
+  __syncthreads();
   for (int e = threadIdx.x; e < nh * D; e += 256) {
     const int h = e / D, d = e % D;
-    float M = -INFINITY;
-    for (int c = 0; c < nc; ++c) M = fmaxf(M, part[c * stride + (size_t)h * (D + 2) + D]);
-    float O = 0.f, L = 0.f;
-    if (M != -INFINITY) {
-      for (int c = 0; c < nc; ++c) {
-        const float* ph = part + c * stride + (size_t)h * (D + 2);
-        const float mc = ph[D];
-        if (mc == -INFINITY) continue;  // a chunk without a live key
-        const float f = exp2f(mc - M);
-        O = fmaf(f, ph[d], O);
-        L = fmaf(f, ph[D + 1], L);
-      }
+    const float* ph = part + (size_t)h * (D + 2) + d;
+    const float* w = wt + h * a.nchunk;
+    float O = 0.f;
+    int c = 0;
+    for (; c + 4 <= nc; c += 4) {
+      const float x0 = ph[c * stride], x1 = ph[(c + 1) * stride], x2 = ph[(c + 2) * stride], x3 = ph[(c + 3) * stride];
+      O = fmaf(w[c], x0, O);
+      O = fmaf(w[c + 1], x1, O);
+      O = fmaf(w[c + 2], x2, O);
+      O = fmaf(w[c + 3], x3, O);
     }
+    for (; c < nc; ++c) O = fmaf(w[c], ph[c * stride], O);
+    const float L = Lh[h];
     from_f32(L > 0.f ? O / L : 0.f, out + (size_t)h * D + d);
   }
 }

@@ -325,6 +325,15 @@ size_t split_workspace_bytes(int num_seqs, int num_q_heads, int num_kv_heads, in
   return (size_t)num_seqs * num_kv_heads * nhc * nchunk * hc * (head_dim + 2) * sizeof(float);
 }
 
+// The merge keeps every chunk's weight and sum of a workgroup's heads in LDS: at most
+// 64 KiB (contexts up to ~500k tokens at 16 heads a workgroup); longer ones take the
+// generic kernel.
+bool split_merge_lds_ok(const emx::GenericArgs& ga) {
+  int hc, nhc, nchunk;
+  split_geometry(ga.Hq, ga.Hkv, ga.max_blocks, ga.bs, hc, nhc, nchunk);
+  return (2 * (size_t)hc * nchunk + hc) * sizeof(float) <= 65536;
+}
+
 template <typename QT, typename KV>
 int launch_split(const emx::GenericArgs& ga, const KV& kv, float* part, hipStream_t st) {
   emx::SplitArgs sa;
@@ -351,8 +360,9 @@ int launch_split(const emx::GenericArgs& ga, const KV& kv, float* part, hipStrea
   else
     hipLaunchKernelGGL((emx::decode_split<QT, KV, 16>), grid, dim3(64), lds, st, sa, kv);
   if (int r = check_launch("decode_split")) return r;
-  hipLaunchKernelGGL((emx::decode_split_merge<QT>), dim3((unsigned)(ga.Hkv * nhc), (unsigned)ga.S), dim3(256), 0, st,
-                     sa);
+  const size_t merge_lds = (2 * (size_t)sa.hc * sa.nchunk + sa.hc) * sizeof(float);  // chunk weights and sums
+  hipLaunchKernelGGL((emx::decode_split_merge<QT>), dim3((unsigned)(ga.Hkv * nhc), (unsigned)ga.S), dim3(256),
+                     merge_lds, st, sa);
   return check_launch("decode_split_merge");
 }
 
@@ -364,7 +374,7 @@ int launch_generic_only(const emx::GenericArgs& ga, const KV& kv, hipStream_t st
 template <typename QT, typename KV>
 int launch_generic(const emx::GenericArgs& ga, const KV& kv, hipStream_t st, void* ws = nullptr,
                    size_t ws_bytes = 0) {
-  if (ga.decode && ws && ga.S == ga.T && emx::split_kv_ok(kv) &&
+  if (ga.decode && ws && ga.S == ga.T && emx::split_kv_ok(kv) && split_merge_lds_ok(ga) &&
       ws_bytes >= (size_t)kPartialsInt * sizeof(int) +
                       split_workspace_bytes(ga.S, ga.Hq, ga.Hkv, ga.D, ga.max_blocks, ga.bs) &&
       split_workspace_bytes(ga.S, ga.Hq, ga.Hkv, ga.D, ga.max_blocks, ga.bs) > 0)
