@@ -379,12 +379,12 @@ def aux_c4(dev):
 
 def aux_shapes(dev):
     """The c2 batch (seed 2 lengths, 4-bit, group 64) at other page sizes and head sizes: page 16 (the
-    reference's PageCacheConfig default), 32 and 64, and head_dim 256, each over its own rotated pools."""
+    reference's PageCacheConfig default), 32 and 64, and head_dim 64 and 256, each over its own rotated pools."""
     from easymlx_amd.workloads import decode_workload
 
     res = {}
     for name, kw in (("page16", dict(block_size=16)), ("page32", dict(block_size=32)),
-                     ("page64", dict(block_size=64)), ("d256", dict(head_dim=256))):
+                     ("page64", dict(block_size=64)), ("d64", dict(head_dim=64)), ("d256", dict(head_dim=256))):
         wl = decode_workload(name, seed=2, bits=4, **kw)
         st = Setup(wl, 1.0, dev)
         warm(st.call, 0.3)
