@@ -11,7 +11,8 @@
 //   decode_split: one wave per (sequence, kv head, <= 16 query heads, chunk of
 //     kSplitChunk keys).  The query rows sit in LDS; per 64-key step lane L
 //     takes key L: its K row 32 dims at a time through the cache's loader
-//     (vector loads of the packed codes, the group's scale and bias) against
+//     (vector loads of the packed codes, the group's scale and bias; on affine
+//     pages every piece of the row is loaded before the first is decoded) against
 //     every query head of the GQA group, an online softmax in base 2 over the
 //     wave, then lane L takes dims L, L + 64, .. and walks the 64 keys in
 //     groups of 8 (one value word of 4-bit pages) with the probabilities from
@@ -19,6 +20,9 @@
 //   decode_split_merge: one workgroup per (sequence, kv head, head chunk)
 //     combines the chunks: O = sum 2^(m_c - M) acc_c, L = sum 2^(m_c - M) l_c,
 //     out = O / L (page_attention.py:2006-2059); zero rows for empty sequences.
+//     Every chunk's (m, l) goes to LDS in one round of loads and the weights
+//     2^(m_c - M) are formed there, so each output value is one pass of
+//     independent loads over the chunks.
 //
 // Chunks start on 64-key boundaries (the first one at the window start rounded
 // down); keys outside [start_k, kv_len) or on pages with an invalid id are
