@@ -93,6 +93,8 @@ SPLIT_CASES = [
     ("affine", 64, 8, 8, 2, 8, 32, (1, 900), 9, 0),
     ("affine", 96, 32, 24, 8, 4, 32, (60, 1200), 5, 0),      # GQA 3
     ("affine", 128, 128, 64, 2, 4, 64, (300, 2000), 3, 0),   # GQA 32: two head chunks per kv head
+    ("affine", 64, 128, 8, 2, 4, 64, (16000, 30000), 3, 0),  # 60-120 chunks per row merged through LDS
+    ("affine", 256, 64, 16, 4, 8, 64, (20000, 24000), 2, 5000),  # long rows under a window
     ("dense", 256, 16, 32, 8, None, 64, (1, 2000), 6, 0),
     ("dense", 96, 32, 12, 4, None, 64, (1, 700), 5, 99),
 ]
