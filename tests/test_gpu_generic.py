@@ -130,3 +130,20 @@ def test_split_decode_shapes(cuda, case):
     torch.cuda.synchronize()
     assert_attention_close(got, oracle_expected(wl, sliding_window=window), f"split decode {case}")
     assert np.array_equal(run().float().cpu().numpy(), got), "repeat differs"
+
+
+def test_split_decode_very_wide_table_takes_generic(cuda):
+    """A block table wider than the split-K merge's LDS holds (5000 pages of 128 tokens: more
+    than 2,500 chunks per row) sends the decode to the generic kernel; same results."""
+    print("[split decode wide table]", flush=True)
+    wl = decode_workload(seed=77, num_seqs=3, num_q_heads=8, num_kv_heads=2, head_dim=64, block_size=128,
+                         ctx_range=(100, 900), bits=4, group_size=64)
+    view = gpu_cache(wl, cuda)
+    wide = np.full((wl.block_tables.shape[0], 5000), -1, np.int32)
+    wide[:, :wl.block_tables.shape[1]] = wl.block_tables
+    q = torch.from_numpy(wl.q).to(cuda)
+    qsl = torch.from_numpy(wl.query_start_loc).to(cuda)
+    out = paged_attention(q, view.k_codes, view.v_codes, torch.from_numpy(wide).to(cuda), view.kv_lens, qsl,
+                          k_scales=view.k_scales, k_biases=view.k_biases, v_scales=view.v_scales,
+                          v_biases=view.v_biases, bits=4, group_size=64, single_token_decode=True)
+    assert_attention_close(out.float().cpu().numpy(), oracle_expected(wl), "wide table")
